@@ -1,0 +1,215 @@
+/*
+ * irontensor_hip.h -- C ABI of the MI355X (gfx950) matmul path for IronTensor.
+ *
+ * This is the drop-in boundary that IronTensor's Rust ops API binds through `extern "C"` (the Rust
+ * side is shown in INTEGRATION.md). Everything is plain pointers and sizes: no Rust, C++ or torch
+ * types cross it.
+ *
+ * Conventions
+ *   - Every function returns it_status (0 == IT_OK). On failure a thread-local message is left in
+ *     it_last_error(). Argument errors are detected before any device work is enqueued.
+ *   - Matrices are row-major (IronTensor tensors are contiguous row-major, src/tensor.rs:11-302).
+ *   - One context owns one HIP stream on one device. All work is stream-ordered on it; a context is
+ *     not thread-safe (IronTensor's CommandBatch state is thread-local, src/command_batch.rs:49-53).
+ *   - Device buffers come from it_malloc (a caching arena over hipMalloc) or any hipMalloc'd memory;
+ *     the caller owns them. Library scratch (split-K partials) belongs to the context.
+ *   - it_dtype values follow the reference's Precision enum order (src/precision.rs:1-6).
+ */
+#ifndef IRONTENSOR_HIP_H
+#define IRONTENSOR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum it_status {
+    IT_OK = 0,
+    IT_ERR_INNER_DIM = 1,   /* TensorError::InnerDimensionMismatch (src/error.rs:28-33) */
+    IT_ERR_SHAPE = 2,       /* TensorError::ShapeMismatch (src/error.rs:9-14) */
+    IT_ERR_PRECISION = 3,   /* TensorError::PrecisionMismatch (src/error.rs:22-27) */
+    IT_ERR_DIMS = 4,        /* TensorError::UnsupportedDimensions (src/error.rs:15-21) */
+    IT_ERR_INVALID = 5,     /* TensorError::InvalidValue (src/error.rs:38-42): bad enum, ld, flag */
+    IT_ERR_NULL = 6,        /* a required pointer is NULL */
+    IT_ERR_OOM = 7,         /* device allocation failed (reference panics, src/tensor.rs:71-74) */
+    IT_ERR_NO_DEVICE = 8,   /* no HIP device / bad ordinal (reference panics, src/device.rs:18-20) */
+    IT_ERR_HIP = 9,         /* any other HIP runtime error */
+    IT_ERR_NOT_READY = 10   /* it_event_query: work not finished yet (not a failure) */
+} it_status;
+
+typedef enum it_dtype { IT_F32 = 0, IT_F16 = 1, IT_BF16 = 2 } it_dtype;
+typedef enum it_op { IT_OP_N = 0, IT_OP_T = 1 } it_op;
+
+typedef struct it_context it_context;
+typedef struct it_event it_event;
+
+/* ---------------------------------------------------------------- runtime (device.rs, command_batch.rs) */
+
+/* Replaces MetalContext::new/global (src/device.rs:15-29): selects `device`, creates the stream. */
+it_status it_init(int device, it_context **out_ctx);
+/* Drains the stream, releases cached memory and the stream. */
+it_status it_shutdown(it_context *ctx);
+/* Thread-local message for the last failing call on this thread ("" if none). */
+const char *it_last_error(void);
+const char *it_status_string(it_status status);
+/* Number of visible HIP devices (0 when none); never fails. */
+int it_device_count(void);
+/* Device name and compute-unit count, for reports. */
+it_status it_device_info(it_context *ctx, char *name, size_t name_len, int *num_cus,
+                         int *clock_khz);
+
+/* Device memory (replaces per-op MTLBuffer allocation, src/tensor.rs:63-88, src/ops/kernel.rs:70-80). */
+it_status it_malloc(it_context *ctx, size_t bytes, void **out_ptr);
+it_status it_free(it_context *ctx, void *ptr);
+/* Bytes currently handed out (gpu_memory_allocated, src/device.rs:43-71). */
+size_t it_mem_allocated(it_context *ctx);
+/* Returns cached blocks to the device. */
+it_status it_empty_cache(it_context *ctx);
+
+/* Copies. h2d and d2d are stream-ordered; d2h blocks until the data is on the host (the reference's
+ * as_f32_slice reads after a sync, src/tensor.rs:136-159). */
+it_status it_memcpy_h2d(it_context *ctx, void *dst, const void *src, size_t bytes);
+it_status it_memcpy_d2h(it_context *ctx, void *dst, const void *src, size_t bytes);
+it_status it_memcpy_d2d(it_context *ctx, void *dst, const void *src, size_t bytes);
+/* Zero-fill with a kernel (safe to capture in a graph; replaces Tensor::zeros' CPU memset). */
+it_status it_zero(it_context *ctx, void *dst, size_t bytes);
+
+/* CommandBatch::sync (src/command_batch.rs:191-207). */
+it_status it_stream_sync(it_context *ctx);
+/* The HIP stream (hipStream_t) the context launches on, for callers that interoperate. */
+void *it_stream(it_context *ctx);
+/* commit_async / is_async_complete / wait_for_completion (src/command_batch.rs:228-272). */
+it_status it_event_create(it_context *ctx, it_event **out_ev);
+it_status it_event_record(it_context *ctx, it_event *ev);
+it_status it_event_query(it_event *ev);    /* IT_OK when complete, IT_ERR_NOT_READY otherwise */
+it_status it_event_sync(it_event *ev);
+it_status it_event_elapsed_ms(it_event *start, it_event *end, float *ms);
+it_status it_event_destroy(it_event *ev);
+
+/* ---------------------------------------------------------------- GEMM */
+
+/* Epilogue flags (it_epilogue.flags). */
+#define IT_EPI_BIAS 0x1u        /* C[m,n] += bias[n]            (Linear bias, src/nn/linear.rs:8-18) */
+#define IT_EPI_SWIGLU 0x2u      /* dual-B: C = silu(op(A).op(B)) * (op(A).op(B2)) (ffn, elementwise.metal:100-115) */
+#define IT_EPI_CAUSAL 0x4u      /* C[m,n] = -inf where n > m + causal_offset (attention.metal:186-207) */
+
+typedef struct it_epilogue {
+    uint32_t flags;
+    const float *bias;      /* IT_EPI_BIAS: [N] f32 */
+    const void *B2;         /* IT_EPI_SWIGLU: up-projection weight, same dtype/layout/ldb/strideB as B */
+    void *gate_out;         /* IT_EPI_SWIGLU (optional): pre-activation gate, out dtype, ldc/strideC */
+    void *up_out;           /* IT_EPI_SWIGLU (optional): pre-activation up, out dtype, ldc/strideC */
+    int64_t causal_offset;  /* IT_EPI_CAUSAL: mask columns n > m + causal_offset */
+} it_epilogue;
+
+/*
+ * C[b] = alpha * op(A[b]) . op(B[b]) + beta * C[b]  (then the epilogue), for b in [0, batch).
+ *   op(A) is [M,K]: transA == IT_OP_N -> A stored [M,K], lda >= K; IT_OP_T -> A stored [K,M], lda >= M.
+ *   op(B) is [K,N]: transB == IT_OP_N -> B stored [K,N], ldb >= N; IT_OP_T -> B stored [N,K], ldb >= K.
+ *   C stored [M,N], ldc >= N. stride* are element strides between batch matrices (0 = broadcast).
+ * dtype_in IT_F32: FP32 MFMA; IT_BF16: BF16 MFMA with FP32 accumulation. dtype_out IT_F32 or IT_BF16
+ * (RNE of the FP32 result, as bfloat(sum) in src/shaders/bf16_ops.metal:93).
+ * Replaces MPSMatrixMultiplication with transposeLeft/transposeRight (src/ops/mps_gemm.rs:169-181,
+ * :278-290, :390-402, :519-537) and every Metal GEMM kernel (src/shaders/gemm.metal,
+ * src/shaders/backward/gemm.metal, src/shaders/bf16_ops.metal:25-122).
+ * epi may be NULL. beta != 0 is not combined with IT_EPI_SWIGLU or IT_EPI_CAUSAL.
+ */
+it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_op transB,
+                  int64_t M, int64_t N, int64_t K, float alpha,
+                  const void *A, int64_t lda, int64_t strideA,
+                  const void *B, int64_t ldb, int64_t strideB,
+                  float beta, void *C, int64_t ldc, int64_t strideC,
+                  int64_t batch, const it_epilogue *epi);
+
+/* Validates it_gemm's arguments without touching the device (same status and message as it_gemm). */
+it_status it_gemm_check(it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_op transB,
+                        int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, int64_t strideA,
+                        const void *B, int64_t ldb, int64_t strideB, float beta, const void *C,
+                        int64_t ldc, int64_t strideC, int64_t batch, const it_epilogue *epi);
+
+/* ---------------------------------------------------------------- precision (src/ops/bf16_ops/precision.rs) */
+
+/* to_bf16_gpu (precision.rs:15-46): RNE, NaN stays NaN. */
+it_status it_f32_to_bf16(it_context *ctx, const float *src, uint16_t *dst, int64_t n);
+/* to_f32_gpu (precision.rs:48-78): exact widening. */
+it_status it_bf16_to_f32(it_context *ctx, const uint16_t *src, float *dst, int64_t n);
+
+/* ---------------------------------------------------------------- attention contractions */
+
+/*
+ * Softmax over rows of an FP32 matrix (src/shaders/softmax.metal), optionally causal: columns
+ * c > r + causal_offset are treated as -inf and written as 0. P may be FP32 or BF16 (dtype_p).
+ * rows are grouped into `batch` matrices of `rows` x `cols` (row r of each matrix is its local row).
+ */
+it_status it_softmax_rows(it_context *ctx, const float *S, void *P, it_dtype dtype_p,
+                          int64_t batch, int64_t rows, int64_t cols, int causal,
+                          int64_t causal_offset);
+
+/*
+ * Softmax backward dX = Y * (dY - rowdot(dY, Y)) (src/shaders/backward/softmax.metal:22-45).
+ * Y is FP32 or BF16 (dtype_y, the dtype P was stored in); dX is FP32 or BF16 (dtype_dx).
+ * Causal: columns c > r are written as 0 without reading.
+ */
+it_status it_softmax_backward(it_context *ctx, const float *dY, const void *Y, it_dtype dtype_y,
+                              void *dX, it_dtype dtype_dx, int64_t batch, int64_t rows,
+                              int64_t cols, int causal);
+
+/*
+ * Per-head operand layout: element (bh, s, d) lives at
+ *   (bh / heads) * batch_stride + (bh % heads) * head_stride + s * row_stride + d.
+ * [B,H,S,D] contiguous: heads = 1, batch_stride = S*D, head_stride = 0, row_stride = D.
+ * [B,S,H,D] contiguous: heads = H, batch_stride = S*H*D, head_stride = D, row_stride = H*D.
+ * A NULL layout pointer means [B,H,S,D] contiguous.
+ */
+typedef struct it_attn_layout {
+    int64_t heads;
+    int64_t batch_stride;
+    int64_t head_stride;
+    int64_t row_stride;
+} it_attn_layout;
+
+/*
+ * Forward attention contractions (ops::attention after its layout transposes,
+ * src/ops/attention.rs:286-377): Sc = scale * Q.K^T (NT GEMM; causal tiles above the diagonal are
+ * skipped), P = softmax(Sc) (causal: columns > row are 0), O = P.V (NN GEMM; causal: only k <= row).
+ * Q, O: [BH, seq_q, D] through q_layout; K, V: [BH, seq_kv, D] through kv_layout (NULL = q_layout).
+ * Sc: [BH, seq_q, seq_kv] f32 workspace; P: [BH, seq_q, seq_kv] of dtype; O: f32.
+ * dtype IT_F32: everything FP32. IT_BF16: Q, K, V and P are BF16 (FP32 accumulation).
+ * causal requires seq_q == seq_kv (as the reference asserts, src/ops/attention.rs:346-350).
+ */
+it_status it_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
+                               int64_t seq_kv, int64_t head_dim, float scale, int causal,
+                               const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                               const void *Q, const void *K, const void *V,
+                               float *Sc, void *P, float *O);
+
+/*
+ * attention_backward_recompute (src/train/helpers.rs:120-193) on [BH, seq, D] operands sharing one
+ * layout: recompute Sc, P; dV = P^T.dO (TN); dP = dO.V^T (NT); dS = softmax_backward(dP, P);
+ * dQ = scale * dS.K (NN); dK = scale * dS^T.Q (TN).
+ * IT_F32: all FP32. IT_BF16: Q, K, V, dO BF16; Sc, dP FP32; P, dS BF16; dQ, dK, dV FP32.
+ * Workspaces Sc, dP: [BH,S,S] f32; P, dS: [BH,S,S] of dtype.
+ */
+it_status it_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
+                                int64_t head_dim, float scale, int causal,
+                                const it_attn_layout *layout,
+                                const void *dO, const void *Q, const void *K, const void *V,
+                                float *Sc, void *P, float *dP, void *dS,
+                                float *dQ, float *dK, float *dV);
+
+/* ---------------------------------------------------------------- profiling (src/profile) */
+
+/* Shape-keyed per-launch GPU timing with hipEvents on the context's stream, mirroring
+ * Profiler::record_matmul_shape (src/ops/mps_gemm.rs:22-30,84-88). enable=0 turns it off. */
+it_status it_profiler_enable(it_context *ctx, int enable);
+it_status it_profiler_reset(it_context *ctx);
+/* Writes a JSON object {"<kernel>|<shape key>": {"calls": n, "total_ms": t}, ...} (syncs first).
+ * Returns IT_ERR_INVALID with *needed set when buf_len is too small. */
+it_status it_profiler_report(it_context *ctx, char *buf, size_t buf_len, size_t *needed);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IRONTENSOR_HIP_H */

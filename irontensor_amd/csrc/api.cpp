@@ -1,0 +1,378 @@
+// C ABI entry points for the contractions: argument validation (the reference's TensorError cases,
+// src/ops/mps_gemm.rs:45-108,439-452), GEMM dispatch, precision conversion, and the attention
+// forward / backward compositions (src/ops/attention.rs:286-377, src/train/helpers.rs:120-193).
+#include <cmath>
+#include <cstdint>
+#include <string>
+
+#include "internal.hpp"
+
+using it::fail;
+
+namespace {
+
+const char *dtype_name(it_dtype d) {
+    switch (d) {
+    case IT_F32: return "FP32";
+    case IT_F16: return "FP16";
+    case IT_BF16: return "BF16";
+    }
+    return "unknown";
+}
+
+bool vec_ok(const void *p, int elem_bytes, int64_t ld, int64_t s1, int64_t s2) {
+    const int64_t vec = 16 / elem_bytes;
+    return ((uintptr_t)p % 16 == 0) && ld % vec == 0 && s1 % vec == 0 && s2 % vec == 0;
+}
+
+std::string i64(int64_t v) { return std::to_string((long long)v); }
+
+}  // namespace
+
+extern "C" {
+
+it_status it_gemm_check(it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_op transB,
+                        int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, int64_t strideA,
+                        const void *B, int64_t ldb, int64_t strideB, float beta, const void *C,
+                        int64_t ldc, int64_t strideC, int64_t batch, const it_epilogue *epi) {
+    if (dtype_in != IT_F32 && dtype_in != IT_BF16)
+        return fail(IT_ERR_PRECISION, std::string("matmul: precision mismatch, expected FP32 or BF16, got ") +
+                                          dtype_name(dtype_in));
+    if (dtype_out != IT_F32 && dtype_out != IT_BF16)
+        return fail(IT_ERR_PRECISION, std::string("matmul: precision mismatch, expected FP32 or BF16 output, got ") +
+                                          dtype_name(dtype_out));
+    if ((transA != IT_OP_N && transA != IT_OP_T) || (transB != IT_OP_N && transB != IT_OP_T))
+        return fail(IT_ERR_INVALID, "matmul: transA/transB must be IT_OP_N or IT_OP_T");
+    if (M < 0 || N < 0 || K < 0 || batch < 0)
+        return fail(IT_ERR_INVALID, "matmul: negative size (M=" + i64(M) + ", N=" + i64(N) +
+                                        ", K=" + i64(K) + ", batch=" + i64(batch) + ")");
+    const int64_t min_lda = transA == IT_OP_T ? M : K;
+    const int64_t min_ldb = transB == IT_OP_T ? K : N;
+    if (lda < (min_lda > 1 ? min_lda : 1))
+        return fail(IT_ERR_INVALID, "matmul: lda " + i64(lda) + " < " + i64(min_lda));
+    if (ldb < (min_ldb > 1 ? min_ldb : 1))
+        return fail(IT_ERR_INVALID, "matmul: ldb " + i64(ldb) + " < " + i64(min_ldb));
+    if (ldc < (N > 1 ? N : 1)) return fail(IT_ERR_INVALID, "matmul: ldc " + i64(ldc) + " < " + i64(N));
+    if (strideA < 0 || strideB < 0 || strideC < 0)
+        return fail(IT_ERR_INVALID, "matmul: negative batch stride");
+    const bool has_out = M > 0 && N > 0 && batch > 0;
+    if (has_out && !C) return fail(IT_ERR_NULL, "matmul: C is NULL");
+    if (has_out && K > 0 && (!A || !B)) return fail(IT_ERR_NULL, "matmul: A or B is NULL");
+    if (epi) {
+        const uint32_t known = IT_EPI_BIAS | IT_EPI_SWIGLU | IT_EPI_CAUSAL;
+        if (epi->flags & ~known) return fail(IT_ERR_INVALID, "matmul: unknown epilogue flags");
+        if ((epi->flags & IT_EPI_BIAS) && !epi->bias)
+            return fail(IT_ERR_NULL, "matmul: bias epilogue without a bias pointer");
+        if (epi->flags & IT_EPI_SWIGLU) {
+            if (!epi->B2 && has_out && K > 0)
+                return fail(IT_ERR_NULL, "matmul: SwiGLU epilogue without B2");
+            if (transA != IT_OP_N || transB != IT_OP_T)
+                return fail(IT_ERR_INVALID, "matmul: SwiGLU epilogue needs transA=N, transB=T (Y = X.W^T)");
+            if (epi->flags & (IT_EPI_BIAS | IT_EPI_CAUSAL))
+                return fail(IT_ERR_INVALID, "matmul: SwiGLU epilogue cannot be combined with bias or causal");
+        }
+        if ((epi->flags & (IT_EPI_SWIGLU | IT_EPI_CAUSAL)) && beta != 0.f)
+            return fail(IT_ERR_INVALID, "matmul: beta != 0 cannot be combined with SwiGLU or causal");
+    }
+    return IT_OK;
+}
+
+it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_op transB,
+                  int64_t M, int64_t N, int64_t K, float alpha,
+                  const void *A, int64_t lda, int64_t strideA,
+                  const void *B, int64_t ldb, int64_t strideB,
+                  float beta, void *C, int64_t ldc, int64_t strideC,
+                  int64_t batch, const it_epilogue *epi) {
+    it_status st = it_gemm_check(dtype_in, dtype_out, transA, transB, M, N, K, A, lda, strideA, B,
+                                 ldb, strideB, beta, C, ldc, strideC, batch, epi);
+    if (st != IT_OK) return st;
+    if (!ctx) return fail(IT_ERR_NULL, "matmul: ctx is NULL");
+    if (M == 0 || N == 0 || batch == 0) return IT_OK;
+
+    const int eb = dtype_in == IT_BF16 ? 2 : 4;
+    it::GemmArgs a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.sA_in = strideA;
+    a.sB_in = strideB;
+    a.sC_in = strideC;
+    a.batch_inner = batch;
+    a.batch = batch;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.out_bf16 = dtype_out == IT_BF16;
+    a.a_vec_ok = vec_ok(A, eb, lda, strideA, 0);
+    a.b_vec_ok = vec_ok(B, eb, ldb, strideB, 0);
+    if (epi) {
+        a.has_bias = (epi->flags & IT_EPI_BIAS) != 0;
+        a.bias = epi->bias;
+        if (epi->flags & IT_EPI_SWIGLU) {
+            a.dual = 1;
+            a.B2 = epi->B2;
+            a.G = epi->gate_out;
+            a.U = epi->up_out;
+            a.b_vec_ok = a.b_vec_ok && vec_ok(epi->B2, eb, ldb, strideB, 0);
+        }
+        if (epi->flags & IT_EPI_CAUSAL) {
+            a.causal = it::CAUSAL_WRITE;
+            a.causal_offset = epi->causal_offset;
+        }
+    }
+    return it::launch_gemm(ctx, dtype_in, transA == IT_OP_T, transB == IT_OP_T, a, "");
+}
+
+it_status it_f32_to_bf16(it_context *ctx, const float *src, uint16_t *dst, int64_t n) {
+    if (!ctx) return fail(IT_ERR_NULL, "to_bf16_gpu: ctx is NULL");
+    if (n < 0) return fail(IT_ERR_INVALID, "to_bf16_gpu: negative length");
+    if (n == 0) return IT_OK;
+    if (!src || !dst) return fail(IT_ERR_NULL, "to_bf16_gpu: NULL buffer");
+    return it::launch_f32_to_bf16(ctx->stream, src, dst, n);
+}
+
+it_status it_bf16_to_f32(it_context *ctx, const uint16_t *src, float *dst, int64_t n) {
+    if (!ctx) return fail(IT_ERR_NULL, "to_f32_gpu: ctx is NULL");
+    if (n < 0) return fail(IT_ERR_INVALID, "to_f32_gpu: negative length");
+    if (n == 0) return IT_OK;
+    if (!src || !dst) return fail(IT_ERR_NULL, "to_f32_gpu: NULL buffer");
+    return it::launch_bf16_to_f32(ctx->stream, src, dst, n);
+}
+
+it_status it_softmax_rows(it_context *ctx, const float *S, void *P, it_dtype dtype_p,
+                          int64_t batch, int64_t rows, int64_t cols, int causal,
+                          int64_t causal_offset) {
+    if (!ctx) return fail(IT_ERR_NULL, "softmax: ctx is NULL");
+    if (dtype_p != IT_F32 && dtype_p != IT_BF16)
+        return fail(IT_ERR_PRECISION, std::string("softmax: precision mismatch, expected FP32 or BF16, got ") +
+                                          dtype_name(dtype_p));
+    if (batch < 0 || rows < 0 || cols < 0) return fail(IT_ERR_INVALID, "softmax: negative size");
+    if (batch * rows * cols == 0) return IT_OK;
+    if (!S || !P) return fail(IT_ERR_NULL, "softmax: NULL buffer");
+    return it::launch_softmax_rows(ctx->stream, S, P, dtype_p == IT_BF16, batch, rows, cols,
+                                   causal != 0, causal_offset, rows * cols, rows * cols);
+}
+
+it_status it_softmax_backward(it_context *ctx, const float *dY, const void *Y, it_dtype dtype_y,
+                              void *dX, it_dtype dtype_dx, int64_t batch, int64_t rows,
+                              int64_t cols, int causal) {
+    if (!ctx) return fail(IT_ERR_NULL, "softmax_backward: ctx is NULL");
+    if ((dtype_y != IT_F32 && dtype_y != IT_BF16) || (dtype_dx != IT_F32 && dtype_dx != IT_BF16))
+        return fail(IT_ERR_PRECISION, "softmax_backward: precision mismatch, expected FP32 or BF16");
+    if (batch < 0 || rows < 0 || cols < 0) return fail(IT_ERR_INVALID, "softmax_backward: negative size");
+    if (batch * rows * cols == 0) return IT_OK;
+    if (!dY || !Y || !dX) return fail(IT_ERR_NULL, "softmax_backward: NULL buffer");
+    return it::launch_softmax_backward(ctx->stream, dY, Y, dtype_y == IT_BF16, dX,
+                                       dtype_dx == IT_BF16, batch, rows, cols, causal != 0);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ attention compositions
+
+namespace {
+
+struct AttnGeom {
+    int64_t bh, Sq, Skv, D;
+    it_attn_layout lay;     // Q, O, dQ, dO
+    it_attn_layout kv_lay;  // K, V, dK, dV
+};
+
+bool bad_layout(const it_attn_layout &l, int64_t head_dim) {
+    return l.heads < 1 || l.row_stride < head_dim || l.batch_stride < 0 || l.head_stride < 0;
+}
+
+it_status check_attention(const char *op, it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
+                          int64_t seq_kv, int64_t head_dim, const it_attn_layout *q_layout,
+                          const it_attn_layout *kv_layout, AttnGeom *g) {
+    if (!ctx) return fail(IT_ERR_NULL, std::string(op) + ": ctx is NULL");
+    if (dtype != IT_F32 && dtype != IT_BF16)
+        return fail(IT_ERR_PRECISION, std::string(op) + ": precision mismatch, expected FP32 or BF16, got " +
+                                          dtype_name(dtype));
+    if (bh < 0 || seq_q < 0 || seq_kv < 0 || head_dim < 0)
+        return fail(IT_ERR_INVALID, std::string(op) + ": negative size");
+    it_attn_layout lay{1, seq_q * head_dim, 0, head_dim};
+    if (q_layout) lay = *q_layout;
+    it_attn_layout kv{1, seq_kv * head_dim, 0, head_dim};
+    if (kv_layout)
+        kv = *kv_layout;
+    else if (q_layout)
+        kv = *q_layout;
+    if (bad_layout(lay, head_dim) || bad_layout(kv, head_dim))
+        return fail(IT_ERR_INVALID, std::string(op) + ": bad layout strides");
+    if (bh % lay.heads != 0 || bh % kv.heads != 0 || lay.heads != kv.heads)
+        return fail(IT_ERR_SHAPE, std::string(op) + ": shape mismatch, expected batch*heads divisible by heads " +
+                                      i64(lay.heads) + ", got " + i64(bh));
+    *g = AttnGeom{bh, seq_q, seq_kv, head_dim, lay, kv};
+    return IT_OK;
+}
+
+// Base GEMM arguments for a [S or D] x [S or D] contraction over the BH batch, with the per-head
+// operands addressed through the two-level layout and the [BH,S,S] workspaces contiguous.
+it::GemmArgs attn_args(const AttnGeom &g, int64_t M, int64_t N, int64_t K, int eb) {
+    it::GemmArgs a{};
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.batch = g.bh;
+    a.batch_inner = g.lay.heads;
+    a.alpha = 1.f;
+    (void)eb;
+    return a;
+}
+
+struct Operand {
+    const void *p;
+    int64_t ld, s_in, s_out;
+};
+
+Operand q_operand(const AttnGeom &g, const void *p) {
+    return Operand{p, g.lay.row_stride, g.lay.head_stride, g.lay.batch_stride};
+}
+
+Operand kv_operand(const AttnGeom &g, const void *p) {
+    return Operand{p, g.kv_lay.row_stride, g.kv_lay.head_stride, g.kv_lay.batch_stride};
+}
+
+// [BH, Sq, Skv] contiguous score-shaped workspace.
+Operand score_operand(const AttnGeom &g, const void *p) {
+    return Operand{p, g.Skv, g.Sq * g.Skv, g.lay.heads * g.Sq * g.Skv};
+}
+
+void set_A(it::GemmArgs &a, const Operand &o, int eb) {
+    a.A = o.p;
+    a.lda = o.ld;
+    a.sA_in = o.s_in;
+    a.sA_out = o.s_out;
+    a.a_vec_ok = vec_ok(o.p, eb, o.ld, o.s_in, o.s_out);
+}
+
+void set_B(it::GemmArgs &a, const Operand &o, int eb) {
+    a.B = o.p;
+    a.ldb = o.ld;
+    a.sB_in = o.s_in;
+    a.sB_out = o.s_out;
+    a.b_vec_ok = vec_ok(o.p, eb, o.ld, o.s_in, o.s_out);
+}
+
+void set_C(it::GemmArgs &a, const Operand &o, bool bf16_out) {
+    a.C = const_cast<void *>(o.p);
+    a.ldc = o.ld;
+    a.sC_in = o.s_in;
+    a.sC_out = o.s_out;
+    a.out_bf16 = bf16_out;
+}
+
+// Sc = scale * Q.K^T (causal tiles skipped), P = softmax(Sc).
+it_status attn_scores(it_context *ctx, it_dtype dtype, const AttnGeom &g, float scale, int causal,
+                      const void *Q, const void *K, float *Sc, void *P) {
+    const int eb = dtype == IT_BF16 ? 2 : 4;
+    it::GemmArgs a = attn_args(g, g.Sq, g.Skv, g.D, eb);
+    set_A(a, q_operand(g, Q), eb);
+    set_B(a, kv_operand(g, K), eb);
+    set_C(a, score_operand(g, Sc), false);
+    a.alpha = scale;
+    a.causal = causal ? it::CAUSAL_SKIP : it::CAUSAL_NONE;
+    it_status st = it::launch_gemm(ctx, dtype, false, true, a, "attn.S=QK^T");
+    if (st != IT_OK) return st;
+    return it::launch_softmax_rows(ctx->stream, Sc, P, dtype == IT_BF16, g.bh, g.Sq, g.Skv,
+                                   causal != 0, 0, g.Sq * g.Skv, g.Sq * g.Skv);
+}
+
+}  // namespace
+
+extern "C" {
+
+it_status it_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
+                               int64_t seq_kv, int64_t head_dim, float scale, int causal,
+                               const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                               const void *Q, const void *K, const void *V,
+                               float *Sc, void *P, float *O) {
+    AttnGeom g;
+    it_status st = check_attention("attention", ctx, dtype, bh, seq_q, seq_kv, head_dim, q_layout,
+                                   kv_layout, &g);
+    if (st != IT_OK) return st;
+    if (causal && seq_q != seq_kv)
+        return fail(IT_ERR_SHAPE, "attention: shape mismatch, expected seq_q == seq_kv for causal, got " +
+                                      i64(seq_q) + " and " + i64(seq_kv));
+    if (bh == 0 || seq_q == 0 || head_dim == 0) return IT_OK;
+    if (!Q || !O) return fail(IT_ERR_NULL, "attention: NULL buffer");
+    const int eb = dtype == IT_BF16 ? 2 : 4;
+    if (seq_kv > 0) {
+        if (!K || !V || !Sc || !P) return fail(IT_ERR_NULL, "attention: NULL buffer");
+        st = attn_scores(ctx, dtype, g, scale, causal, Q, K, Sc, P);
+        if (st != IT_OK) return st;
+    }
+    // With seq_kv == 0 this GEMM has K = 0 and writes zeros (the reference returns zeros).
+    // O = P.V (NN); with a causal P only k <= row contributes.
+    it::GemmArgs a = attn_args(g, g.Sq, g.D, g.Skv, eb);
+    set_A(a, score_operand(g, P), eb);
+    set_B(a, kv_operand(g, V), eb);
+    set_C(a, q_operand(g, O), false);
+    a.kmode = causal ? it::KMODE_LOWER : it::KMODE_FULL;
+    return it::launch_gemm(ctx, dtype, false, false, a, "attn.O=PV");
+}
+
+it_status it_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
+                                int64_t head_dim, float scale, int causal,
+                                const it_attn_layout *layout,
+                                const void *dO, const void *Q, const void *K, const void *V,
+                                float *Sc, void *P, float *dP, void *dS,
+                                float *dQ, float *dK, float *dV) {
+    AttnGeom g;
+    it_status st = check_attention("attention_backward", ctx, dtype, bh, seq, seq, head_dim, layout,
+                                   layout, &g);
+    if (st != IT_OK) return st;
+    if (bh == 0 || seq == 0 || head_dim == 0) return IT_OK;
+    if (!dO || !Q || !K || !V || !Sc || !P || !dP || !dS || !dQ || !dK || !dV)
+        return fail(IT_ERR_NULL, "attention_backward: NULL buffer");
+    const int eb = dtype == IT_BF16 ? 2 : 4;
+    st = attn_scores(ctx, dtype, g, scale, causal, Q, K, Sc, P);
+    if (st != IT_OK) return st;
+
+    // dV = P^T.dO (TN): op(A)[j][i] = P[i][j], nonzero only for i >= j under the causal mask.
+    it::GemmArgs a = attn_args(g, g.Sq, g.D, g.Sq, eb);
+    set_A(a, score_operand(g, P), eb);
+    set_B(a, q_operand(g, dO), eb);
+    set_C(a, kv_operand(g, dV), false);
+    a.kmode = causal ? it::KMODE_UPPER : it::KMODE_FULL;
+    if ((st = it::launch_gemm(ctx, dtype, true, false, a, "attn.dV=P^TdO")) != IT_OK) return st;
+
+    // dP = dO.V^T (NT); above-diagonal tiles are never read.
+    a = attn_args(g, g.Sq, g.Sq, g.D, eb);
+    set_A(a, q_operand(g, dO), eb);
+    set_B(a, kv_operand(g, V), eb);
+    set_C(a, score_operand(g, dP), false);
+    a.causal = causal ? it::CAUSAL_SKIP : it::CAUSAL_NONE;
+    if ((st = it::launch_gemm(ctx, dtype, false, true, a, "attn.dP=dOV^T")) != IT_OK) return st;
+
+    // dS = P * (dP - rowdot(dP, P))
+    st = it::launch_softmax_backward(ctx->stream, dP, P, dtype == IT_BF16, dS, dtype == IT_BF16,
+                                     g.bh, g.Sq, g.Sq, causal != 0);
+    if (st != IT_OK) return st;
+
+    // dQ = scale * dS.K (NN), dS lower-triangular under the mask.
+    a = attn_args(g, g.Sq, g.D, g.Sq, eb);
+    set_A(a, score_operand(g, dS), eb);
+    set_B(a, kv_operand(g, K), eb);
+    set_C(a, q_operand(g, dQ), false);
+    a.alpha = scale;
+    a.kmode = causal ? it::KMODE_LOWER : it::KMODE_FULL;
+    if ((st = it::launch_gemm(ctx, dtype, false, false, a, "attn.dQ=dSK")) != IT_OK) return st;
+
+    // dK = scale * dS^T.Q (TN)
+    a = attn_args(g, g.Sq, g.D, g.Sq, eb);
+    set_A(a, score_operand(g, dS), eb);
+    set_B(a, q_operand(g, Q), eb);
+    set_C(a, kv_operand(g, dK), false);
+    a.alpha = scale;
+    a.kmode = causal ? it::KMODE_UPPER : it::KMODE_FULL;
+    return it::launch_gemm(ctx, dtype, true, false, a, "attn.dK=dS^TQ");
+}
+
+}  // extern "C"

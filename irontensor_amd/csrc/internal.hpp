@@ -1,0 +1,140 @@
+// Internal declarations shared by the runtime, the dispatch layer and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "irontensor_hip.h"
+
+namespace it {
+
+// ------------------------------------------------------------------ errors
+
+// Records `msg` as this thread's last error and returns `st`.
+it_status fail(it_status st, const std::string &msg);
+it_status fail_hip(hipError_t err, const char *what);
+void clear_error();
+
+#define IT_HIP_TRY(expr)                                         \
+    do {                                                         \
+        hipError_t _e = (expr);                                  \
+        if (_e != hipSuccess) return ::it::fail_hip(_e, #expr);  \
+    } while (0)
+
+// ------------------------------------------------------------------ context
+
+struct ProfileRecord {
+    std::string key;
+    hipEvent_t start, stop;
+};
+
+struct ProfileStat {
+    int64_t calls = 0;
+    double total_ms = 0.0;
+};
+
+}  // namespace it
+
+struct it_context {
+    int device = 0;
+    int num_cus = 0;
+    int clock_khz = 0;
+    char name[256] = {0};
+    hipStream_t stream = nullptr;
+
+    // Caching allocator: freed blocks are kept per exact size and reused (single stream, so reuse
+    // is stream-ordered and needs no events).
+    std::map<void *, size_t> live;
+    std::multimap<size_t, void *> cache;
+    size_t bytes_live = 0;
+
+    // Library-owned scratch (split-K partials), grown on demand.
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+
+    // Profiler state.
+    bool profiling = false;
+    std::vector<it::ProfileRecord> pending;
+    std::vector<hipEvent_t> event_pool;
+    std::map<std::string, it::ProfileStat> stats;
+};
+
+struct it_event {
+    hipEvent_t ev = nullptr;
+};
+
+namespace it {
+
+// Grows the context scratch to at least `bytes` (synchronises before freeing the old block).
+it_status ensure_scratch(it_context *ctx, size_t bytes, void **out);
+
+// Profiler hooks around one kernel launch.
+void profile_begin(it_context *ctx, const std::string &key, hipEvent_t *start_out);
+void profile_end(it_context *ctx, const std::string &key, hipEvent_t start);
+
+// ------------------------------------------------------------------ kernel launch parameters
+
+enum KMode : int {
+    KMODE_FULL = 0,   // k in [0, K)
+    KMODE_LOWER = 1,  // op(A)[m,k] == 0 for k > m: k in [0, min(K, m_block_end))
+    KMODE_UPPER = 2,  // op(A)[m,k] == 0 for k < m: k in [m_block_begin, K)
+};
+
+enum CausalMode : int {
+    CAUSAL_NONE = 0,
+    CAUSAL_WRITE = 1,  // masked elements are written as -inf (the public epilogue)
+    CAUSAL_SKIP = 2,   // fully masked tiles are not written (consumer is causal-aware)
+};
+
+struct GemmArgs {
+    const void *A;
+    const void *B;
+    const void *B2;
+    void *C;
+    void *G;  // SwiGLU gate pre-activation (optional)
+    void *U;  // SwiGLU up pre-activation (optional)
+    const float *bias;
+    float *partial;  // split-K partial sums [splits][batch][M][N] (f32)
+
+    int64_t M, N, K;
+    int64_t lda, ldb, ldc;
+    // Batch index z splits into (z / batch_inner, z % batch_inner) with separate strides.
+    int64_t sA_in, sA_out, sB_in, sB_out, sC_in, sC_out;
+    int64_t batch_inner;
+    int64_t batch;
+    int splits;
+    int64_t k_per_split;  // multiple of the kernel's BK
+
+    float alpha, beta;
+    int has_bias;
+    int dual;
+    int causal;  // CausalMode
+    int64_t causal_offset;
+    int kmode;  // KMode
+    int out_bf16;
+    int a_vec_ok, b_vec_ok;  // 16-byte vector loads are legal for the operand
+    int tiles_m, tiles_n;
+};
+
+// Launches the MFMA GEMM for `dtype_in` (IT_F32 / IT_BF16). Chooses tile shape and split-K.
+it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool transB, GemmArgs args,
+                      const char *profile_tag);
+
+// Elementwise and row kernels (kernels_misc.hip).
+it_status launch_zero(hipStream_t s, void *dst, size_t bytes);
+it_status launch_f32_to_bf16(hipStream_t s, const float *src, uint16_t *dst, int64_t n);
+it_status launch_bf16_to_f32(hipStream_t s, const uint16_t *src, float *dst, int64_t n);
+it_status launch_softmax_rows(hipStream_t s, const float *S, void *P, int p_bf16, int64_t batch,
+                              int64_t rows, int64_t cols, int causal, int64_t causal_offset,
+                              int64_t s_ld_batch, int64_t p_ld_batch);
+it_status launch_softmax_backward(hipStream_t s, const float *dY, const void *Y, int y_bf16,
+                                  void *dX, int dx_bf16, int64_t batch, int64_t rows,
+                                  int64_t cols, int causal);
+it_status launch_splitk_reduce(hipStream_t s, const GemmArgs &a);
+
+}  // namespace it

@@ -1,0 +1,471 @@
+// MFMA GEMM kernels for gfx950 (CDNA4): FP32 (v_mfma_f32_16x16x4_f32) and BF16-in / FP32-accumulate
+// (v_mfma_f32_16x16x32_bf16), with the transposed-operand variant chosen at launch, strided and
+// two-level batching, split-K with a deterministic reduction, and fused epilogues (alpha/beta,
+// bias, SwiGLU dual-B, causal mask).
+//
+// Replaces the Metal GEMMs gemm_f32/_tiled/_batched (src/shaders/gemm.metal:15-119), the backward
+// gemm_grad_a/_b and batched forms (src/shaders/backward/gemm.metal:20-120), the BF16 GEMMs
+// (src/shaders/bf16_ops.metal:25-122) and the closed MPSMatrixMultiplication calls
+// (src/ops/mps_gemm.rs:169-198,278-306,390-418,519-553).
+//
+// Design (per 256-thread workgroup = 4 wave64s):
+//   * Block tile BM x BN, k-tile BK = 128 bytes of one operand row (32 f32 or 64 bf16).
+//   * Operands whose global layout is k-contiguous are copied global -> LDS with 128-bit loads and
+//     stores into a [rows][BK] tile with a 144-byte pitch; a lane's MFMA fragment is then one
+//     128-bit LDS read (16 lanes on 16 rows at one k offset hit disjoint banks with that pitch).
+//   * mn-contiguous operands (A stored [K,M], B stored [K,N]): FP32 keeps the [k][mn] tile and reads
+//     its fragment as four 32-bit LDS loads; BF16 transposes 4 k-rows x 8 columns in registers on
+//     the way into LDS so the fragment stays a single 128-bit read. No transpose is ever
+//     materialised in HBM.
+//   * Two LDS stages: global loads of tile t+1 are in flight while tile t is multiplied; one
+//     barrier per k-tile.
+//   * A lane's fragment covers k = 4g..4g+3 (FP32) or 8g..8g+7 (BF16) of a 16/32-wide k step, where
+//     g = lane / 16. A and B use the same k assignment, so every MFMA sums the right products; the
+//     summation order differs from a sequential loop only by FP32 rounding.
+//   * Tiles are enumerated XCD-aware: the 8 XCDs each receive a contiguous range of the grouped
+//     tile order, so blocks sharing A rows or B columns hit the same L2.
+#include <cmath>
+#include <cstdio>
+#include <string>
+
+#include "internal.hpp"
+
+namespace it {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int NTHREADS = 256;
+constexpr int ROW_PITCH = 144;  // LDS bytes per row of a [rows][BK] tile (128 data + 16 pad)
+
+template <typename T>
+struct ET;
+template <>
+struct ET<float> {
+    static constexpr int VEC = 4;    // elements per 16 bytes
+    static constexpr int BK = 32;    // k per tile
+    static constexpr int KSTEP = 16; // k per fragment step (4 lane groups x 4)
+};
+template <>
+struct ET<uint16_t> {
+    static constexpr int VEC = 8;
+    static constexpr int BK = 64;
+    static constexpr int KSTEP = 32;
+};
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+    uint32_t b = __float_as_uint(x);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((b >> 16) | 0x40u);  // quiet NaN
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+__device__ __forceinline__ float load_out(const void *C, int64_t idx, int bf16) {
+    return bf16 ? bf16_to_f32(((const uint16_t *)C)[idx]) : ((const float *)C)[idx];
+}
+
+__device__ __forceinline__ void store_out(void *C, int64_t idx, float v, int bf16) {
+    if (bf16)
+        ((uint16_t *)C)[idx] = f32_to_bf16_rne(v);
+    else
+        ((float *)C)[idx] = v;
+}
+
+// Loads VEC consecutive elements starting at base[off]; elements at positions c + e >= clim (or the
+// whole vector when !row_ok) read as zero.
+template <typename T>
+__device__ __forceinline__ u32x4 load_vec(const T *base, int64_t off, bool row_ok, int64_t c,
+                                          int64_t clim, bool vec_ok) {
+    constexpr int VEC = ET<T>::VEC;
+    if (row_ok && vec_ok && c + VEC <= clim) return *(const u32x4 *)(base + off);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (row_ok) {
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (c + e < clim) v[e] = __float_as_uint(base[off + e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (c + e < clim) v[e >> 1] |= (uint32_t)base[off + e] << ((e & 1) * 16);
+        }
+    }
+    return v;
+}
+
+// One operand's k-tile: global -> registers -> LDS, and LDS -> MFMA fragments.
+//   KCONTIG: global element (r, k) at base[r * ld + k] (A not transposed, or B transposed).
+//   otherwise: global element (r, k) at base[k * ld + r].
+template <typename T, bool KCONTIG, int ROWS>
+struct Operand {
+    static constexpr int VEC = ET<T>::VEC;
+    static constexpr int BK = ET<T>::BK;
+    static constexpr bool TRANSPOSE = !KCONTIG && sizeof(T) == 2;  // bf16 [k][mn] -> LDS [mn][k]
+    static constexpr bool KMAJOR_LDS = !KCONTIG && sizeof(T) == 4;  // f32 keeps [k][mn] in LDS
+    static constexpr int KMAJOR_PITCH = ROWS * 4 + 16;
+    static constexpr int STAGE_BYTES = KMAJOR_LDS ? BK * KMAJOR_PITCH : ROWS * ROW_PITCH;
+    static constexpr int ITEMS = TRANSPOSE ? (BK / 4) * (ROWS / VEC) : ROWS * BK / VEC;
+    static constexpr int LOADS = TRANSPOSE ? 4 : 1;
+    static constexpr int ITERS = (ITEMS + NTHREADS - 1) / NTHREADS;
+
+    u32x4 reg[ITERS][LOADS];
+
+    __device__ __forceinline__ void load(const T *base, int64_t ld, int64_t r0, int64_t k0,
+                                         int64_t rlim, int64_t klim, bool vec_ok, int tid) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int item = tid + it * NTHREADS;
+            if (ITEMS % NTHREADS != 0 && item >= ITEMS) continue;
+            if constexpr (KCONTIG) {
+                const int rr = item / (BK / VEC), kc = item % (BK / VEC);
+                const int64_t gr = r0 + rr, gk = k0 + kc * VEC;
+                reg[it][0] = load_vec<T>(base, gr * ld + gk, gr < rlim, gk, klim, vec_ok);
+            } else if constexpr (!TRANSPOSE) {
+                const int kk = item / (ROWS / VEC), rc = item % (ROWS / VEC);
+                const int64_t gk = k0 + kk, gr = r0 + rc * VEC;
+                reg[it][0] = load_vec<T>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
+            } else {
+                const int kg = item / (ROWS / VEC), rc = item % (ROWS / VEC);
+                const int64_t gr = r0 + rc * VEC;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int64_t gk = k0 + kg * 4 + q;
+                    reg[it][q] = load_vec<T>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(char *lds, int tid) const {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int item = tid + it * NTHREADS;
+            if (ITEMS % NTHREADS != 0 && item >= ITEMS) continue;
+            if constexpr (KCONTIG) {
+                const int rr = item / (BK / VEC), kc = item % (BK / VEC);
+                *(u32x4 *)(lds + rr * ROW_PITCH + kc * 16) = reg[it][0];
+            } else if constexpr (!TRANSPOSE) {
+                const int kk = item / (ROWS / VEC), rc = item % (ROWS / VEC);
+                *(u32x4 *)(lds + kk * KMAJOR_PITCH + rc * 16) = reg[it][0];
+            } else {
+                const int kg = item / (ROWS / VEC), rc = item % (ROWS / VEC);
+                const u32x4 &v0 = reg[it][0], &v1 = reg[it][1], &v2 = reg[it][2], &v3 = reg[it][3];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    // columns 2d (low halves) and 2d+1 (high halves) of the 4 loaded k-rows
+                    u32x2 lo, hi;
+                    lo[0] = (v0[d] & 0xffffu) | (v1[d] << 16);
+                    lo[1] = (v2[d] & 0xffffu) | (v3[d] << 16);
+                    hi[0] = (v0[d] >> 16) | (v1[d] & 0xffff0000u);
+                    hi[1] = (v2[d] >> 16) | (v3[d] & 0xffff0000u);
+                    *(u32x2 *)(lds + (rc * 8 + 2 * d) * ROW_PITCH + kg * 8) = lo;
+                    *(u32x2 *)(lds + (rc * 8 + 2 * d + 1) * ROW_PITCH + kg * 8) = hi;
+                }
+            }
+        }
+    }
+
+    // Fragment of the 16 rows starting at `row` for fragment step `ks`.
+    __device__ __forceinline__ static u32x4 frag(const char *lds, int row, int ks, int lane) {
+        const int i = lane & 15, g = lane >> 4;
+        if constexpr (!KMAJOR_LDS) {
+            return *(const u32x4 *)(lds + (row + i) * ROW_PITCH + ks * 64 + g * 16);
+        } else {
+            u32x4 v;
+            const int k = ks * 16 + g * 4;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) v[s] = *(const uint32_t *)(lds + (k + s) * KMAJOR_PITCH + (row + i) * 4);
+            return v;
+        }
+    }
+};
+
+template <typename T>
+__device__ __forceinline__ void mma(f32x4 &acc, const u32x4 &a, const u32x4 &b) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[s]), __uint_as_float(b[s]),
+                                                       acc, 0, 0, 0);
+    } else {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                      __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+    }
+}
+
+// Tile order: XCD-aware remap then GROUP_M-grouped raster.
+__device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int &tm, int &tn) {
+    constexpr int NXCD = 8, GROUP = 8;
+    const int total = tiles_m * tiles_n;
+    if (total % NXCD == 0) pid = (pid % NXCD) * (total / NXCD) + pid / NXCD;
+    const int span = GROUP * tiles_n;
+    const int first_m = (pid / span) * GROUP;
+    const int gsize = min(tiles_m - first_m, GROUP);
+    const int in = pid % span;
+    tm = first_m + in % gsize;
+    tn = in / gsize;
+}
+
+// Final value of one output element (alpha, beta, bias, causal), shared by the GEMM epilogue and
+// the split-K reduction.
+__device__ __forceinline__ void finish_store(const GemmArgs &p, void *C, int64_t idx, float acc,
+                                             int64_t row, int64_t col) {
+    float v = p.alpha * acc;
+    if (p.beta != 0.f) v += p.beta * load_out(C, idx, p.out_bf16);
+    if (p.has_bias) v += p.bias[col];
+    if (p.causal != CAUSAL_NONE && col > row + p.causal_offset) v = -INFINITY;
+    store_out(C, idx, v, p.out_bf16);
+}
+
+__device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
+
+template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL>
+__global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
+    static_assert(WM * WN == 4, "4 waves per block");
+    constexpr int BK = ET<T>::BK;
+    constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
+    using OA = Operand<T, !TA, BM>;
+    using OB = Operand<T, TB, BN>;
+    constexpr int SA = OA::STAGE_BYTES, SB = OB::STAGE_BYTES;
+    constexpr int STAGE = SA + SB * (DUAL ? 2 : 1);
+    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int64_t z = blockIdx.y;
+    const int64_t b = z % p.batch, split = z / p.batch;
+    const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
+    const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in;
+    const T *B = (const T *)p.B + bo * p.sB_out + bi * p.sB_in;
+    const T *B2 = DUAL ? (const T *)p.B2 + bo * p.sB_out + bi * p.sB_in : nullptr;
+    const int64_t coff = bo * p.sC_out + bi * p.sC_in;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    if (p.causal != CAUSAL_NONE && n0 > m0 + BM - 1 + p.causal_offset) {
+        // Entire tile is above the diagonal: no products needed.
+        if (p.causal == CAUSAL_WRITE) {
+            for (int e = tid; e < BM * BN; e += NTHREADS) {
+                const int64_t row = m0 + e / BN, col = n0 + e % BN;
+                if (row < p.M && col < p.N) store_out(p.C, coff + row * p.ldc + col, -INFINITY, p.out_bf16);
+            }
+        }
+        return;
+    }
+
+    int64_t kb = split * p.k_per_split;
+    int64_t ke = min(p.K, kb + p.k_per_split);
+    if (p.kmode == KMODE_LOWER) ke = min(ke, m0 + BM);
+    if (p.kmode == KMODE_UPPER) kb = max(kb, (m0 / BK) * BK);
+    const int ntiles = ke > kb ? (int)((ke - kb + BK - 1) / BK) : 0;
+
+    f32x4 acc[FM][FN];
+    f32x4 acc2[DUAL ? FM : 1][DUAL ? FN : 1];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (DUAL) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    OA oa;
+    OB ob, ob2;
+    if (ntiles > 0) {
+        oa.load(A, p.lda, m0, kb, p.M, ke, p.a_vec_ok, tid);
+        ob.load(B, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
+        if constexpr (DUAL) ob2.load(B2, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
+        oa.store(smem, tid);
+        ob.store(smem + SA, tid);
+        if constexpr (DUAL) ob2.store(smem + SA + SB, tid);
+        __syncthreads();
+    }
+
+    for (int t = 0; t < ntiles; ++t) {
+        char *cur = smem + (t & 1) * STAGE;
+        char *nxt = smem + ((t + 1) & 1) * STAGE;
+        const bool more = t + 1 < ntiles;
+        if (more) {
+            const int64_t k = kb + (int64_t)(t + 1) * BK;
+            oa.load(A, p.lda, m0, k, p.M, ke, p.a_vec_ok, tid);
+            ob.load(B, p.ldb, n0, k, p.N, ke, p.b_vec_ok, tid);
+            if constexpr (DUAL) ob2.load(B2, p.ldb, n0, k, p.N, ke, p.b_vec_ok, tid);
+        }
+#pragma unroll
+        for (int ks = 0; ks < BK / ET<T>::KSTEP; ++ks) {
+            u32x4 af[FM], bfr[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[i] = OA::frag(cur, wm * WTM + i * 16, ks, lane);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bfr[j] = OB::frag(cur + SA, wn * WTN + j * 16, ks, lane);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) mma<T>(acc[i][j], af[i], bfr[j]);
+            if constexpr (DUAL) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) bfr[j] = OB::frag(cur + SA + SB, wn * WTN + j * 16, ks, lane);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) mma<T>(acc2[i][j], af[i], bfr[j]);
+            }
+        }
+        if (more) {
+            oa.store(nxt, tid);
+            ob.store(nxt + SA, tid);
+            if constexpr (DUAL) ob2.store(nxt + SA + SB, tid);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue. Lane l of a 16x16 MFMA block holds rows 4*(l/16)+r (r = 0..3), column l%16.
+    const int64_t rbase = m0 + wm * WTM + (lane >> 4) * 4;
+    const int64_t cbase = n0 + wn * WTN + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = rbase + i * 16 + r, col = cbase + j * 16;
+                if (row >= p.M || col >= p.N) continue;
+                if (p.splits > 1) {
+                    p.partial[(z * p.M + row) * p.N + col] = acc[i][j][r];
+                    continue;
+                }
+                const int64_t idx = coff + row * p.ldc + col;
+                if constexpr (DUAL) {
+                    const float g = p.alpha * acc[i][j][r], u = p.alpha * acc2[i][j][r];
+                    if (p.G) store_out(p.G, idx, g, p.out_bf16);
+                    if (p.U) store_out(p.U, idx, u, p.out_bf16);
+                    store_out(p.C, idx, silu(g) * u, p.out_bf16);
+                } else {
+                    finish_store(p, p.C, idx, acc[i][j][r], row, col);
+                }
+            }
+}
+
+// Deterministic split-K reduction: partial sums are added in split order.
+__global__ __launch_bounds__(256) void splitk_reduce(const GemmArgs p) {
+    const int64_t total = p.batch * p.M * p.N;
+    const int64_t mn = p.M * p.N;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t b = e / mn, rem = e % mn, row = rem / p.N, col = rem % p.N;
+        float s = 0.f;
+        for (int sp = 0; sp < p.splits; ++sp) s += p.partial[(int64_t)sp * total + e];
+        const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
+        finish_store(p, p.C, bo * p.sC_out + bi * p.sC_in + row * p.ldc + col, s, row, col);
+    }
+}
+
+struct TileCfg {
+    int bm, bn;
+};
+
+template <typename T, bool TA, bool TB, bool DUAL>
+hipError_t launch_cfg(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
+    if (cfg.bm == 128)
+        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 128, 128, 2, 2, DUAL>), grid, dim3(NTHREADS), 0, s, a);
+    else
+        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 64, 64, 2, 2, DUAL>), grid, dim3(NTHREADS), 0, s, a);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_typed(bool ta, bool tb, bool dual, const TileCfg &cfg, const GemmArgs &a, dim3 grid,
+                        hipStream_t s) {
+    if (dual) return launch_cfg<T, false, true, true>(cfg, a, grid, s);
+    if (!ta && !tb) return launch_cfg<T, false, false, false>(cfg, a, grid, s);
+    if (!ta && tb) return launch_cfg<T, false, true, false>(cfg, a, grid, s);
+    if (ta && !tb) return launch_cfg<T, true, false, false>(cfg, a, grid, s);
+    return launch_cfg<T, true, true, false>(cfg, a, grid, s);
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+it_status launch_splitk_reduce(hipStream_t s, const GemmArgs &a) {
+    const int64_t total = a.batch * a.M * a.N;
+    const int64_t blocks = std::min<int64_t>(cdiv(total, 256), 65536);
+    hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    IT_HIP_TRY(hipGetLastError());
+    return IT_OK;
+}
+
+it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool transB, GemmArgs a,
+                      const char *profile_tag) {
+    const bool bf16 = dtype_in == IT_BF16;
+    const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
+    const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+
+    // Tile shape: 128x128 when that already fills the chip, else 64x64 (+ split-K when even that
+    // leaves CUs idle and the reduction is long).
+    TileCfg cfg{128, 128};
+    int64_t tiles = cdiv(a.M, 128) * cdiv(a.N, 128) * a.batch;
+    if (tiles < cus) {
+        cfg = TileCfg{64, 64};
+        tiles = cdiv(a.M, 64) * cdiv(a.N, 64) * a.batch;
+    }
+    int splits = 1;
+    if (tiles < cus && !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL) {
+        const int64_t want = cdiv(2 * cus, tiles);
+        const int64_t max_by_k = a.K / (4 * bk);  // at least 4 k-tiles per split
+        splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 32}));
+    }
+    a.tiles_m = (int)cdiv(a.M, cfg.bm);
+    a.tiles_n = (int)cdiv(a.N, cfg.bn);
+    int64_t kps = cdiv(a.K, splits);
+    kps = cdiv(kps, bk) * bk;
+    if (kps == 0) kps = bk;
+    splits = (int)std::max<int64_t>(1, cdiv(a.K, kps));
+    a.k_per_split = kps;
+    a.splits = splits;
+    if (splits > 1) {
+        void *ws = nullptr;
+        it_status st = ensure_scratch(ctx, (size_t)splits * a.batch * a.M * a.N * sizeof(float), &ws);
+        if (st != IT_OK) return st;
+        a.partial = (float *)ws;
+    }
+
+    const int64_t gx = (int64_t)a.tiles_m * a.tiles_n;
+    const int64_t gy = a.batch * splits;
+    if (gx > 0x7fffffff || gy > 65535)
+        return fail(IT_ERR_DIMS, "it_gemm: grid too large (tiles " + std::to_string(gx) +
+                                     ", batch*splits " + std::to_string(gy) + ")");
+    dim3 grid((unsigned)gx, (unsigned)gy);
+
+    std::string key;
+    hipEvent_t ev = nullptr;
+    if (ctx->profiling) {
+        char buf[192];
+        std::snprintf(buf, sizeof(buf), "gemm_%s_%c%c_%dx%d|%s[%lld,%lld,%lld]x%lld s%d",
+                      bf16 ? "bf16" : "f32", transA ? 'T' : 'N', transB ? 'T' : 'N', cfg.bm, cfg.bn,
+                      profile_tag ? profile_tag : "", (long long)a.M, (long long)a.N,
+                      (long long)a.K, (long long)a.batch, splits);
+        key = buf;
+        profile_begin(ctx, key, &ev);
+    }
+    hipError_t e = bf16 ? launch_typed<uint16_t>(transA, transB, a.dual, cfg, a, grid, ctx->stream)
+                        : launch_typed<float>(transA, transB, a.dual, cfg, a, grid, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "gemm_mfma launch");
+    if (splits > 1) {
+        it_status st = launch_splitk_reduce(ctx->stream, a);
+        if (st != IT_OK) return st;
+    }
+    if (ctx->profiling) profile_end(ctx, key, ev);
+    return IT_OK;
+}
+
+}  // namespace it

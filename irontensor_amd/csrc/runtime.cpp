@@ -1,0 +1,347 @@
+// Runtime under the matmul path: device context, one HIP stream, a caching allocator, events,
+// thread-local errors and the shape-keyed launch profiler.
+//
+// Replaces, for a discrete-HBM GPU, IronTensor's MetalContext singleton (src/device.rs:10-71), the
+// CommandBatch sync/async modes (src/command_batch.rs:166-391) and per-op MTLBuffer allocation
+// (src/tensor.rs:63-88, src/ops/kernel.rs:70-80).
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "internal.hpp"
+
+namespace it {
+
+static thread_local std::string g_last_error;
+
+it_status fail(it_status st, const std::string &msg) {
+    g_last_error = msg;
+    return st;
+}
+
+it_status fail_hip(hipError_t err, const char *what) {
+    std::string msg = std::string(what) + ": " + hipGetErrorName(err) + " (" +
+                      hipGetErrorString(err) + ")";
+    if (err == hipErrorOutOfMemory || err == hipErrorMemoryAllocation)
+        return fail(IT_ERR_OOM, msg);
+    if (err == hipErrorNoDevice || err == hipErrorInvalidDevice) return fail(IT_ERR_NO_DEVICE, msg);
+    return fail(IT_ERR_HIP, msg);
+}
+
+void clear_error() { g_last_error.clear(); }
+
+it_status ensure_scratch(it_context *ctx, size_t bytes, void **out) {
+    if (ctx->scratch_bytes < bytes) {
+        if (ctx->scratch) {
+            IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+            IT_HIP_TRY(hipFree(ctx->scratch));
+            ctx->scratch = nullptr;
+            ctx->scratch_bytes = 0;
+        }
+        size_t want = bytes < (size_t(64) << 20) ? (size_t(64) << 20) : bytes;
+        IT_HIP_TRY(hipMalloc(&ctx->scratch, want));
+        ctx->scratch_bytes = want;
+    }
+    *out = ctx->scratch;
+    return IT_OK;
+}
+
+static hipEvent_t pool_event(it_context *ctx) {
+    if (!ctx->event_pool.empty()) {
+        hipEvent_t e = ctx->event_pool.back();
+        ctx->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void profile_begin(it_context *ctx, const std::string &, hipEvent_t *start_out) {
+    *start_out = nullptr;
+    if (!ctx->profiling) return;
+    hipEvent_t e = pool_event(ctx);
+    if (e && hipEventRecord(e, ctx->stream) == hipSuccess) *start_out = e;
+}
+
+void profile_end(it_context *ctx, const std::string &key, hipEvent_t start) {
+    if (!ctx->profiling || !start) return;
+    hipEvent_t e = pool_event(ctx);
+    if (!e || hipEventRecord(e, ctx->stream) != hipSuccess) {
+        ctx->event_pool.push_back(start);
+        return;
+    }
+    ctx->pending.push_back(ProfileRecord{key, start, e});
+}
+
+static it_status profile_drain(it_context *ctx) {
+    if (ctx->pending.empty()) return IT_OK;
+    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    for (auto &r : ctx->pending) {
+        float ms = 0.f;
+        IT_HIP_TRY(hipEventElapsedTime(&ms, r.start, r.stop));
+        auto &st = ctx->stats[r.key];
+        st.calls += 1;
+        st.total_ms += ms;
+        ctx->event_pool.push_back(r.start);
+        ctx->event_pool.push_back(r.stop);
+    }
+    ctx->pending.clear();
+    return IT_OK;
+}
+
+}  // namespace it
+
+using it::fail;
+
+extern "C" {
+
+const char *it_last_error(void) { return it::g_last_error.c_str(); }
+
+const char *it_status_string(it_status s) {
+    switch (s) {
+    case IT_OK: return "ok";
+    case IT_ERR_INNER_DIM: return "inner dimensions don't match";
+    case IT_ERR_SHAPE: return "shape mismatch";
+    case IT_ERR_PRECISION: return "precision mismatch";
+    case IT_ERR_DIMS: return "unsupported dimensions";
+    case IT_ERR_INVALID: return "invalid value";
+    case IT_ERR_NULL: return "null pointer";
+    case IT_ERR_OOM: return "out of device memory";
+    case IT_ERR_NO_DEVICE: return "no HIP device";
+    case IT_ERR_HIP: return "HIP runtime error";
+    case IT_ERR_NOT_READY: return "not ready";
+    }
+    return "unknown status";
+}
+
+int it_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+it_status it_init(int device, it_context **out_ctx) {
+    if (!out_ctx) return fail(IT_ERR_NULL, "it_init: out_ctx is NULL");
+    *out_ctx = nullptr;
+    int n = it_device_count();
+    if (n <= 0) return fail(IT_ERR_NO_DEVICE, "it_init: no HIP device found");
+    if (device < 0 || device >= n)
+        return fail(IT_ERR_NO_DEVICE, "it_init: device ordinal " + std::to_string(device) +
+                                          " out of range (" + std::to_string(n) + " devices)");
+    IT_HIP_TRY(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    IT_HIP_TRY(hipGetDeviceProperties(&prop, device));
+    auto *ctx = new it_context();
+    ctx->device = device;
+    ctx->num_cus = prop.multiProcessorCount;
+    ctx->clock_khz = prop.clockRate;
+    std::snprintf(ctx->name, sizeof(ctx->name), "%s", prop.gcnArchName);
+    // Default priority only: streams of mixed priority are avoided on purpose.
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return it::fail_hip(e, "hipStreamCreateWithFlags");
+    }
+    *out_ctx = ctx;
+    it::clear_error();
+    return IT_OK;
+}
+
+it_status it_shutdown(it_context *ctx) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_shutdown: ctx is NULL");
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto &r : ctx->pending) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
+    for (auto &kv : ctx->cache) (void)hipFree(kv.second);
+    for (auto &kv : ctx->live) (void)hipFree(kv.first);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return IT_OK;
+}
+
+it_status it_device_info(it_context *ctx, char *name, size_t name_len, int *num_cus,
+                         int *clock_khz) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_device_info: ctx is NULL");
+    if (name && name_len) std::snprintf(name, name_len, "%s", ctx->name);
+    if (num_cus) *num_cus = ctx->num_cus;
+    if (clock_khz) *clock_khz = ctx->clock_khz;
+    return IT_OK;
+}
+
+it_status it_malloc(it_context *ctx, size_t bytes, void **out_ptr) {
+    if (!ctx || !out_ptr) return fail(IT_ERR_NULL, "it_malloc: NULL argument");
+    *out_ptr = nullptr;
+    // Round to 256 B so cached blocks are reusable across nearby sizes and every block is aligned
+    // for 128-bit loads.
+    size_t sz = bytes == 0 ? 256 : ((bytes + 255) / 256) * 256;
+    auto it = ctx->cache.find(sz);
+    void *p = nullptr;
+    if (it != ctx->cache.end()) {
+        p = it->second;
+        ctx->cache.erase(it);
+    } else {
+        hipError_t e = hipMalloc(&p, sz);
+        if (e != hipSuccess) {
+            // Release the cache once and retry before giving up.
+            (void)hipStreamSynchronize(ctx->stream);
+            for (auto &kv : ctx->cache) (void)hipFree(kv.second);
+            ctx->cache.clear();
+            (void)hipGetLastError();
+            e = hipMalloc(&p, sz);
+            if (e != hipSuccess)
+                return fail(IT_ERR_OOM, "it_malloc: failed to allocate " + std::to_string(sz) +
+                                            " bytes: " + hipGetErrorString(e));
+        }
+    }
+    ctx->live[p] = sz;
+    ctx->bytes_live += sz;
+    *out_ptr = p;
+    return IT_OK;
+}
+
+it_status it_free(it_context *ctx, void *ptr) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_free: ctx is NULL");
+    if (!ptr) return IT_OK;
+    auto it = ctx->live.find(ptr);
+    if (it == ctx->live.end()) return fail(IT_ERR_INVALID, "it_free: pointer not from it_malloc");
+    ctx->bytes_live -= it->second;
+    ctx->cache.emplace(it->second, ptr);
+    ctx->live.erase(it);
+    return IT_OK;
+}
+
+size_t it_mem_allocated(it_context *ctx) { return ctx ? ctx->bytes_live : 0; }
+
+it_status it_empty_cache(it_context *ctx) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_empty_cache: ctx is NULL");
+    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    for (auto &kv : ctx->cache) IT_HIP_TRY(hipFree(kv.second));
+    ctx->cache.clear();
+    return IT_OK;
+}
+
+it_status it_memcpy_h2d(it_context *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(IT_ERR_NULL, "it_memcpy_h2d: NULL");
+    if (!bytes) return IT_OK;
+    IT_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    // Pageable host memory: the copy has consumed `src` only once the stream reaches it.
+    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return IT_OK;
+}
+
+it_status it_memcpy_d2h(it_context *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(IT_ERR_NULL, "it_memcpy_d2h: NULL");
+    if (!bytes) return IT_OK;
+    IT_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return IT_OK;
+}
+
+it_status it_memcpy_d2d(it_context *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(IT_ERR_NULL, "it_memcpy_d2d: NULL");
+    if (!bytes) return IT_OK;
+    IT_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return IT_OK;
+}
+
+it_status it_zero(it_context *ctx, void *dst, size_t bytes) {
+    if (!ctx || (!dst && bytes)) return fail(IT_ERR_NULL, "it_zero: NULL");
+    if (!bytes) return IT_OK;
+    return it::launch_zero(ctx->stream, dst, bytes);
+}
+
+it_status it_stream_sync(it_context *ctx) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_stream_sync: ctx is NULL");
+    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return IT_OK;
+}
+
+void *it_stream(it_context *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+it_status it_event_create(it_context *ctx, it_event **out_ev) {
+    if (!ctx || !out_ev) return fail(IT_ERR_NULL, "it_event_create: NULL argument");
+    auto *ev = new it_event();
+    hipError_t e = hipEventCreate(&ev->ev);
+    if (e != hipSuccess) {
+        delete ev;
+        return it::fail_hip(e, "hipEventCreate");
+    }
+    *out_ev = ev;
+    return IT_OK;
+}
+
+it_status it_event_record(it_context *ctx, it_event *ev) {
+    if (!ctx || !ev) return fail(IT_ERR_NULL, "it_event_record: NULL argument");
+    IT_HIP_TRY(hipEventRecord(ev->ev, ctx->stream));
+    return IT_OK;
+}
+
+it_status it_event_query(it_event *ev) {
+    if (!ev) return fail(IT_ERR_NULL, "it_event_query: NULL event");
+    hipError_t e = hipEventQuery(ev->ev);
+    if (e == hipSuccess) return IT_OK;
+    if (e == hipErrorNotReady) return IT_ERR_NOT_READY;
+    return it::fail_hip(e, "hipEventQuery");
+}
+
+it_status it_event_sync(it_event *ev) {
+    if (!ev) return fail(IT_ERR_NULL, "it_event_sync: NULL event");
+    IT_HIP_TRY(hipEventSynchronize(ev->ev));
+    return IT_OK;
+}
+
+it_status it_event_elapsed_ms(it_event *start, it_event *end, float *ms) {
+    if (!start || !end || !ms) return fail(IT_ERR_NULL, "it_event_elapsed_ms: NULL argument");
+    IT_HIP_TRY(hipEventElapsedTime(ms, start->ev, end->ev));
+    return IT_OK;
+}
+
+it_status it_event_destroy(it_event *ev) {
+    if (!ev) return IT_OK;
+    (void)hipEventDestroy(ev->ev);
+    delete ev;
+    return IT_OK;
+}
+
+it_status it_profiler_enable(it_context *ctx, int enable) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_profiler_enable: ctx is NULL");
+    ctx->profiling = enable != 0;
+    return IT_OK;
+}
+
+it_status it_profiler_reset(it_context *ctx) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_profiler_reset: ctx is NULL");
+    it_status st = it::profile_drain(ctx);
+    ctx->stats.clear();
+    return st;
+}
+
+it_status it_profiler_report(it_context *ctx, char *buf, size_t buf_len, size_t *needed) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_profiler_report: ctx is NULL");
+    it_status st = it::profile_drain(ctx);
+    if (st != IT_OK) return st;
+    std::string out = "{";
+    bool first = true;
+    for (auto &kv : ctx->stats) {
+        char tmp[128];
+        std::snprintf(tmp, sizeof(tmp), "{\"calls\": %lld, \"total_ms\": %.6f}",
+                      (long long)kv.second.calls, kv.second.total_ms);
+        if (!first) out += ", ";
+        first = false;
+        out += "\"" + kv.first + "\": " + tmp;
+    }
+    out += "}";
+    if (needed) *needed = out.size() + 1;
+    if (!buf || buf_len < out.size() + 1)
+        return fail(IT_ERR_INVALID, "it_profiler_report: buffer too small");
+    std::memcpy(buf, out.c_str(), out.size() + 1);
+    return IT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,195 @@
+"""ctypes wrapper of the CPU oracle (oracle/liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use this package, and only
+as the checker / the timed CPU baseline. The product (irontensor_amd) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    """Compiles liboracle.so with gcc (oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        build()
+    lib = C.CDLL(str(LIB_PATH))
+    vp, i64, i = C.c_void_p, C.c_int64, C.c_int
+    lib.ref_f32_to_bf16.restype = C.c_uint16
+    lib.ref_f32_to_bf16.argtypes = [C.c_float]
+    lib.ref_bf16_to_f32.restype = C.c_float
+    lib.ref_bf16_to_f32.argtypes = [C.c_uint16]
+    lib.ref_f32_to_bf16_n.argtypes = [vp, vp, i64]
+    lib.ref_bf16_to_f32_n.argtypes = [vp, vp, i64]
+    gemm_args = [i, i, i64, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, i64, i64, i]
+    lib.ref_gemm_f32.argtypes = gemm_args
+    lib.ref_gemm_f64.argtypes = gemm_args
+    lib.ref_gemm_bf16.argtypes = [i, i, i64, i64, i64, vp, i64, i64, vp, i64, i64, vp, i, i64, i64,
+                                  i64, i]
+    lib.ref_add_bias.argtypes = [vp, vp, i64, i64]
+    lib.ref_swiglu.argtypes = [vp, vp, vp, i64]
+    lib.ref_swiglu_backward.argtypes = [vp, vp, vp, vp, vp, i64]
+    lib.ref_softmax_rows.argtypes = [vp, i64, i64]
+    lib.ref_softmax_backward.argtypes = [vp, vp, vp, i64, i64]
+    lib.ref_attention_bshd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i, i]
+    lib.ref_attention_fwd_bhsd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, C.c_float, i, i]
+    lib.ref_attention_bwd_bhsd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, C.c_float, i, i]
+    lib.ref_default_threads.restype = i
+    _lib = lib
+    return lib
+
+
+def default_threads() -> int:
+    env = os.environ.get("ORACLE_THREADS")
+    if env:
+        return max(1, int(env))
+    return min(16, int(load().ref_default_threads()))
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _gemm_dims(a: np.ndarray, b: np.ndarray, trans_a: bool, trans_b: bool):
+    batched = a.ndim == 3
+    batch = a.shape[0] if batched else 1
+    ra, ca = a.shape[-2:]
+    rb, cb = b.shape[-2:]
+    m, k = (ca, ra) if trans_a else (ra, ca)
+    k2, n = (cb, rb) if trans_b else (rb, cb)
+    assert k == k2, (a.shape, b.shape, trans_a, trans_b)
+    s_a = ra * ca if batched else 0
+    s_b = rb * cb if b.ndim == 3 else 0
+    return batched, batch, m, n, k, ca, cb, s_a, s_b
+
+
+def gemm_f32(a, b, trans_a=False, trans_b=False, threads=None) -> np.ndarray:
+    """op(A).op(B) with the reference's sequential f32 loop (2D, or 3D batched)."""
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    batched, batch, m, n, k, lda, ldb, s_a, s_b = _gemm_dims(a, b, trans_a, trans_b)
+    out = np.empty((batch, m, n) if batched else (m, n), dtype=np.float32)
+    load().ref_gemm_f32(int(trans_a), int(trans_b), m, n, k, _p(a), lda, s_a, _p(b), ldb, s_b,
+                        _p(out), n, m * n, batch, threads or default_threads())
+    return out
+
+
+def gemm_f64(a, b, trans_a=False, trans_b=False, threads=None) -> np.ndarray:
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    batched, batch, m, n, k, lda, ldb, s_a, s_b = _gemm_dims(a, b, trans_a, trans_b)
+    out = np.empty((batch, m, n) if batched else (m, n), dtype=np.float64)
+    load().ref_gemm_f64(int(trans_a), int(trans_b), m, n, k, _p(a), lda, s_a, _p(b), ldb, s_b,
+                        _p(out), n, m * n, batch, threads or default_threads())
+    return out
+
+
+def gemm_bf16(a_u16, b_u16, trans_a=False, trans_b=False, out_bf16=False, threads=None) -> np.ndarray:
+    a, b = _c(a_u16, np.uint16), _c(b_u16, np.uint16)
+    batched, batch, m, n, k, lda, ldb, s_a, s_b = _gemm_dims(a, b, trans_a, trans_b)
+    shape = (batch, m, n) if batched else (m, n)
+    out = np.empty(shape, dtype=np.uint16 if out_bf16 else np.float32)
+    load().ref_gemm_bf16(int(trans_a), int(trans_b), m, n, k, _p(a), lda, s_a, _p(b), ldb, s_b,
+                         _p(out), int(out_bf16), n, m * n, batch, threads or default_threads())
+    return out
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    load().ref_f32_to_bf16_n(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_to_f32(x) -> np.ndarray:
+    x = _c(x, np.uint16)
+    out = np.empty(x.shape, dtype=np.float32)
+    load().ref_bf16_to_f32_n(_p(x), _p(out), x.size)
+    return out
+
+
+def add_bias(y, bias) -> np.ndarray:
+    y = _c(y, np.float32).copy()
+    bias = _c(bias, np.float32)
+    load().ref_add_bias(_p(y), _p(bias), y.shape[0], y.shape[1])
+    return y
+
+
+def swiglu(gate, up) -> np.ndarray:
+    g, u = _c(gate, np.float32), _c(up, np.float32)
+    out = np.empty_like(g)
+    load().ref_swiglu(_p(g), _p(u), _p(out), g.size)
+    return out
+
+
+def swiglu_backward(grad_out, gate, up):
+    go, g, u = _c(grad_out, np.float32), _c(gate, np.float32), _c(up, np.float32)
+    gg, gu = np.empty_like(g), np.empty_like(g)
+    load().ref_swiglu_backward(_p(go), _p(g), _p(u), _p(gg), _p(gu), g.size)
+    return gg, gu
+
+
+def softmax_rows(x) -> np.ndarray:
+    x = _c(x, np.float32).copy()
+    cols = x.shape[-1]
+    load().ref_softmax_rows(_p(x), x.size // cols, cols)
+    return x
+
+
+def softmax_backward(grad_y, y) -> np.ndarray:
+    gy, yy = _c(grad_y, np.float32), _c(y, np.float32)
+    out = np.empty_like(yy)
+    cols = yy.shape[-1]
+    load().ref_softmax_backward(_p(gy), _p(yy), _p(out), yy.size // cols, cols)
+    return out
+
+
+def attention_bshd(q, k, v, causal: bool, threads=None) -> np.ndarray:
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    b, s, h, d = q.shape
+    out = np.empty_like(q)
+    load().ref_attention_bshd(_p(q), _p(k), _p(v), _p(out), b, s, h, d, int(causal),
+                              threads or default_threads())
+    return out
+
+
+def attention_fwd_bhsd(q, k, v, scale: float, causal: bool, threads=None):
+    """q, k, v: [BH, S, D] (or [B,H,S,D]); returns (O, P)."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    s, d = q.shape[-2:]
+    bh = q.size // (s * d)
+    out = np.empty_like(q)
+    p = np.empty((bh, s, s), dtype=np.float32)
+    load().ref_attention_fwd_bhsd(_p(q), _p(k), _p(v), _p(out), _p(p), bh, s, d, float(scale),
+                                  int(causal), threads or default_threads())
+    return out, p
+
+
+def attention_bwd_bhsd(d_o, q, k, v, scale: float, causal: bool, threads=None):
+    """Returns (dQ, dK, dV) in the shape of q."""
+    d_o, q, k, v = (_c(t, np.float32) for t in (d_o, q, k, v))
+    s, d = q.shape[-2:]
+    bh = q.size // (s * d)
+    dq, dk, dv = np.empty_like(q), np.empty_like(q), np.empty_like(q)
+    load().ref_attention_bwd_bhsd(_p(d_o), _p(q), _p(k), _p(v), _p(dq), _p(dk), _p(dv), bh, s, d,
+                                  float(scale), int(causal), threads or default_threads())
+    return dq, dk, dv

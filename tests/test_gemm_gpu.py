@@ -1,0 +1,277 @@
+"""GPU parity of the MFMA GEMMs against the CPU oracle, through the C ABI (Python mirror).
+
+FP32: normwise relative error <= 1e-5 against the oracle's sequential f32 loop on the same inputs,
+and bit-exact on small-integer inputs (exact arithmetic in any summation order).
+BF16: bit-exact on small-integer inputs; relative Frobenius error <= 1e-2 against the f32 oracle on
+the unrounded f32 inputs for Gaussian data.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from irontensor_amd import synth
+from tests.numerics import BF16_FROB_TOL, FP32_TOL, frob_rel, normwise_rel, op
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+# ------------------------------------------------------------------ reference known answers
+
+def test_kat_matmul_2x2(it):
+    # src/ops/gemm.rs:291-306
+    a = it.Tensor.from_f32_slice([1.0, 2.0, 3.0, 4.0], [2, 2])
+    b = it.Tensor.from_f32_slice([5.0, 6.0, 7.0, 8.0], [2, 2])
+    c = it.matmul(a, b)
+    assert c.shape() == [2, 2]
+    assert c.as_f32_slice().tolist() == [19.0, 22.0, 43.0, 50.0]
+
+
+def test_kat_matmul_larger(it, oracle):
+    # src/ops/gemm.rs:308-351 (tolerance 1e-3 absolute there)
+    m, k, n = 64, 32, 48
+    i, j = np.meshgrid(np.arange(m), np.arange(k), indexing="ij")
+    a = (i + j).astype(np.float32) * np.float32(0.01)
+    i, j = np.meshgrid(np.arange(k), np.arange(n), indexing="ij")
+    b = (i * j).astype(np.float32) * np.float32(0.01)
+    c = it.matmul(it.Tensor.from_f32_slice(a, [m, k]), it.Tensor.from_f32_slice(b, [k, n]))
+    ref = oracle.gemm_f32(a, b)
+    got = c.as_f32_slice().reshape(m, n)
+    assert np.max(np.abs(got - ref)) < 1e-3
+    assert normwise_rel(got, ref) <= FP32_TOL
+
+
+def test_kat_matmul_batched(it, oracle):
+    # src/ops/gemm.rs:353-386 and src/ops/mps_gemm.rs:612-635
+    for (bt, m, k, n) in ((2, 3, 4, 2), (2, 3, 4, 5)):
+        a = np.arange(bt * m * k, dtype=np.float32) * np.float32(0.1)
+        b = np.arange(bt * k * n, dtype=np.float32) * np.float32(0.1)
+        c = it.matmul(it.Tensor.from_f32_slice(a, [bt, m, k]), it.Tensor.from_f32_slice(b, [bt, k, n]))
+        assert c.shape() == [bt, m, n]
+        ref = oracle.gemm_f32(a.reshape(bt, m, k), b.reshape(bt, k, n))
+        assert np.max(np.abs(c.as_f32_slice().reshape(bt, m, n) - ref)) < 1e-3
+
+
+def test_kat_mps_matches_reference(it):
+    # src/ops/mps_gemm.rs:637-668 -- integer data: exact
+    m, k, n = 16, 8, 12
+    a = ((np.arange(m * k) % 7) - 3).astype(np.float32)
+    b = ((np.arange(k * n) % 5) - 2).astype(np.float32)
+    c = it.matmul_mps(it.Tensor.from_f32_slice(a, [m, k]), it.Tensor.from_f32_slice(b, [k, n]))
+    exact = a.reshape(m, k).astype(np.int64) @ b.reshape(k, n).astype(np.int64)
+    assert np.array_equal(c.as_f32_slice().reshape(m, n), exact.astype(np.float32))
+
+
+def test_kat_matmul_backward(it, oracle):
+    # src/ops/backward/gemm.rs:457-586 (2D, batched, 4D)
+    for shape_a, shape_b in (([3, 4], [4, 2]), ([2, 3, 4], [2, 4, 2]), ([2, 3, 4, 5], [2, 3, 5, 6])):
+        a = (np.arange(np.prod(shape_a), dtype=np.float32) * np.float32(0.01)) % np.float32(1.0)
+        b = (np.arange(np.prod(shape_b), dtype=np.float32) * np.float32(0.01)) % np.float32(1.0)
+        gshape = shape_a[:-1] + [shape_b[-1]]
+        gc = np.ones(int(np.prod(gshape)), np.float32)
+        ga, gb = it.matmul_backward(it.Tensor.from_f32_slice(gc, gshape), it.Tensor.from_f32_slice(a, shape_a),
+                                    it.Tensor.from_f32_slice(b, shape_b))
+        assert ga.shape() == shape_a and gb.shape() == shape_b
+        bt = int(np.prod(shape_a[:-2])) if len(shape_a) > 2 else 0
+        a3 = a.reshape(([bt] if bt else []) + shape_a[-2:])
+        b3 = b.reshape(([bt] if bt else []) + shape_b[-2:])
+        g3 = gc.reshape(([bt] if bt else []) + gshape[-2:])
+        ref_a = oracle.gemm_f32(g3, b3, trans_b=True)
+        ref_b = oracle.gemm_f32(a3, g3, trans_a=True)
+        assert np.max(np.abs(ga.as_f32_slice() - ref_a.ravel())) < 1e-4
+        assert np.max(np.abs(gb.as_f32_slice() - ref_b.ravel())) < 1e-4
+
+
+def test_kat_matmul_bf16(it):
+    # src/ops/bf16_ops/mod.rs:34-49
+    a = it.Tensor.from_f32_as_bf16([1.0, 2.0, 3.0, 4.0, 5.0, 6.0], [2, 3])
+    b = it.Tensor.from_f32_as_bf16([1.0, 2.0, 3.0, 4.0, 5.0, 6.0], [3, 2])
+    c = it.matmul_bf16(a, b)
+    assert c.shape() == [2, 2] and c.precision() == it.Precision.BF16
+    assert it.bf16_to_f32(c.as_bf16_slice()).tolist() == [22.0, 28.0, 49.0, 64.0]
+
+
+def test_kat_linear_with_bias(it):
+    # src/nn/linear.rs:224-238
+    layer = it.Linear.from_weight(it.Tensor.from_f32_slice([1.0, 0.0, 0.0, 1.0], [2, 2]),
+                                  it.Tensor.from_f32_slice([1.0, 2.0], [2]))
+    out = layer.forward(it.Tensor.from_f32_slice([1.0, 2.0], [1, 2]))
+    assert out.as_f32_slice().tolist() == [2.0, 4.0]
+
+
+# ------------------------------------------------------------------ FP32 parity sweep
+
+SHAPES = [(1, 1, 1), (2, 3, 4), (16, 16, 16), (17, 33, 65), (64, 64, 64), (127, 129, 131),
+          (1, 300, 257), (300, 1, 77), (256, 688, 256), (96, 80, 2048)]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_f32_parity_layouts(it, oracle, ta, tb, m, n, k):
+    _log(f"[f32 parity] ta={ta} tb={tb} m={m} n={n} k={k}")
+    a = synth.normal(1000 + m + n, (k, m) if ta else (m, k))
+    b = synth.normal(2000 + k, (n, k) if tb else (k, n), std=0.02)
+    c = it.gemm(it.Tensor.from_f32_slice(a, a.shape), it.Tensor.from_f32_slice(b, b.shape),
+                trans_a=bool(ta), trans_b=bool(tb))
+    ref = oracle.gemm_f32(a, b, bool(ta), bool(tb))
+    assert normwise_rel(c.numpy(), ref) <= FP32_TOL
+    # exact arithmetic: small integers give the same bits in any order
+    ai = synth.small_ints(3000 + m, a.shape, -3, 3)
+    bi = synth.small_ints(4000 + n, b.shape, -3, 3)
+    ci = it.gemm(it.Tensor.from_f32_slice(ai, ai.shape), it.Tensor.from_f32_slice(bi, bi.shape),
+                 trans_a=bool(ta), trans_b=bool(tb))
+    exact = op(ai, ta).astype(np.int64) @ op(bi, tb).astype(np.int64)
+    assert np.array_equal(ci.numpy(), exact.astype(np.float32))
+
+
+def test_config1_qkv_projection(it, oracle):
+    """X [4096,256] ~N(0,1), W [768,256] ~N(0,0.02), Y = X.W^T (FP32)."""
+    x = synth.normal(1, (4096, 256))
+    w = synth.normal(2, (768, 256), std=0.02)
+    y = it.matmul_mps_nt(it.Tensor.from_f32_slice(x, x.shape), it.Tensor.from_f32_slice(w, w.shape))
+    ref = oracle.gemm_f32(x, w, trans_b=True)
+    got = y.numpy()
+    err = normwise_rel(got, ref)
+    bound = 1e-5 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    _log(f"[config1] normwise rel err {err:.3e}; per-element bound violations "
+         f"{int(np.sum(np.abs(got - ref) > bound))}")
+    assert err <= FP32_TOL
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 4096), (688, 256, 4096), (256, 16384 // 16, 4096)])
+def test_f32_split_k_weight_gradients(it, oracle, m, n, k):
+    """dW = dY^T.X (TN) with a long reduction: exercises split-K and its ordered reduction."""
+    _log(f"[split-K] m={m} n={n} k={k}")
+    dy = synth.normal(5 + m, (k, m))
+    x = synth.normal(6 + n, (k, n))
+    dw = it.matmul_tn(it.Tensor.from_f32_slice(dy, dy.shape), it.Tensor.from_f32_slice(x, x.shape))
+    ref = oracle.gemm_f32(dy, x, trans_a=True)
+    assert normwise_rel(dw.numpy(), ref) <= FP32_TOL
+    again = it.matmul_tn(it.Tensor.from_f32_slice(dy, dy.shape), it.Tensor.from_f32_slice(x, x.shape))
+    assert np.array_equal(dw.numpy(), again.numpy())  # deterministic reduction
+
+
+def test_f32_alpha_beta_and_broadcast_batch(it, oracle):
+    a = synth.normal(7, (3, 40, 24))
+    b = synth.normal(8, (24, 56))          # broadcast over the batch
+    c0 = synth.normal(9, (3, 40, 56))
+    out = it.Tensor.from_f32_slice(c0, c0.shape)
+    it.gemm(it.Tensor.from_f32_slice(a, a.shape), it.Tensor.from_f32_slice(b, b.shape),
+            alpha=0.5, beta=2.0, out=out)
+    ref = 0.5 * np.stack([oracle.gemm_f32(a[i], b) for i in range(3)]).astype(np.float64) + 2.0 * c0
+    assert normwise_rel(out.numpy(), ref) <= FP32_TOL
+
+
+def test_f32_bias_epilogue(it, oracle):
+    x = synth.normal(10, (2, 33, 96))
+    w = synth.normal(11, (80, 96), std=0.02)
+    bias = synth.normal(12, (80,))
+    y = it.linear(it.Tensor.from_f32_slice(x, x.shape), it.Tensor.from_f32_slice(w, w.shape),
+                  it.Tensor.from_f32_slice(bias, bias.shape))
+    assert y.shape() == [2, 33, 80]
+    ref = oracle.add_bias(oracle.gemm_f32(x.reshape(66, 96), w, trans_b=True), bias)
+    assert normwise_rel(y.numpy().reshape(66, 80), ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_causal_epilogue(it, oracle, dtype):
+    s, d = 200, 64
+    q = synth.normal(13, (s, d))
+    k = synth.normal(14, (s, d))
+    mk = (lambda x: it.Tensor.from_f32_slice(x, x.shape)) if dtype == "f32" else \
+        (lambda x: it.Tensor.from_f32_as_bf16(x, x.shape))
+    out = it.gemm(mk(q), mk(k), trans_b=True, alpha=0.125, causal=True).numpy()
+    upper = np.triu(np.ones((s, s), bool), 1)
+    assert np.all(np.isneginf(out[upper]))
+    if dtype == "f32":
+        ref = oracle.gemm_f32(q, k, trans_b=True) * np.float32(0.125)
+    else:
+        ref = oracle.gemm_bf16(oracle.f32_to_bf16(q), oracle.f32_to_bf16(k), trans_b=True) * np.float32(0.125)
+    assert normwise_rel(out[~upper], ref[~upper]) <= FP32_TOL
+
+
+@pytest.mark.parametrize("rows,h,f", [(64, 32, 48), (333, 256, 688)])
+def test_f32_swiglu_dual_epilogue(it, oracle, rows, h, f):
+    x = synth.normal(15, (rows, h))
+    wg = synth.normal(16, (f, h), std=0.05)
+    wu = synth.normal(17, (f, h), std=0.05)
+    hh, g, u = it.swiglu_up(it.Tensor.from_f32_slice(x, x.shape), it.Tensor.from_f32_slice(wg, wg.shape),
+                            it.Tensor.from_f32_slice(wu, wu.shape))
+    g_ref = oracle.gemm_f32(x, wg, trans_b=True)
+    u_ref = oracle.gemm_f32(x, wu, trans_b=True)
+    assert normwise_rel(g.numpy(), g_ref) <= FP32_TOL
+    assert normwise_rel(u.numpy(), u_ref) <= FP32_TOL
+    assert normwise_rel(hh.numpy(), oracle.swiglu(g_ref, u_ref)) <= FP32_TOL
+
+
+# ------------------------------------------------------------------ BF16
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("m,n,k", [(16, 16, 32), (33, 65, 129), (128, 256, 320), (1, 11008 // 8, 4096)])
+def test_bf16_exact_integers(it, oracle, ta, tb, m, n, k):
+    _log(f"[bf16 exact] ta={ta} tb={tb} m={m} n={n} k={k}")
+    a = synth.small_ints(50 + m, (k, m) if ta else (m, k), -8, 8)
+    b = synth.small_ints(60 + n, (n, k) if tb else (k, n), -8, 8)
+    ta_, tb_ = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    c = it.gemm(ta_, tb_, trans_a=bool(ta), trans_b=bool(tb))
+    exact = (op(a, ta).astype(np.int64) @ op(b, tb).astype(np.int64)).astype(np.float32)
+    assert np.array_equal(c.numpy(), exact)
+    c16 = it.gemm(ta_, tb_, trans_a=bool(ta), trans_b=bool(tb), out_precision=it.Precision.BF16)
+    ref16 = oracle.gemm_bf16(oracle.f32_to_bf16(a), oracle.f32_to_bf16(b), bool(ta), bool(tb), out_bf16=True)
+    assert np.array_equal(c16.as_bf16_slice().reshape(ref16.shape), ref16)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_bf16_gaussian_frobenius(it, oracle, ta, tb):
+    m, n, k = 512, 384, 1024
+    a = synth.normal(70, (k, m) if ta else (m, k))
+    b = synth.normal(71, (n, k) if tb else (k, n))
+    c = it.gemm(it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape),
+                trans_a=bool(ta), trans_b=bool(tb))
+    ref = oracle.gemm_f32(a, b, bool(ta), bool(tb))
+    err = frob_rel(c.numpy(), ref)
+    _log(f"[bf16 frob] ta={ta} tb={tb}: {err:.3e}")
+    assert err <= BF16_FROB_TOL
+    # against the oracle on the same BF16 operands the only difference is summation order
+    ref16 = oracle.gemm_bf16(oracle.f32_to_bf16(a), oracle.f32_to_bf16(b), bool(ta), bool(tb))
+    assert normwise_rel(c.numpy(), ref16) <= FP32_TOL
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_bf16_decode_shapes(it, oracle, m, ta, tb):
+    """BASELINE config 5b: M in {1,4,16}, K=4096, N=11008."""
+    k, n = 4096, 11008
+    _log(f"[decode] m={m} ta={ta} tb={tb}")
+    a = synth.normal(80 + m, (k, m) if ta else (m, k))
+    b = synth.normal(81, (n, k) if tb else (k, n))
+    c = it.gemm(it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape),
+                trans_a=bool(ta), trans_b=bool(tb))
+    ref16 = oracle.gemm_bf16(oracle.f32_to_bf16(a), oracle.f32_to_bf16(b), bool(ta), bool(tb))
+    assert normwise_rel(c.numpy(), ref16) <= FP32_TOL
+    assert frob_rel(c.numpy(), oracle.gemm_f32(a, b, bool(ta), bool(tb))) <= BF16_FROB_TOL
+
+
+@pytest.mark.parametrize("n", [2048, 4096])
+def test_bf16_square_freivalds(it, n):
+    """Full-size property check (the oracle would take minutes): (A.B).x == A.(B.x) in float64 for
+    random x, on the BF16-rounded operands (Freivalds); error relative to |A|.(|B|.|x|)."""
+    _log(f"[freivalds] n={n}")
+    a = synth.normal(90, (n, n))
+    b = synth.normal(91, (n, n))
+    ta, tb = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    a64 = it.bf16_to_f32(ta.as_bf16_slice()).reshape(n, n).astype(np.float64)
+    b64 = it.bf16_to_f32(tb.as_bf16_slice()).reshape(n, n).astype(np.float64)
+    x = synth.normal(92, (n,)).astype(np.float64)
+    for trans_b in (False, True):
+        c = it.gemm(ta, tb, trans_b=trans_b).numpy().astype(np.float64)
+        bb = b64.T if trans_b else b64
+        lhs = c @ x
+        rhs = a64 @ (bb @ x)
+        scale = np.abs(a64) @ (np.abs(bb) @ np.abs(x))
+        assert np.max(np.abs(lhs - rhs) / scale) < 1e-5, trans_b
