@@ -174,30 +174,48 @@ typedef struct it_attn_layout {
  * Forward attention contractions (ops::attention after its layout transposes,
  * src/ops/attention.rs:286-377): Sc = scale * Q.K^T (NT GEMM; causal tiles above the diagonal are
  * skipped), P = softmax(Sc) (causal: columns > row are 0), O = P.V (NN GEMM; causal: only k <= row).
- * Q, O: [BH, seq_q, D] through q_layout; K, V: [BH, seq_kv, D] through kv_layout (NULL = q_layout).
- * Sc: [BH, seq_q, seq_kv] f32 workspace; P: [BH, seq_q, seq_kv] of dtype; O: f32.
+ * Q: [BH, seq_q, D] through q_layout; K, V: [BH, seq_kv, D] through kv_layout (NULL = q_layout);
+ * O: [BH, seq_q, D] f32 through o_layout (NULL = q_layout).
+ * Sc: [BH, seq_q, seq_kv] f32 workspace; P: [BH, seq_q, seq_kv] of dtype.
  * dtype IT_F32: everything FP32. IT_BF16: Q, K, V and P are BF16 (FP32 accumulation).
  * causal requires seq_q == seq_kv (as the reference asserts, src/ops/attention.rs:346-350).
  */
 it_status it_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
                                int64_t seq_kv, int64_t head_dim, float scale, int causal,
                                const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                               const it_attn_layout *o_layout,
                                const void *Q, const void *K, const void *V,
                                float *Sc, void *P, float *O);
 
 /*
- * attention_backward_recompute (src/train/helpers.rs:120-193) on [BH, seq, D] operands sharing one
- * layout: recompute Sc, P; dV = P^T.dO (TN); dP = dO.V^T (NT); dS = softmax_backward(dP, P);
+ * attention_backward_recompute (src/train/helpers.rs:120-193) on [BH, seq, D] operands:
+ * recompute Sc, P; dV = P^T.dO (TN); dP = dO.V^T (NT); dS = softmax_backward(dP, P);
  * dQ = scale * dS.K (NN); dK = scale * dS^T.Q (TN).
+ * Q and dQ use q_layout; K, V, dK, dV use kv_layout (NULL = q_layout); dO uses o_layout
+ * (NULL = q_layout). dQ, dK, dV are f32, so with dtype BF16 their layouts are read as f32 strides.
  * IT_F32: all FP32. IT_BF16: Q, K, V, dO BF16; Sc, dP FP32; P, dS BF16; dQ, dK, dV FP32.
  * Workspaces Sc, dP: [BH,S,S] f32; P, dS: [BH,S,S] of dtype.
  */
 it_status it_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
                                 int64_t head_dim, float scale, int causal,
-                                const it_attn_layout *layout,
+                                const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                const it_attn_layout *o_layout,
                                 const void *dO, const void *Q, const void *K, const void *V,
                                 float *Sc, void *P, float *dP, void *dS,
                                 float *dQ, float *dK, float *dV);
+
+/* ---------------------------------------------------------------- graphs (launch-bound loops) */
+
+typedef struct it_graph it_graph;
+
+/* Starts capturing the context's stream into a HIP graph. Until it_capture_end, no call may need a
+ * new device allocation (it fails with IT_ERR_INVALID instead): run the work once eagerly first. */
+it_status it_capture_begin(it_context *ctx);
+/* Ends the capture and instantiates the graph. */
+it_status it_capture_end(it_context *ctx, it_graph **out_graph);
+/* Replays the graph on the context's stream. */
+it_status it_graph_launch(it_context *ctx, it_graph *graph);
+it_status it_graph_destroy(it_graph *graph);
 
 /* ---------------------------------------------------------------- profiling (src/profile) */
 

@@ -92,11 +92,17 @@ _SIGNATURES = {
                                     c_i64, c_i64, c_i64, c_int]),
     "it_attention_forward": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_i64, c_float, c_int,
                                      C.POINTER(AttnLayout), C.POINTER(AttnLayout),
+                                     C.POINTER(AttnLayout),
                                      c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "it_attention_backward": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_float, c_int,
+                                      C.POINTER(AttnLayout), C.POINTER(AttnLayout),
                                       C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p]),
+    "it_capture_begin": (c_int, [c_void_p]),
+    "it_capture_end": (c_int, [c_void_p, C.POINTER(c_void_p)]),
+    "it_graph_launch": (c_int, [c_void_p, c_void_p]),
+    "it_graph_destroy": (c_int, [c_void_p]),
     "it_profiler_enable": (c_int, [c_void_p, c_int]),
     "it_profiler_reset": (c_int, [c_void_p]),
     "it_profiler_report": (c_int, [c_void_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),

@@ -179,8 +179,9 @@ namespace {
 
 struct AttnGeom {
     int64_t bh, Sq, Skv, D;
-    it_attn_layout lay;     // Q, O, dQ, dO
+    it_attn_layout lay;     // Q, dQ
     it_attn_layout kv_lay;  // K, V, dK, dV
+    it_attn_layout o_lay;   // O, dO
 };
 
 bool bad_layout(const it_attn_layout &l, int64_t head_dim) {
@@ -189,7 +190,8 @@ bool bad_layout(const it_attn_layout &l, int64_t head_dim) {
 
 it_status check_attention(const char *op, it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
                           int64_t seq_kv, int64_t head_dim, const it_attn_layout *q_layout,
-                          const it_attn_layout *kv_layout, AttnGeom *g) {
+                          const it_attn_layout *kv_layout, const it_attn_layout *o_layout,
+                          AttnGeom *g) {
     if (!ctx) return fail(IT_ERR_NULL, std::string(op) + ": ctx is NULL");
     if (dtype != IT_F32 && dtype != IT_BF16)
         return fail(IT_ERR_PRECISION, std::string(op) + ": precision mismatch, expected FP32 or BF16, got " +
@@ -203,12 +205,13 @@ it_status check_attention(const char *op, it_context *ctx, it_dtype dtype, int64
         kv = *kv_layout;
     else if (q_layout)
         kv = *q_layout;
-    if (bad_layout(lay, head_dim) || bad_layout(kv, head_dim))
+    it_attn_layout ol = o_layout ? *o_layout : lay;
+    if (bad_layout(lay, head_dim) || bad_layout(kv, head_dim) || bad_layout(ol, head_dim))
         return fail(IT_ERR_INVALID, std::string(op) + ": bad layout strides");
-    if (bh % lay.heads != 0 || bh % kv.heads != 0 || lay.heads != kv.heads)
+    if (bh % lay.heads != 0 || lay.heads != kv.heads || lay.heads != ol.heads)
         return fail(IT_ERR_SHAPE, std::string(op) + ": shape mismatch, expected batch*heads divisible by heads " +
                                       i64(lay.heads) + ", got " + i64(bh));
-    *g = AttnGeom{bh, seq_q, seq_kv, head_dim, lay, kv};
+    *g = AttnGeom{bh, seq_q, seq_kv, head_dim, lay, kv, ol};
     return IT_OK;
 }
 
@@ -233,6 +236,10 @@ struct Operand {
 
 Operand q_operand(const AttnGeom &g, const void *p) {
     return Operand{p, g.lay.row_stride, g.lay.head_stride, g.lay.batch_stride};
+}
+
+Operand o_operand(const AttnGeom &g, const void *p) {
+    return Operand{p, g.o_lay.row_stride, g.o_lay.head_stride, g.o_lay.batch_stride};
 }
 
 Operand kv_operand(const AttnGeom &g, const void *p) {
@@ -291,11 +298,12 @@ extern "C" {
 it_status it_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
                                int64_t seq_kv, int64_t head_dim, float scale, int causal,
                                const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                               const it_attn_layout *o_layout,
                                const void *Q, const void *K, const void *V,
                                float *Sc, void *P, float *O) {
     AttnGeom g;
     it_status st = check_attention("attention", ctx, dtype, bh, seq_q, seq_kv, head_dim, q_layout,
-                                   kv_layout, &g);
+                                   kv_layout, o_layout, &g);
     if (st != IT_OK) return st;
     if (causal && seq_q != seq_kv)
         return fail(IT_ERR_SHAPE, "attention: shape mismatch, expected seq_q == seq_kv for causal, got " +
@@ -313,20 +321,21 @@ it_status it_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int6
     it::GemmArgs a = attn_args(g, g.Sq, g.D, g.Skv, eb);
     set_A(a, score_operand(g, P), eb);
     set_B(a, kv_operand(g, V), eb);
-    set_C(a, q_operand(g, O), false);
+    set_C(a, o_operand(g, O), false);
     a.kmode = causal ? it::KMODE_LOWER : it::KMODE_FULL;
     return it::launch_gemm(ctx, dtype, false, false, a, "attn.O=PV");
 }
 
 it_status it_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
                                 int64_t head_dim, float scale, int causal,
-                                const it_attn_layout *layout,
+                                const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                const it_attn_layout *o_layout,
                                 const void *dO, const void *Q, const void *K, const void *V,
                                 float *Sc, void *P, float *dP, void *dS,
                                 float *dQ, float *dK, float *dV) {
     AttnGeom g;
-    it_status st = check_attention("attention_backward", ctx, dtype, bh, seq, seq, head_dim, layout,
-                                   layout, &g);
+    it_status st = check_attention("attention_backward", ctx, dtype, bh, seq, seq, head_dim, q_layout,
+                                   kv_layout, o_layout, &g);
     if (st != IT_OK) return st;
     if (bh == 0 || seq == 0 || head_dim == 0) return IT_OK;
     if (!dO || !Q || !K || !V || !Sc || !P || !dP || !dS || !dQ || !dK || !dV)
@@ -338,14 +347,14 @@ it_status it_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int
     // dV = P^T.dO (TN): op(A)[j][i] = P[i][j], nonzero only for i >= j under the causal mask.
     it::GemmArgs a = attn_args(g, g.Sq, g.D, g.Sq, eb);
     set_A(a, score_operand(g, P), eb);
-    set_B(a, q_operand(g, dO), eb);
+    set_B(a, o_operand(g, dO), eb);
     set_C(a, kv_operand(g, dV), false);
     a.kmode = causal ? it::KMODE_UPPER : it::KMODE_FULL;
     if ((st = it::launch_gemm(ctx, dtype, true, false, a, "attn.dV=P^TdO")) != IT_OK) return st;
 
     // dP = dO.V^T (NT); above-diagonal tiles are never read.
     a = attn_args(g, g.Sq, g.Sq, g.D, eb);
-    set_A(a, q_operand(g, dO), eb);
+    set_A(a, o_operand(g, dO), eb);
     set_B(a, kv_operand(g, V), eb);
     set_C(a, score_operand(g, dP), false);
     a.causal = causal ? it::CAUSAL_SKIP : it::CAUSAL_NONE;

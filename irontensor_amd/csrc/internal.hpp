@@ -57,6 +57,9 @@ struct it_context {
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
 
+    // True between it_capture_begin and it_capture_end: nothing may allocate.
+    bool capturing = false;
+
     // Profiler state.
     bool profiling = false;
     std::vector<it::ProfileRecord> pending;
@@ -66,6 +69,11 @@ struct it_context {
 
 struct it_event {
     hipEvent_t ev = nullptr;
+};
+
+struct it_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 namespace it {

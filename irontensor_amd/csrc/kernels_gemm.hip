@@ -450,8 +450,9 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     hipEvent_t ev = nullptr;
     if (ctx->profiling) {
         char buf[192];
-        std::snprintf(buf, sizeof(buf), "gemm_%s_%c%c_%dx%d|%s[%lld,%lld,%lld]x%lld s%d",
+        std::snprintf(buf, sizeof(buf), "gemm_%s_%c%c_%dx%d%s%s|%s[%lld,%lld,%lld]x%lld s%d",
                       bf16 ? "bf16" : "f32", transA ? 'T' : 'N', transB ? 'T' : 'N', cfg.bm, cfg.bn,
+                      a.dual ? "_swiglu" : "", a.causal || a.kmode ? "_causal" : "",
                       profile_tag ? profile_tag : "", (long long)a.M, (long long)a.N,
                       (long long)a.K, (long long)a.batch, splits);
         key = buf;

@@ -31,6 +31,9 @@ it_status fail_hip(hipError_t err, const char *what) {
 void clear_error() { g_last_error.clear(); }
 
 it_status ensure_scratch(it_context *ctx, size_t bytes, void **out) {
+    if (ctx->scratch_bytes < bytes && ctx->capturing)
+        return fail(IT_ERR_INVALID, "scratch of " + std::to_string(bytes) +
+                                        " bytes needed during graph capture: run the work once before capturing");
     if (ctx->scratch_bytes < bytes) {
         if (ctx->scratch) {
             IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
@@ -59,7 +62,7 @@ static hipEvent_t pool_event(it_context *ctx) {
 
 void profile_begin(it_context *ctx, const std::string &, hipEvent_t *start_out) {
     *start_out = nullptr;
-    if (!ctx->profiling) return;
+    if (!ctx->profiling || ctx->capturing) return;
     hipEvent_t e = pool_event(ctx);
     if (e && hipEventRecord(e, ctx->stream) == hipSuccess) *start_out = e;
 }
@@ -186,6 +189,9 @@ it_status it_malloc(it_context *ctx, size_t bytes, void **out_ptr) {
         p = it->second;
         ctx->cache.erase(it);
     } else {
+        if (ctx->capturing)
+            return fail(IT_ERR_INVALID, "it_malloc: no cached block of " + std::to_string(sz) +
+                                            " bytes during graph capture");
         hipError_t e = hipMalloc(&p, sz);
         if (e != hipSuccess) {
             // Release the cache once and retry before giving up.
@@ -306,6 +312,45 @@ it_status it_event_destroy(it_event *ev) {
     if (!ev) return IT_OK;
     (void)hipEventDestroy(ev->ev);
     delete ev;
+    return IT_OK;
+}
+
+it_status it_capture_begin(it_context *ctx) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_capture_begin: ctx is NULL");
+    if (ctx->capturing) return fail(IT_ERR_INVALID, "it_capture_begin: already capturing");
+    IT_HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    return IT_OK;
+}
+
+it_status it_capture_end(it_context *ctx, it_graph **out_graph) {
+    if (!ctx || !out_graph) return fail(IT_ERR_NULL, "it_capture_end: NULL argument");
+    if (!ctx->capturing) return fail(IT_ERR_INVALID, "it_capture_end: not capturing");
+    ctx->capturing = false;
+    *out_graph = nullptr;
+    auto *g = new it_graph();
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        if (g->graph) (void)hipGraphDestroy(g->graph);
+        delete g;
+        return it::fail_hip(e, "hipStreamEndCapture/hipGraphInstantiate");
+    }
+    *out_graph = g;
+    return IT_OK;
+}
+
+it_status it_graph_launch(it_context *ctx, it_graph *graph) {
+    if (!ctx || !graph) return fail(IT_ERR_NULL, "it_graph_launch: NULL argument");
+    IT_HIP_TRY(hipGraphLaunch(graph->exec, ctx->stream));
+    return IT_OK;
+}
+
+it_status it_graph_destroy(it_graph *graph) {
+    if (!graph) return IT_OK;
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
     return IT_OK;
 }
 

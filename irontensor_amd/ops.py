@@ -370,7 +370,7 @@ def attention(q: Tensor, k: Tensor, v: Tensor, causal: bool) -> Tensor:
     lq, lkv = _layout_bshd(b, sq, h, d), _layout_bshd(b, skv, h, d)
     st = q.ctx.lib.it_attention_forward(q.ctx.handle, _lib.IT_F32, bh, sq, skv, d,
                                         1.0 / math.sqrt(d), int(causal), C.byref(lq), C.byref(lkv),
-                                        _vp(q), _vp(k), _vp(v), _vp(sc), _vp(p), _vp(out))
+                                        C.byref(lq), _vp(q), _vp(k), _vp(v), _vp(sc), _vp(p), _vp(out))
     check(st, "attention")
     return out
 
@@ -386,7 +386,7 @@ def attention_forward_bhsd(q: Tensor, k: Tensor, v: Tensor, causal: bool = True,
     o = Tensor.empty([b, h, s, d], _P.FP32, q.ctx)
     lay = _layout_bhsd(s, d)
     check(q.ctx.lib.it_attention_forward(q.ctx.handle, int(prec), b * h, s, s, d, float(scale),
-                                         int(causal), C.byref(lay), C.byref(lay), _vp(q), _vp(k),
+                                         int(causal), C.byref(lay), None, None, _vp(q), _vp(k),
                                          _vp(v), _vp(sc), _vp(p), _vp(o)), "attention")
     return o, p
 
@@ -419,7 +419,7 @@ def attention_backward_recompute(grad_output: Tensor, q: Tensor, k: Tensor, v: T
     dv = Tensor.empty([b, h, s, d], _P.FP32, ctx)
     lay = _layout_bhsd(s, d)
     check(ctx.lib.it_attention_backward(ctx.handle, int(prec), bh, s, d, float(scale), int(causal),
-                                        C.byref(lay), _vp(grad_output), _vp(q), _vp(k), _vp(v),
+                                        C.byref(lay), None, None, _vp(grad_output), _vp(q), _vp(k), _vp(v),
                                         _vp(sc), _vp(p), _vp(dp), _vp(ds), _vp(dq), _vp(dk), _vp(dv)),
           "attention_backward")
     return dq, dk, dv

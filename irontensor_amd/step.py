@@ -1,0 +1,265 @@
+"""The contractions of one Llama-style training step at a model's real shapes, in step order on one
+stream: the GEMM-set driver for the TINY and medium configurations.
+
+Follows the reference trainer's call order (src/train/trainer/train_step.rs:39-236,
+src/train/forward.rs:79-212, src/train/backward.rs:21-177) for every contraction it makes:
+
+  forward, per layer:  QKV = X.Wqkv^T (one NT GEMM; the reference issues three, forward.rs:101-103)
+                       attention contractions S = scale.Q.K^T (causal), P = softmax(S), O = P.V,
+                       read in place from the QKV buffer's [B,S,H,D] layout (no transposes)
+                       Y = O.Wo^T                                         (forward.rs:146)
+                       h = silu(X2.Wg^T) * (X2.Wu^T), fused dual-B GEMM   (forward.rs:166-172)
+                       Z = h.Wd^T                                         (forward.rs:175)
+  LM head:             logits = Hf.E^T                                    (trainer/mod.rs:229-235)
+  backward, LM head:   dE = dlogits^T.Hf (TN), dHf = dlogits.E (NN)       (train_step.rs:206-210)
+  backward, per layer: down, gate|up (one GEMM each for dX and dW over the concatenated Wg|Wu),
+                       Wo, attention_backward_recompute (5 GEMMs + softmax and its backward),
+                       QKV                                                (backward.rs:53-147)
+
+The elementwise work between contractions (RMSNorm, RoPE, residual adds, SwiGLU backward, cross
+entropy) is outside this path: each layer's normalised inputs and each upstream gradient are
+seeded N(0,1) buffers standing where those ops would write, so every GEMM runs at its real shape
+on realistic data. Weights are N(0, 0.02).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+from typing import List, Optional, Tuple
+
+import numpy as np
+
+from . import _lib, synth
+from .errors import check
+from .tensor import Context, Precision, Tensor
+
+
+@dataclass(frozen=True)
+class ModelShape:
+    name: str
+    layers: int
+    hidden: int
+    heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+    batch: int
+    seq: int
+
+    @property
+    def tokens(self) -> int:
+        return self.batch * self.seq
+
+
+# BASELINE configs[1] and configs[3]
+TINY = ModelShape("tiny", 4, 256, 4, 64, 688, 16384, 16, 256)
+MEDIUM = ModelShape("medium", 12, 1024, 16, 64, 2816, 32768, 8, 1024)
+
+
+class _Launch:
+    """One recorded contraction for reporting: name and dense-equivalent FLOPs."""
+
+    __slots__ = ("name", "flops")
+
+    def __init__(self, name: str, flops: float):
+        self.name, self.flops = name, flops
+
+
+class GemmStep:
+    """Owns every buffer of the step and enqueues its contractions (eagerly or into a HIP graph)."""
+
+    def __init__(self, shape: ModelShape, precision: Precision = Precision.FP32,
+                 ctx: Optional[Context] = None, seed: int = 1234):
+        if shape.heads * shape.head_dim != shape.hidden:
+            raise ValueError("heads * head_dim must equal hidden")
+        self.s = shape
+        self.prec = Precision(precision)
+        self.ctx = ctx or Context.global_()
+        self.lib = self.ctx.lib
+        self.graph = None
+        s, P = shape, self.prec
+        T, H, F, V, L = s.tokens, s.hidden, s.ffn, s.vocab, s.layers
+        bh = s.batch * s.heads
+        self._seed = seed
+
+        def w(shape_, std=0.02):
+            return self._tensor(shape_, std)
+
+        def act(shape_):
+            return self._tensor(shape_, 1.0)
+
+        def empty(shape_, prec=P):
+            return Tensor.empty(shape_, prec, self.ctx)
+
+        # Weights (layer-major lists), stored as the reference stores them: [out, in].
+        self.Wqkv = [w([3 * H, H]) for _ in range(L)]
+        self.Wo = [w([H, H]) for _ in range(L)]
+        self.Wgu = [w([2 * F, H]) for _ in range(L)]   # gate rows then up rows
+        self.Wd = [w([H, F]) for _ in range(L)]
+        self.E = w([V, H])                             # untied LM head
+        # Forward caches
+        self.X = [act([T, H]) for _ in range(L)]       # attention-norm output
+        self.X2 = [act([T, H]) for _ in range(L)]      # ffn-norm output
+        self.QKV = [empty([T, 3 * H]) for _ in range(L)]
+        self.O = [empty([T, H], Precision.FP32) for _ in range(L)]
+        self.Oin = self.O if P is Precision.FP32 else [act([T, H]) for _ in range(L)]
+        self.Y = [empty([T, H]) for _ in range(L)]
+        self.G = [empty([T, F]) for _ in range(L)]
+        self.U = [empty([T, F]) for _ in range(L)]
+        self.Hh = [empty([T, F]) for _ in range(L)]
+        self.Z = [empty([T, H]) for _ in range(L)]
+        self.Hf = act([T, H])
+        self.logits = empty([T, V])
+        # Backward: upstream gradients (seeded) and results
+        self.dlogits = act([T, V])
+        self.dZ = act([T, H])
+        self.dGU = act([T, 2 * F])
+        self.dY = act([T, H])
+        self.dO = act([T, H])
+        self.dE = empty([V, H], Precision.FP32)
+        self.dHf = empty([T, H], Precision.FP32)
+        self.dHh = empty([T, F], Precision.FP32)
+        self.dX2 = empty([T, H], Precision.FP32)
+        self.dOp = empty([T, H], Precision.FP32)
+        self.dQKV = empty([T, 3 * H], Precision.FP32)
+        self.dX = empty([T, H], Precision.FP32)
+        self.dWd = [empty([H, F], Precision.FP32) for _ in range(L)]
+        self.dWgu = [empty([2 * F, H], Precision.FP32) for _ in range(L)]
+        self.dWo = [empty([H, H], Precision.FP32) for _ in range(L)]
+        self.dWqkv = [empty([3 * H, H], Precision.FP32) for _ in range(L)]
+        # Attention workspaces, shared by all layers
+        self.Sc = empty([bh, s.seq, s.seq], Precision.FP32)
+        self.Pw = empty([bh, s.seq, s.seq])
+        self.dP = empty([bh, s.seq, s.seq], Precision.FP32)
+        self.dS = empty([bh, s.seq, s.seq])
+        self.launches: List[_Launch] = []
+        self._record = True
+
+    # ---------------------------------------------------------------- helpers
+    def _tensor(self, shape_, std) -> Tensor:
+        self._seed += 1
+        data = synth.normal(self._seed, shape_, std=std)
+        if self.prec is Precision.BF16:
+            return Tensor.from_f32_as_bf16(data, shape_, self.ctx)
+        return Tensor.from_f32_slice(data, shape_, self.ctx)
+
+    def _gemm(self, name, A: Tensor, B: Tensor, Cout: Tensor, ta: bool, tb: bool, M, N, K,
+              alpha=1.0, epi: Optional[_lib.Epilogue] = None, a_off=0, lda=None):
+        lda = lda if lda is not None else (A.shape()[-1])
+        ldb = B.shape()[-1]
+        ldc = Cout.shape()[-1]
+        eb = self.prec.byte_size()
+        st = self.lib.it_gemm(self.ctx.handle, int(self.prec), int(Cout.precision()),
+                              int(ta), int(tb), M, N, K, float(alpha),
+                              C.c_void_p(A.ptr + a_off * eb), lda, 0, C.c_void_p(B.ptr), ldb, 0,
+                              0.0, C.c_void_p(Cout.ptr), ldc, 0, 1,
+                              C.byref(epi) if epi is not None else None)
+        check(st, name)
+        if self._record:
+            mult = 2 if (epi is not None and epi.flags & _lib.IT_EPI_SWIGLU) else 1
+            self.launches.append(_Launch(name, 2.0 * M * N * K * mult))
+
+    def _layouts(self):
+        s = self.s
+        qkv = _lib.AttnLayout(s.heads, s.seq * 3 * s.hidden, s.head_dim, 3 * s.hidden)
+        o = _lib.AttnLayout(s.heads, s.seq * s.hidden, s.head_dim, s.hidden)
+        return qkv, o
+
+    # ---------------------------------------------------------------- the step
+    def forward_layer(self, l: int) -> None:
+        s, P = self.s, self.prec
+        T, H, F = s.tokens, s.hidden, s.ffn
+        eb = P.byte_size()
+        self._gemm("qkv", self.X[l], self.Wqkv[l], self.QKV[l], False, True, T, 3 * H, H)
+        qkv, o = self._layouts()
+        base = self.QKV[l].ptr
+        st = self.lib.it_attention_forward(
+            self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.seq, s.head_dim,
+            1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o),
+            C.c_void_p(base), C.c_void_p(base + H * eb), C.c_void_p(base + 2 * H * eb),
+            C.c_void_p(self.Sc.ptr), C.c_void_p(self.Pw.ptr), C.c_void_p(self.O[l].ptr))
+        check(st, "attention")
+        if self._record:
+            attn = 2.0 * s.batch * s.heads * s.seq * s.seq * s.head_dim
+            self.launches += [_Launch("attn.S", attn), _Launch("attn.O", attn)]
+        self._gemm("wo", self.Oin[l], self.Wo[l], self.Y[l], False, True, T, H, H)
+        epi = _lib.Epilogue(flags=_lib.IT_EPI_SWIGLU, B2=self.Wgu[l].ptr + F * H * eb,
+                            gate_out=self.G[l].ptr, up_out=self.U[l].ptr)
+        self._gemm("gate_up_swiglu", self.X2[l], self.Wgu[l], self.Hh[l], False, True, T, F, H, epi=epi)
+        self._gemm("down", self.Hh[l], self.Wd[l], self.Z[l], False, True, T, H, F)
+
+    def backward_layer(self, l: int) -> None:
+        s, P = self.s, self.prec
+        T, H, F = s.tokens, s.hidden, s.ffn
+        # down: dHh = dZ.Wd (NN), dWd = dZ^T.Hh (TN)
+        self._gemm("down.dX", self.dZ, self.Wd[l], self.dHh, False, False, T, F, H)
+        self._gemm("down.dW", self.dZ, self.Hh[l], self.dWd[l], True, False, H, F, T)
+        # gate|up: dX2 = [dG dU].[Wg;Wu] (NN, K = 2F), dWgu = [dG dU]^T.X2 (TN)
+        self._gemm("gate_up.dX", self.dGU, self.Wgu[l], self.dX2, False, False, T, H, 2 * F)
+        self._gemm("gate_up.dW", self.dGU, self.X2[l], self.dWgu[l], True, False, 2 * F, H, T)
+        # Wo: dO = dY.Wo (NN), dWo = dY^T.O (TN)
+        self._gemm("wo.dX", self.dY, self.Wo[l], self.dOp, False, False, T, H, H)
+        self._gemm("wo.dW", self.dY, self.Oin[l], self.dWo[l], True, False, H, H, T)
+        # attention_backward_recompute into the dQKV buffer (f32, same [B,S,3,H,D] layout)
+        qkv, o = self._layouts()
+        eb = P.byte_size()
+        base = self.QKV[l].ptr
+        dbase = self.dQKV.ptr
+        st = self.lib.it_attention_backward(
+            self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.head_dim,
+            1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o),
+            C.c_void_p(self.dO.ptr), C.c_void_p(base), C.c_void_p(base + H * eb),
+            C.c_void_p(base + 2 * H * eb), C.c_void_p(self.Sc.ptr), C.c_void_p(self.Pw.ptr),
+            C.c_void_p(self.dP.ptr), C.c_void_p(self.dS.ptr), C.c_void_p(dbase),
+            C.c_void_p(dbase + H * 4), C.c_void_p(dbase + 2 * H * 4))
+        check(st, "attention_backward")
+        if self._record:
+            attn = 2.0 * s.batch * s.heads * s.seq * s.seq * s.head_dim
+            self.launches += [_Launch(n, attn) for n in ("attn.S", "attn.dV", "attn.dP", "attn.dQ", "attn.dK")]
+        # QKV: dX = dQKV.Wqkv (NN), dWqkv = dQKV^T.X (TN). dQKV is f32; in BF16 mode the
+        # projection backward reads the seeded BF16 gradient stand-in instead.
+        dqkv = self.dQKV if P is Precision.FP32 else self._dqkv_bf16()
+        self._gemm("qkv.dX", dqkv, self.Wqkv[l], self.dX, False, False, T, H, 3 * H)
+        self._gemm("qkv.dW", dqkv, self.X[l], self.dWqkv[l], True, False, 3 * H, H, T)
+
+    def _dqkv_bf16(self) -> Tensor:
+        if not hasattr(self, "_dqkv16"):
+            self._dqkv16 = self._tensor([self.s.tokens, 3 * self.s.hidden], 1.0)
+        return self._dqkv16
+
+    def enqueue(self) -> None:
+        """Issues one full step on the context stream."""
+        s = self.s
+        if self._record:
+            self.launches = []
+        for l in range(s.layers):
+            self.forward_layer(l)
+        self._gemm("lm_head", self.Hf, self.E, self.logits, False, True, s.tokens, s.vocab, s.hidden)
+        self._gemm("lm_head.dW", self.dlogits, self.Hf, self.dE, True, False, s.vocab, s.hidden, s.tokens)
+        self._gemm("lm_head.dX", self.dlogits, self.E, self.dHf, False, False, s.tokens, s.hidden, s.vocab)
+        for l in reversed(range(s.layers)):
+            self.backward_layer(l)
+        self._record = False
+
+    def flops(self) -> float:
+        return float(sum(x.flops for x in self.launches))
+
+    def capture(self) -> None:
+        """Captures one step into a HIP graph (run enqueue() once first so scratch is sized)."""
+        check(self.lib.it_capture_begin(self.ctx.handle), "capture")
+        try:
+            self.enqueue()
+        finally:
+            g = C.c_void_p()
+            st = self.lib.it_capture_end(self.ctx.handle, C.byref(g))
+        check(st, "capture")
+        self.graph = g
+
+    def replay(self) -> None:
+        check(self.lib.it_graph_launch(self.ctx.handle, self.graph), "graph launch")
+
+    def close(self) -> None:
+        if self.graph is not None:
+            self.lib.it_graph_destroy(self.graph)
+            self.graph = None

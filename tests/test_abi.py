@@ -108,7 +108,7 @@ def test_null_context_calls_fail_cleanly():
     assert lib.it_malloc(None, 16, C.byref(C.c_void_p())) == _lib.IT_ERR_NULL
     assert lib.it_stream_sync(None) == _lib.IT_ERR_NULL
     assert lib.it_mem_allocated(None) == 0
-    assert lib.it_attention_forward(None, _lib.IT_F32, 1, 1, 1, 1, 1.0, 0, None, None,
+    assert lib.it_attention_forward(None, _lib.IT_F32, 1, 1, 1, 1, 1.0, 0, None, None, None,
                                     None, None, None, None, None, None) == _lib.IT_ERR_NULL
 
 
