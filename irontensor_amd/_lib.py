@@ -6,9 +6,10 @@ with a message that says how to build it.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libirontensor_hip.so"
+LIB_PATH = Path(os.environ.get("IRONTENSOR_LIB") or Path(__file__).resolve().parent / "libirontensor_hip.so")
 
 IT_OK = 0
 IT_ERR_INNER_DIM = 1

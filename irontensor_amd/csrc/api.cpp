@@ -20,6 +20,12 @@ const char *dtype_name(it_dtype d) {
     return "unknown";
 }
 
+// 4 consecutive output elements per store: 16 B for f32, 8 B for bf16.
+bool out_vec_ok(const void *p, bool bf16, int64_t ld, int64_t s1, int64_t s2) {
+    const uintptr_t align = bf16 ? 8 : 16;
+    return ((uintptr_t)p % align == 0) && ld % 4 == 0 && s1 % 4 == 0 && s2 % 4 == 0;
+}
+
 bool vec_ok(const void *p, int elem_bytes, int64_t ld, int64_t s1, int64_t s2) {
     const int64_t vec = 16 / elem_bytes;
     return ((uintptr_t)p % 16 == 0) && ld % vec == 0 && s1 % vec == 0 && s2 % vec == 0;
@@ -110,6 +116,7 @@ it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op 
     a.out_bf16 = dtype_out == IT_BF16;
     a.a_vec_ok = vec_ok(A, eb, lda, strideA, 0);
     a.b_vec_ok = vec_ok(B, eb, ldb, strideB, 0);
+    a.c_vec_ok = out_vec_ok(C, a.out_bf16, ldc, strideC, 0);
     if (epi) {
         a.has_bias = (epi->flags & IT_EPI_BIAS) != 0;
         a.bias = epi->bias;
@@ -273,6 +280,7 @@ void set_C(it::GemmArgs &a, const Operand &o, bool bf16_out) {
     a.sC_in = o.s_in;
     a.sC_out = o.s_out;
     a.out_bf16 = bf16_out;
+    a.c_vec_ok = out_vec_ok(o.p, bf16_out, o.ld, o.s_in, o.s_out);
 }
 
 // Sc = scale * Q.K^T (causal tiles skipped), P = softmax(Sc).

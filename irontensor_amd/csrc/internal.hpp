@@ -126,6 +126,7 @@ struct GemmArgs {
     int kmode;  // KMode
     int out_bf16;
     int a_vec_ok, b_vec_ok;  // 16-byte vector loads are legal for the operand
+    int c_vec_ok;            // 4-element vector loads/stores of C (and G, U) are legal
     int tiles_m, tiles_n;
 };
 

@@ -27,6 +27,7 @@
 #include <cmath>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "internal.hpp"
 
@@ -112,9 +113,21 @@ struct Operand {
     static constexpr int ITEMS = TRANSPOSE ? (BK / 4) * (ROWS / VEC) : ROWS * BK / VEC;
     static constexpr int LOADS = TRANSPOSE ? 4 : 1;
     static constexpr int ITERS = (ITEMS + NTHREADS - 1) / NTHREADS;
+    static constexpr int KGROUPS = BK / 4;
 
     u32x4 reg[ITERS][LOADS];
 
+    // Transposed units are (k-group of 4 rows, 8 columns). Lane bit 0 picks one of two adjacent
+    // column chunks and bits 1..4 the k-group, so the 8-byte LDS stores of 32 consecutive lanes
+    // land in 64 distinct banks (two rows 8 apart, 16 k offsets each).
+    __device__ __forceinline__ static void unit(int item, int &kg, int &rc) {
+        rc = (item & 1) | ((item / (2 * KGROUPS)) << 1);
+        kg = (item >> 1) % KGROUPS;
+    }
+
+    // EDGE = false: the caller guarantees the whole tile is in bounds and 16-byte aligned, so
+    // every load is one unconditional 128-bit load.
+    template <bool EDGE = true>
     __device__ __forceinline__ void load(const T *base, int64_t ld, int64_t r0, int64_t k0,
                                          int64_t rlim, int64_t klim, bool vec_ok, int tid) {
 #pragma unroll
@@ -124,18 +137,28 @@ struct Operand {
             if constexpr (KCONTIG) {
                 const int rr = item / (BK / VEC), kc = item % (BK / VEC);
                 const int64_t gr = r0 + rr, gk = k0 + kc * VEC;
-                reg[it][0] = load_vec<T>(base, gr * ld + gk, gr < rlim, gk, klim, vec_ok);
+                if constexpr (EDGE)
+                    reg[it][0] = load_vec<T>(base, gr * ld + gk, gr < rlim, gk, klim, vec_ok);
+                else
+                    reg[it][0] = *(const u32x4 *)(base + gr * ld + gk);
             } else if constexpr (!TRANSPOSE) {
                 const int kk = item / (ROWS / VEC), rc = item % (ROWS / VEC);
                 const int64_t gk = k0 + kk, gr = r0 + rc * VEC;
-                reg[it][0] = load_vec<T>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
+                if constexpr (EDGE)
+                    reg[it][0] = load_vec<T>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
+                else
+                    reg[it][0] = *(const u32x4 *)(base + gk * ld + gr);
             } else {
-                const int kg = item / (ROWS / VEC), rc = item % (ROWS / VEC);
+                int kg, rc;
+                unit(item, kg, rc);
                 const int64_t gr = r0 + rc * VEC;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int64_t gk = k0 + kg * 4 + q;
-                    reg[it][q] = load_vec<T>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
+                    if constexpr (EDGE)
+                        reg[it][q] = load_vec<T>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
+                    else
+                        reg[it][q] = *(const u32x4 *)(base + gk * ld + gr);
                 }
             }
         }
@@ -153,7 +176,8 @@ struct Operand {
                 const int kk = item / (ROWS / VEC), rc = item % (ROWS / VEC);
                 *(u32x4 *)(lds + kk * KMAJOR_PITCH + rc * 16) = reg[it][0];
             } else {
-                const int kg = item / (ROWS / VEC), rc = item % (ROWS / VEC);
+                int kg, rc;
+                unit(item, kg, rc);
                 const u32x4 &v0 = reg[it][0], &v1 = reg[it][1], &v2 = reg[it][2], &v3 = reg[it][3];
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
@@ -168,6 +192,12 @@ struct Operand {
                 }
             }
         }
+    }
+
+    // v_mfma_f32_32x32x16_bf16 fragment: lane l supplies row `row + l % 32` and the 8 k values
+    // 8*(l/32)..8*(l/32)+7 of the 16-wide k step `ks` (bf16 tiles in [rows][BK] layout only).
+    __device__ __forceinline__ static u32x4 frag32(const char *lds, int row, int ks, int lane) {
+        return *(const u32x4 *)(lds + (row + (lane & 31)) * ROW_PITCH + ks * 32 + (lane >> 5) * 16);
     }
 
     // Fragment of the 16 rows starting at `row` for fragment step `ks`.
@@ -355,6 +385,227 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
             }
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Final values of 4 consecutive output columns (the vector form of finish_store), or raw partial
+// sums for split-K. Falls back to element stores at the right edge or for unaligned outputs.
+template <bool EDGE>
+__device__ __forceinline__ void finish4(const GemmArgs &p, f32x4 v, int64_t row, int64_t col,
+                                        int64_t coff, int64_t z) {
+    if (EDGE && (row >= p.M || col >= p.N)) return;
+    const bool full = !EDGE || col + 4 <= p.N;
+    if (p.splits > 1) {
+        float *dst = p.partial + (z * p.M + row) * p.N + col;
+        if (full && p.N % 4 == 0) {
+            *(f32x4 *)dst = v;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < p.N) dst[e] = v[e];
+        }
+        return;
+    }
+    const int64_t idx = coff + row * p.ldc + col;
+    if (full && p.c_vec_ok) {
+        v *= p.alpha;
+        if (p.beta != 0.f) {
+            f32x4 old;
+            if (p.out_bf16) {
+                const u32x2 o = *(const u32x2 *)((const uint16_t *)p.C + idx);
+                old = f32x4{__uint_as_float(o[0] << 16), __uint_as_float(o[0] & 0xffff0000u),
+                            __uint_as_float(o[1] << 16), __uint_as_float(o[1] & 0xffff0000u)};
+            } else {
+                old = *(const f32x4 *)((const float *)p.C + idx);
+            }
+            v += p.beta * old;
+        }
+        if (p.has_bias) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] += p.bias[col + e];
+        }
+        if (p.causal != CAUSAL_NONE) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e > row + p.causal_offset) v[e] = -INFINITY;
+        }
+        if (p.out_bf16) {
+            u32x2 o;
+            o[0] = (uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16);
+            o[1] = (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16);
+            *(u32x2 *)((uint16_t *)p.C + idx) = o;
+        } else {
+            *(f32x4 *)((float *)p.C + idx) = v;
+        }
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (col + e < p.N) finish_store(p, p.C, idx + e, v[e], row, col + e);
+}
+
+// Large-tile BF16 GEMM: 256x256 block tile, four waves each owning a 128x128 sub-tile built from
+// 4x4 v_mfma_f32_32x32x16_bf16 blocks (256 FP32 accumulators per lane, held in AGPRs). Per 64-wide
+// k-tile a wave issues 64 MFMAs against 32 128-bit LDS reads, half the LDS traffic per FLOP of the
+// 64x64 wave tile of gemm_mfma.
+//
+// One wave per SIMD, so latency is hidden inside the wave by software pipelining:
+//   * MFMA fragments are double-buffered: the LDS reads of k-step s+1 are in flight while the 16
+//     MFMAs of step s issue;
+//   * the global loads of tile t+1 are issued with the first MFMAs of tile t and written to the free
+//     LDS stage during its last k-step;
+//   * sched_group_barrier interleaves the DS reads, global loads and DS writes with the MFMAs.
+// The loop body has no branches: the prefetch after the last tile re-reads the last tile (in
+// bounds) and its LDS writes land in the stage nobody reads again.
+namespace sg {
+constexpr int MFMA = 0x008, VMEM_READ = 0x020, DS_READ = 0x100, DS_WRITE = 0x200;
+}
+
+template <bool TA, bool TB, bool EDGE>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_256(const GemmArgs p) {
+    using T = uint16_t;
+    constexpr int BM = 256, BN = 256, BK = ET<T>::BK, WT = 128, F = 4;
+    using OA = Operand<T, !TA, BM>;
+    using OB = Operand<T, TB, BN>;
+    constexpr int SA = OA::STAGE_BYTES, SB = OB::STAGE_BYTES, STAGE = SA + SB;
+    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int64_t z = blockIdx.y;
+    const int64_t b = z % p.batch, split = z / p.batch;
+    const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
+    const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in;
+    const T *B = (const T *)p.B + bo * p.sB_out + bi * p.sB_in;
+    const int64_t coff = bo * p.sC_out + bi * p.sC_in;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    if (p.causal != CAUSAL_NONE && n0 > m0 + BM - 1 + p.causal_offset) {
+        if (p.causal == CAUSAL_WRITE) {
+            for (int e = tid; e < BM * BN; e += NTHREADS) {
+                const int64_t row = m0 + e / BN, col = n0 + e % BN;
+                if (row < p.M && col < p.N) store_out(p.C, coff + row * p.ldc + col, -INFINITY, p.out_bf16);
+            }
+        }
+        return;
+    }
+
+    int64_t kb = split * p.k_per_split;
+    int64_t ke = min(p.K, kb + p.k_per_split);
+    if (p.kmode == KMODE_LOWER) ke = min(ke, m0 + BM);
+    if (p.kmode == KMODE_UPPER) kb = max(kb, (m0 / BK) * BK);
+    const int ntiles = ke > kb ? (int)((ke - kb + BK - 1) / BK) : 0;
+
+    const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    f32x16 acc[F][F];
+#pragma unroll
+    for (int i = 0; i < F; ++i)
+#pragma unroll
+        for (int j = 0; j < F; ++j) acc[i][j] = zero;
+
+    if (ntiles > 0) {
+        OA ga;
+        OB gb;
+        u32x4 fa0[F], fb0[F], fa1[F], fb1[F];
+        const int last = ntiles - 1;
+        auto frags = [&](u32x4 (&fa)[F], u32x4 (&fb)[F], const char *st, int ks) {
+#pragma unroll
+            for (int i = 0; i < F; ++i) fa[i] = OA::frag32(st, wm * WT + i * 32, ks, lane);
+#pragma unroll
+            for (int j = 0; j < F; ++j) fb[j] = OB::frag32(st + SA, wn * WT + j * 32, ks, lane);
+        };
+        auto mfma16 = [&](const u32x4 (&fa)[F], const u32x4 (&fb)[F]) {
+#pragma unroll
+            for (int i = 0; i < F; ++i)
+#pragma unroll
+                for (int j = 0; j < F; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8, fa[i]), __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
+        };
+        // Tile k0: global loads into registers now, LDS writes in put().
+        auto fetch = [&](int64_t k0) {
+            ga.template load<EDGE>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
+            gb.template load<EDGE>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
+        };
+        auto put = [&](char *stage) {
+            ga.store(stage, tid);
+            gb.store(stage + SA, tid);
+        };
+        // DS writes per k-tile, spread over the 8 MFMA pairs of the last k-step.
+        constexpr int DSW = (OA::ITERS * (OA::TRANSPOSE ? 8 : 1) + OB::ITERS * (OB::TRANSPOSE ? 8 : 1) + 7) / 8;
+        constexpr int VMR = (OA::ITERS * OA::LOADS + OB::ITERS * OB::LOADS + 7) / 8;
+
+        fetch(kb);
+        put(smem);
+        __syncthreads();
+        frags(fa0, fb0, smem, 0);
+        for (int t = 0; t < ntiles; ++t) {
+            const char *cur = smem + (t & 1) * STAGE;
+            char *nxt = smem + ((t + 1) & 1) * STAGE;
+            // Tile t+1 (the last tile again at the end: in bounds, written to a dead stage).
+            frags(fa1, fb1, cur, 1);
+            fetch(kb + (int64_t)min(t + 1, last) * BK);
+            mfma16(fa0, fb0);
+            frags(fa0, fb0, cur, 2);
+            mfma16(fa1, fb1);
+            frags(fa1, fb1, cur, 3);
+            mfma16(fa0, fb0);
+            put(nxt);
+            mfma16(fa1, fb1);
+            if constexpr (!EDGE) {
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(sg::DS_READ, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(sg::VMEM_READ, VMR, 0);
+                    __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
+                }
+#pragma unroll
+                for (int g = 0; g < 16; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(sg::DS_READ, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
+                }
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(sg::DS_WRITE, DSW, 0);
+                    __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
+                }
+            }
+            __syncthreads();
+            frags(fa0, fb0, nxt, 0);
+        }
+    }
+    __syncthreads();
+
+    // Epilogue through LDS (free after the last barrier): each wave stages a quarter of its 128x128
+    // tile (128 x 32 f32) with static register indices, then finishes it row-major with 4-column
+    // vectors, so stores are coalesced and the accumulators never need dynamic indexing.
+    // Lane l of a 32x32 block holds column l%32 and rows 8*(r/4) + 4*(l/32) + r%4, r = 0..15.
+    constexpr int EC = 32, EP = EC * 4 + 16;
+    static_assert(4 * WT * EP <= 2 * STAGE, "epilogue staging fits in the operand stages");
+    char *wl = smem + wave * (WT * EP);
+#pragma unroll
+    for (int h = 0; h < F; ++h) {
+#pragma unroll
+        for (int i = 0; i < F; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rl = i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                const int cl = lane & 31;
+                *(float *)(wl + rl * EP + cl * 4) = acc[i][h][r];
+            }
+        __syncthreads();
+        for (int it = 0; it < WT * EC / 256; ++it) {
+            const int e = (it * 64 + lane) * 4;
+            const int rl = e / EC, cl = e % EC;
+            const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
+            finish4<EDGE>(p, v, m0 + wm * WT + rl, n0 + wn * WT + h * EC + cl, coff, z);
+        }
+        __syncthreads();
+    }
+}
+
 // Deterministic split-K reduction: partial sums are added in split order.
 __global__ __launch_bounds__(256) void splitk_reduce(const GemmArgs p) {
     const int64_t total = p.batch * p.M * p.N;
@@ -372,6 +623,28 @@ __global__ __launch_bounds__(256) void splitk_reduce(const GemmArgs p) {
 struct TileCfg {
     int bm, bn;
 };
+
+template <bool EDGE>
+void launch_bf16_256_e(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipStream_t s) {
+    if (!ta && !tb) hipLaunchKernelGGL((gemm_bf16_256<false, false, EDGE>), grid, dim3(NTHREADS), 0, s, a);
+    else if (!ta && tb) hipLaunchKernelGGL((gemm_bf16_256<false, true, EDGE>), grid, dim3(NTHREADS), 0, s, a);
+    else if (ta && !tb) hipLaunchKernelGGL((gemm_bf16_256<true, false, EDGE>), grid, dim3(NTHREADS), 0, s, a);
+    else hipLaunchKernelGGL((gemm_bf16_256<true, true, EDGE>), grid, dim3(NTHREADS), 0, s, a);
+}
+
+// Tiles need no bounds checks when every tile (and every split's k range) is whole and aligned.
+bool tiles_exact(const GemmArgs &a, int bm, int bn, int bk) {
+    return a.M % bm == 0 && a.N % bn == 0 && a.K % bk == 0 && a.k_per_split % bk == 0 &&
+           a.a_vec_ok && a.b_vec_ok;
+}
+
+hipError_t launch_bf16_256(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipStream_t s) {
+    if (tiles_exact(a, 256, 256, ET<uint16_t>::BK))
+        launch_bf16_256_e<false>(ta, tb, a, grid, s);
+    else
+        launch_bf16_256_e<true>(ta, tb, a, grid, s);
+    return hipGetLastError();
+}
 
 template <typename T, bool TA, bool TB, bool DUAL>
 hipError_t launch_cfg(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
@@ -410,11 +683,17 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
 
-    // Tile shape: 128x128 when that already fills the chip, else 64x64 (+ split-K when even that
-    // leaves CUs idle and the reduction is long).
+    // Tile shape: 256x256 (BF16 only) or 128x128 when that already fills the chip, else 64x64
+    // (+ split-K when even that leaves CUs idle and the reduction is long).
     TileCfg cfg{128, 128};
     int64_t tiles = cdiv(a.M, 128) * cdiv(a.N, 128) * a.batch;
-    if (tiles < cus) {
+    const int64_t tiles256 = cdiv(a.M, 256) * cdiv(a.N, 256) * a.batch;
+    // 256x256 only when it fills most of the chip and wastes little of each tile on edges.
+    const double fill256 = (double)a.M * a.N * a.batch / ((double)tiles256 * 256.0 * 256.0);
+    if (bf16 && !a.dual && tiles256 * 4 >= cus * 3 && fill256 >= 0.7) {
+        cfg = TileCfg{256, 256};
+        tiles = tiles256;
+    } else if (tiles < cus) {
         cfg = TileCfg{64, 64};
         tiles = cdiv(a.M, 64) * cdiv(a.N, 64) * a.batch;
     }
@@ -458,8 +737,9 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
         key = buf;
         profile_begin(ctx, key, &ev);
     }
-    hipError_t e = bf16 ? launch_typed<uint16_t>(transA, transB, a.dual, cfg, a, grid, ctx->stream)
-                        : launch_typed<float>(transA, transB, a.dual, cfg, a, grid, ctx->stream);
+    hipError_t e = cfg.bm == 256 ? launch_bf16_256(transA, transB, a, grid, ctx->stream)
+                   : bf16        ? launch_typed<uint16_t>(transA, transB, a.dual, cfg, a, grid, ctx->stream)
+                                 : launch_typed<float>(transA, transB, a.dual, cfg, a, grid, ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "gemm_mfma launch");
     if (splits > 1) {
         it_status st = launch_splitk_reduce(ctx->stream, a);

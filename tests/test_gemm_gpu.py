@@ -275,3 +275,35 @@ def test_bf16_square_freivalds(it, n):
         rhs = a64 @ (bb @ x)
         scale = np.abs(a64) @ (np.abs(bb) @ np.abs(x))
         assert np.max(np.abs(lhs - rhs) / scale) < 1e-5, trans_b
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_large_tile_ragged_batched(it, ta, tb):
+    """Ragged batched shapes big enough for the 256x256 kernel's bounds-checked path: exact small
+    integers, checked against a float64 product (exact for these magnitudes)."""
+    bt, m, n, k = 24, 740, 730, 136
+    a = synth.small_ints(200, (bt, k, m) if ta else (bt, m, k), -8, 8)
+    b = synth.small_ints(201, (bt, n, k) if tb else (bt, k, n), -8, 8)
+    c = it.gemm(it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape),
+                trans_a=bool(ta), trans_b=bool(tb))
+    exact = np.matmul(op(a, ta).astype(np.float64), op(b, tb).astype(np.float64))
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+
+
+def test_bf16_large_tile_epilogues(it, oracle):
+    """alpha/beta with BF16 output and a bias on a shape that takes the 256x256 kernel."""
+    m, n, k = 4096, 3072, 192
+    a = synth.small_ints(210, (m, k), -4, 4)
+    b = synth.small_ints(211, (n, k), -4, 4)
+    c0 = synth.small_ints(212, (m, n), -4, 4)
+    out = it.Tensor.from_f32_as_bf16(c0, c0.shape)
+    it.gemm(it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape),
+            trans_b=True, alpha=0.5, beta=2.0, out=out)
+    exact = 0.5 * (a.astype(np.float64) @ b.astype(np.float64).T) + 2.0 * c0
+    ref16 = oracle.f32_to_bf16(exact.astype(np.float32))
+    assert np.array_equal(out.as_bf16_slice().reshape(m, n), ref16)
+    bias = synth.normal(213, (n,))
+    y = it.gemm(it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape),
+                trans_b=True, bias=it.Tensor.from_f32_slice(bias, bias.shape))
+    ref = (a.astype(np.float64) @ b.astype(np.float64).T) + bias
+    assert normwise_rel(y.numpy(), ref) <= FP32_TOL
