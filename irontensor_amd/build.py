@@ -63,5 +63,22 @@ def build_library(verbose: bool = False) -> Path:
     return LIB
 
 
+CPP_TEST_SRC = ROOT / "tests" / "cpp" / "test_host_api.cpp"
+CPP_TEST_BIN = ROOT / "tests" / "cpp" / "_build" / "test_host_api"
+
+
+def build_cpp_tests() -> Path:
+    """Builds the C++ host-API test program against the in-tree library (rpath-relative)."""
+    CPP_TEST_BIN.parent.mkdir(parents=True, exist_ok=True)
+    cmd = ["g++", "-std=c++17", "-O1", "-Wall", f"-I{ROOT / 'include'}", str(CPP_TEST_SRC),
+           "-o", str(CPP_TEST_BIN), f"-L{PKG}", "-lirontensor_hip",
+           "-Wl,-rpath,$ORIGIN/../../../irontensor_amd", "-Wl,-rpath,/opt/rocm/lib"]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"C++ host API test build failed:\n{res.stdout}")
+    return CPP_TEST_BIN
+
+
 if __name__ == "__main__":
     print(build_library(verbose=True))
+    print(build_cpp_tests())

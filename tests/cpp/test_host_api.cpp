@@ -1,0 +1,236 @@
+// Tests of the C++ host API (include/irontensor.hpp), written like the reference's inline Rust
+// tests: each KAT follows the test it names (file:line in the reference), with the expected values
+// computed by the same inline CPU loops those tests use.
+//   test_host_api --cpu   error types, BF16 rounding and argument checks; no device needed
+//   test_host_api         everything, on device 0
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "irontensor.hpp"
+
+using namespace irontensor;
+
+static int g_failed = 0, g_passed = 0;
+
+#define CHECK(cond)                                                              \
+    do {                                                                         \
+        if (!(cond)) {                                                           \
+            std::printf("  FAILED %s:%d: %s\n", __FILE__, __LINE__, #cond);      \
+            throw std::runtime_error("check failed");                            \
+        }                                                                        \
+    } while (0)
+
+static void run(const char *name, const std::function<void()> &fn) {
+    try {
+        fn();
+        ++g_passed;
+        std::printf("ok   %s\n", name);
+    } catch (const std::exception &e) {
+        ++g_failed;
+        std::printf("FAIL %s: %s\n", name, e.what());
+    }
+    std::fflush(stdout);
+}
+
+template <typename E, typename F>
+static std::string expect_throw(F &&f) {
+    try {
+        f();
+    } catch (const E &e) {
+        return e.what();
+    }
+    throw std::runtime_error("expected exception not thrown");
+}
+
+static void cpu_tests() {
+    run("error_display_formats", [] {  // src/error.rs:43-66
+        CHECK(std::string(ShapeMismatch("op", "a", "b").what()) == "op: shape mismatch, expected a, got b");
+        CHECK(std::string(UnsupportedDimensions("op", "2D", {1, 2}).what()) == "op: unsupported dimensions, expected 2D, got [1, 2]");
+        CHECK(std::string(PrecisionMismatch("op", "FP32", "BF16").what()) == "op: precision mismatch, expected FP32, got BF16");
+        CHECK(std::string(InnerDimensionMismatch("op", {1, 2}, {3, 4}).what()) == "op: inner dimensions don't match, A=[1, 2], B=[3, 4]");
+        CHECK(std::string(EmptyTensor("op").what()) == "op: empty tensor not supported");
+    });
+    run("bf16_conversion_roundtrip", [] {  // src/precision.rs:51-65
+        for (float v : {0.0f, 1.0f, -1.0f, 0.5f, -0.5f, 100.0f, -100.0f, 1e-5f, 1e5f}) {
+            float back = bf16_to_f32(f32_to_bf16(v));
+            float rel = std::fabs(v) > 1e-10f ? std::fabs((back - v) / v) : std::fabs(back - v);
+            CHECK(rel < 0.01f);
+        }
+        CHECK(f32_to_bf16(1.0f + 1.0f / 256) == 0x3F80);       // tie -> even
+        CHECK(f32_to_bf16(1.0f + 3.0f / 256) == 0x3F82);       // tie -> even (up)
+        CHECK(std::isinf(bf16_to_f32(f32_to_bf16(INFINITY))));
+        CHECK(std::isnan(bf16_to_f32(f32_to_bf16(NAN))));
+    });
+    run("gemm_check_rejects_bad_arguments", [] {
+        int dummy;
+        CHECK(it_gemm_check(IT_F16, IT_F32, IT_OP_N, IT_OP_N, 2, 2, 2, &dummy, 2, 0, &dummy, 2, 0, 0.f, &dummy, 2, 0, 1, nullptr) == IT_ERR_PRECISION);
+        CHECK(it_gemm_check(IT_F32, IT_F32, IT_OP_N, IT_OP_N, 2, 2, 3, &dummy, 2, 0, &dummy, 2, 0, 0.f, &dummy, 2, 0, 1, nullptr) == IT_ERR_INVALID);
+        CHECK(it_gemm_check(IT_F32, IT_F32, IT_OP_N, IT_OP_N, 2, 2, 2, &dummy, 2, 0, &dummy, 2, 0, 0.f, nullptr, 2, 0, 1, nullptr) == IT_ERR_NULL);
+        CHECK(it_gemm_check(IT_F32, IT_F32, IT_OP_N, IT_OP_N, 2, 2, 2, &dummy, 2, 0, &dummy, 2, 0, 0.f, &dummy, 2, 0, 1, nullptr) == IT_OK);
+        CHECK(std::string(it_last_error()).find("C is NULL") != std::string::npos);
+    });
+}
+
+static std::vector<float> cpu_matmul(const std::vector<float> &a, const std::vector<float> &b, size_t m, size_t k, size_t n) {
+    std::vector<float> c(m * n);
+    for (size_t i = 0; i < m; ++i)
+        for (size_t j = 0; j < n; ++j) {
+            float acc = 0.0f;
+            for (size_t p = 0; p < k; ++p) acc += a[i * k + p] * b[p * n + j];
+            c[i * n + j] = acc;
+        }
+    return c;
+}
+
+static void gpu_tests() {
+    run("matmul_2x2", [] {  // src/ops/gemm.rs:291-306
+        Tensor a = Tensor::from_f32_slice({1, 2, 3, 4}, {2, 2}), b = Tensor::from_f32_slice({5, 6, 7, 8}, {2, 2});
+        auto r = matmul(a, b).as_f32_slice();
+        CHECK(r.size() == 4 && r[0] == 19 && r[1] == 22 && r[2] == 43 && r[3] == 50);
+    });
+    run("matmul_larger", [] {  // src/ops/gemm.rs:308-351
+        const size_t m = 64, k = 32, n = 48;
+        std::vector<float> a(m * k), b(k * n);
+        for (size_t i = 0; i < m; ++i)
+            for (size_t j = 0; j < k; ++j) a[i * k + j] = (float)(i + j) * 0.01f;
+        for (size_t i = 0; i < k; ++i)
+            for (size_t j = 0; j < n; ++j) b[i * n + j] = (float)(i * j) * 0.01f;
+        auto r = matmul(Tensor::from_f32_slice(a, {m, k}), Tensor::from_f32_slice(b, {k, n})).as_f32_slice();
+        auto e = cpu_matmul(a, b, m, k, n);
+        for (size_t i = 0; i < m * n; ++i) CHECK(std::fabs(r[i] - e[i]) < 1e-3f);
+    });
+    run("matmul_batched", [] {  // src/ops/gemm.rs:353-386
+        const size_t bt = 2, m = 3, k = 4, n = 2;
+        std::vector<float> a(bt * m * k), b(bt * k * n);
+        for (size_t i = 0; i < a.size(); ++i) a[i] = (float)i * 0.1f;
+        for (size_t i = 0; i < b.size(); ++i) b[i] = (float)i * 0.1f;
+        Tensor c = matmul(Tensor::from_f32_slice(a, {bt, m, k}), Tensor::from_f32_slice(b, {bt, k, n}));
+        CHECK((c.shape() == std::vector<size_t>{bt, m, n}));
+        auto r = c.as_f32_slice();
+        for (size_t q = 0; q < bt; ++q) {
+            std::vector<float> aa(a.begin() + q * m * k, a.begin() + (q + 1) * m * k);
+            std::vector<float> bb(b.begin() + q * k * n, b.begin() + (q + 1) * k * n);
+            auto e = cpu_matmul(aa, bb, m, k, n);
+            for (size_t i = 0; i < m * n; ++i) CHECK(std::fabs(r[q * m * n + i] - e[i]) < 1e-3f);
+        }
+    });
+    run("mps_matches_reference", [] {  // src/ops/mps_gemm.rs:637-668 (exact integers)
+        const size_t m = 16, k = 8, n = 12;
+        std::vector<float> a(m * k), b(k * n);
+        for (size_t i = 0; i < a.size(); ++i) a[i] = (float)(i % 7) - 3.0f;
+        for (size_t i = 0; i < b.size(); ++i) b[i] = (float)(i % 5) - 2.0f;
+        auto r = matmul_mps(Tensor::from_f32_slice(a, {m, k}), Tensor::from_f32_slice(b, {k, n})).as_f32_slice();
+        CHECK(r == cpu_matmul(a, b, m, k, n));
+    });
+    run("matmul_backward_2d", [] {  // src/ops/backward/gemm.rs:457-509
+        const size_t m = 3, k = 4, n = 2;
+        std::vector<float> a(m * k), b(k * n), gc(m * n, 1.0f);
+        for (size_t i = 0; i < a.size(); ++i) a[i] = (float)i * 0.1f;
+        for (size_t i = 0; i < b.size(); ++i) b[i] = (float)i * 0.1f;
+        auto g = matmul_backward(Tensor::from_f32_slice(gc, {m, n}), Tensor::from_f32_slice(a, {m, k}),
+                                 Tensor::from_f32_slice(b, {k, n}));
+        auto ga = g.first.as_f32_slice(), gb = g.second.as_f32_slice();
+        for (size_t i = 0; i < m; ++i)
+            for (size_t j = 0; j < k; ++j) {
+                float e = 0;
+                for (size_t l = 0; l < n; ++l) e += gc[i * n + l] * b[j * n + l];
+                CHECK(std::fabs(ga[i * k + j] - e) < 1e-4f);
+            }
+        for (size_t i = 0; i < k; ++i)
+            for (size_t j = 0; j < n; ++j) {
+                float e = 0;
+                for (size_t l = 0; l < m; ++l) e += a[l * k + i] * gc[l * n + j];
+                CHECK(std::fabs(gb[i * n + j] - e) < 1e-4f);
+            }
+    });
+    run("matmul_backward_4d", [] {  // src/ops/backward/gemm.rs:548-586
+        const size_t b1 = 2, b2 = 3, m = 4, k = 5, n = 6;
+        std::vector<float> a(b1 * b2 * m * k), b(b1 * b2 * k * n), gc(b1 * b2 * m * n, 1.0f);
+        for (size_t i = 0; i < a.size(); ++i) a[i] = std::fmod((float)i * 0.01f, 1.0f);
+        for (size_t i = 0; i < b.size(); ++i) b[i] = std::fmod((float)i * 0.01f, 1.0f);
+        auto g = matmul_backward(Tensor::from_f32_slice(gc, {b1, b2, m, n}), Tensor::from_f32_slice(a, {b1, b2, m, k}),
+                                 Tensor::from_f32_slice(b, {b1, b2, k, n}));
+        CHECK((g.first.shape() == std::vector<size_t>{b1, b2, m, k}));
+        CHECK((g.second.shape() == std::vector<size_t>{b1, b2, k, n}));
+        float e = 0;
+        for (size_t l = 0; l < n; ++l) e += gc[l] * b[l];
+        CHECK(std::fabs(g.first.as_f32_slice()[0] - e) < 1e-3f);
+    });
+    run("matmul_bf16", [] {  // src/ops/bf16_ops/mod.rs:34-49
+        Tensor c = matmul_bf16(Tensor::from_f32_as_bf16({1, 2, 3, 4, 5, 6}, {2, 3}),
+                               Tensor::from_f32_as_bf16({1, 2, 3, 4, 5, 6}, {3, 2}));
+        CHECK(c.precision() == Precision::BF16);
+        auto r = c.as_bf16_slice();
+        CHECK(bf16_to_f32(r[0]) == 22 && bf16_to_f32(r[1]) == 28 && bf16_to_f32(r[2]) == 49 && bf16_to_f32(r[3]) == 64);
+    });
+    run("linear_with_bias", [] {  // src/nn/linear.rs:224-238
+        Tensor w = Tensor::from_f32_slice({1, 0, 0, 1}, {2, 2}), bias = Tensor::from_f32_slice({1, 2}, {2});
+        auto r = linear(Tensor::from_f32_slice({1, 2}, {1, 2}), w, &bias).as_f32_slice();
+        CHECK(r[0] == 2 && r[1] == 4);
+    });
+    run("linear_forward_backward_shapes", [] {  // src/train/helpers.rs:48-76
+        Tensor x = Tensor::from_f32_slice(std::vector<float>(8 * 4, 0.5f), {8, 4});
+        Tensor w = Tensor::from_f32_slice(std::vector<float>(3 * 4, 0.25f), {3, 4});
+        Tensor y = linear_forward(x, w);
+        CHECK((y.shape() == std::vector<size_t>{8, 3}) && y.as_f32_slice()[0] == 0.5f);
+        auto g = linear_backward(Tensor::from_f32_slice(std::vector<float>(8 * 3, 1.0f), {8, 3}), x, w);
+        CHECK((g.first.shape() == std::vector<size_t>{8, 4}) && g.first.as_f32_slice()[0] == 0.75f);
+        CHECK((g.second.shape() == std::vector<size_t>{3, 4}) && g.second.as_f32_slice()[0] == 4.0f);
+    });
+    run("attention_causal_rows", [] {  // src/ops/attention.rs:653-679 inputs, closed-form check
+        const size_t b = 1, s = 4, h = 1, d = 4;
+        std::vector<float> q(b * s * h * d, 0.0f), v(b * s * h * d);
+        for (size_t i = 0; i < v.size(); ++i) v[i] = (float)(i + 1) * 0.1f;
+        // Q = 0: uniform weights over the visible keys, so row r is the mean of V rows 0..r.
+        auto o = attention(Tensor::from_f32_slice(q, {b, s, h, d}), Tensor::from_f32_slice(v, {b, s, h, d}),
+                           Tensor::from_f32_slice(v, {b, s, h, d}), true).as_f32_slice();
+        for (size_t r = 0; r < s; ++r)
+            for (size_t c = 0; c < d; ++c) {
+                float mean = 0;
+                for (size_t j = 0; j <= r; ++j) mean += v[j * d + c];
+                mean /= (float)(r + 1);
+                CHECK(std::fabs(o[r * d + c] - mean) < 1e-5f);
+            }
+    });
+    run("typed_errors", [] {  // src/ops/mps_gemm.rs:45-108
+        Tensor f = Tensor::zeros({2, 3}, Precision::FP32), g = Tensor::zeros({4, 5}, Precision::FP32);
+        CHECK(expect_throw<InnerDimensionMismatch>([&] { matmul(f, g); }).find("A=[2, 3], B=[4, 5]") != std::string::npos);
+        Tensor h = Tensor::zeros({2, 2}, Precision::BF16);
+        expect_throw<PrecisionMismatch>([&] { matmul(h, h); });
+        Tensor t4 = Tensor::zeros({1, 1, 2, 2}, Precision::FP32);
+        expect_throw<UnsupportedDimensions>([&] { matmul(t4, t4); });
+        expect_throw<Panic>([&] { matmul_mps_nt(f, g); });
+        expect_throw<Panic>([&] { Tensor::from_f32_slice({1, 2, 3}, {2, 2}); });
+    });
+    run("command_batch_async", [] {  // src/command_batch.rs:174-390
+        CommandBatch::begin();
+        CHECK(CommandBatch::is_active());
+        Tensor a = Tensor::from_f32_slice(std::vector<float>(64 * 64, 1.0f), {64, 64});
+        Tensor c = matmul(a, a);
+        CommandBatch::commit_async();
+        CommandBatch::wait_for_completion();
+        CHECK(CommandBatch::is_async_complete());
+        CommandBatch::end();
+        CHECK(!CommandBatch::is_active());
+        CHECK(c.as_f32_slice()[0] == 64.0f);
+        CHECK(gpu_memory_allocated() > 0);
+    });
+}
+
+int main(int argc, char **argv) {
+    const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+    cpu_tests();
+    if (!cpu_only) {
+        if (it_device_count() == 0) {
+            std::printf("FAIL no HIP device visible\n");
+            return 2;
+        }
+        gpu_tests();
+    }
+    std::printf("%d passed, %d failed\n", g_passed, g_failed);
+    return g_failed ? 1 : 0;
+}
