@@ -99,6 +99,27 @@ __device__ __forceinline__ u32x4 load_vec(const T *base, int64_t off, bool row_o
     return v;
 }
 
+// How an operand tile is read from global memory:
+//   LOAD_EXACT   every tile is whole and aligned: plain 128-bit loads;
+//   LOAD_MASKED  16-byte vectors are aligned and never straddle an edge, so a vector is either
+//                wholly in bounds or wholly out: branch-free load of a safe address + select;
+//   LOAD_CHECKED anything else: per-element bounds checks.
+enum LoadMode : int { LOAD_EXACT = 0, LOAD_MASKED = 1, LOAD_CHECKED = 2 };
+
+template <int MODE, typename T>
+__device__ __forceinline__ u32x4 load_mode(const T *base, int64_t off, bool row_ok, int64_t c,
+                                           int64_t clim, bool vec_ok) {
+    if constexpr (MODE == LOAD_EXACT) {
+        return *(const u32x4 *)(base + off);
+    } else if constexpr (MODE == LOAD_MASKED) {
+        const bool ok = row_ok && c < clim;
+        const u32x4 v = *(const u32x4 *)(base + (ok ? off : 0));
+        return ok ? v : u32x4{0u, 0u, 0u, 0u};
+    } else {
+        return load_vec<T>(base, off, row_ok, c, clim, vec_ok);
+    }
+}
+
 // One operand's k-tile: global -> registers -> LDS, and LDS -> MFMA fragments.
 //   KCONTIG: global element (r, k) at base[r * ld + k] (A not transposed, or B transposed).
 //   otherwise: global element (r, k) at base[k * ld + r].
@@ -125,9 +146,7 @@ struct Operand {
         kg = (item >> 1) % KGROUPS;
     }
 
-    // EDGE = false: the caller guarantees the whole tile is in bounds and 16-byte aligned, so
-    // every load is one unconditional 128-bit load.
-    template <bool EDGE = true>
+    template <int MODE = LOAD_CHECKED>
     __device__ __forceinline__ void load(const T *base, int64_t ld, int64_t r0, int64_t k0,
                                          int64_t rlim, int64_t klim, bool vec_ok, int tid) {
 #pragma unroll
@@ -137,17 +156,11 @@ struct Operand {
             if constexpr (KCONTIG) {
                 const int rr = item / (BK / VEC), kc = item % (BK / VEC);
                 const int64_t gr = r0 + rr, gk = k0 + kc * VEC;
-                if constexpr (EDGE)
-                    reg[it][0] = load_vec<T>(base, gr * ld + gk, gr < rlim, gk, klim, vec_ok);
-                else
-                    reg[it][0] = *(const u32x4 *)(base + gr * ld + gk);
+                reg[it][0] = load_mode<MODE>(base, gr * ld + gk, gr < rlim, gk, klim, vec_ok);
             } else if constexpr (!TRANSPOSE) {
                 const int kk = item / (ROWS / VEC), rc = item % (ROWS / VEC);
                 const int64_t gk = k0 + kk, gr = r0 + rc * VEC;
-                if constexpr (EDGE)
-                    reg[it][0] = load_vec<T>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
-                else
-                    reg[it][0] = *(const u32x4 *)(base + gk * ld + gr);
+                reg[it][0] = load_mode<MODE>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
             } else {
                 int kg, rc;
                 unit(item, kg, rc);
@@ -155,10 +168,7 @@ struct Operand {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int64_t gk = k0 + kg * 4 + q;
-                    if constexpr (EDGE)
-                        reg[it][q] = load_vec<T>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
-                    else
-                        reg[it][q] = *(const u32x4 *)(base + gk * ld + gr);
+                    reg[it][q] = load_mode<MODE>(base, gk * ld + gr, gk < klim, gr, rlim, vec_ok);
                 }
             }
         }
@@ -254,139 +264,6 @@ __device__ __forceinline__ void finish_store(const GemmArgs &p, void *C, int64_t
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
 
-template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL>
-__global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
-    static_assert(WM * WN == 4, "4 waves per block");
-    constexpr int BK = ET<T>::BK;
-    constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
-    using OA = Operand<T, !TA, BM>;
-    using OB = Operand<T, TB, BN>;
-    constexpr int SA = OA::STAGE_BYTES, SB = OB::STAGE_BYTES;
-    constexpr int STAGE = SA + SB * (DUAL ? 2 : 1);
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int64_t z = blockIdx.y;
-    const int64_t b = z % p.batch, split = z / p.batch;
-    const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
-    const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in;
-    const T *B = (const T *)p.B + bo * p.sB_out + bi * p.sB_in;
-    const T *B2 = DUAL ? (const T *)p.B2 + bo * p.sB_out + bi * p.sB_in : nullptr;
-    const int64_t coff = bo * p.sC_out + bi * p.sC_in;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-
-    if (p.causal != CAUSAL_NONE && n0 > m0 + BM - 1 + p.causal_offset) {
-        // Entire tile is above the diagonal: no products needed.
-        if (p.causal == CAUSAL_WRITE) {
-            for (int e = tid; e < BM * BN; e += NTHREADS) {
-                const int64_t row = m0 + e / BN, col = n0 + e % BN;
-                if (row < p.M && col < p.N) store_out(p.C, coff + row * p.ldc + col, -INFINITY, p.out_bf16);
-            }
-        }
-        return;
-    }
-
-    int64_t kb = split * p.k_per_split;
-    int64_t ke = min(p.K, kb + p.k_per_split);
-    if (p.kmode == KMODE_LOWER) ke = min(ke, m0 + BM);
-    if (p.kmode == KMODE_UPPER) kb = max(kb, (m0 / BK) * BK);
-    const int ntiles = ke > kb ? (int)((ke - kb + BK - 1) / BK) : 0;
-
-    f32x4 acc[FM][FN];
-    f32x4 acc2[DUAL ? FM : 1][DUAL ? FN : 1];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (DUAL) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    OA oa;
-    OB ob, ob2;
-    if (ntiles > 0) {
-        oa.load(A, p.lda, m0, kb, p.M, ke, p.a_vec_ok, tid);
-        ob.load(B, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
-        if constexpr (DUAL) ob2.load(B2, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
-        oa.store(smem, tid);
-        ob.store(smem + SA, tid);
-        if constexpr (DUAL) ob2.store(smem + SA + SB, tid);
-        __syncthreads();
-    }
-
-    for (int t = 0; t < ntiles; ++t) {
-        char *cur = smem + (t & 1) * STAGE;
-        char *nxt = smem + ((t + 1) & 1) * STAGE;
-        const bool more = t + 1 < ntiles;
-        if (more) {
-            const int64_t k = kb + (int64_t)(t + 1) * BK;
-            oa.load(A, p.lda, m0, k, p.M, ke, p.a_vec_ok, tid);
-            ob.load(B, p.ldb, n0, k, p.N, ke, p.b_vec_ok, tid);
-            if constexpr (DUAL) ob2.load(B2, p.ldb, n0, k, p.N, ke, p.b_vec_ok, tid);
-        }
-#pragma unroll
-        for (int ks = 0; ks < BK / ET<T>::KSTEP; ++ks) {
-            u32x4 af[FM], bfr[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) af[i] = OA::frag(cur, wm * WTM + i * 16, ks, lane);
-#pragma unroll
-            for (int j = 0; j < FN; ++j) bfr[j] = OB::frag(cur + SA, wn * WTN + j * 16, ks, lane);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j) mma<T>(acc[i][j], af[i], bfr[j]);
-            if constexpr (DUAL) {
-#pragma unroll
-                for (int j = 0; j < FN; ++j) bfr[j] = OB::frag(cur + SA + SB, wn * WTN + j * 16, ks, lane);
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j) mma<T>(acc2[i][j], af[i], bfr[j]);
-            }
-        }
-        if (more) {
-            oa.store(nxt, tid);
-            ob.store(nxt + SA, tid);
-            if constexpr (DUAL) ob2.store(nxt + SA + SB, tid);
-        }
-        __syncthreads();
-    }
-
-    // Epilogue. Lane l of a 16x16 MFMA block holds rows 4*(l/16)+r (r = 0..3), column l%16.
-    const int64_t rbase = m0 + wm * WTM + (lane >> 4) * 4;
-    const int64_t cbase = n0 + wn * WTN + (lane & 15);
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t row = rbase + i * 16 + r, col = cbase + j * 16;
-                if (row >= p.M || col >= p.N) continue;
-                if (p.splits > 1) {
-                    p.partial[(z * p.M + row) * p.N + col] = acc[i][j][r];
-                    continue;
-                }
-                const int64_t idx = coff + row * p.ldc + col;
-                if constexpr (DUAL) {
-                    const float g = p.alpha * acc[i][j][r], u = p.alpha * acc2[i][j][r];
-                    if (p.G) store_out(p.G, idx, g, p.out_bf16);
-                    if (p.U) store_out(p.U, idx, u, p.out_bf16);
-                    store_out(p.C, idx, silu(g) * u, p.out_bf16);
-                } else {
-                    finish_store(p, p.C, idx, acc[i][j][r], row, col);
-                }
-            }
-}
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
 // Final values of 4 consecutive output columns (the vector form of finish_store), or raw partial
 // sums for split-K. Falls back to element stores at the right edge or for unaligned outputs.
 template <bool EDGE>
@@ -443,6 +320,224 @@ __device__ __forceinline__ void finish4(const GemmArgs &p, f32x4 v, int64_t row,
         if (col + e < p.N) finish_store(p, p.C, idx + e, v[e], row, col + e);
 }
 
+namespace sg {
+constexpr int MFMA = 0x008, VMEM_READ = 0x020, DS_READ = 0x100, DS_WRITE = 0x200;
+}
+
+template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL, int LM>
+__global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
+    static_assert(WM * WN == 4, "4 waves per block");
+    constexpr int BK = ET<T>::BK;
+    constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
+    using OA = Operand<T, !TA, BM>;
+    using OB = Operand<T, TB, BN>;
+    constexpr int SA = OA::STAGE_BYTES, SB = OB::STAGE_BYTES;
+    constexpr int STAGE = SA + SB * (DUAL ? 2 : 1);
+    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int64_t z = blockIdx.y;
+    const int64_t b = z % p.batch, split = z / p.batch;
+    const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
+    const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in;
+    const T *B = (const T *)p.B + bo * p.sB_out + bi * p.sB_in;
+    const T *B2 = DUAL ? (const T *)p.B2 + bo * p.sB_out + bi * p.sB_in : nullptr;
+    const int64_t coff = bo * p.sC_out + bi * p.sC_in;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    if (p.causal != CAUSAL_NONE && n0 > m0 + BM - 1 + p.causal_offset) {
+        // Entire tile is above the diagonal: no products needed.
+        if (p.causal == CAUSAL_WRITE) {
+            for (int e = tid; e < BM * BN; e += NTHREADS) {
+                const int64_t row = m0 + e / BN, col = n0 + e % BN;
+                if (row < p.M && col < p.N) store_out(p.C, coff + row * p.ldc + col, -INFINITY, p.out_bf16);
+            }
+        }
+        return;
+    }
+
+    int64_t kb = split * p.k_per_split;
+    int64_t ke = min(p.K, kb + p.k_per_split);
+    if (p.kmode == KMODE_LOWER) ke = min(ke, m0 + BM);
+    if (p.kmode == KMODE_UPPER) kb = max(kb, (m0 / BK) * BK);
+    const int ntiles = ke > kb ? (int)((ke - kb + BK - 1) / BK) : 0;
+
+    f32x4 acc[FM][FN];
+    f32x4 acc2[DUAL ? FM : 1][DUAL ? FN : 1];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (DUAL) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    OA oa;
+    OB ob, ob2;
+    if constexpr (!DUAL) {
+        // Software-pipelined loop: fragments of k-step 1 are read while the MFMAs of k-step 0
+        // issue; the next tile's global loads go out with k-step 0 and land in the other LDS stage
+        // during k-step 1; the prefetch after the last tile re-reads it into a dead stage.
+        if (ntiles > 0) {
+            u32x4 fa0[FM], fb0[FN], fa1[FM], fb1[FN];
+            const int last = ntiles - 1;
+            auto frags = [&](u32x4 (&fa)[FM], u32x4 (&fb)[FN], const char *st, int ks) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[i] = OA::frag(st, wm * WTM + i * 16, ks, lane);
+#pragma unroll
+                for (int j = 0; j < FN; ++j) fb[j] = OB::frag(st + SA, wn * WTN + j * 16, ks, lane);
+            };
+            auto mmas = [&](const u32x4 (&fa)[FM], const u32x4 (&fb)[FN]) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) mma<T>(acc[i][j], fa[i], fb[j]);
+            };
+            static_assert(BK / ET<T>::KSTEP == 2, "two fragment steps per k-tile");
+            constexpr int MF = FM * FN * (sizeof(T) == 4 ? 4 : 1);
+            constexpr int DSR = FM * (OA::KMAJOR_LDS ? 4 : 1) + FN * (OB::KMAJOR_LDS ? 4 : 1);
+            constexpr int VMR = OA::ITERS * OA::LOADS + OB::ITERS * OB::LOADS;
+            constexpr int DSW = OA::ITERS * (OA::TRANSPOSE ? 8 : 1) + OB::ITERS * (OB::TRANSPOSE ? 8 : 1);
+            constexpr int G = MF < 8 ? MF : 8;
+            oa.template load<LM>(A, p.lda, m0, kb, p.M, ke, p.a_vec_ok, tid);
+            ob.template load<LM>(B, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
+            oa.store(smem, tid);
+            ob.store(smem + SA, tid);
+            __syncthreads();
+            frags(fa0, fb0, smem, 0);
+            for (int t = 0; t < ntiles; ++t) {
+                const char *cur = smem + (t & 1) * STAGE;
+                char *nxt = smem + ((t + 1) & 1) * STAGE;
+                const int64_t k1 = kb + (int64_t)min(t + 1, last) * BK;
+                frags(fa1, fb1, cur, 1);
+                oa.template load<LM>(A, p.lda, m0, k1, p.M, ke, p.a_vec_ok, tid);
+                ob.template load<LM>(B, p.ldb, n0, k1, p.N, ke, p.b_vec_ok, tid);
+                mmas(fa0, fb0);
+                oa.store(nxt, tid);
+                ob.store(nxt + SA, tid);
+                mmas(fa1, fb1);
+                if constexpr (LM != LOAD_CHECKED) {
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        __builtin_amdgcn_sched_group_barrier(sg::DS_READ, (DSR + G - 1) / G, 0);
+                        __builtin_amdgcn_sched_group_barrier(sg::VMEM_READ, (VMR + G - 1) / G, 0);
+                        __builtin_amdgcn_sched_group_barrier(sg::MFMA, MF / G, 0);
+                    }
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        __builtin_amdgcn_sched_group_barrier(sg::DS_WRITE, (DSW + G - 1) / G, 0);
+                        __builtin_amdgcn_sched_group_barrier(sg::MFMA, MF / G, 0);
+                    }
+                }
+                __syncthreads();
+                frags(fa0, fb0, nxt, 0);
+            }
+        }
+    } else {
+        if (ntiles > 0) {
+            oa.template load<LM>(A, p.lda, m0, kb, p.M, ke, p.a_vec_ok, tid);
+            ob.template load<LM>(B, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
+            ob2.template load<LM>(B2, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
+            oa.store(smem, tid);
+            ob.store(smem + SA, tid);
+            ob2.store(smem + SA + SB, tid);
+            __syncthreads();
+        }
+        for (int t = 0; t < ntiles; ++t) {
+            char *cur = smem + (t & 1) * STAGE;
+            char *nxt = smem + ((t + 1) & 1) * STAGE;
+            const bool more = t + 1 < ntiles;
+            if (more) {
+                const int64_t k = kb + (int64_t)(t + 1) * BK;
+                oa.template load<LM>(A, p.lda, m0, k, p.M, ke, p.a_vec_ok, tid);
+                ob.template load<LM>(B, p.ldb, n0, k, p.N, ke, p.b_vec_ok, tid);
+                ob2.template load<LM>(B2, p.ldb, n0, k, p.N, ke, p.b_vec_ok, tid);
+            }
+#pragma unroll
+            for (int ks = 0; ks < BK / ET<T>::KSTEP; ++ks) {
+                u32x4 af[FM], bfr[FN];
+#pragma unroll
+                for (int i = 0; i < FM; ++i) af[i] = OA::frag(cur, wm * WTM + i * 16, ks, lane);
+#pragma unroll
+                for (int j = 0; j < FN; ++j) bfr[j] = OB::frag(cur + SA, wn * WTN + j * 16, ks, lane);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) mma<T>(acc[i][j], af[i], bfr[j]);
+#pragma unroll
+                for (int j = 0; j < FN; ++j) bfr[j] = OB::frag(cur + SA + SB, wn * WTN + j * 16, ks, lane);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) mma<T>(acc2[i][j], af[i], bfr[j]);
+            }
+            if (more) {
+                oa.store(nxt, tid);
+                ob.store(nxt + SA, tid);
+                ob2.store(nxt + SA + SB, tid);
+            }
+            __syncthreads();
+        }
+    }
+
+    if constexpr (!DUAL) {
+        // Epilogue through LDS: each wave stages half of its tile (WTM x WTN/2 f32) with static
+        // register indices, then finishes it row-major with 4-column vectors.
+        // Lane l of a 16x16 MFMA block holds rows 4*(l/16)+r (r = 0..3), column l%16.
+        constexpr int EC = WTN / 2, EP = EC * 4 + 16;
+        static_assert(4 * WTM * EP <= 2 * STAGE, "epilogue staging fits in the operand stages");
+        __syncthreads();
+        char *wl = smem + wave * (WTM * EP);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int jj = 0; jj < FN / 2; ++jj)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int rl = i * 16 + (lane >> 4) * 4 + r;
+                        const int cl = jj * 16 + (lane & 15);
+                        *(float *)(wl + rl * EP + cl * 4) = acc[i][h * (FN / 2) + jj][r];
+                    }
+            __syncthreads();
+            for (int it = 0; it < WTM * EC / 256; ++it) {
+                const int e = (it * 64 + lane) * 4;
+                const int rl = e / EC, cl = e % EC;
+                const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
+                finish4<true>(p, v, m0 + wm * WTM + rl, n0 + wn * WTN + h * EC + cl, coff, z);
+            }
+            __syncthreads();
+        }
+    } else {
+        // SwiGLU epilogue per element: gate, up and silu(gate) * up.
+        const int64_t rbase = m0 + wm * WTM + (lane >> 4) * 4;
+        const int64_t cbase = n0 + wn * WTN + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = rbase + i * 16 + r, col = cbase + j * 16;
+                    if (row >= p.M || col >= p.N) continue;
+                    const int64_t idx = coff + row * p.ldc + col;
+                    const float g = p.alpha * acc[i][j][r], u = p.alpha * acc2[i][j][r];
+                    if (p.G) store_out(p.G, idx, g, p.out_bf16);
+                    if (p.U) store_out(p.U, idx, u, p.out_bf16);
+                    store_out(p.C, idx, silu(g) * u, p.out_bf16);
+                }
+    }
+}
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
 // Large-tile BF16 GEMM: 256x256 block tile, four waves each owning a 128x128 sub-tile built from
 // 4x4 v_mfma_f32_32x32x16_bf16 blocks (256 FP32 accumulators per lane, held in AGPRs). Per 64-wide
 // k-tile a wave issues 64 MFMAs against 32 128-bit LDS reads, half the LDS traffic per FLOP of the
@@ -456,10 +551,6 @@ __device__ __forceinline__ void finish4(const GemmArgs &p, f32x4 v, int64_t row,
 //   * sched_group_barrier interleaves the DS reads, global loads and DS writes with the MFMAs.
 // The loop body has no branches: the prefetch after the last tile re-reads the last tile (in
 // bounds) and its LDS writes land in the stage nobody reads again.
-namespace sg {
-constexpr int MFMA = 0x008, VMEM_READ = 0x020, DS_READ = 0x100, DS_WRITE = 0x200;
-}
-
 template <bool TA, bool TB, bool EDGE>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_256(const GemmArgs p) {
@@ -526,8 +617,8 @@ void gemm_bf16_256(const GemmArgs p) {
         };
         // Tile k0: global loads into registers now, LDS writes in put().
         auto fetch = [&](int64_t k0) {
-            ga.template load<EDGE>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
-            gb.template load<EDGE>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
+            ga.template load<EDGE ? LOAD_CHECKED : LOAD_EXACT>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
+            gb.template load<EDGE ? LOAD_CHECKED : LOAD_EXACT>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
         };
         auto put = [&](char *stage) {
             ga.store(stage, tid);
@@ -646,12 +737,27 @@ hipError_t launch_bf16_256(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipSt
     return hipGetLastError();
 }
 
+template <typename T, bool TA, bool TB, bool DUAL, int LM>
+void launch_cfg_lm(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
+    if (cfg.bm == 128)
+        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 128, 128, 2, 2, DUAL, LM>), grid, dim3(NTHREADS), 0, s, a);
+    else
+        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 64, 64, 2, 2, DUAL, LM>), grid, dim3(NTHREADS), 0, s, a);
+}
+
+// Branch-free masked loads need aligned 16-byte vectors that never straddle an edge.
+template <typename T>
+bool vectors_exact(const GemmArgs &a, bool ta, bool tb) {
+    constexpr int VEC = ET<T>::VEC;
+    return a.a_vec_ok && a.b_vec_ok && a.K % VEC == 0 && (!ta || a.M % VEC == 0) && (tb || a.N % VEC == 0);
+}
+
 template <typename T, bool TA, bool TB, bool DUAL>
 hipError_t launch_cfg(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
-    if (cfg.bm == 128)
-        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 128, 128, 2, 2, DUAL>), grid, dim3(NTHREADS), 0, s, a);
+    if (vectors_exact<T>(a, TA, TB))
+        launch_cfg_lm<T, TA, TB, DUAL, LOAD_MASKED>(cfg, a, grid, s);
     else
-        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 64, 64, 2, 2, DUAL>), grid, dim3(NTHREADS), 0, s, a);
+        launch_cfg_lm<T, TA, TB, DUAL, LOAD_CHECKED>(cfg, a, grid, s);
     return hipGetLastError();
 }
 
@@ -666,6 +772,59 @@ hipError_t launch_typed(bool ta, bool tb, bool dual, const TileCfg &cfg, const G
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+struct Plan {
+    int bm, bn, splits;
+};
+
+// Picks the tile shape and split-K factor with a cost model calibrated on MI355X timings of these
+// kernels: a CU runs up to `occ` blocks at once, sharing its MFMA rate; each round of blocks pays
+// a fixed prologue/epilogue cost; the steady-state MFMA efficiency depends on the tile; split-K
+// adds its partial-sum traffic and a reduction launch. Estimated seconds, lowest wins.
+Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
+    struct Cand {
+        int b, occ;
+        double eff;
+    };
+    // The dual-B (SwiGLU) kernel keeps two B tiles in LDS, which halves its occupancy, and uses
+    // the unpipelined loop: lower efficiencies for it.
+    const Cand f32c[] = {{128, a.dual ? 1 : 2, a.dual ? 0.45 : 0.70}, {64, a.dual ? 2 : 4, 0.55}};
+    const Cand b16c[] = {{256, 1, 0.55}, {128, a.dual ? 1 : 2, 0.40}, {64, a.dual ? 2 : 4, 0.25}};
+    const Cand *cands = bf16 ? b16c : f32c;
+    const int ncand = bf16 ? 3 : 2;
+    const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
+    const double cu_peak = (bf16 ? 2.5e15 : 157.3e12) / 256.0;  // FLOP/s per CU
+    const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = 4e12;
+    const bool can_split = !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL;
+    Plan best{64, 64, 1};
+    double best_t = 1e30;
+    for (int c = 0; c < ncand; ++c) {
+        const Cand &cd = cands[c];
+        const int64_t tiles = cdiv(a.M, cd.b) * cdiv(a.N, cd.b) * a.batch;
+        if (cd.b == 256) {
+            const double fill = (double)a.M * a.N * a.batch / ((double)tiles * 256.0 * 256.0);
+            if (a.dual || fill < 0.7 || tiles * 4 < cus * 3) continue;
+        }
+        for (int s = 1; s <= 32; s *= 2) {
+            if (s > 1 && !can_split) break;
+            const int64_t kps = cdiv(cdiv(a.K, s), bk) * bk;
+            if (s > 1 && kps < 4 * bk) break;
+            const int64_t splits = s > 1 ? cdiv(a.K, kps) : 1;
+            const int64_t blocks = tiles * splits;
+            const int64_t per_cu = cdiv(blocks, cus);
+            const int64_t conc = std::min<int64_t>(per_cu, cd.occ);
+            const int64_t rounds = cdiv(per_cu, cd.occ);
+            const double flops = (a.dual ? 4.0 : 2.0) * cd.b * cd.b * (double)std::max<int64_t>(kps, bk);
+            double t = rounds * (round_overhead + conc * flops / (cu_peak * cd.eff));
+            if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
+            if (t < best_t * 0.97) {  // prefer the earlier (larger, unsplit) plan on near ties
+                best_t = t;
+                best = Plan{cd.b, cd.b, (int)splits};
+            }
+        }
+    }
+    return best;
+}
 
 }  // namespace
 
@@ -682,27 +841,9 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     const bool bf16 = dtype_in == IT_BF16;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-
-    // Tile shape: 256x256 (BF16 only) or 128x128 when that already fills the chip, else 64x64
-    // (+ split-K when even that leaves CUs idle and the reduction is long).
-    TileCfg cfg{128, 128};
-    int64_t tiles = cdiv(a.M, 128) * cdiv(a.N, 128) * a.batch;
-    const int64_t tiles256 = cdiv(a.M, 256) * cdiv(a.N, 256) * a.batch;
-    // 256x256 only when it fills most of the chip and wastes little of each tile on edges.
-    const double fill256 = (double)a.M * a.N * a.batch / ((double)tiles256 * 256.0 * 256.0);
-    if (bf16 && !a.dual && tiles256 * 4 >= cus * 3 && fill256 >= 0.7) {
-        cfg = TileCfg{256, 256};
-        tiles = tiles256;
-    } else if (tiles < cus) {
-        cfg = TileCfg{64, 64};
-        tiles = cdiv(a.M, 64) * cdiv(a.N, 64) * a.batch;
-    }
-    int splits = 1;
-    if (tiles < cus && !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL) {
-        const int64_t want = cdiv(2 * cus, tiles);
-        const int64_t max_by_k = a.K / (4 * bk);  // at least 4 k-tiles per split
-        splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 32}));
-    }
+    const Plan plan = choose_plan(a, bf16, cus);
+    TileCfg cfg{plan.bm, plan.bn};
+    int splits = plan.splits;
     a.tiles_m = (int)cdiv(a.M, cfg.bm);
     a.tiles_n = (int)cdiv(a.N, cfg.bn);
     int64_t kps = cdiv(a.K, splits);
