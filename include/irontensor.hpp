@@ -493,6 +493,29 @@ inline Tensor attention(const Tensor &q, const Tensor &k, const Tensor &v, bool 
     return out;
 }
 
+// ops::attention fused for head_dim 64 (no [seq, seq] buffers); same checks as attention().
+inline Tensor flash_attention(const Tensor &q, const Tensor &k, const Tensor &v, bool causal) {
+    detail::require(q.is_f32() && k.is_f32() && v.is_f32(), "assertion `left == right` failed: attention requires FP32");
+    detail::require(q.shape().size() == 4, "Q must be 4D [batch, seq, heads, dim]");
+    detail::require(k.shape().size() == 4, "K must be 4D [batch, seq, heads, dim]");
+    detail::require(v.shape().size() == 4, "V must be 4D [batch, seq, heads, dim]");
+    const size_t b = q.shape()[0], sq = q.shape()[1], h = q.shape()[2], d = q.shape()[3], skv = k.shape()[1];
+    detail::require(k.shape()[0] == b && v.shape()[0] == b, "Batch size mismatch");
+    detail::require(k.shape()[2] == h && v.shape()[2] == h, "Num heads mismatch");
+    detail::require(k.shape()[3] == d && v.shape()[3] == d, "Head dim mismatch");
+    detail::require(v.shape()[1] == skv, "K and V seq_len must match");
+    if (b == 0 || sq == 0 || skv == 0) return Tensor::zeros({b, sq, h, d}, Precision::FP32);
+    detail::require(!causal || sq == skv, "Causal attention requires Q and K to have same seq_len");
+    Tensor out = Tensor::empty({b, sq, h, d}, Precision::FP32);
+    it_attn_layout lq{(int64_t)h, (int64_t)(sq * h * d), (int64_t)d, (int64_t)(h * d)};
+    it_attn_layout lkv{(int64_t)h, (int64_t)(skv * h * d), (int64_t)d, (int64_t)(h * d)};
+    check(it_flash_attention_forward(Context::global().handle(), IT_F32, (int64_t)(b * h), (int64_t)sq,
+                                     (int64_t)skv, (int64_t)d, 1.f / std::sqrt((float)d), causal ? 1 : 0, &lq,
+                                     &lkv, &lq, q.data(), k.data(), v.data(), (float *)out.data(), nullptr),
+          "attention");
+    return out;
+}
+
 // attention_backward_recompute (src/train/helpers.rs:120-193) on [B,H,S,D]: (dQ, dK, dV).
 struct AttentionGrads {
     Tensor dq, dk, dv;
@@ -510,6 +533,22 @@ inline AttentionGrads attention_backward_recompute(const Tensor &grad_output, co
                                 1.f / std::sqrt((float)d), 1, nullptr, nullptr, nullptr, grad_output.data(), q.data(),
                                 k.data(), v.data(), (float *)sc.data(), p.data(), (float *)dp.data(), ds.data(),
                                 (float *)g.dq.data(), (float *)g.dk.data(), (float *)g.dv.data()),
+          "attention_backward");
+    return g;
+}
+
+// attention_backward_recompute fused for head_dim 64 on [B,H,S,D]; deterministic (no atomics).
+inline AttentionGrads flash_attention_backward(const Tensor &grad_output, const Tensor &q, const Tensor &k,
+                                               const Tensor &v) {
+    const auto &s = q.shape();
+    detail::require(s.size() == 4, "attention_backward requires [batch, heads, seq, dim]");
+    const size_t b = s[0], h = s[1], n = s[2], d = s[3];
+    const Precision pr = q.precision();
+    AttentionGrads g{Tensor::empty(s, Precision::FP32), Tensor::empty(s, Precision::FP32), Tensor::empty(s, Precision::FP32)};
+    check(it_flash_attention_backward(Context::global().handle(), (it_dtype)pr, (int64_t)(b * h), (int64_t)n,
+                                      (int64_t)d, 1.f / std::sqrt((float)d), 1, nullptr, nullptr, nullptr,
+                                      grad_output.data(), q.data(), k.data(), v.data(), nullptr, nullptr,
+                                      (float *)g.dq.data(), (float *)g.dk.data(), (float *)g.dv.data()),
           "attention_backward");
     return g;
 }

@@ -204,6 +204,37 @@ it_status it_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int
                                 float *Sc, void *P, float *dP, void *dS,
                                 float *dQ, float *dK, float *dV);
 
+/*
+ * Fused ("flash") forms of the two calls above for head_dim 64: the same mathematics as
+ * ops::attention and attention_backward_recompute (src/ops/attention.rs:286-377,
+ * src/train/helpers.rs:120-193), with no [seq, seq] buffer. The softmax runs online over 64-key
+ * blocks (running row max and sum), so results match the materialised form to rounding.
+ *
+ * Forward: O = softmax(scale * Q.K^T [causal]).V, layouts and dtypes as it_attention_forward.
+ * lse (NULL allowed): [BH, seq_q] f32 row log-sum-exp of scale * Q.K^T, for the backward.
+ * seq_kv == 0 gives O = 0 (the reference returns zeros).
+ *
+ * Backward: dQ, dK, dV as it_attention_backward. O ([BH, seq, 64] f32 through o_layout, as
+ * written by the forward) and lse are the forward's outputs; pass both NULL to recompute them
+ * into library workspace (which grows once per shape; not during capture). dK and dV are summed
+ * per key block and dQ per query block, without atomics, so results are deterministic.
+ * IT_BF16 rounds P and dS to BF16 before their MFMA, as the materialised form stores them.
+ *
+ * Requires head_dim == 64 and 16-byte aligned operands whose strides are multiples of 16 bytes
+ * (IT_ERR_DIMS otherwise); causal requires seq_q == seq_kv.
+ */
+it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
+                                     int64_t seq_kv, int64_t head_dim, float scale, int causal,
+                                     const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                     const it_attn_layout *o_layout, const void *Q, const void *K,
+                                     const void *V, float *O, float *lse);
+it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
+                                      int64_t head_dim, float scale, int causal,
+                                      const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                      const it_attn_layout *o_layout, const void *dO, const void *Q,
+                                      const void *K, const void *V, const float *O, const float *lse,
+                                      float *dQ, float *dK, float *dV);
+
 /* ---------------------------------------------------------------- graphs (launch-bound loops) */
 
 typedef struct it_graph it_graph;

@@ -100,6 +100,14 @@ _SIGNATURES = {
                                       C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p]),
+    "it_flash_attention_forward": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_i64, c_float, c_int,
+                                           C.POINTER(AttnLayout), C.POINTER(AttnLayout),
+                                           C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
+                                           c_void_p, c_void_p]),
+    "it_flash_attention_backward": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_float, c_int,
+                                            C.POINTER(AttnLayout), C.POINTER(AttnLayout),
+                                            C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
+                                            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "it_capture_begin": (c_int, [c_void_p]),
     "it_capture_end": (c_int, [c_void_p, C.POINTER(c_void_p)]),
     "it_graph_launch": (c_int, [c_void_p, c_void_p]),

@@ -393,3 +393,138 @@ it_status it_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------------ fused (flash) attention
+
+namespace {
+
+it::FlashArgs flash_args(const AttnGeom &g, float scale, int causal) {
+    it::FlashArgs f{};
+    f.bh = g.bh;
+    f.sq = g.Sq;
+    f.skv = g.Skv;
+    f.head_dim = g.D;
+    f.heads = g.lay.heads;
+    f.q_bs = g.lay.batch_stride;
+    f.q_hs = g.lay.head_stride;
+    f.q_rs = g.lay.row_stride;
+    f.kv_bs = g.kv_lay.batch_stride;
+    f.kv_hs = g.kv_lay.head_stride;
+    f.kv_rs = g.kv_lay.row_stride;
+    f.o_bs = f.do_bs = g.o_lay.batch_stride;
+    f.o_hs = f.do_hs = g.o_lay.head_stride;
+    f.o_rs = f.do_rs = g.o_lay.row_stride;
+    f.scale = scale;
+    f.causal = causal ? 1 : 0;
+    return f;
+}
+
+std::string flash_key(const char *what, bool bf16, const AttnGeom &g, int causal) {
+    return std::string(what) + (bf16 ? "_bf16" : "_f32") + (causal ? "_causal" : "") + "[bh=" + i64(g.bh) +
+           ",sq=" + i64(g.Sq) + ",skv=" + i64(g.Skv) + "]";
+}
+
+}  // namespace
+
+extern "C" {
+
+it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
+                                     int64_t seq_kv, int64_t head_dim, float scale, int causal,
+                                     const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                     const it_attn_layout *o_layout, const void *Q, const void *K,
+                                     const void *V, float *O, float *lse) {
+    AttnGeom g;
+    it_status st = check_attention("flash_attention", ctx, dtype, bh, seq_q, seq_kv, head_dim, q_layout,
+                                   kv_layout, o_layout, &g);
+    if (st != IT_OK) return st;
+    if (causal && seq_q != seq_kv)
+        return fail(IT_ERR_SHAPE, "flash_attention: shape mismatch, expected seq_q == seq_kv for causal, got " +
+                                      i64(seq_q) + " and " + i64(seq_kv));
+    if (head_dim != 64)
+        return fail(IT_ERR_DIMS, "flash_attention: unsupported dimensions, head_dim must be 64, got " +
+                                     i64(head_dim));
+    if (bh == 0 || seq_q == 0) return IT_OK;
+    if (!Q || !O || (seq_kv > 0 && (!K || !V))) return fail(IT_ERR_NULL, "flash_attention: NULL buffer");
+    it::FlashArgs f = flash_args(g, scale, causal);
+    f.Q = Q;
+    // With seq_kv == 0 the kernel reads no key; give it a valid pointer to form addresses from.
+    f.K = seq_kv > 0 ? K : Q;
+    f.V = seq_kv > 0 ? V : Q;
+    f.O = O;
+    f.lse = lse;
+    const int eb = dtype == IT_BF16 ? 2 : 4;
+    if (!it::flash_supported(f, eb, false))
+        return fail(IT_ERR_DIMS, "flash_attention: unsupported dimensions, operands must be 16-byte aligned "
+                                 "with strides that are multiples of 16 bytes");
+    hipEvent_t ev = nullptr;
+    std::string key;
+    if (ctx->profiling) {
+        key = flash_key("flash_fwd", dtype == IT_BF16, g, causal);
+        it::profile_begin(ctx, key, &ev);
+    }
+    st = it::launch_flash_fwd(ctx->stream, f, dtype == IT_BF16);
+    if (ctx->profiling) it::profile_end(ctx, key, ev);
+    return st;
+}
+
+it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
+                                      int64_t head_dim, float scale, int causal,
+                                      const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                      const it_attn_layout *o_layout, const void *dO, const void *Q,
+                                      const void *K, const void *V, const float *O, const float *lse,
+                                      float *dQ, float *dK, float *dV) {
+    AttnGeom g;
+    it_status st = check_attention("flash_attention_backward", ctx, dtype, bh, seq, seq, head_dim, q_layout,
+                                   kv_layout, o_layout, &g);
+    if (st != IT_OK) return st;
+    if (head_dim != 64)
+        return fail(IT_ERR_DIMS, "flash_attention_backward: unsupported dimensions, head_dim must be 64, got " +
+                                     i64(head_dim));
+    if ((O == nullptr) != (lse == nullptr))
+        return fail(IT_ERR_INVALID, "flash_attention_backward: pass both O and lse, or neither");
+    if (bh == 0 || seq == 0) return IT_OK;
+    if (!dO || !Q || !K || !V || !dQ || !dK || !dV)
+        return fail(IT_ERR_NULL, "flash_attention_backward: NULL buffer");
+    it::FlashArgs f = flash_args(g, scale, causal);
+    f.Q = Q;
+    f.K = K;
+    f.V = V;
+    f.dO = dO;
+    f.dQ = dQ;
+    f.dK = dK;
+    f.dV = dV;
+    const int eb = dtype == IT_BF16 ? 2 : 4;
+    if (!it::flash_supported(f, eb, true))
+        return fail(IT_ERR_DIMS, "flash_attention_backward: unsupported dimensions, operands must be 16-byte "
+                                 "aligned with strides that are multiples of 16 bytes");
+    const size_t rows = (size_t)bh * (size_t)seq;
+    // Workspace: when the forward is recomputed, O [rows, 64] and lse [rows]; then dlt [rows].
+    const size_t bytes = rows * 4 * (O ? 1 : 64 + 2);
+    void *ws = nullptr;
+    if ((st = it::ensure_attn_scratch(ctx, bytes, &ws)) != IT_OK) return st;
+    f.dlt = (float *)ws + (O ? 0 : rows * 65);
+    const bool bf16 = dtype == IT_BF16;
+    hipEvent_t ev = nullptr;
+    std::string key;
+    if (ctx->profiling) {
+        key = flash_key(O ? "flash_bwd" : "flash_bwd_recompute", bf16, g, causal);
+        it::profile_begin(ctx, key, &ev);
+    }
+    if (O) {
+        f.O = const_cast<float *>(O);
+        f.lse = const_cast<float *>(lse);
+    } else {
+        f.O = (float *)ws;  // 256-byte aligned, so its float4 stores are aligned
+        f.lse = f.O + rows * 64;
+        // Recomputed O is [bh, seq, 64] contiguous.
+        f.o_bs = f.heads * seq * 64;
+        f.o_hs = seq * 64;
+        f.o_rs = 64;
+        st = it::launch_flash_fwd(ctx->stream, f, bf16);
+    }
+    if (st == IT_OK) st = it::launch_flash_bwd(ctx->stream, f, bf16);
+    if (ctx->profiling) it::profile_end(ctx, key, ev);
+    return st;
+}
+
+}  // extern "C"

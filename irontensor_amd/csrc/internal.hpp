@@ -53,9 +53,11 @@ struct it_context {
     std::multimap<size_t, void *> cache;
     size_t bytes_live = 0;
 
-    // Library-owned scratch (split-K partials), grown on demand.
+    // Library-owned scratch (split-K partials; attention recompute buffers), grown on demand.
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    void *attn_scratch = nullptr;
+    size_t attn_scratch_bytes = 0;
 
     // True between it_capture_begin and it_capture_end: nothing may allocate.
     bool capturing = false;
@@ -80,6 +82,7 @@ namespace it {
 
 // Grows the context scratch to at least `bytes` (synchronises before freeing the old block).
 it_status ensure_scratch(it_context *ctx, size_t bytes, void **out);
+it_status ensure_attn_scratch(it_context *ctx, size_t bytes, void **out);
 
 // Profiler hooks around one kernel launch.
 void profile_begin(it_context *ctx, const std::string &key, hipEvent_t *start_out);
@@ -133,6 +136,25 @@ struct GemmArgs {
 // Launches the MFMA GEMM for `dtype_in` (IT_F32 / IT_BF16). Chooses tile shape and split-K.
 it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool transB, GemmArgs args,
                       const char *profile_tag);
+
+// Fused attention (kernels_flash.hip), head_dim 64. Per-head addressing of each operand:
+// (bh / heads) * bs + (bh % heads) * hs + row * rs + col (element strides).
+struct FlashArgs {
+    const void *Q, *K, *V, *dO;  // operand dtype
+    float *O;                    // forward output / backward input (f32)
+    float *lse, *dlt;            // [bh][sq] row log-sum-exp, rowsum(dO * O)
+    float *dQ, *dK, *dV;         // f32 gradients
+    int64_t bh, sq, skv, head_dim, heads;
+    int64_t q_bs, q_hs, q_rs;     // Q and dQ
+    int64_t kv_bs, kv_hs, kv_rs;  // K, V, dK, dV
+    int64_t o_bs, o_hs, o_rs;     // O
+    int64_t do_bs, do_hs, do_rs;  // dO
+    float scale;
+    int causal;
+};
+bool flash_supported(const FlashArgs &p, int elem_bytes, bool backward);
+it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16);
+it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16);
 
 // Elementwise and row kernels (kernels_misc.hip).
 it_status launch_zero(hipStream_t s, void *dst, size_t bytes);

@@ -1,0 +1,554 @@
+// Fused attention contractions for head_dim 64 on gfx950 MFMA ("flash" form: S and P never reach
+// HBM). Same mathematics as ops::attention / attention_backward_recompute
+// (src/ops/attention.rs:286-377, src/train/helpers.rs:120-193): S = scale * Q.K^T, causal -inf above
+// the diagonal, P = softmax(S) per row, O = P.V; backward dV = P^T.dO, dP = dO.V^T,
+// dS = P * (dP - rowsum(dP * P)), dQ = scale * dS.K, dK = scale * dS^T.Q. The softmax runs online
+// over 64-key blocks (running max and sum, rescaling the partial output), and the backward uses
+// rowsum(dP * P) = rowsum(dO * O) and P = exp(S - LSE) with the row log-sum-exp saved by the forward.
+//
+// Layout choice: every block owns 64 rows (queries or keys), one wave per 16 rows. Products are
+// arranged so that a lane's accumulator values belong to one query (S^T = K.Q^T puts the query on
+// the lane's column), which keeps the softmax statistics to two cross-lane shuffles and lets the
+// probabilities feed the next MFMA straight from the accumulators:
+//   forward : S^T = K.Q^T,       O^T += V^T.P^T
+//   dK / dV : S = Q.K^T, dP = dO.V^T (keys on the lane's column), dV += P^T.dO, dK += dS^T.Q
+//   dQ      : S^T = K.Q^T, dP^T = V.dO^T,                          dQ^T += K^T.dS^T
+// The backward is deterministic: dK/dV and dQ come from two kernels instead of atomics.
+// BF16 operands accumulate in FP32; P and dS are rounded to BF16 before their MFMA. When a
+// fragment comes from accumulators (P, dS), a BF16 lane group g holds keys {4g..4g+3} and
+// {16+4g..16+4g+3} of a 32-key chunk, and the LDS operand it meets is read with the same split.
+#include <cmath>
+
+#include "internal.hpp"
+#include "mfma.hpp"
+
+namespace it {
+namespace {
+
+constexpr int HD = 64;   // head dim
+constexpr int TR = 64;   // rows per tile
+constexpr int NTH = 256;
+
+template <typename T>
+struct FE;
+template <>
+struct FE<float> {
+    static constexpr int KC = 16;  // k per fragment chunk
+    static constexpr int VEC = 4;  // elements per 16 bytes
+};
+template <>
+struct FE<uint16_t> {
+    static constexpr int KC = 32;
+    static constexpr int VEC = 8;
+};
+
+template <typename T>
+constexpr int pitch() { return HD * (int)sizeof(T) + 16; }  // LDS bytes per tile row
+template <typename T>
+constexpr int tile_bytes() { return TR * pitch<T>(); }
+
+struct Head {
+    int64_t heads, bs, hs, rs;
+    __device__ __forceinline__ int64_t base(int64_t bh) const { return (bh / heads) * bs + (bh % heads) * hs; }
+};
+
+__device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
+
+// A 64x64 tile of T from a per-head matrix (rows beyond `rows` read as zero), held in registers
+// between its global load and its LDS store, in row-major or transposed LDS layout.
+template <typename T, bool TRANSPOSED>
+struct TileRegs {
+    static constexpr int VEC = FE<T>::VEC;
+    static constexpr int UNITS = TRANSPOSED ? (TR / 4) * (HD / VEC) : TR * HD / VEC;
+    static constexpr int LOADS = TRANSPOSED ? 4 : 1;
+    static constexpr int ITERS = (UNITS + NTH - 1) / NTH;
+    u32x4 r[ITERS][LOADS];
+
+    __device__ __forceinline__ void load(const T *m, int64_t rs, int row0, int rows, int tid) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int u = tid + it * NTH;
+            if (UNITS % NTH != 0 && u >= UNITS) continue;
+            if constexpr (!TRANSPOSED) {
+                const int row = u / (HD / VEC), cc = u % (HD / VEC);
+                const bool ok = row0 + row < rows;
+                const u32x4 v = ld16(m + (ok ? (int64_t)(row0 + row) * rs + cc * VEC : 0));
+                r[it][0] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+            } else {
+                const int cc = u % (HD / VEC), rg = u / (HD / VEC);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int row = rg * 4 + q;
+                    const bool ok = row0 + row < rows;
+                    const u32x4 v = ld16(m + (ok ? (int64_t)(row0 + row) * rs + cc * VEC : 0));
+                    r[it][q] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(char *lds, int tid) const {
+        constexpr int P = pitch<T>();
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int u = tid + it * NTH;
+            if (UNITS % NTH != 0 && u >= UNITS) continue;
+            if constexpr (!TRANSPOSED) {
+                const int row = u / (HD / VEC), cc = u % (HD / VEC);
+                *(u32x4 *)(lds + row * P + cc * 16) = r[it][0];
+            } else {
+                const int cc = u % (HD / VEC), rg = u / (HD / VEC);
+                const u32x4 &v0 = r[it][0], &v1 = r[it][1], &v2 = r[it][2], &v3 = r[it][3];
+                if constexpr (sizeof(T) == 4) {
+                    // 4 rows x 4 columns -> LDS rows 4cc+j, columns 4rg..4rg+3
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        *(u32x4 *)(lds + (cc * 4 + j) * P + rg * 16) = u32x4{v0[j], v1[j], v2[j], v3[j]};
+                } else {
+                    // 4 rows x 8 bf16 columns -> LDS rows 8cc+j, columns 4rg..4rg+3 (8 bytes)
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        u32x2 lo, hi;
+                        lo[0] = (v0[d] & 0xffffu) | (v1[d] << 16);
+                        lo[1] = (v2[d] & 0xffffu) | (v3[d] << 16);
+                        hi[0] = (v0[d] >> 16) | (v1[d] & 0xffff0000u);
+                        hi[1] = (v2[d] >> 16) | (v3[d] & 0xffff0000u);
+                        *(u32x2 *)(lds + (cc * 8 + 2 * d) * P + rg * 8) = lo;
+                        *(u32x2 *)(lds + (cc * 8 + 2 * d + 1) * P + rg * 8) = hi;
+                    }
+                }
+            }
+        }
+    }
+};
+
+// Fragment of LDS tile row `row`, contiguous k chunk c (lane group g).
+template <typename T>
+__device__ __forceinline__ u32x4 frag_c(const char *tile, int row, int c, int g) {
+    return *(const u32x4 *)(tile + row * pitch<T>() + (c * FE<T>::KC + g * FE<T>::VEC) * (int)sizeof(T));
+}
+
+// Fragment whose k assignment matches an accumulator-derived operand: FP32 chunk c = keys
+// 16c + 4g..+3 (same as frag_c); BF16 chunk c = keys 32c + 4g..+3 and 32c + 16 + 4g..+3.
+template <typename T>
+__device__ __forceinline__ u32x4 frag_s(const char *tile, int row, int c, int g) {
+    if constexpr (sizeof(T) == 4) {
+        return frag_c<T>(tile, row, c, g);
+    } else {
+        const char *p = tile + row * pitch<T>();
+        const u32x2 lo = *(const u32x2 *)(p + (32 * c + 4 * g) * 2);
+        const u32x2 hi = *(const u32x2 *)(p + (32 * c + 16 + 4 * g) * 2);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+}
+
+// Operand fragment from accumulator blocks (rows 4g + r of 16-row blocks): FP32 uses block c,
+// BF16 packs blocks 2c and 2c+1.
+template <typename T>
+__device__ __forceinline__ u32x4 frag_acc(const f32x4 *blk, int c) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(u32x4, blk[c]);
+    } else {
+        const f32x4 a = blk[2 * c], b = blk[2 * c + 1];
+        return u32x4{(uint32_t)f32_to_bf16_rne(a[0]) | ((uint32_t)f32_to_bf16_rne(a[1]) << 16),
+                     (uint32_t)f32_to_bf16_rne(a[2]) | ((uint32_t)f32_to_bf16_rne(a[3]) << 16),
+                     (uint32_t)f32_to_bf16_rne(b[0]) | ((uint32_t)f32_to_bf16_rne(b[1]) << 16),
+                     (uint32_t)f32_to_bf16_rne(b[2]) | ((uint32_t)f32_to_bf16_rne(b[3]) << 16)};
+    }
+}
+
+__device__ __forceinline__ float xmax(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float xsum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+constexpr int NCHUNK_F32 = HD / 16;
+
+// ------------------------------------------------------------------ forward
+
+template <typename T>
+__global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
+    constexpr int KT = tile_bytes<T>();      // K tile [keys][d]
+    constexpr int STAGE = 2 * KT;            // + V^T tile [d][keys]
+    constexpr int NC = HD / FE<T>::KC;       // d chunks
+    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 15, g = lane >> 4;
+    const int qb = blockIdx.x;
+    const int64_t bh = blockIdx.y;
+    const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
+        ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
+    const T *Q = (const T *)p.Q + hq.base(bh);
+    const T *K = (const T *)p.K + hk.base(bh);
+    const T *V = (const T *)p.V + hk.base(bh);
+    float *O = (float *)p.O + ho.base(bh);
+    const int q = qb * TR + wave * 16 + ql;  // this lane's query
+    const bool qok = q < p.sq;
+
+    u32x4 qf[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const u32x4 v = ld16(Q + (qok ? (int64_t)q * p.q_rs + c * FE<T>::KC + g * FE<T>::VEC : 0));
+        qf[c] = qok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+    f32x4 o[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+
+    const int kblocks = (p.skv + TR - 1) / TR;
+    const int nkb = p.causal ? min(kblocks, qb + 1) : kblocks;
+    TileRegs<T, false> kr;
+    TileRegs<T, true> vr;
+    if (nkb > 0) {
+        kr.load(K, p.kv_rs, 0, p.skv, tid);
+        vr.load(V, p.kv_rs, 0, p.skv, tid);
+        kr.store(smem, tid);
+        vr.store(smem + KT, tid);
+        __syncthreads();
+    }
+    for (int kb = 0; kb < nkb; ++kb) {
+        const char *kt = smem + (kb & 1) * STAGE, *vt = kt + KT;
+        char *nxt = smem + ((kb + 1) & 1) * STAGE;
+        const bool more = kb + 1 < nkb;
+        if (more) {
+            kr.load(K, p.kv_rs, (kb + 1) * TR, p.skv, tid);
+            vr.load(V, p.kv_rs, (kb + 1) * TR, p.skv, tid);
+        }
+        // S^T blocks: keys 16mb + 4g + r of this tile, query q.
+        f32x4 s[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            s[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) mma16<T>(s[mb], frag_c<T>(kt, mb * 16 + ql, c, g), qf[c]);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = kb * TR + mb * 16 + g * 4 + r;
+                float v = s[mb][r] * p.scale;
+                if (key >= p.skv || (p.causal && key > q)) v = -INFINITY;
+                s[mb][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        const float mnew = fmaxf(m, xmax(mx));
+        const float msafe = mnew == -INFINITY ? 0.f : mnew;
+        const float alpha = expf(m - msafe);
+        float ls = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = expf(s[mb][r] - msafe);
+                s[mb][r] = e;
+                ls += e;
+            }
+        l = l * alpha + xsum(ls);
+        m = mnew;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) o[d] *= alpha;
+        // O^T (d x q) += V^T (d x keys) . P^T (keys x q)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int c = 0; c < TR / FE<T>::KC; ++c) mma16<T>(o[d], frag_s<T>(vt, d * 16 + ql, c, g), frag_acc<T>(s, c));
+        if (more) {
+            kr.store(nxt, tid);
+            vr.store(nxt + KT, tid);
+        }
+        __syncthreads();
+    }
+    if (qok) {
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) *(f32x4 *)(O + (int64_t)q * p.o_rs + d * 16 + g * 4) = o[d] * inv;
+        if (g == 0 && p.lse) p.lse[bh * p.sq + q] = m + logf(l);
+    }
+}
+
+
+// ------------------------------------------------------------------ backward
+
+// dlt[bh][q] = sum_d dO[q][d] * O[q][d] (= rowsum(dP * P)); one thread per row.
+template <typename T>
+__global__ __launch_bounds__(NTH) void flash_dlt(const FlashArgs p) {
+    const int64_t row = (int64_t)blockIdx.x * NTH + threadIdx.x;
+    if (row >= p.bh * p.sq) return;
+    const int64_t bh = row / p.sq, q = row % p.sq;
+    const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
+    const T *dO = (const T *)p.dO + hd.base(bh) + q * p.do_rs;
+    const float *O = p.O + ho.base(bh) + q * p.o_rs;
+    float acc = 0.f;
+#pragma unroll 8
+    for (int d = 0; d < HD; ++d) {
+        const float g = sizeof(T) == 4 ? ((const float *)dO)[d] : bf16_to_f32(((const uint16_t *)dO)[d]);
+        acc += g * O[d];
+    }
+    p.dlt[row] = acc;
+}
+
+// dK, dV for 64 keys per block (16 per wave), looping over the query blocks that see them.
+template <typename T>
+__global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
+    constexpr int T_ = tile_bytes<T>();
+    constexpr int STAGE = 4 * T_ + 2 * TR * 4;  // Q, Q^T, dO, dO^T tiles + lse, dlt rows
+    constexpr int NC = HD / FE<T>::KC;
+    constexpr int NQ = TR / FE<T>::KC;  // q chunks per tile
+    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 15, g = lane >> 4;
+    const int kb = blockIdx.x;
+    const int64_t bh = blockIdx.y;
+    const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
+        hd{p.heads, p.do_bs, p.do_hs, p.do_rs};
+    const T *Q = (const T *)p.Q + hq.base(bh);
+    const T *K = (const T *)p.K + hk.base(bh);
+    const T *V = (const T *)p.V + hk.base(bh);
+    const T *dO = (const T *)p.dO + hd.base(bh);
+    const float *lse = p.lse + bh * p.sq, *dlt = p.dlt + bh * p.sq;
+    const int key = kb * TR + wave * 16 + ql;  // this lane's key (column of S = Q.K^T)
+    const bool kok = key < p.skv;
+
+    u32x4 kf[NC], vf[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int64_t off = kok ? (int64_t)key * p.kv_rs + c * FE<T>::KC + g * FE<T>::VEC : 0;
+        const u32x4 a = ld16(K + off), b = ld16(V + off);
+        kf[c] = kok ? a : u32x4{0u, 0u, 0u, 0u};
+        vf[c] = kok ? b : u32x4{0u, 0u, 0u, 0u};
+    }
+    f32x4 dk[4], dv[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) dk[n] = dv[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int qblocks = (p.sq + TR - 1) / TR;
+    const int qb0 = p.causal ? kb : 0;
+    TileRegs<T, false> qr, dr;
+    TileRegs<T, true> qtr, dtr;
+    auto load = [&](int qb) {
+        qr.load(Q, p.q_rs, qb * TR, p.sq, tid);
+        qtr.load(Q, p.q_rs, qb * TR, p.sq, tid);
+        dr.load(dO, p.do_rs, qb * TR, p.sq, tid);
+        dtr.load(dO, p.do_rs, qb * TR, p.sq, tid);
+    };
+    auto store = [&](int qb, char *st) {
+        qr.store(st, tid);
+        qtr.store(st + T_, tid);
+        dr.store(st + 2 * T_, tid);
+        dtr.store(st + 3 * T_, tid);
+        if (tid < TR) {
+            const int q = qb * TR + tid;
+            ((float *)(st + 4 * T_))[tid] = q < p.sq ? lse[q] : 0.f;
+            ((float *)(st + 4 * T_ + TR * 4))[tid] = q < p.sq ? dlt[q] : 0.f;
+        }
+    };
+    if (qb0 < qblocks) {
+        load(qb0);
+        store(qb0, smem);
+        __syncthreads();
+    }
+    for (int qb = qb0; qb < qblocks; ++qb) {
+        const char *st = smem + ((qb - qb0) & 1) * STAGE;
+        char *nxt = smem + ((qb - qb0 + 1) & 1) * STAGE;
+        const bool more = qb + 1 < qblocks;
+        if (more) load(qb + 1);
+        const char *qt = st, *qtt = st + T_, *dot = st + 2 * T_, *dott = st + 3 * T_;
+        const float *ls = (const float *)(st + 4 * T_), *dl = ls + TR;
+        // S = Q.K^T and dP = dO.V^T: rows q = 16mb + 4g + r of the tile, column = this key.
+        f32x4 sp[4], dp[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            sp[mb] = dp[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                mma16<T>(sp[mb], frag_c<T>(qt, mb * 16 + ql, c, g), kf[c]);
+                mma16<T>(dp[mb], frag_c<T>(dot, mb * 16 + ql, c, g), vf[c]);
+            }
+        }
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int ql_ = mb * 16 + g * 4 + r, q = qb * TR + ql_;
+                const bool live = q < p.sq && kok && !(p.causal && key > q);
+                const float pr = live ? expf(sp[mb][r] * p.scale - ls[ql_]) : 0.f;
+                sp[mb][r] = pr;
+                dp[mb][r] = pr * (dp[mb][r] - dl[ql_]);
+            }
+        // dV (keys x d) += P^T (keys x q) . dO (q x d);  dK += dS^T . Q
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int c = 0; c < NQ; ++c) {
+                mma16<T>(dv[n], frag_acc<T>(sp, c), frag_s<T>(dott, n * 16 + ql, c, g));
+                mma16<T>(dk[n], frag_acc<T>(dp, c), frag_s<T>(qtt, n * 16 + ql, c, g));
+            }
+        if (more) store(qb + 1, nxt);
+        __syncthreads();
+    }
+    // Lane l holds rows (keys) 16*wave + 4g + r and column d = 16n + l%16.
+    const Head hdk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs};
+    float *dK = p.dK + hdk.base(bh), *dV = p.dV + hdk.base(bh);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int k = kb * TR + wave * 16 + g * 4 + r;
+        if (k >= p.skv) continue;
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            dK[(int64_t)k * p.kv_rs + n * 16 + ql] = dk[n][r] * p.scale;
+            dV[(int64_t)k * p.kv_rs + n * 16 + ql] = dv[n][r];
+        }
+    }
+}
+
+// dQ for 64 queries per block (16 per wave), looping over the key blocks they see.
+template <typename T>
+__global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
+    constexpr int T_ = tile_bytes<T>();
+    constexpr int STAGE = 3 * T_;  // K, V, K^T
+    constexpr int NC = HD / FE<T>::KC;
+    constexpr int NK = TR / FE<T>::KC;
+    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 15, g = lane >> 4;
+    const int qb = blockIdx.x;
+    const int64_t bh = blockIdx.y;
+    const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
+        hd{p.heads, p.do_bs, p.do_hs, p.do_rs};
+    const T *Q = (const T *)p.Q + hq.base(bh);
+    const T *K = (const T *)p.K + hk.base(bh);
+    const T *V = (const T *)p.V + hk.base(bh);
+    const T *dO = (const T *)p.dO + hd.base(bh);
+    const int q = qb * TR + wave * 16 + ql;
+    const bool qok = q < p.sq;
+    const float lse = qok ? p.lse[bh * p.sq + q] : 0.f, dl = qok ? p.dlt[bh * p.sq + q] : 0.f;
+
+    u32x4 qf[NC], of[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const u32x4 a = ld16(Q + (qok ? (int64_t)q * p.q_rs + c * FE<T>::KC + g * FE<T>::VEC : 0));
+        const u32x4 b = ld16(dO + (qok ? (int64_t)q * p.do_rs + c * FE<T>::KC + g * FE<T>::VEC : 0));
+        qf[c] = qok ? a : u32x4{0u, 0u, 0u, 0u};
+        of[c] = qok ? b : u32x4{0u, 0u, 0u, 0u};
+    }
+    f32x4 dq[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int kblocks = (p.skv + TR - 1) / TR;
+    const int nkb = p.causal ? min(kblocks, qb + 1) : kblocks;
+    TileRegs<T, false> kr, vr;
+    TileRegs<T, true> ktr;
+    if (nkb > 0) {
+        kr.load(K, p.kv_rs, 0, p.skv, tid);
+        vr.load(V, p.kv_rs, 0, p.skv, tid);
+        ktr.load(K, p.kv_rs, 0, p.skv, tid);
+        kr.store(smem, tid);
+        vr.store(smem + T_, tid);
+        ktr.store(smem + 2 * T_, tid);
+        __syncthreads();
+    }
+    for (int kb = 0; kb < nkb; ++kb) {
+        const char *kt = smem + (kb & 1) * STAGE, *vt = kt + T_, *ktt = kt + 2 * T_;
+        char *nxt = smem + ((kb + 1) & 1) * STAGE;
+        const bool more = kb + 1 < nkb;
+        if (more) {
+            kr.load(K, p.kv_rs, (kb + 1) * TR, p.skv, tid);
+            vr.load(V, p.kv_rs, (kb + 1) * TR, p.skv, tid);
+            ktr.load(K, p.kv_rs, (kb + 1) * TR, p.skv, tid);
+        }
+        // S^T = K.Q^T and dP^T = V.dO^T: rows = keys 16mb + 4g + r, column = this query.
+        f32x4 sp[4], dp[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            sp[mb] = dp[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                mma16<T>(sp[mb], frag_c<T>(kt, mb * 16 + ql, c, g), qf[c]);
+                mma16<T>(dp[mb], frag_c<T>(vt, mb * 16 + ql, c, g), of[c]);
+            }
+        }
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = kb * TR + mb * 16 + g * 4 + r;
+                const bool live = qok && key < p.skv && !(p.causal && key > q);
+                const float pr = live ? expf(sp[mb][r] * p.scale - lse) : 0.f;
+                dp[mb][r] = pr * (dp[mb][r] - dl);
+            }
+        // dQ^T (d x q) += K^T (d x keys) . dS^T (keys x q)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int c = 0; c < NK; ++c) mma16<T>(dq[d], frag_s<T>(ktt, d * 16 + ql, c, g), frag_acc<T>(dp, c));
+        if (more) {
+            kr.store(nxt, tid);
+            vr.store(nxt + T_, tid);
+            ktr.store(nxt + 2 * T_, tid);
+        }
+        __syncthreads();
+    }
+    if (qok) {
+        float *dQ = p.dQ + hq.base(bh) + (int64_t)q * p.q_rs;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) *(f32x4 *)(dQ + d * 16 + g * 4) = dq[d] * p.scale;
+    }
+}
+
+}  // namespace
+
+bool flash_supported(const FlashArgs &p, int elem_bytes, bool backward) {
+    const int64_t vec = 16 / elem_bytes;
+    auto ok = [&](const void *ptr, int64_t bs, int64_t hs, int64_t rs, int64_t v) {
+        return ptr && (uintptr_t)ptr % 16 == 0 && bs % v == 0 && hs % v == 0 && rs % v == 0;
+    };
+    bool r = p.head_dim == HD && ok(p.Q, p.q_bs, p.q_hs, p.q_rs, vec) && ok(p.K, p.kv_bs, p.kv_hs, p.kv_rs, vec) &&
+             ok(p.V, p.kv_bs, p.kv_hs, p.kv_rs, vec);
+    if (backward)
+        r = r && ok(p.dO, p.do_bs, p.do_hs, p.do_rs, vec) && ok(p.dQ, p.q_bs, p.q_hs, p.q_rs, 4) &&
+            ok(p.dK, p.kv_bs, p.kv_hs, p.kv_rs, 4) && ok(p.dV, p.kv_bs, p.kv_hs, p.kv_rs, 4);
+    else
+        r = r && ok(p.O, p.o_bs, p.o_hs, p.o_rs, 4);
+    return r;
+}
+
+it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16) {
+    const int64_t qblocks = (p.sq + TR - 1) / TR;
+    if (qblocks > 0x7fffffff || p.bh > 65535) return fail(IT_ERR_DIMS, "flash attention: grid too large");
+    dim3 grid((unsigned)qblocks, (unsigned)p.bh);
+    if (bf16)
+        hipLaunchKernelGGL(flash_fwd<uint16_t>, grid, dim3(NTH), 0, s, p);
+    else
+        hipLaunchKernelGGL(flash_fwd<float>, grid, dim3(NTH), 0, s, p);
+    IT_HIP_TRY(hipGetLastError());
+    return IT_OK;
+}
+
+it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16) {
+    const int64_t qblocks = (p.sq + TR - 1) / TR, kblocks = (p.skv + TR - 1) / TR;
+    if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || p.bh > 65535)
+        return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
+    const int64_t rows = p.bh * p.sq;
+    const unsigned dlt_blocks = (unsigned)((rows + NTH - 1) / NTH);
+    if (bf16) {
+        hipLaunchKernelGGL(flash_dlt<uint16_t>, dim3(dlt_blocks), dim3(NTH), 0, s, p);
+        hipLaunchKernelGGL(flash_bwd_dkdv<uint16_t>, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+        hipLaunchKernelGGL(flash_bwd_dq<uint16_t>, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+    } else {
+        hipLaunchKernelGGL(flash_dlt<float>, dim3(dlt_blocks), dim3(NTH), 0, s, p);
+        hipLaunchKernelGGL(flash_bwd_dkdv<float>, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+        hipLaunchKernelGGL(flash_bwd_dq<float>, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+    }
+    IT_HIP_TRY(hipGetLastError());
+    return IT_OK;
+}
+
+}  // namespace it

@@ -30,23 +30,31 @@ it_status fail_hip(hipError_t err, const char *what) {
 
 void clear_error() { g_last_error.clear(); }
 
-it_status ensure_scratch(it_context *ctx, size_t bytes, void **out) {
-    if (ctx->scratch_bytes < bytes && ctx->capturing)
+static it_status grow(it_context *ctx, void *&buf, size_t &have, size_t bytes, void **out) {
+    if (have < bytes && ctx->capturing)
         return fail(IT_ERR_INVALID, "scratch of " + std::to_string(bytes) +
                                         " bytes needed during graph capture: run the work once before capturing");
-    if (ctx->scratch_bytes < bytes) {
-        if (ctx->scratch) {
+    if (have < bytes) {
+        if (buf) {
             IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
-            IT_HIP_TRY(hipFree(ctx->scratch));
-            ctx->scratch = nullptr;
-            ctx->scratch_bytes = 0;
+            IT_HIP_TRY(hipFree(buf));
+            buf = nullptr;
+            have = 0;
         }
         size_t want = bytes < (size_t(64) << 20) ? (size_t(64) << 20) : bytes;
-        IT_HIP_TRY(hipMalloc(&ctx->scratch, want));
-        ctx->scratch_bytes = want;
+        IT_HIP_TRY(hipMalloc(&buf, want));
+        have = want;
     }
-    *out = ctx->scratch;
+    *out = buf;
     return IT_OK;
+}
+
+it_status ensure_scratch(it_context *ctx, size_t bytes, void **out) {
+    return grow(ctx, ctx->scratch, ctx->scratch_bytes, bytes, out);
+}
+
+it_status ensure_attn_scratch(it_context *ctx, size_t bytes, void **out) {
+    return grow(ctx, ctx->attn_scratch, ctx->attn_scratch_bytes, bytes, out);
 }
 
 static hipEvent_t pool_event(it_context *ctx) {
@@ -163,6 +171,7 @@ it_status it_shutdown(it_context *ctx) {
     for (auto &kv : ctx->cache) (void)hipFree(kv.second);
     for (auto &kv : ctx->live) (void)hipFree(kv.first);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->attn_scratch) (void)hipFree(ctx->attn_scratch);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return IT_OK;

@@ -11,7 +11,7 @@ import math
 from typing import Optional, Sequence, Tuple
 
 from . import _lib
-from .errors import (InnerDimensionMismatch, Panic, PrecisionMismatch, ShapeMismatch,
+from .errors import (InnerDimensionMismatch, InvalidValue, Panic, PrecisionMismatch, ShapeMismatch,
                      UnsupportedDimensions, check)
 from .tensor import Precision, Tensor
 
@@ -422,6 +422,89 @@ def attention_backward_recompute(grad_output: Tensor, q: Tensor, k: Tensor, v: T
                                         C.byref(lay), None, None, _vp(grad_output), _vp(q), _vp(k), _vp(v),
                                         _vp(sc), _vp(p), _vp(dp), _vp(ds), _vp(dq), _vp(dk), _vp(dv)),
           "attention_backward")
+    return dq, dk, dv
+
+
+def flash_attention(q: Tensor, k: Tensor, v: Tensor, causal: bool) -> Tensor:
+    """ops::attention (src/ops/attention.rs:286-377) on [B,S,H,D] FP32 tensors, fused for D = 64:
+    the scores never leave the chip (online softmax over 64-key blocks). Same checks and panics as
+    `attention`."""
+    for t in (q, k, v):
+        if t.precision() is not _P.FP32:
+            raise Panic("assertion `left == right` failed: attention requires FP32")
+    qs, ks, vs = q.shape(), k.shape(), v.shape()
+    for name, sh in (("Q", qs), ("K", ks), ("V", vs)):
+        if len(sh) != 4:
+            raise Panic(f"{name} must be 4D [batch, seq, heads, dim]")
+    b, sq, h, d = qs
+    skv = ks[1]
+    if ks[0] != b or vs[0] != b:
+        raise Panic("Batch size mismatch")
+    if ks[2] != h or vs[2] != h:
+        raise Panic("Num heads mismatch")
+    if ks[3] != d or vs[3] != d:
+        raise Panic("Head dim mismatch")
+    if vs[1] != skv:
+        raise Panic("K and V seq_len must match")
+    if b == 0 or sq == 0 or skv == 0:
+        return Tensor.zeros([b, sq, h, d], _P.FP32, q.ctx)
+    if causal and sq != skv:
+        raise Panic("Causal attention requires Q and K to have same seq_len")
+    out = Tensor.empty([b, sq, h, d], _P.FP32, q.ctx)
+    lq, lkv = _layout_bshd(b, sq, h, d), _layout_bshd(b, skv, h, d)
+    check(q.ctx.lib.it_flash_attention_forward(q.ctx.handle, _lib.IT_F32, b * h, sq, skv, d,
+                                               1.0 / math.sqrt(d), int(causal), C.byref(lq),
+                                               C.byref(lkv), C.byref(lq), _vp(q), _vp(k), _vp(v),
+                                               _vp(out), None), "attention")
+    return out
+
+
+def flash_attention_forward_bhsd(q: Tensor, k: Tensor, v: Tensor, causal: bool = True,
+                                 scale: Optional[float] = None) -> Tuple[Tensor, Tensor]:
+    """Fused forward on [B,H,S,D] (D = 64, FP32 or BF16). Returns (O f32, lse f32 [B*H, S])."""
+    b, h, sq, d = q.shape()
+    skv = k.shape()[2]
+    prec = q.precision()
+    for t in (k, v):
+        if t.precision() is not prec:
+            raise PrecisionMismatch("flash_attention", _prec_name(prec), _prec_name(t.precision()))
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    o = Tensor.empty([b, h, sq, d], _P.FP32, q.ctx)
+    lse = Tensor.empty([b * h, sq], _P.FP32, q.ctx)
+    lq, lkv = _layout_bhsd(sq, d), _layout_bhsd(skv, d)
+    check(q.ctx.lib.it_flash_attention_forward(q.ctx.handle, int(prec), b * h, sq, skv, d, float(scale),
+                                               int(causal), C.byref(lq), C.byref(lkv), C.byref(lq),
+                                               _vp(q), _vp(k), _vp(v), _vp(o), _vp(lse)),
+          "flash_attention")
+    return o, lse
+
+
+def flash_attention_backward(grad_output: Tensor, q: Tensor, k: Tensor, v: Tensor, causal: bool = True,
+                             scale: Optional[float] = None, o: Optional[Tensor] = None,
+                             lse: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
+    """attention_backward_recompute (src/train/helpers.rs:120-193) fused, on [B,H,S,D] with D = 64.
+    With `o` and `lse` from flash_attention_forward_bhsd the forward is not recomputed. Returns
+    (dQ, dK, dV), FP32; deterministic (no atomics)."""
+    b, h, s, d = q.shape()
+    prec = q.precision()
+    for t in (grad_output, k, v):
+        if t.precision() is not prec:
+            raise PrecisionMismatch("attention_backward", _prec_name(prec), _prec_name(t.precision()))
+        if t.shape() != q.shape():
+            raise ShapeMismatch("attention_backward", str(q.shape()), str(t.shape()))
+    if (o is None) != (lse is None):
+        raise InvalidValue("flash_attention_backward", "pass both o and lse, or neither")
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    ctx = q.ctx
+    dq = Tensor.empty([b, h, s, d], _P.FP32, ctx)
+    dk = Tensor.empty([b, h, s, d], _P.FP32, ctx)
+    dv = Tensor.empty([b, h, s, d], _P.FP32, ctx)
+    lay = _layout_bhsd(s, d)
+    check(ctx.lib.it_flash_attention_backward(ctx.handle, int(prec), b * h, s, d, float(scale), int(causal),
+                                              C.byref(lay), None, None, _vp(grad_output), _vp(q), _vp(k),
+                                              _vp(v), _vp(o) if o is not None else None,
+                                              _vp(lse) if lse is not None else None,
+                                              _vp(dq), _vp(dk), _vp(dv)), "attention_backward")
     return dq, dk, dv
 
 

@@ -6,15 +6,16 @@ src/train/forward.rs:79-212, src/train/backward.rs:21-177) for every contraction
 
   forward, per layer:  QKV = X.Wqkv^T (one NT GEMM; the reference issues three, forward.rs:101-103)
                        attention contractions S = scale.Q.K^T (causal), P = softmax(S), O = P.V,
-                       read in place from the QKV buffer's [B,S,H,D] layout (no transposes)
+                       read in place from the QKV buffer's [B,S,H,D] layout (no transposes);
+                       fused into one kernel for head_dim 64 (S and P stay on chip)
                        Y = O.Wo^T                                         (forward.rs:146)
                        h = silu(X2.Wg^T) * (X2.Wu^T), fused dual-B GEMM   (forward.rs:166-172)
                        Z = h.Wd^T                                         (forward.rs:175)
   LM head:             logits = Hf.E^T                                    (trainer/mod.rs:229-235)
   backward, LM head:   dE = dlogits^T.Hf (TN), dHf = dlogits.E (NN)       (train_step.rs:206-210)
   backward, per layer: down, gate|up (one GEMM each for dX and dW over the concatenated Wg|Wu),
-                       Wo, attention_backward_recompute (5 GEMMs + softmax and its backward),
-                       QKV                                                (backward.rs:53-147)
+                       Wo, attention_backward_recompute (5 GEMMs + softmax and its backward;
+                       fused into dK/dV and dQ kernels for head_dim 64), QKV (backward.rs:53-147)
 
 The elementwise work between contractions (RMSNorm, RoPE, residual adds, SwiGLU backward, cross
 entropy) is outside this path: each layer's normalised inputs and each upstream gradient are
@@ -70,7 +71,7 @@ class GemmStep:
     """Owns every buffer of the step and enqueues its contractions (eagerly or into a HIP graph)."""
 
     def __init__(self, shape: ModelShape, precision: Precision = Precision.FP32,
-                 ctx: Optional[Context] = None, seed: int = 1234):
+                 ctx: Optional[Context] = None, seed: int = 1234, fused_attention: Optional[bool] = None):
         if shape.heads * shape.head_dim != shape.hidden:
             raise ValueError("heads * head_dim must equal hidden")
         self.s = shape
@@ -128,11 +129,16 @@ class GemmStep:
         self.dWgu = [empty([2 * F, H], Precision.FP32) for _ in range(L)]
         self.dWo = [empty([H, H], Precision.FP32) for _ in range(L)]
         self.dWqkv = [empty([3 * H, H], Precision.FP32) for _ in range(L)]
-        # Attention workspaces, shared by all layers
-        self.Sc = empty([bh, s.seq, s.seq], Precision.FP32)
-        self.Pw = empty([bh, s.seq, s.seq])
-        self.dP = empty([bh, s.seq, s.seq], Precision.FP32)
-        self.dS = empty([bh, s.seq, s.seq])
+        # Attention: the fused kernels keep each layer's row log-sum-exp for the backward; the
+        # materialised form needs [BH, S, S] workspaces, shared by all layers.
+        self.fused = (s.head_dim == 64) if fused_attention is None else bool(fused_attention)
+        if self.fused:
+            self.lse = [empty([bh, s.seq], Precision.FP32) for _ in range(L)]
+        else:
+            self.Sc = empty([bh, s.seq, s.seq], Precision.FP32)
+            self.Pw = empty([bh, s.seq, s.seq])
+            self.dP = empty([bh, s.seq, s.seq], Precision.FP32)
+            self.dS = empty([bh, s.seq, s.seq])
         self.launches: List[_Launch] = []
         self._record = True
 
@@ -174,11 +180,17 @@ class GemmStep:
         self._gemm("qkv", self.X[l], self.Wqkv[l], self.QKV[l], False, True, T, 3 * H, H)
         qkv, o = self._layouts()
         base = self.QKV[l].ptr
-        st = self.lib.it_attention_forward(
-            self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.seq, s.head_dim,
-            1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o),
-            C.c_void_p(base), C.c_void_p(base + H * eb), C.c_void_p(base + 2 * H * eb),
-            C.c_void_p(self.Sc.ptr), C.c_void_p(self.Pw.ptr), C.c_void_p(self.O[l].ptr))
+        q, k, v = (C.c_void_p(base + i * H * eb) for i in range(3))
+        if self.fused:
+            st = self.lib.it_flash_attention_forward(
+                self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.seq, s.head_dim,
+                1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o), q, k, v,
+                C.c_void_p(self.O[l].ptr), C.c_void_p(self.lse[l].ptr))
+        else:
+            st = self.lib.it_attention_forward(
+                self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.seq, s.head_dim,
+                1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o), q, k, v,
+                C.c_void_p(self.Sc.ptr), C.c_void_p(self.Pw.ptr), C.c_void_p(self.O[l].ptr))
         check(st, "attention")
         if self._record:
             attn = 2.0 * s.batch * s.heads * s.seq * s.seq * s.head_dim
@@ -206,13 +218,20 @@ class GemmStep:
         eb = P.byte_size()
         base = self.QKV[l].ptr
         dbase = self.dQKV.ptr
-        st = self.lib.it_attention_backward(
-            self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.head_dim,
-            1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o),
-            C.c_void_p(self.dO.ptr), C.c_void_p(base), C.c_void_p(base + H * eb),
-            C.c_void_p(base + 2 * H * eb), C.c_void_p(self.Sc.ptr), C.c_void_p(self.Pw.ptr),
-            C.c_void_p(self.dP.ptr), C.c_void_p(self.dS.ptr), C.c_void_p(dbase),
-            C.c_void_p(dbase + H * 4), C.c_void_p(dbase + 2 * H * 4))
+        q, k, v = (C.c_void_p(base + i * H * eb) for i in range(3))
+        dq, dk, dv = (C.c_void_p(dbase + i * H * 4) for i in range(3))
+        if self.fused:
+            st = self.lib.it_flash_attention_backward(
+                self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.head_dim,
+                1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o),
+                C.c_void_p(self.dO.ptr), q, k, v, C.c_void_p(self.O[l].ptr),
+                C.c_void_p(self.lse[l].ptr), dq, dk, dv)
+        else:
+            st = self.lib.it_attention_backward(
+                self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.head_dim,
+                1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o),
+                C.c_void_p(self.dO.ptr), q, k, v, C.c_void_p(self.Sc.ptr), C.c_void_p(self.Pw.ptr),
+                C.c_void_p(self.dP.ptr), C.c_void_p(self.dS.ptr), dq, dk, dv)
         check(st, "attention_backward")
         if self._record:
             attn = 2.0 * s.batch * s.heads * s.seq * s.seq * s.head_dim

@@ -196,6 +196,32 @@ static void gpu_tests() {
                 CHECK(std::fabs(o[r * d + c] - mean) < 1e-5f);
             }
     });
+    run("flash_attention_causal_rows", [] {  // same closed form at head_dim 64, ragged seq 70
+        const size_t b = 1, s = 70, h = 2, d = 64;
+        std::vector<float> q(b * s * h * d, 0.0f), v(b * s * h * d);
+        for (size_t i = 0; i < v.size(); ++i) v[i] = (float)((i * 37) % 101) * 0.01f - 0.5f;
+        auto o = flash_attention(Tensor::from_f32_slice(q, {b, s, h, d}), Tensor::from_f32_slice(v, {b, s, h, d}),
+                                 Tensor::from_f32_slice(v, {b, s, h, d}), true).as_f32_slice();
+        for (size_t r = 0; r < s; ++r)
+            for (size_t hh = 0; hh < h; ++hh)
+                for (size_t c = 0; c < d; ++c) {
+                    double mean = 0;
+                    for (size_t j = 0; j <= r; ++j) mean += v[(j * h + hh) * d + c];
+                    mean /= (double)(r + 1);
+                    CHECK(std::fabs(o[(r * h + hh) * d + c] - mean) < 1e-5);
+                }
+        Tensor small = Tensor::zeros({1, 4, 1, 32}, Precision::FP32);
+        expect_throw<InvalidValue>([&] { flash_attention(small, small, small, false); });
+    });
+    run("flash_attention_backward_zero_grad", [] {  // dO = 0 gives dQ = dK = dV = 0 exactly
+        const size_t b = 1, h = 2, n = 100, d = 64;
+        std::vector<float> x(b * h * n * d);
+        for (size_t i = 0; i < x.size(); ++i) x[i] = (float)((i * 13) % 29) * 0.05f - 0.7f;
+        Tensor t = Tensor::from_f32_slice(x, {b, h, n, d});
+        auto g = flash_attention_backward(Tensor::zeros({b, h, n, d}, Precision::FP32), t, t, t);
+        for (const Tensor *r : {&g.dq, &g.dk, &g.dv})
+            for (float f : r->as_f32_slice()) CHECK(f == 0.0f);
+    });
     run("typed_errors", [] {  // src/ops/mps_gemm.rs:45-108
         Tensor f = Tensor::zeros({2, 3}, Precision::FP32), g = Tensor::zeros({4, 5}, Precision::FP32);
         CHECK(expect_throw<InnerDimensionMismatch>([&] { matmul(f, g); }).find("A=[2, 3], B=[4, 5]") != std::string::npos);
