@@ -2,13 +2,19 @@
 
 Workload: every contraction of one TINY training step, forward and backward,
 FP32 (4 layers, hidden 256, 4 heads x 64, SwiGLU FFN 688, untied vocab 16384, batch 16 x seq 256):
-115 dense-equivalent GEMMs = 195.82 GFLOP, issued by irontensor_amd.step.GemmStep as 75 GEMM
-launches (fused QKV and gate|up) plus the attention softmax / softmax-backward, captured once into
-a HIP graph and replayed. A "step" is one replay; inputs are resident in HBM before timing starts.
+115 dense-equivalent GEMMs = 195.82 GFLOP, issued by irontensor_amd.step.GemmStep as 51 GEMM
+launches (fused QKV and gate|up) plus the fused attention kernels (forward, and dK/dV + dQ
+backward, per layer), captured once into a HIP graph and replayed. A "step" is one replay; inputs
+are resident in HBM before timing starts.
 
-Prints ONE JSON line (rank 0 = this process). Extra figures (config 1, the BF16 square and decode
-GEMMs) go under "extra". The CPU baseline is the oracle's reference loop on host cores over a
-bounded sample of the same workload.
+Prints ONE JSON line (rank 0 = this process). Extra figures (configs 1, 3, 4 and 5: the FP32 QKV
+projection, BF16 attention, the medium BF16 step, the BF16 square and decode GEMMs) go under
+"extra". The CPU baseline is the oracle's reference loop on host cores over a bounded sample of the
+same workload.
+
+`--kernel-only` runs just a calibration copy (f32 -> bf16 conversion of a known size) and the
+dominant TINY kernel, for `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` runs that give the
+`roofline.traffic` figure (read back from profiles/tiny_dominant_kernel_traffic.md).
 """
 from __future__ import annotations
 
@@ -84,38 +90,179 @@ def time_gemm(it, timer, a, b, out, trans_a, trans_b, iters, warm=3) -> float:
     return timer.stop_ms() / iters
 
 
-def extras(it, timer) -> dict:
-    """Config 1 (FP32 QKV projection) and the BF16 square / decode GEMMs, timed with hipEvents."""
+def _bf16(it, x):
+    return it.Tensor.from_f32_as_bf16(x, list(x.shape))
+
+
+def extra_config1(it, timer) -> dict:
+    """Config 1: the FP32 QKV projection Y = X.W^T, X [4096,256], W [768,256]."""
     from irontensor_amd import synth
-    P = it.Precision
-    out = {}
     x = it.Tensor.from_f32_slice(synth.normal(1, (4096, 256)), [4096, 256])
     w = it.Tensor.from_f32_slice(synth.normal(2, (768, 256), std=0.02), [768, 256])
     y = it.Tensor.empty([4096, 768])
     ms = time_gemm(it, timer, x, w, y, False, True, 50)
     tf = 2 * 4096 * 768 * 256 / (ms * 1e-3) / 1e12
-    out["config1_fp32_qkv_4096x768x256_NT"] = {"ms": round(ms, 5), "tflops": round(tf, 2),
-                                               "frac_fp32_peak": round(tf / PEAK_TFLOPS["f32"], 4)}
-    for n in (4096, 8192):
-        a = it.Tensor.from_f32_as_bf16(synth.normal(3, (n, n)), [n, n])
-        b = it.Tensor.from_f32_as_bf16(synth.normal(4, (n, n)), [n, n])
+    return {"config1_fp32_qkv_4096x768x256_NT": {"ms": round(ms, 5), "tflops": round(tf, 2),
+                                                 "frac_fp32_peak": round(tf / PEAK_TFLOPS["f32"], 4)}}
+
+
+def extra_attention(it, timer) -> dict:
+    """Config 3: BF16 attention, Q, K, V, dO [16,8,1024,64], causal, scale 1/8. The fused kernels
+    (forward; backward from the saved O and row log-sum-exp) next to the materialised five-GEMM
+    form. FLOPs are dense-equivalent (2 GEMMs forward, 5 backward, 2*BH*S*S*D each); the causal
+    useful fraction is (S+1)/(2S)."""
+    from irontensor_amd import synth
+    b, h, s, d = 16, 8, 1024, 64
+    q, k, v, do = (_bf16(it, synth.pooled_normal(30 + i, (b, h, s, d))) for i in range(4))
+    ctx = it.Context.global_()
+
+    def run(fn, iters):
+        fn()
+        ctx.sync()
+        timer.start()
+        for _ in range(iters):
+            fn()
+        return timer.stop_ms() / iters
+
+    o, lse = it.flash_attention_forward_bhsd(q, k, v, causal=True, scale=0.125)
+    f_ms = run(lambda: it.flash_attention_forward_bhsd(q, k, v, causal=True, scale=0.125), 10)
+    b_ms = run(lambda: it.flash_attention_backward(do, q, k, v, causal=True, scale=0.125, o=o, lse=lse), 5)
+    mf_ms = run(lambda: it.attention_forward_bhsd(q, k, v, causal=True, scale=0.125), 3)
+    mb_ms = run(lambda: it.attention_backward_recompute(do, q, k, v, causal=True, scale=0.125), 3)
+    unit = 2.0 * b * h * s * s * d
+    useful = (s + 1) / (2 * s)
+    res = {}
+    for name, ms, n in (("fused_forward", f_ms, 2), ("fused_backward", b_ms, 5),
+                        ("materialised_forward", mf_ms, 2), ("materialised_backward_recompute", mb_ms, 7)):
+        tf = n * unit / (ms * 1e-3) / 1e12
+        res[name] = {"ms": round(ms, 4), "tflops_dense_equiv": round(tf, 1),
+                     "tflops_useful": round(tf * useful, 1),
+                     "frac_bf16_peak_useful": round(tf * useful / PEAK_TFLOPS["bf16"], 4)}
+    res["useful_fraction"] = round(useful, 5)
+    return {"config3_bf16_attention_16x8x1024x64_causal": res}
+
+
+def extra_med_step(it, timer, steps=5, warmup=2) -> dict:
+    """Config 4: the medium BF16 step (12 layers, hidden 1024, 16 x 64 heads, SwiGLU FFN 2816 with
+    the fused bias + SwiGLU epilogue, vocab 32768, batch 8 x seq 1024): every contraction forward
+    and backward, graph-replayed like the TINY step. Inputs from synth.pooled_normal."""
+    from irontensor_amd.step import MEDIUM, GemmStep
+    ctx = it.Context.global_()
+    step = GemmStep(MEDIUM, it.Precision.BF16, ctx, pooled_data=True, ffn_bias=True)
+    try:
+        step.enqueue()
+        ctx.sync()
+        flops = step.flops()
+        step.capture()
+        for _ in range(warmup):
+            step.replay()
+        ctx.sync()
+        timer.start()
+        for _ in range(steps):
+            step.replay()
+        ms = timer.stop_ms() / steps
+        ctx.lib.it_profiler_reset(ctx.handle)
+        ctx.lib.it_profiler_enable(ctx.handle, 1)
+        step.enqueue()
+        stats = profiler_stats(ctx)
+        ctx.lib.it_profiler_enable(ctx.handle, 0)
+    finally:
+        step.close()
+    top = sorted(stats.items(), key=lambda kv: -kv[1]["total_ms"])[:6]
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"config4_bf16_medium_step": {
+        "ms_per_step": round(ms, 3), "gflop_per_step": round(flops / 1e9, 1), "tflops": round(tf, 1),
+        "frac_bf16_peak": round(tf / PEAK_TFLOPS["bf16"], 4), "steps": steps,
+        "top_kernels": [{"key": k, "ms_per_step": round(v["total_ms"], 3), "calls": v["calls"]} for k, v in top]}}
+
+
+def extra_sweep(it, timer) -> dict:
+    """Config 5: BF16 square GEMMs n^3, n in {1024 .. 16384}, NN/NT/TN, BF16 out; and the decode
+    shapes M in {1, 4, 16}, K 4096, N 11008 (HBM-bound: weight bytes / time against 8 TB/s).
+    Operands from synth.pooled_normal (N(0,1))."""
+    from irontensor_amd import synth
+    P = it.Precision
+    out = {}
+    for n, iters in ((1024, 50), (2048, 20), (4096, 10), (8192, 4), (16384, 2)):
+        a = _bf16(it, synth.pooled_normal(3, (n, n)))
+        b = _bf16(it, synth.pooled_normal(4, (n, n)))
         c = it.Tensor.empty([n, n], P.BF16)
         for lay, (ta, tb) in (("NN", (False, False)), ("NT", (False, True)), ("TN", (True, False))):
-            ms = time_gemm(it, timer, a, b, c, ta, tb, 10 if n == 4096 else 4)
+            ms = time_gemm(it, timer, a, b, c, ta, tb, iters, warm=2)
             tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
             out[f"bf16_square_{n}_{lay}"] = {"ms": round(ms, 4), "tflops": round(tf, 1),
                                              "frac_bf16_peak": round(tf / PEAK_TFLOPS["bf16"], 4)}
         del a, b, c
     k, n = 4096, 11008
-    wt = it.Tensor.from_f32_as_bf16(synth.normal(5, (n, k)), [n, k])
+    w_nk = _bf16(it, synth.pooled_normal(5, (n, k)))
+    w_kn = _bf16(it, synth.pooled_normal(7, (k, n)))
     for m in (1, 4, 16):
-        xa = it.Tensor.from_f32_as_bf16(synth.normal(6, (m, k)), [m, k])
+        xa = _bf16(it, synth.pooled_normal(6, (m, k)))
+        xt = _bf16(it, synth.pooled_normal(8, (k, m)))
         yo = it.Tensor.empty([m, n], P.BF16)
-        ms = time_gemm(it, timer, xa, wt, yo, False, True, 20)
-        gbs = (n * k * 2 + m * k * 2 + m * n * 2) / (ms * 1e-3) / 1e9
-        out[f"bf16_decode_m{m}_k4096_n11008_NT"] = {"ms": round(ms, 5), "GBps": round(gbs, 1),
-                                                    "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+        for lay, (A, B, ta, tb) in (("NT", (xa, w_nk, False, True)), ("NN", (xa, w_kn, False, False)),
+                                    ("TN", (xt, w_kn, True, False))):
+            ms = time_gemm(it, timer, A, B, yo, ta, tb, 20)
+            gbs = (n * k * 2 + m * k * 2 + m * n * 2) / (ms * 1e-3) / 1e9
+            out[f"bf16_decode_m{m}_k4096_n11008_{lay}"] = {"ms": round(ms, 5), "GBps": round(gbs, 1),
+                                                           "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
     return out
+
+
+def extras(it, timer) -> dict:
+    out = {}
+    for fn in (extra_config1, extra_attention, extra_sweep, extra_med_step):
+        log(f"[bench] extra: {fn.__name__}")
+        out.update(fn(it, timer))
+    return out
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "tiny_dominant_kernel_traffic.md"
+
+
+def committed_traffic(key: str):
+    """HBM bytes per launch of `key` from the committed rocprofv3 --pmc summary, or None. The file
+    holds a line 'traffic_bytes_per_launch <key> = <bytes>'."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        m = re.match(r"\s*traffic_bytes_per_launch (.+) = (\d+)\s*$", line)
+        if m and m.group(1) == key:
+            return int(m.group(2))
+    return None
+
+
+def kernel_only(it, ctx, step, iters: int) -> int:
+    """Calibration copy, then each of the step's largest GEMMs (the LM-head forward, dX and dW, any
+    of which can be the dominant kernel) `iters` times in a row, for rocprofv3 --pmc passes. Prints
+    the order of the groups with their profiler keys, to map dispatches back to keys."""
+    from irontensor_amd import synth
+    n = 1 << 26  # 256 MiB read, 128 MiB written
+    src = it.Tensor.from_f32_slice(synth.pooled_normal(9, (n,)), [n])
+    dst = it.Tensor.empty([n], it.Precision.BF16)
+    ctx.sync()
+    for _ in range(5):
+        if ctx.lib.it_f32_to_bf16(ctx.handle, C.c_void_p(src.ptr), C.c_void_p(dst.ptr), n) != 0:
+            raise RuntimeError("conversion failed")
+    ctx.sync()
+    biggest = max(2.0 * M * N * K for (_, _, M, N, K) in step._calls)
+    groups = []
+    for (ta, tb, M, N, K) in list(step._calls):
+        if 2.0 * M * N * K < 0.9 * biggest:
+            continue
+        ctx.lib.it_profiler_reset(ctx.handle)
+        ctx.lib.it_profiler_enable(ctx.handle, 1)
+        for _ in range(iters):
+            name = step.reissue(ta, tb, M, N, K)
+        stats = profiler_stats(ctx)
+        ctx.lib.it_profiler_enable(ctx.handle, 0)
+        (key, st), = stats.items()
+        groups.append({"key": key, "step_gemm": name, "launches": iters,
+                       "avg_us_events": round(st["total_ms"] / st["calls"] * 1e3, 2)})
+    print(json.dumps({"calibration": {"kernel": "f32_to_bf16_kernel", "elements": n, "read_bytes": 4 * n,
+                                      "write_bytes": 2 * n, "launches": 5},
+                      "groups": groups}), flush=True)
+    return 0
 
 
 def cpu_baseline(step) -> dict:
@@ -150,7 +297,23 @@ def cpu_baseline(step) -> dict:
     oracle.attention_bwd_bhsd(do, q, k, v, 0.125, True, threads=thr)
     flops += 7 * 2.0 * bh * s.seq * s.seq * s.head_dim
     dt = time.perf_counter() - t0
+    # config 1 on one thread, for the per-core figure
+    x1, w1 = a((4096, 256), 30), w((768, 256), 31)
+    t1 = time.perf_counter()
+    oracle.gemm_f32(x1, w1, False, True, threads=1)
+    dt1 = time.perf_counter() - t1
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": thr,
+            "host_cpus": os.cpu_count(), "cpu_model": model,
+            "config1_one_thread_ms": round(dt1 * 1e3, 1),
+            "config1_one_thread_gflops": round(2 * 4096 * 768 * 256 / dt1 / 1e9, 3),
             "kind": "port",
             "sample": (f"layer 0 forward+backward contractions (12 linear GEMMs, 7 attention GEMMs) "
                        f"+ LM-head forward GEMM of the TINY step, {flops / 1e9:.1f} GFLOP in "
@@ -166,6 +329,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the extra GEMM figures")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="run only a calibration copy and the dominant kernel (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -189,6 +354,8 @@ def main() -> int:
     ctx.sync()
     total_flops = step.flops()
     log(f"[bench] TINY step: {len(step.launches)} contractions, {total_flops / 1e9:.2f} GFLOP")
+    if args.kernel_only:
+        return kernel_only(it, ctx, step, args.steps)
     step.capture()
     for _ in range(args.warmup):
         step.replay()
@@ -248,7 +415,7 @@ def main() -> int:
             "peak": PEAK_TFLOPS["f32"],
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS["f32"], 4),
-            "traffic": None,
+            "traffic": committed_traffic(dom_key),
             "kernel": dom_key,
             "avg_us": round(avg_ms * 1e3, 2),
             "flops_per_launch": dom_flops,

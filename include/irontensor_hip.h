@@ -97,7 +97,7 @@ it_status it_event_destroy(it_event *ev);
 
 typedef struct it_epilogue {
     uint32_t flags;
-    const float *bias;      /* IT_EPI_BIAS: [N] f32 */
+    const float *bias;      /* IT_EPI_BIAS: [N] f32; with IT_EPI_SWIGLU [2N]: gate bias, then up bias */
     const void *B2;         /* IT_EPI_SWIGLU: up-projection weight, same dtype/layout/ldb/strideB as B */
     void *gate_out;         /* IT_EPI_SWIGLU (optional): pre-activation gate, out dtype, ldc/strideC */
     void *up_out;           /* IT_EPI_SWIGLU (optional): pre-activation up, out dtype, ldc/strideC */

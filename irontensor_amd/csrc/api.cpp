@@ -74,8 +74,8 @@ it_status it_gemm_check(it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_
                 return fail(IT_ERR_NULL, "matmul: SwiGLU epilogue without B2");
             if (transA != IT_OP_N || transB != IT_OP_T)
                 return fail(IT_ERR_INVALID, "matmul: SwiGLU epilogue needs transA=N, transB=T (Y = X.W^T)");
-            if (epi->flags & (IT_EPI_BIAS | IT_EPI_CAUSAL))
-                return fail(IT_ERR_INVALID, "matmul: SwiGLU epilogue cannot be combined with bias or causal");
+            if (epi->flags & IT_EPI_CAUSAL)
+                return fail(IT_ERR_INVALID, "matmul: SwiGLU epilogue cannot be combined with causal");
         }
         if ((epi->flags & (IT_EPI_SWIGLU | IT_EPI_CAUSAL)) && beta != 0.f)
             return fail(IT_ERR_INVALID, "matmul: beta != 0 cannot be combined with SwiGLU or causal");

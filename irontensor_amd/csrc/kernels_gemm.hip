@@ -516,7 +516,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
             __syncthreads();
         }
     } else {
-        // SwiGLU epilogue per element: gate, up and silu(gate) * up.
+        // SwiGLU epilogue per element: gate, up (each with its bias) and silu(gate) * up.
         const int64_t rbase = m0 + wm * WTM + (lane >> 4) * 4;
         const int64_t cbase = n0 + wn * WTN + (lane & 15);
 #pragma unroll
@@ -528,7 +528,11 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
                     const int64_t row = rbase + i * 16 + r, col = cbase + j * 16;
                     if (row >= p.M || col >= p.N) continue;
                     const int64_t idx = coff + row * p.ldc + col;
-                    const float g = p.alpha * acc[i][j][r], u = p.alpha * acc2[i][j][r];
+                    float g = p.alpha * acc[i][j][r], u = p.alpha * acc2[i][j][r];
+                    if (p.has_bias) {  // [gate bias | up bias], N each
+                        g += p.bias[col];
+                        u += p.bias[p.N + col];
+                    }
                     if (p.G) store_out(p.G, idx, g, p.out_bf16);
                     if (p.U) store_out(p.U, idx, u, p.out_bf16);
                     store_out(p.C, idx, silu(g) * u, p.out_bf16);

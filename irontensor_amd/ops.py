@@ -302,12 +302,14 @@ class Linear:
 
 
 def swiglu_up(x: Tensor, w_gate: Tensor, w_up: Tensor, out_precision: Optional[Precision] = None,
-              keep_pre_activations: bool = True) -> Tuple[Tensor, Optional[Tensor], Optional[Tensor]]:
-    """FFN up-projection with the fused SwiGLU epilogue: h = silu(x.Wg^T) * (x.Wu^T).
+              keep_pre_activations: bool = True,
+              bias: Optional[Tensor] = None) -> Tuple[Tensor, Optional[Tensor], Optional[Tensor]]:
+    """FFN up-projection with the fused SwiGLU epilogue: h = silu(x.Wg^T + bg) * (x.Wu^T + bu).
 
     Replaces the two linear_forward calls plus swiglu (src/train/forward.rs:166-172,
-    src/ops/elementwise.rs:351-354, src/shaders/elementwise.metal:100-115). Returns (h, gate, up);
-    gate and up are the pre-activations the backward needs (src/train/cache.rs:23-27).
+    src/ops/elementwise.rs:351-354, src/shaders/elementwise.metal:100-115), and with `bias` the two
+    Linear biases (src/nn/linear.rs:8-18): an FP32 [2F] tensor, gate bias then up bias. Returns
+    (h, gate, up); gate and up are the pre-activations the backward needs (src/train/cache.rs:23-27).
     """
     prec = out_precision if out_precision is not None else (
         _P.BF16 if x.precision() is _P.BF16 else _P.FP32)
@@ -315,10 +317,12 @@ def swiglu_up(x: Tensor, w_gate: Tensor, w_up: Tensor, out_precision: Optional[P
     f = w_gate.shape()[0]
     if w_up.shape() != w_gate.shape():
         raise ShapeMismatch("swiglu", str(w_gate.shape()), str(w_up.shape()))
+    if bias is not None and (bias.numel() != 2 * f or bias.precision() is not _P.FP32):
+        raise ShapeMismatch("swiglu", f"FP32 bias of {2 * f} elements", str(bias.shape()))
     g = Tensor.empty([rows, f], prec, x.ctx) if keep_pre_activations else None
     u = Tensor.empty([rows, f], prec, x.ctx) if keep_pre_activations else None
     h = gemm(x, w_gate, trans_b=True, b2=w_up, gate_out=g, up_out=u, out_precision=prec,
-             op="swiglu")
+             bias=bias, op="swiglu")
     return h, g, u
 
 

@@ -71,7 +71,8 @@ class GemmStep:
     """Owns every buffer of the step and enqueues its contractions (eagerly or into a HIP graph)."""
 
     def __init__(self, shape: ModelShape, precision: Precision = Precision.FP32,
-                 ctx: Optional[Context] = None, seed: int = 1234, fused_attention: Optional[bool] = None):
+                 ctx: Optional[Context] = None, seed: int = 1234, fused_attention: Optional[bool] = None,
+                 pooled_data: bool = False, ffn_bias: bool = False):
         if shape.heads * shape.head_dim != shape.hidden:
             raise ValueError("heads * head_dim must equal hidden")
         self.s = shape
@@ -83,6 +84,7 @@ class GemmStep:
         T, H, F, V, L = s.tokens, s.hidden, s.ffn, s.vocab, s.layers
         bh = s.batch * s.heads
         self._seed = seed
+        self._pooled = pooled_data  # timing-only inputs from synth.pooled_normal (fast at MED sizes)
 
         def w(shape_, std=0.02):
             return self._tensor(shape_, std)
@@ -98,6 +100,9 @@ class GemmStep:
         self.Wo = [w([H, H]) for _ in range(L)]
         self.Wgu = [w([2 * F, H]) for _ in range(L)]   # gate rows then up rows
         self.Wd = [w([H, F]) for _ in range(L)]
+        # Optional gate|up biases (FP32 [2F]) applied in the fused SwiGLU epilogue
+        self.bgu = [Tensor.from_f32_slice(synth.normal(self._seed + 7 + l, (2 * F,), std=0.02), [2 * F],
+                                          self.ctx) for l in range(L)] if ffn_bias else None
         self.E = w([V, H])                             # untied LM head
         # Forward caches
         self.X = [act([T, H]) for _ in range(L)]       # attention-norm output
@@ -140,12 +145,14 @@ class GemmStep:
             self.dP = empty([bh, s.seq, s.seq], Precision.FP32)
             self.dS = empty([bh, s.seq, s.seq])
         self.launches: List[_Launch] = []
+        self._calls: dict = {}
         self._record = True
 
     # ---------------------------------------------------------------- helpers
     def _tensor(self, shape_, std) -> Tensor:
         self._seed += 1
-        data = synth.normal(self._seed, shape_, std=std)
+        gen = synth.pooled_normal if self._pooled else synth.normal
+        data = gen(self._seed, shape_, std=std)
         if self.prec is Precision.BF16:
             return Tensor.from_f32_as_bf16(data, shape_, self.ctx)
         return Tensor.from_f32_slice(data, shape_, self.ctx)
@@ -165,6 +172,9 @@ class GemmStep:
         if self._record:
             mult = 2 if (epi is not None and epi.flags & _lib.IT_EPI_SWIGLU) else 1
             self.launches.append(_Launch(name, 2.0 * M * N * K * mult))
+            key = (bool(ta), bool(tb), M, N, K)
+            if key not in self._calls:
+                self._calls[key] = (name, A, B, Cout, ta, tb, M, N, K, alpha, epi, a_off, lda)
 
     def _layouts(self):
         s = self.s
@@ -198,6 +208,9 @@ class GemmStep:
         self._gemm("wo", self.Oin[l], self.Wo[l], self.Y[l], False, True, T, H, H)
         epi = _lib.Epilogue(flags=_lib.IT_EPI_SWIGLU, B2=self.Wgu[l].ptr + F * H * eb,
                             gate_out=self.G[l].ptr, up_out=self.U[l].ptr)
+        if self.bgu is not None:
+            epi.flags |= _lib.IT_EPI_BIAS
+            epi.bias = self.bgu[l].ptr
         self._gemm("gate_up_swiglu", self.X2[l], self.Wgu[l], self.Hh[l], False, True, T, F, H, epi=epi)
         self._gemm("down", self.Hh[l], self.Wd[l], self.Z[l], False, True, T, H, F)
 
@@ -260,6 +273,17 @@ class GemmStep:
         for l in reversed(range(s.layers)):
             self.backward_layer(l)
         self._record = False
+
+    def reissue(self, ta: bool, tb: bool, M: int, N: int, K: int) -> str:
+        """Launches again the first GEMM of the step with this layout and shape (for profiling one
+        kernel in isolation); returns its name. enqueue() must have run once."""
+        name, A, B, Cout, ta_, tb_, M_, N_, K_, alpha, epi, a_off, lda = self._calls[(ta, tb, M, N, K)]
+        rec, self._record = self._record, False
+        try:
+            self._gemm(name, A, B, Cout, ta_, tb_, M_, N_, K_, alpha=alpha, epi=epi, a_off=a_off, lda=lda)
+        finally:
+            self._record = rec
+        return name
 
     def flops(self) -> float:
         return float(sum(x.flops for x in self.launches))

@@ -209,6 +209,28 @@ def test_f32_swiglu_dual_epilogue(it, oracle, rows, h, f):
     assert normwise_rel(hh.numpy(), oracle.swiglu(g_ref, u_ref)) <= FP32_TOL
 
 
+@pytest.mark.parametrize("prec", ["f32", "bf16"])
+def test_swiglu_dual_epilogue_with_bias(it, oracle, prec):
+    """The MED config's fused bias + SwiGLU: gate = x.Wg^T + bg, up = x.Wu^T + bu, h = silu(gate)*up."""
+    rows, h, f = 200, 128, 344
+    x = synth.normal(18, (rows, h))
+    wg = synth.normal(19, (f, h), std=0.05)
+    wu = synth.normal(20, (f, h), std=0.05)
+    b = synth.normal(21, (2 * f,), std=0.1)
+    mk = it.Tensor.from_f32_slice if prec == "f32" else it.Tensor.from_f32_as_bf16
+    hh, g, u = it.swiglu_up(mk(x, x.shape), mk(wg, wg.shape), mk(wu, wu.shape),
+                            out_precision=it.Precision.FP32, bias=it.Tensor.from_f32_slice(b, [2 * f]))
+    g_ref = oracle.add_bias(oracle.gemm_f32(x, wg, trans_b=True), b[:f])
+    u_ref = oracle.add_bias(oracle.gemm_f32(x, wu, trans_b=True), b[f:])
+    h_ref = oracle.swiglu(g_ref, u_ref)
+    if prec == "f32":
+        for got, ref in ((g, g_ref), (u, u_ref), (hh, h_ref)):
+            assert normwise_rel(got.numpy(), ref) <= FP32_TOL
+    else:
+        for got, ref in ((g, g_ref), (u, u_ref), (hh, h_ref)):
+            assert frob_rel(got.numpy(), ref) <= BF16_FROB_TOL
+
+
 # ------------------------------------------------------------------ BF16
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
