@@ -50,14 +50,8 @@ def parse_key_flops(key: str) -> float:
 
 
 def profiler_stats(ctx) -> dict:
-    lib = ctx.lib
-    need = C.c_size_t(0)
-    lib.it_profiler_report(ctx.handle, None, 0, C.byref(need))
-    buf = C.create_string_buffer(need.value + 16)
-    st = lib.it_profiler_report(ctx.handle, buf, need.value + 16, C.byref(need))
-    if st != 0:
-        raise RuntimeError("profiler report failed")
-    return json.loads(buf.value.decode())
+    from irontensor_amd import profiler
+    return profiler.stats(ctx)
 
 
 class Timer:

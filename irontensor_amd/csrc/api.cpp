@@ -497,6 +497,10 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
     if (!it::flash_supported(f, eb, true))
         return fail(IT_ERR_DIMS, "flash_attention_backward: unsupported dimensions, operands must be 16-byte "
                                  "aligned with strides that are multiples of 16 bytes");
+    if (O && ((uintptr_t)O % 16 != 0 || g.o_lay.batch_stride % 4 || g.o_lay.head_stride % 4 ||
+              g.o_lay.row_stride % 4))
+        return fail(IT_ERR_DIMS, "flash_attention_backward: unsupported dimensions, O must be 16-byte aligned "
+                                 "with strides that are multiples of 4");
     const size_t rows = (size_t)bh * (size_t)seq;
     // Workspace: when the forward is recomputed, O [rows, 64] and lse [rows]; then dlt [rows].
     const size_t bytes = rows * 4 * (O ? 1 : 64 + 2);

@@ -150,10 +150,8 @@ __device__ __forceinline__ u32x4 frag_acc(const f32x4 *blk, int c) {
         return __builtin_bit_cast(u32x4, blk[c]);
     } else {
         const f32x4 a = blk[2 * c], b = blk[2 * c + 1];
-        return u32x4{(uint32_t)f32_to_bf16_rne(a[0]) | ((uint32_t)f32_to_bf16_rne(a[1]) << 16),
-                     (uint32_t)f32_to_bf16_rne(a[2]) | ((uint32_t)f32_to_bf16_rne(a[3]) << 16),
-                     (uint32_t)f32_to_bf16_rne(b[0]) | ((uint32_t)f32_to_bf16_rne(b[1]) << 16),
-                     (uint32_t)f32_to_bf16_rne(b[2]) | ((uint32_t)f32_to_bf16_rne(b[3]) << 16)};
+        return u32x4{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
+                     pack_bf16x2(b[2], b[3])};
     }
 }
 
@@ -166,7 +164,11 @@ __device__ __forceinline__ float xsum(float v) {
     return v + __shfl_xor(v, 32, 64);
 }
 
-constexpr int NCHUNK_F32 = HD / 16;
+// 2^x on the hardware unit (v_exp_f32, 1 ulp). Scores are carried in the log2 domain: they are
+// multiplied by scale * log2(e) once, so every probability is one subtraction and one exp2.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
 
 // ------------------------------------------------------------------ forward
 
@@ -178,7 +180,9 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
-    const int qb = blockIdx.x;
+    // Causal blocks are enumerated heaviest first (the last query block sees every key block), so
+    // the long blocks start early and the short ones fill the tail.
+    const int qb = p.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
     const int64_t bh = blockIdx.y;
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
@@ -186,6 +190,7 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
     const T *K = (const T *)p.K + hk.base(bh);
     const T *V = (const T *)p.V + hk.base(bh);
     float *O = (float *)p.O + ho.base(bh);
+    const float c2 = p.scale * LOG2E;
     const int q = qb * TR + wave * 16 + ql;  // this lane's query
     const bool qok = q < p.sq;
 
@@ -227,26 +232,37 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
 #pragma unroll
             for (int c = 0; c < NC; ++c) mma16<T>(s[mb], frag_c<T>(kt, mb * 16 + ql, c, g), qf[c]);
         }
+        // Scores to the log2 domain; keys past the diagonal (causal) or past seq_kv are -inf. Only
+        // the last key block of a row block can hold such keys.
         float mx = -INFINITY;
+        if (kb == nkb - 1 && (p.causal || p.skv % TR != 0)) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+            for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = kb * TR + mb * 16 + g * 4 + r;
-                float v = s[mb][r] * p.scale;
-                if (key >= p.skv || (p.causal && key > q)) v = -INFINITY;
-                s[mb][r] = v;
-                mx = fmaxf(mx, v);
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const int key = kb * TR + mb * 16 + g * 4 + r;
+                    const bool dead = key >= p.skv || (p.causal && key > q);
+                    s[mb][r] = dead ? -INFINITY : s[mb][r] * c2;
+                    mx = fmaxf(mx, s[mb][r]);
+                }
+        } else {
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    s[mb][r] *= c2;
+                    mx = fmaxf(mx, s[mb][r]);
+                }
+        }
         const float mnew = fmaxf(m, xmax(mx));
         const float msafe = mnew == -INFINITY ? 0.f : mnew;
-        const float alpha = expf(m - msafe);
+        const float alpha = exp2_fast(m - msafe);
         float ls = 0.f;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = expf(s[mb][r] - msafe);
+                const float e = exp2_fast(s[mb][r] - msafe);
                 s[mb][r] = e;
                 ls += e;
             }
@@ -269,29 +285,38 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
         for (int d = 0; d < 4; ++d) *(f32x4 *)(O + (int64_t)q * p.o_rs + d * 16 + g * 4) = o[d] * inv;
-        if (g == 0 && p.lse) p.lse[bh * p.sq + q] = m + logf(l);
+        if (g == 0 && p.lse) p.lse[bh * p.sq + q] = (m + __log2f(l)) * LN2;  // natural-log LSE
     }
 }
 
 
 // ------------------------------------------------------------------ backward
 
-// dlt[bh][q] = sum_d dO[q][d] * O[q][d] (= rowsum(dP * P)); one thread per row.
+// dlt[bh][q] = sum_d dO[q][d] * O[q][d] (= rowsum(dP * P)). 16 lanes per row, 4 columns each,
+// so a row's dO and O are read as contiguous 16-lane segments.
 template <typename T>
 __global__ __launch_bounds__(NTH) void flash_dlt(const FlashArgs p) {
-    const int64_t row = (int64_t)blockIdx.x * NTH + threadIdx.x;
-    if (row >= p.bh * p.sq) return;
-    const int64_t bh = row / p.sq, q = row % p.sq;
-    const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
-    const T *dO = (const T *)p.dO + hd.base(bh) + q * p.do_rs;
-    const float *O = p.O + ho.base(bh) + q * p.o_rs;
+    const int64_t row = (int64_t)blockIdx.x * (NTH / 16) + threadIdx.x / 16;
+    const int part = threadIdx.x % 16;
     float acc = 0.f;
-#pragma unroll 8
-    for (int d = 0; d < HD; ++d) {
-        const float g = sizeof(T) == 4 ? ((const float *)dO)[d] : bf16_to_f32(((const uint16_t *)dO)[d]);
-        acc += g * O[d];
+    if (row < p.bh * p.sq) {
+        const int64_t bh = row / p.sq, q = row % p.sq;
+        const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
+        const T *dO = (const T *)p.dO + hd.base(bh) + q * p.do_rs + part * 4;
+        const f32x4 o = *(const f32x4 *)(p.O + ho.base(bh) + q * p.o_rs + part * 4);
+        f32x4 g;
+        if constexpr (sizeof(T) == 4) {
+            g = *(const f32x4 *)dO;
+        } else {
+            const u32x2 h = *(const u32x2 *)dO;
+            g = f32x4{__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u),
+                      __uint_as_float(h[1] << 16), __uint_as_float(h[1] & 0xffff0000u)};
+        }
+        acc = g[0] * o[0] + g[1] * o[1] + g[2] * o[2] + g[3] * o[3];
     }
-    p.dlt[row] = acc;
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 16);
+    if (part == 0 && row < p.bh * p.sq) p.dlt[row] = acc;
 }
 
 // dK, dV for 64 keys per block (16 per wave), looping over the query blocks that see them.
@@ -315,6 +340,7 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
     const float *lse = p.lse + bh * p.sq, *dlt = p.dlt + bh * p.sq;
     const int key = kb * TR + wave * 16 + ql;  // this lane's key (column of S = Q.K^T)
     const bool kok = key < p.skv;
+    const float c2 = p.scale * LOG2E;
 
     u32x4 kf[NC], vf[NC];
 #pragma unroll
@@ -345,7 +371,7 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
         dtr.store(st + 3 * T_, tid);
         if (tid < TR) {
             const int q = qb * TR + tid;
-            ((float *)(st + 4 * T_))[tid] = q < p.sq ? lse[q] : 0.f;
+            ((float *)(st + 4 * T_))[tid] = q < p.sq ? lse[q] * LOG2E : 0.f;
             ((float *)(st + 4 * T_ + TR * 4))[tid] = q < p.sq ? dlt[q] : 0.f;
         }
     };
@@ -372,13 +398,18 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
                 mma16<T>(dp[mb], frag_c<T>(dot, mb * 16 + ql, c, g), vf[c]);
             }
         }
+        // P = exp2(S * scale * log2(e) - LSE2). Rows past seq_q need no mask: their Q and dO rows
+        // load as zeros (and their LSE as 0), so they add nothing. A key past seq_kv only reaches
+        // its own dK, dV row, which is not stored. Only the causal diagonal block masks keys above
+        // the query.
+        const bool diag = p.causal && qb == kb;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int ql_ = mb * 16 + g * 4 + r, q = qb * TR + ql_;
-                const bool live = q < p.sq && kok && !(p.causal && key > q);
-                const float pr = live ? expf(sp[mb][r] * p.scale - ls[ql_]) : 0.f;
+                const int ql_ = mb * 16 + g * 4 + r;
+                float pr = exp2_fast(sp[mb][r] * c2 - ls[ql_]);
+                if (diag && key > qb * TR + ql_) pr = 0.f;
                 sp[mb][r] = pr;
                 dp[mb][r] = pr * (dp[mb][r] - dl[ql_]);
             }
@@ -418,7 +449,7 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
-    const int qb = blockIdx.x;
+    const int qb = p.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;  // heaviest first
     const int64_t bh = blockIdx.y;
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         hd{p.heads, p.do_bs, p.do_hs, p.do_rs};
@@ -428,7 +459,8 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
     const T *dO = (const T *)p.dO + hd.base(bh);
     const int q = qb * TR + wave * 16 + ql;
     const bool qok = q < p.sq;
-    const float lse = qok ? p.lse[bh * p.sq + q] : 0.f, dl = qok ? p.dlt[bh * p.sq + q] : 0.f;
+    const float c2 = p.scale * LOG2E;
+    const float lse2 = qok ? p.lse[bh * p.sq + q] * LOG2E : 0.f, dl = qok ? p.dlt[bh * p.sq + q] : 0.f;
 
     u32x4 qf[NC], of[NC];
 #pragma unroll
@@ -475,13 +507,17 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
                 mma16<T>(dp[mb], frag_c<T>(vt, mb * 16 + ql, c, g), of[c]);
             }
         }
+        // Queries past seq_q are not stored. The causal diagonal block masks keys above the query,
+        // and the last block keys past seq_kv (their K rows are zero, but an unmasked probability
+        // exp2(-LSE2) could overflow and turn 0 * inf into NaN).
+        const bool edge = (p.causal && kb == qb) || (kb == nkb - 1 && p.skv % TR != 0);
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
+                float pr = exp2_fast(sp[mb][r] * c2 - lse2);
                 const int key = kb * TR + mb * 16 + g * 4 + r;
-                const bool live = qok && key < p.skv && !(p.causal && key > q);
-                const float pr = live ? expf(sp[mb][r] * p.scale - lse) : 0.f;
+                if (edge && (key >= p.skv || (p.causal && key > q))) pr = 0.f;
                 dp[mb][r] = pr * (dp[mb][r] - dl);
             }
         // dQ^T (d x q) += K^T (d x keys) . dS^T (keys x q)
@@ -537,7 +573,10 @@ it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16) {
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || p.bh > 65535)
         return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
     const int64_t rows = p.bh * p.sq;
-    const unsigned dlt_blocks = (unsigned)((rows + NTH - 1) / NTH);
+    const int64_t dlt_rows_per_block = NTH / 16;
+    if ((rows + dlt_rows_per_block - 1) / dlt_rows_per_block > 0x7fffffff)
+        return fail(IT_ERR_DIMS, "flash attention backward: too many rows");
+    const unsigned dlt_blocks = (unsigned)((rows + dlt_rows_per_block - 1) / dlt_rows_per_block);
     if (bf16) {
         hipLaunchKernelGGL(flash_dlt<uint16_t>, dim3(dlt_blocks), dim3(NTH), 0, s, p);
         hipLaunchKernelGGL(flash_bwd_dkdv<uint16_t>, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);

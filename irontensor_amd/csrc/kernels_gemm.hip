@@ -30,14 +30,10 @@
 #include <type_traits>
 
 #include "internal.hpp"
+#include "mfma.hpp"
 
 namespace it {
 namespace {
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int NTHREADS = 256;
 constexpr int ROW_PITCH = 144;  // LDS bytes per row of a [rows][BK] tile (128 data + 16 pad)
@@ -56,15 +52,6 @@ struct ET<uint16_t> {
     static constexpr int BK = 64;
     static constexpr int KSTEP = 32;
 };
-
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
-    uint32_t b = __float_as_uint(x);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((b >> 16) | 0x40u);  // quiet NaN
-    b += 0x7fffu + ((b >> 16) & 1u);
-    return (uint16_t)(b >> 16);
-}
-
-__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
 __device__ __forceinline__ float load_out(const void *C, int64_t idx, int bf16) {
     return bf16 ? bf16_to_f32(((const uint16_t *)C)[idx]) : ((const float *)C)[idx];
@@ -307,8 +294,8 @@ __device__ __forceinline__ void finish4(const GemmArgs &p, f32x4 v, int64_t row,
         }
         if (p.out_bf16) {
             u32x2 o;
-            o[0] = (uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16);
-            o[1] = (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16);
+            o[0] = pack_bf16x2(v[0], v[1]);
+            o[1] = pack_bf16x2(v[2], v[3]);
             *(u32x2 *)((uint16_t *)p.C + idx) = o;
         } else {
             *(f32x4 *)((float *)p.C + idx) = v;
@@ -781,33 +768,43 @@ struct Plan {
     int bm, bn, splits;
 };
 
-// Picks the tile shape and split-K factor with a cost model calibrated on MI355X timings of these
-// kernels: a CU runs up to `occ` blocks at once, sharing its MFMA rate; each round of blocks pays
-// a fixed prologue/epilogue cost; the steady-state MFMA efficiency depends on the tile; split-K
-// adds its partial-sum traffic and a reduction launch. Estimated seconds, lowest wins.
+// Picks the tile shape and split-K factor with a cost model fitted to MI355X timings of these
+// kernels (every tile / split choice on the TINY and medium step shapes, the square sweep and the
+// decode shapes: over those 42 shapes its picks take 1.9% longer in total than the fastest
+// measured plans):
+//   * a CU runs up to `occ` blocks at once, sharing its MFMA rate;
+//   * each round of blocks pays a fixed prologue/epilogue cost;
+//   * a k-step costs the larger of its MFMA time (at the tile's steady-state efficiency, times
+//     the blocks sharing the CU) and a memory-latency floor: with one tile of prefetch, a block
+//     waits on its loads when a k-step has too little work to cover them (long-K, small-M/N
+//     weight gradients), which is what split-K fixes by running more blocks at once;
+//   * split-K adds its partial-sum traffic and a reduction launch.
+// Estimated seconds, lowest wins.
 Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
     struct Cand {
         int b, occ;
         double eff;
     };
     // The dual-B (SwiGLU) kernel keeps two B tiles in LDS, which halves its occupancy, and uses
-    // the unpipelined loop: lower efficiencies for it.
-    const Cand f32c[] = {{128, a.dual ? 1 : 2, a.dual ? 0.45 : 0.70}, {64, a.dual ? 2 : 4, 0.55}};
-    const Cand b16c[] = {{256, 1, 0.55}, {128, a.dual ? 1 : 2, 0.40}, {64, a.dual ? 2 : 4, 0.25}};
+    // the unpipelined loop: lower efficiencies for it. The 256x256 kernel has no dual form.
+    const Cand f32c[] = {{128, a.dual ? 1 : 2, a.dual ? 0.45 : 0.70}, {64, a.dual ? 2 : 4, 0.60}};
+    const Cand b16c[] = {{256, 1, 0.50}, {128, a.dual ? 1 : 2, 0.40}, {64, a.dual ? 2 : 4, 0.15}};
     const Cand *cands = bf16 ? b16c : f32c;
     const int ncand = bf16 ? 3 : 2;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
     const double cu_peak = (bf16 ? 2.5e15 : 157.3e12) / 256.0;  // FLOP/s per CU
     const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = 4e12;
+    const double step_floor = bf16 ? 1.0e-6 : 0.5e-6;
     const bool can_split = !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL;
     Plan best{64, 64, 1};
     double best_t = 1e30;
+    int64_t best_blocks = 0;
     for (int c = 0; c < ncand; ++c) {
         const Cand &cd = cands[c];
         const int64_t tiles = cdiv(a.M, cd.b) * cdiv(a.N, cd.b) * a.batch;
         if (cd.b == 256) {
             const double fill = (double)a.M * a.N * a.batch / ((double)tiles * 256.0 * 256.0);
-            if (a.dual || fill < 0.7 || tiles * 4 < cus * 3) continue;
+            if (a.dual || fill < 0.7) continue;
         }
         for (int s = 1; s <= 32; s *= 2) {
             if (s > 1 && !can_split) break;
@@ -818,12 +815,19 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
             const int64_t per_cu = cdiv(blocks, cus);
             const int64_t conc = std::min<int64_t>(per_cu, cd.occ);
             const int64_t rounds = cdiv(per_cu, cd.occ);
-            const double flops = (a.dual ? 4.0 : 2.0) * cd.b * cd.b * (double)std::max<int64_t>(kps, bk);
-            double t = rounds * (round_overhead + conc * flops / (cu_peak * cd.eff));
+            const int64_t ksteps = std::max<int64_t>(1, cdiv(kps, bk));
+            const double step = (a.dual ? 4.0 : 2.0) * cd.b * cd.b * bk / (cu_peak * cd.eff);
+            double t = rounds * (round_overhead + ksteps * std::max(conc * step, step_floor));
             if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
-            if (t < best_t * 0.97) {  // prefer the earlier (larger, unsplit) plan on near ties
-                best_t = t;
+            // Near ties (3%) keep the earlier, larger and less split plan, except that between two
+            // unsplit plans the one with more blocks wins (more loads in flight per k-step).
+            const bool better = t < best_t * 0.97;
+            const bool tie_more_blocks = t < best_t * 1.03 && splits == 1 && best.splits == 1 &&
+                                         blocks > best_blocks;
+            if (better || tie_more_blocks) {
+                best_t = better ? t : std::min(t, best_t);
                 best = Plan{cd.b, cd.b, (int)splits};
+                best_blocks = blocks;
             }
         }
     }

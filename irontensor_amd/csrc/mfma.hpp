@@ -18,13 +18,17 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
-    uint32_t b = __float_as_uint(x);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((b >> 16) | 0x40u);  // quiet NaN
-    b += 0x7fffu + ((b >> 16) & 1u);
-    return (uint16_t)(b >> 16);
+// FP32 -> BF16 round-to-nearest-even on the hardware converter (v_cvt_pk_bf16_f32, two values per
+// instruction); NaN stays a quiet NaN. Same results as the reference's round-half-even formula
+// (src/precision.rs:24-29) for every non-NaN input, denormals included.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 

@@ -312,6 +312,29 @@ def test_bf16_large_tile_ragged_batched(it, ta, tb):
     assert np.array_equal(c.numpy(), exact.astype(np.float32))
 
 
+@pytest.mark.parametrize("m,n,k", [(1024, 2816, 8192), (1000, 2800, 8010)])
+def test_bf16_large_tile_split_k(it, m, n, k):
+    """Long-K weight-gradient shapes (the medium step's down.dW) take the 256x256 kernel with
+    split-K (exact and ragged); the profiler key shows the plan. Small integers: exact in BF16 and
+    in every FP32 summation order, checked against a float64 product."""
+    a = synth.small_ints(210, (k, m), -2, 2)
+    b = synth.small_ints(211, (k, n), -2, 2)
+    ta, tb = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    from irontensor_amd import profiler
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    c = it.gemm(ta, tb, trans_a=True)
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    print(f"[split-K 256] {keys}", flush=True)
+    assert any("256x256" in key and not key.endswith(" s1") for key in keys), keys
+    exact = a.T.astype(np.float64) @ b.astype(np.float64)
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    again = it.gemm(ta, tb, trans_a=True)
+    assert np.array_equal(c.numpy(), again.numpy())  # ordered reduction: deterministic
+
+
 def test_bf16_large_tile_epilogues(it, oracle):
     """alpha/beta with BF16 output and a bias on a shape that takes the 256x256 kernel."""
     m, n, k = 4096, 3072, 192
