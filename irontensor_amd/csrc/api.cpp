@@ -125,6 +125,9 @@ it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op 
             a.B2 = epi->B2;
             a.G = epi->gate_out;
             a.U = epi->up_out;
+            // The pre-activations are stored with C's vector width when all three allow it.
+            a.c_vec_ok = a.c_vec_ok && (!a.G || out_vec_ok(a.G, a.out_bf16, ldc, strideC, 0)) &&
+                         (!a.U || out_vec_ok(a.U, a.out_bf16, ldc, strideC, 0));
             a.b_vec_ok = a.b_vec_ok && vec_ok(epi->B2, eb, ldb, strideB, 0);
         }
         if (epi->flags & IT_EPI_CAUSAL) {

@@ -307,6 +307,51 @@ __device__ __forceinline__ void finish4(const GemmArgs &p, f32x4 v, int64_t row,
         if (col + e < p.N) finish_store(p, p.C, idx + e, v[e], row, col + e);
 }
 
+// SwiGLU epilogue for 4 consecutive columns: gate = alpha*g (+ gate bias), up = alpha*u (+ up bias
+// at bias[N + col]); stores gate and up when asked for, and silu(gate) * up.
+template <bool EDGE>
+__device__ __forceinline__ void finish_swiglu4(const GemmArgs &p, f32x4 g, f32x4 u, int64_t row, int64_t col,
+                                               int64_t coff) {
+    if (EDGE && (row >= p.M || col >= p.N)) return;
+    g *= p.alpha;
+    u *= p.alpha;
+    const bool full = !EDGE || col + 4 <= p.N;
+    if (p.has_bias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (full || col + e < p.N) {
+                g[e] += p.bias[col + e];
+                u[e] += p.bias[p.N + col + e];
+            }
+    }
+    f32x4 h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = silu(g[e]) * u[e];
+    const int64_t idx = coff + row * p.ldc + col;
+    if (full && p.c_vec_ok) {
+        if (p.out_bf16) {
+            auto st = [&](void *dst, f32x4 v) {
+                *(u32x2 *)((uint16_t *)dst + idx) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            };
+            if (p.G) st(p.G, g);
+            if (p.U) st(p.U, u);
+            st(p.C, h);
+        } else {
+            if (p.G) *(f32x4 *)((float *)p.G + idx) = g;
+            if (p.U) *(f32x4 *)((float *)p.U + idx) = u;
+            *(f32x4 *)((float *)p.C + idx) = h;
+        }
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (col + e >= p.N) break;
+        if (p.G) store_out(p.G, idx + e, g[e], p.out_bf16);
+        if (p.U) store_out(p.U, idx + e, u[e], p.out_bf16);
+        store_out(p.C, idx + e, h[e], p.out_bf16);
+    }
+}
+
 namespace sg {
 constexpr int MFMA = 0x008, VMEM_READ = 0x020, DS_READ = 0x100, DS_WRITE = 0x200;
 }
@@ -542,13 +587,18 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 //   * sched_group_barrier interleaves the DS reads, global loads and DS writes with the MFMAs.
 // The loop body has no branches: the prefetch after the last tile re-reads the last tile (in
 // bounds) and its LDS writes land in the stage nobody reads again.
-template <bool TA, bool TB, bool EDGE>
+template <bool TA, bool TB, bool EDGE, bool DUAL = false>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_256(const GemmArgs p) {
     using T = uint16_t;
     constexpr int BM = 256, BN = 256, BK = ET<T>::BK, WT = 128, F = 4;
     using OA = Operand<T, !TA, BM>;
     using OB = Operand<T, TB, BN>;
+    // SwiGLU dual-B form: the B tile's rows 0..127 are 128 gate-weight rows and rows 128..255 the
+    // same 128 rows of the up weight, so waves wn = 0 accumulate gate and wn = 1 up for one 256 x 128
+    // output tile; the epilogue pairs them.
+    using OBH = Operand<T, TB, BN / 2>;
+    static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
     constexpr int SA = OA::STAGE_BYTES, SB = OB::STAGE_BYTES, STAGE = SA + SB;
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
 
@@ -562,7 +612,8 @@ void gemm_bf16_256(const GemmArgs p) {
     const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in;
     const T *B = (const T *)p.B + bo * p.sB_out + bi * p.sB_in;
     const int64_t coff = bo * p.sC_out + bi * p.sC_in;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (DUAL ? BN / 2 : BN);
+    const T *B2 = DUAL ? (const T *)p.B2 + bo * p.sB_out + bi * p.sB_in : nullptr;
 
     if (p.causal != CAUSAL_NONE && n0 > m0 + BM - 1 + p.causal_offset) {
         if (p.causal == CAUSAL_WRITE) {
@@ -589,7 +640,8 @@ void gemm_bf16_256(const GemmArgs p) {
 
     if (ntiles > 0) {
         OA ga;
-        OB gb;
+        std::conditional_t<DUAL, OBH, OB> gb;
+        std::conditional_t<DUAL, OBH, char> gb2;
         u32x4 fa0[F], fb0[F], fa1[F], fb1[F];
         const int last = ntiles - 1;
         auto frags = [&](u32x4 (&fa)[F], u32x4 (&fb)[F], const char *st, int ks) {
@@ -608,14 +660,18 @@ void gemm_bf16_256(const GemmArgs p) {
         };
         // Tile k0: global loads into registers now, LDS writes in put().
         auto fetch = [&](int64_t k0) {
-            ga.template load<EDGE ? LOAD_CHECKED : LOAD_EXACT>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
-            gb.template load<EDGE ? LOAD_CHECKED : LOAD_EXACT>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
+            constexpr int LM = EDGE ? LOAD_CHECKED : LOAD_EXACT;
+            ga.template load<LM>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
+            gb.template load<LM>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
+            if constexpr (DUAL) gb2.template load<LM>(B2, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
         };
         auto put = [&](char *stage) {
             ga.store(stage, tid);
             gb.store(stage + SA, tid);
+            if constexpr (DUAL) gb2.store(stage + SA + OBH::STAGE_BYTES, tid);
         };
-        // DS writes per k-tile, spread over the 8 MFMA pairs of the last k-step.
+        // DS writes per k-tile, spread over the 8 MFMA pairs of the last k-step (the dual halves
+        // together issue what one 256-row B operand does).
         constexpr int DSW = (OA::ITERS * (OA::TRANSPOSE ? 8 : 1) + OB::ITERS * (OB::TRANSPOSE ? 8 : 1) + 7) / 8;
         constexpr int VMR = (OA::ITERS * OA::LOADS + OB::ITERS * OB::LOADS + 7) / 8;
 
@@ -678,11 +734,23 @@ void gemm_bf16_256(const GemmArgs p) {
                 *(float *)(wl + rl * EP + cl * 4) = acc[i][h][r];
             }
         __syncthreads();
-        for (int it = 0; it < WT * EC / 256; ++it) {
-            const int e = (it * 64 + lane) * 4;
-            const int rl = e / EC, cl = e % EC;
-            const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
-            finish4<EDGE>(p, v, m0 + wm * WT + rl, n0 + wn * WT + h * EC + cl, coff, z);
+        if constexpr (DUAL) {
+            // The two waves of row half wm (gate: wn = 0, up: wn = 1) finish its 128 x 32 slice.
+            const char *gl = smem + (wm * 2) * (WT * EP), *ul = gl + WT * EP;
+            const int pt = wn * 64 + lane;
+            for (int it = 0; it < WT * EC / 512; ++it) {
+                const int e = (it * 128 + pt) * 4;
+                const int rl = e / EC, cl = e % EC;
+                finish_swiglu4<EDGE>(p, *(const f32x4 *)(gl + rl * EP + cl * 4), *(const f32x4 *)(ul + rl * EP + cl * 4),
+                                     m0 + wm * WT + rl, n0 + h * EC + cl, coff);
+            }
+        } else {
+            for (int it = 0; it < WT * EC / 256; ++it) {
+                const int e = (it * 64 + lane) * 4;
+                const int rl = e / EC, cl = e % EC;
+                const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
+                finish4<EDGE>(p, v, m0 + wm * WT + rl, n0 + wn * WT + h * EC + cl, coff, z);
+            }
         }
         __syncthreads();
     }
@@ -708,7 +776,8 @@ struct TileCfg {
 
 template <bool EDGE>
 void launch_bf16_256_e(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipStream_t s) {
-    if (!ta && !tb) hipLaunchKernelGGL((gemm_bf16_256<false, false, EDGE>), grid, dim3(NTHREADS), 0, s, a);
+    if (a.dual) hipLaunchKernelGGL((gemm_bf16_256<false, true, EDGE, true>), grid, dim3(NTHREADS), 0, s, a);
+    else if (!ta && !tb) hipLaunchKernelGGL((gemm_bf16_256<false, false, EDGE>), grid, dim3(NTHREADS), 0, s, a);
     else if (!ta && tb) hipLaunchKernelGGL((gemm_bf16_256<false, true, EDGE>), grid, dim3(NTHREADS), 0, s, a);
     else if (ta && !tb) hipLaunchKernelGGL((gemm_bf16_256<true, false, EDGE>), grid, dim3(NTHREADS), 0, s, a);
     else hipLaunchKernelGGL((gemm_bf16_256<true, true, EDGE>), grid, dim3(NTHREADS), 0, s, a);
@@ -721,7 +790,7 @@ bool tiles_exact(const GemmArgs &a, int bm, int bn, int bk) {
 }
 
 hipError_t launch_bf16_256(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipStream_t s) {
-    if (tiles_exact(a, 256, 256, ET<uint16_t>::BK))
+    if (tiles_exact(a, 256, a.dual ? 128 : 256, ET<uint16_t>::BK))
         launch_bf16_256_e<false>(ta, tb, a, grid, s);
     else
         launch_bf16_256_e<true>(ta, tb, a, grid, s);
@@ -785,10 +854,11 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
         int b, occ;
         double eff;
     };
-    // The dual-B (SwiGLU) kernel keeps two B tiles in LDS, which halves its occupancy, and uses
-    // the unpipelined loop: lower efficiencies for it. The 256x256 kernel has no dual form.
+    // The dual-B (SwiGLU) form of the 64/128 kernels keeps two B tiles in LDS, which halves its
+    // occupancy, and uses the unpipelined loop: lower efficiencies for it. The 256 kernel's dual
+    // form runs its usual loop.
     const Cand f32c[] = {{128, a.dual ? 1 : 2, a.dual ? 0.45 : 0.70}, {64, a.dual ? 2 : 4, 0.60}};
-    const Cand b16c[] = {{256, 1, 0.50}, {128, a.dual ? 1 : 2, 0.40}, {64, a.dual ? 2 : 4, 0.15}};
+    const Cand b16c[] = {{256, 1, 0.50}, {128, a.dual ? 1 : 2, a.dual ? 0.25 : 0.40}, {64, a.dual ? 2 : 4, 0.15}};
     const Cand *cands = bf16 ? b16c : f32c;
     const int ncand = bf16 ? 3 : 2;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
@@ -801,10 +871,12 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
     int64_t best_blocks = 0;
     for (int c = 0; c < ncand; ++c) {
         const Cand &cd = cands[c];
-        const int64_t tiles = cdiv(a.M, cd.b) * cdiv(a.N, cd.b) * a.batch;
+        // The 256 kernel's dual form covers 256 x 128 outputs (its 256 B rows are gate and up).
+        const int bn = cd.b == 256 && a.dual ? 128 : cd.b;
+        const int64_t tiles = cdiv(a.M, cd.b) * cdiv(a.N, bn) * a.batch;
         if (cd.b == 256) {
-            const double fill = (double)a.M * a.N * a.batch / ((double)tiles * 256.0 * 256.0);
-            if (a.dual || fill < 0.7) continue;
+            const double fill = (double)a.M * a.N * a.batch / ((double)tiles * 256.0 * bn);
+            if (fill < 0.7) continue;
         }
         for (int s = 1; s <= 32; s *= 2) {
             if (s > 1 && !can_split) break;
@@ -816,7 +888,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
             const int64_t conc = std::min<int64_t>(per_cu, cd.occ);
             const int64_t rounds = cdiv(per_cu, cd.occ);
             const int64_t ksteps = std::max<int64_t>(1, cdiv(kps, bk));
-            const double step = (a.dual ? 4.0 : 2.0) * cd.b * cd.b * bk / (cu_peak * cd.eff);
+            const double step = (a.dual ? 4.0 : 2.0) * cd.b * bn * bk / (cu_peak * cd.eff);
             double t = rounds * (round_overhead + ksteps * std::max(conc * step, step_floor));
             if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
             // Near ties (3%) keep the earlier, larger and less split plan, except that between two
@@ -826,7 +898,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
                                          blocks > best_blocks;
             if (better || tie_more_blocks) {
                 best_t = better ? t : std::min(t, best_t);
-                best = Plan{cd.b, cd.b, (int)splits};
+                best = Plan{cd.b, bn, (int)splits};
                 best_blocks = blocks;
             }
         }

@@ -231,6 +231,33 @@ def test_swiglu_dual_epilogue_with_bias(it, oracle, prec):
             assert frob_rel(got.numpy(), ref) <= BF16_FROB_TOL
 
 
+@pytest.mark.parametrize("rows,h,f", [(4096, 128, 2048), (4000, 200, 2000)])
+def test_bf16_swiglu_large_tile(it, oracle, rows, h, f):
+    """The 256x256 kernel's dual form (gate and up halves of one B tile, 256 x 128 outputs), exact
+    and ragged, with the bias: small integers keep gate and up exact in FP32, so they must equal the
+    oracle bit for bit and h = silu(gate) * up must agree to FP32 rounding."""
+    from irontensor_amd import profiler
+    x = synth.small_ints(220, (rows, h), -2, 2)
+    wg = synth.small_ints(221, (f, h), -2, 2)
+    wu = synth.small_ints(222, (f, h), -2, 2)
+    b = synth.small_ints(223, (2 * f,), -4, 4)
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    hh, g, u = it.swiglu_up(it.Tensor.from_f32_as_bf16(x, x.shape), it.Tensor.from_f32_as_bf16(wg, wg.shape),
+                            it.Tensor.from_f32_as_bf16(wu, wu.shape), out_precision=it.Precision.FP32,
+                            bias=it.Tensor.from_f32_slice(b, [2 * f]))
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    print(f"[swiglu 256] {keys}", flush=True)
+    assert any("256x128_swiglu" in key for key in keys), keys
+    g_ref = oracle.add_bias(oracle.gemm_f32(x, wg, trans_b=True), b[:f])
+    u_ref = oracle.add_bias(oracle.gemm_f32(x, wu, trans_b=True), b[f:])
+    assert np.array_equal(g.numpy(), g_ref)
+    assert np.array_equal(u.numpy(), u_ref)
+    assert normwise_rel(hh.numpy(), oracle.swiglu(g_ref, u_ref)) <= FP32_TOL
+
+
 # ------------------------------------------------------------------ BF16
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
