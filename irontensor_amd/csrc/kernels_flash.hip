@@ -54,73 +54,151 @@ struct Head {
 
 __device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
 
-// A 64x64 tile of T from a per-head matrix (rows beyond `rows` read as zero), held in registers
-// between its global load and its LDS store, in row-major or transposed LDS layout.
-template <typename T, bool TRANSPOSED>
-struct TileRegs {
+// 64x64 tiles move global -> registers -> LDS in units of 4 rows x 16 bytes (4 x VEC elements).
+// From one unit a thread can write both LDS layouts: row-major ([row][d]) and transposed ([d][row],
+// for operands whose MFMA k index is the tile row), so a tensor needed both ways is read from HBM
+// once.
+//
+// Unit u covers rows 4rg..4rg+3 and 16-byte column cc. For a tile that is stored transposed,
+// consecutive lanes take consecutive rg, so the transposed writes of neighbouring lanes fill one LDS
+// row side by side (with cc fastest they would land 8 rows apart, on the same banks); a tile stored
+// only row-major keeps cc fastest (each lane group writes whole 128-byte rows).
+template <typename T>
+struct Unit4 {
     static constexpr int VEC = FE<T>::VEC;
-    static constexpr int UNITS = TRANSPOSED ? (TR / 4) * (HD / VEC) : TR * HD / VEC;
-    static constexpr int LOADS = TRANSPOSED ? 4 : 1;
-    static constexpr int ITERS = (UNITS + NTH - 1) / NTH;
-    u32x4 r[ITERS][LOADS];
+    static constexpr int CPR = HD / VEC;   // 16-byte columns per row
+    static constexpr int RGS = TR / 4;     // row groups
+    u32x4 r[4];
 
-    __device__ __forceinline__ void load(const T *m, int64_t rs, int row0, int rows, int tid) {
-#pragma unroll
-        for (int it = 0; it < ITERS; ++it) {
-            const int u = tid + it * NTH;
-            if (UNITS % NTH != 0 && u >= UNITS) continue;
-            if constexpr (!TRANSPOSED) {
-                const int row = u / (HD / VEC), cc = u % (HD / VEC);
-                const bool ok = row0 + row < rows;
-                const u32x4 v = ld16(m + (ok ? (int64_t)(row0 + row) * rs + cc * VEC : 0));
-                r[it][0] = ok ? v : u32x4{0u, 0u, 0u, 0u};
-            } else {
-                const int cc = u % (HD / VEC), rg = u / (HD / VEC);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int row = rg * 4 + q;
-                    const bool ok = row0 + row < rows;
-                    const u32x4 v = ld16(m + (ok ? (int64_t)(row0 + row) * rs + cc * VEC : 0));
-                    r[it][q] = ok ? v : u32x4{0u, 0u, 0u, 0u};
-                }
-            }
-        }
+    __device__ __forceinline__ static void decode(int u, bool rg_fast, int &rg, int &cc) {
+        rg = rg_fast ? u % RGS : u / CPR;
+        cc = rg_fast ? u / RGS : u % CPR;
     }
 
-    __device__ __forceinline__ void store(char *lds, int tid) const {
+    __device__ __forceinline__ void load(const T *m, int64_t rs, int row0, int rows, int u, bool rg_fast) {
+        int rg, cc;
+        decode(u, rg_fast, rg, cc);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int row = row0 + rg * 4 + q;
+            const bool ok = row < rows;
+            const u32x4 v = ld16(m + (ok ? (int64_t)row * rs + cc * VEC : 0));
+            r[q] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    __device__ __forceinline__ void store_rows(char *lds, int u, bool rg_fast) const {
         constexpr int P = pitch<T>();
+        int rg, cc;
+        decode(u, rg_fast, rg, cc);
 #pragma unroll
-        for (int it = 0; it < ITERS; ++it) {
-            const int u = tid + it * NTH;
-            if (UNITS % NTH != 0 && u >= UNITS) continue;
-            if constexpr (!TRANSPOSED) {
-                const int row = u / (HD / VEC), cc = u % (HD / VEC);
-                *(u32x4 *)(lds + row * P + cc * 16) = r[it][0];
-            } else {
-                const int cc = u % (HD / VEC), rg = u / (HD / VEC);
-                const u32x4 &v0 = r[it][0], &v1 = r[it][1], &v2 = r[it][2], &v3 = r[it][3];
-                if constexpr (sizeof(T) == 4) {
-                    // 4 rows x 4 columns -> LDS rows 4cc+j, columns 4rg..4rg+3
+        for (int q = 0; q < 4; ++q) *(u32x4 *)(lds + (rg * 4 + q) * P + cc * 16) = r[q];
+    }
+    __device__ __forceinline__ void store_cols(char *lds, int u, bool rg_fast) const {
+        constexpr int P = pitch<T>();
+        int rg, cc;
+        decode(u, rg_fast, rg, cc);
+        const u32x4 &v0 = r[0], &v1 = r[1], &v2 = r[2], &v3 = r[3];
+        if constexpr (sizeof(T) == 4) {
+            // 4 rows x 4 columns -> LDS rows 4cc+j, columns 4rg..4rg+3
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        *(u32x4 *)(lds + (cc * 4 + j) * P + rg * 16) = u32x4{v0[j], v1[j], v2[j], v3[j]};
-                } else {
-                    // 4 rows x 8 bf16 columns -> LDS rows 8cc+j, columns 4rg..4rg+3 (8 bytes)
+            for (int j = 0; j < 4; ++j)
+                *(u32x4 *)(lds + (cc * 4 + j) * P + rg * 16) = u32x4{v0[j], v1[j], v2[j], v3[j]};
+        } else {
+            // 4 rows x 8 bf16 columns -> LDS rows 8cc+j, columns 4rg..4rg+3 (8 bytes)
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        u32x2 lo, hi;
-                        lo[0] = (v0[d] & 0xffffu) | (v1[d] << 16);
-                        lo[1] = (v2[d] & 0xffffu) | (v3[d] << 16);
-                        hi[0] = (v0[d] >> 16) | (v1[d] & 0xffff0000u);
-                        hi[1] = (v2[d] >> 16) | (v3[d] & 0xffff0000u);
-                        *(u32x2 *)(lds + (cc * 8 + 2 * d) * P + rg * 8) = lo;
-                        *(u32x2 *)(lds + (cc * 8 + 2 * d + 1) * P + rg * 8) = hi;
-                    }
-                }
+            for (int d = 0; d < 4; ++d) {
+                u32x2 lo, hi;
+                lo[0] = (v0[d] & 0xffffu) | (v1[d] << 16);
+                lo[1] = (v2[d] & 0xffffu) | (v3[d] << 16);
+                hi[0] = (v0[d] >> 16) | (v1[d] & 0xffff0000u);
+                hi[1] = (v2[d] >> 16) | (v3[d] & 0xffff0000u);
+                *(u32x2 *)(lds + (cc * 8 + 2 * d) * P + rg * 8) = lo;
+                *(u32x2 *)(lds + (cc * 8 + 2 * d + 1) * P + rg * 8) = hi;
             }
         }
     }
 };
+
+// Two 64x64 row tiles (tensors 0 and 1, same row blocks) streamed through LDS with two register
+// sets, so the loads of block t+2 are in flight while block t is computed and block t+1 waits in
+// registers. FP32: 256 units per tile, every thread moves one unit of each; BF16: 128 units, waves
+// 0-1 move tensor 0 and waves 2-3 tensor 1. Each tensor goes to LDS row-major, transposed or both
+// (an offset < 0 skips a layout). Optionally two per-row FP32 vectors (aux) ride along, scaled, for
+// rows blk*64 + tid (tid < 64), into `aux_off`.
+template <typename T>
+struct TilePair {
+    static constexpr int PER_TILE = TR * HD / (4 * FE<T>::VEC);
+    static constexpr int SLOTS = 2 * PER_TILE / NTH;
+    const T *m[2];
+    int64_t rs[2];
+    int rows[2];
+    int off_rows[2], off_cols[2];
+    const float *aux[2] = {nullptr, nullptr};
+    float aux_scale[2] = {1.f, 1.f};
+    int aux_off = -1, aux_rows = 0;
+    int tid;
+    Unit4<T> set0[SLOTS], set1[SLOTS];
+    float x0[2], x1[2];
+
+    __device__ __forceinline__ int tensor(int s) const { return SLOTS == 2 ? s : (tid >= PER_TILE ? 1 : 0); }
+    __device__ __forceinline__ int unit() const { return SLOTS == 2 ? tid : tid % PER_TILE; }
+
+    template <int SET>
+    __device__ __forceinline__ void load(int blk) {
+        Unit4<T> *r = SET ? set1 : set0;
+        float *x = SET ? x1 : x0;
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            const int t = tensor(s);
+            r[s].load(m[t], rs[t], blk * TR, rows[t], unit(), off_cols[t] >= 0);
+        }
+        if (aux_off >= 0 && tid < TR) {
+            const int row = blk * TR + tid;
+#pragma unroll
+            for (int a = 0; a < 2; ++a) x[a] = row < aux_rows ? aux[a][row] * aux_scale[a] : 0.f;
+        }
+    }
+    template <int SET>
+    __device__ __forceinline__ void store(char *stage) const {
+        const Unit4<T> *r = SET ? set1 : set0;
+        const float *x = SET ? x1 : x0;
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            const int t = tensor(s);
+            const bool rg_fast = off_cols[t] >= 0;
+            if (off_rows[t] >= 0) r[s].store_rows(stage + off_rows[t], unit(), rg_fast);
+            if (rg_fast) r[s].store_cols(stage + off_cols[t], unit(), rg_fast);
+        }
+        if (aux_off >= 0 && tid < TR) {
+            ((float *)(stage + aux_off))[tid] = x[0];
+            ((float *)(stage + aux_off + TR * 4))[tid] = x[1];
+        }
+    }
+};
+
+// Runs body(t, stage) for t = 0..n-1 on row blocks b0 + t, block t's tiles in LDS stage t % 2.
+// Block t+2 is loaded as body t starts and written to LDS after body t+1, so its loads have two
+// blocks of compute to land.
+template <typename T, typename Body>
+__device__ __forceinline__ void pipelined(TilePair<T> &tp, char *smem, int stage_bytes, int b0, int n, Body body) {
+    if (n > 0) {
+        tp.template load<0>(b0);
+        tp.template store<0>(smem);
+    }
+    if (n > 1) tp.template load<1>(b0 + 1);
+    __syncthreads();
+    for (int t = 0; t < n; t += 2) {
+        if (t + 2 < n) tp.template load<0>(b0 + t + 2);
+        body(t, (const char *)smem);
+        if (t + 1 < n) tp.template store<1>(smem + stage_bytes);
+        __syncthreads();
+        if (t + 1 >= n) break;
+        if (t + 3 < n) tp.template load<1>(b0 + t + 3);
+        body(t + 1, (const char *)(smem + stage_bytes));
+        if (t + 2 < n) tp.template store<0>(smem);
+        __syncthreads();
+    }
+}
 
 // Fragment of LDS tile row `row`, contiguous k chunk c (lane group g).
 template <typename T>
@@ -207,23 +285,18 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
 
     const int kblocks = (p.skv + TR - 1) / TR;
     const int nkb = p.causal ? min(kblocks, qb + 1) : kblocks;
-    TileRegs<T, false> kr;
-    TileRegs<T, true> vr;
-    if (nkb > 0) {
-        kr.load(K, p.kv_rs, 0, p.skv, tid);
-        vr.load(V, p.kv_rs, 0, p.skv, tid);
-        kr.store(smem, tid);
-        vr.store(smem + KT, tid);
-        __syncthreads();
-    }
-    for (int kb = 0; kb < nkb; ++kb) {
-        const char *kt = smem + (kb & 1) * STAGE, *vt = kt + KT;
-        char *nxt = smem + ((kb + 1) & 1) * STAGE;
-        const bool more = kb + 1 < nkb;
-        if (more) {
-            kr.load(K, p.kv_rs, (kb + 1) * TR, p.skv, tid);
-            vr.load(V, p.kv_rs, (kb + 1) * TR, p.skv, tid);
-        }
+    TilePair<T> tp;
+    tp.tid = tid;
+    tp.m[0] = K;  // K row-major
+    tp.m[1] = V;  // V transposed
+    tp.rs[0] = tp.rs[1] = p.kv_rs;
+    tp.rows[0] = tp.rows[1] = (int)p.skv;
+    tp.off_rows[0] = 0;
+    tp.off_cols[0] = -1;
+    tp.off_rows[1] = -1;
+    tp.off_cols[1] = KT;
+    pipelined(tp, smem, STAGE, 0, nkb, [&](int kb, const char *kt) {
+        const char *vt = kt + KT;
         // S^T blocks: keys 16mb + 4g + r of this tile, query q.
         f32x4 s[4];
 #pragma unroll
@@ -275,12 +348,7 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
         for (int d = 0; d < 4; ++d)
 #pragma unroll
             for (int c = 0; c < TR / FE<T>::KC; ++c) mma16<T>(o[d], frag_s<T>(vt, d * 16 + ql, c, g), frag_acc<T>(s, c));
-        if (more) {
-            kr.store(nxt, tid);
-            vr.store(nxt + KT, tid);
-        }
-        __syncthreads();
-    }
+    });
     if (qok) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
@@ -356,35 +424,26 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
 
     const int qblocks = (p.sq + TR - 1) / TR;
     const int qb0 = p.causal ? kb : 0;
-    TileRegs<T, false> qr, dr;
-    TileRegs<T, true> qtr, dtr;
-    auto load = [&](int qb) {
-        qr.load(Q, p.q_rs, qb * TR, p.sq, tid);
-        qtr.load(Q, p.q_rs, qb * TR, p.sq, tid);
-        dr.load(dO, p.do_rs, qb * TR, p.sq, tid);
-        dtr.load(dO, p.do_rs, qb * TR, p.sq, tid);
-    };
-    auto store = [&](int qb, char *st) {
-        qr.store(st, tid);
-        qtr.store(st + T_, tid);
-        dr.store(st + 2 * T_, tid);
-        dtr.store(st + 3 * T_, tid);
-        if (tid < TR) {
-            const int q = qb * TR + tid;
-            ((float *)(st + 4 * T_))[tid] = q < p.sq ? lse[q] * LOG2E : 0.f;
-            ((float *)(st + 4 * T_ + TR * 4))[tid] = q < p.sq ? dlt[q] : 0.f;
-        }
-    };
-    if (qb0 < qblocks) {
-        load(qb0);
-        store(qb0, smem);
-        __syncthreads();
-    }
-    for (int qb = qb0; qb < qblocks; ++qb) {
-        const char *st = smem + ((qb - qb0) & 1) * STAGE;
-        char *nxt = smem + ((qb - qb0 + 1) & 1) * STAGE;
-        const bool more = qb + 1 < qblocks;
-        if (more) load(qb + 1);
+    // Q and dO, each needed row-major (S, dP) and transposed (dK, dV); the rows' LSE (as log2) and
+    // rowsum(dO * O) ride along.
+    TilePair<T> tp;
+    tp.tid = tid;
+    tp.m[0] = Q;
+    tp.m[1] = dO;
+    tp.rs[0] = p.q_rs;
+    tp.rs[1] = p.do_rs;
+    tp.rows[0] = tp.rows[1] = (int)p.sq;
+    tp.off_rows[0] = 0;
+    tp.off_cols[0] = T_;
+    tp.off_rows[1] = 2 * T_;
+    tp.off_cols[1] = 3 * T_;
+    tp.aux[0] = lse;
+    tp.aux[1] = dlt;
+    tp.aux_scale[0] = LOG2E;
+    tp.aux_off = 4 * T_;
+    tp.aux_rows = (int)p.sq;
+    pipelined(tp, smem, STAGE, qb0, qblocks - qb0, [&](int t, const char *st) {
+        const int qb = qb0 + t;
         const char *qt = st, *qtt = st + T_, *dot = st + 2 * T_, *dott = st + 3 * T_;
         const float *ls = (const float *)(st + 4 * T_), *dl = ls + TR;
         // S = Q.K^T and dP = dO.V^T: rows q = 16mb + 4g + r of the tile, column = this key.
@@ -421,9 +480,7 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
                 mma16<T>(dv[n], frag_acc<T>(sp, c), frag_s<T>(dott, n * 16 + ql, c, g));
                 mma16<T>(dk[n], frag_acc<T>(dp, c), frag_s<T>(qtt, n * 16 + ql, c, g));
             }
-        if (more) store(qb + 1, nxt);
-        __syncthreads();
-    }
+    });
     // Lane l holds rows (keys) 16*wave + 4g + r and column d = 16n + l%16.
     const Head hdk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs};
     float *dK = p.dK + hdk.base(bh), *dV = p.dV + hdk.base(bh);
@@ -476,26 +533,19 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
 
     const int kblocks = (p.skv + TR - 1) / TR;
     const int nkb = p.causal ? min(kblocks, qb + 1) : kblocks;
-    TileRegs<T, false> kr, vr;
-    TileRegs<T, true> ktr;
-    if (nkb > 0) {
-        kr.load(K, p.kv_rs, 0, p.skv, tid);
-        vr.load(V, p.kv_rs, 0, p.skv, tid);
-        ktr.load(K, p.kv_rs, 0, p.skv, tid);
-        kr.store(smem, tid);
-        vr.store(smem + T_, tid);
-        ktr.store(smem + 2 * T_, tid);
-        __syncthreads();
-    }
-    for (int kb = 0; kb < nkb; ++kb) {
-        const char *kt = smem + (kb & 1) * STAGE, *vt = kt + T_, *ktt = kt + 2 * T_;
-        char *nxt = smem + ((kb + 1) & 1) * STAGE;
-        const bool more = kb + 1 < nkb;
-        if (more) {
-            kr.load(K, p.kv_rs, (kb + 1) * TR, p.skv, tid);
-            vr.load(V, p.kv_rs, (kb + 1) * TR, p.skv, tid);
-            ktr.load(K, p.kv_rs, (kb + 1) * TR, p.skv, tid);
-        }
+    // K row-major (S^T) and transposed (dQ^T), V row-major (dP^T).
+    TilePair<T> tp;
+    tp.tid = tid;
+    tp.m[0] = K;
+    tp.m[1] = V;
+    tp.rs[0] = tp.rs[1] = p.kv_rs;
+    tp.rows[0] = tp.rows[1] = (int)p.skv;
+    tp.off_rows[0] = 0;
+    tp.off_cols[0] = 2 * T_;
+    tp.off_rows[1] = T_;
+    tp.off_cols[1] = -1;
+    pipelined(tp, smem, STAGE, 0, nkb, [&](int kb, const char *kt) {
+        const char *vt = kt + T_, *ktt = kt + 2 * T_;
         // S^T = K.Q^T and dP^T = V.dO^T: rows = keys 16mb + 4g + r, column = this query.
         f32x4 sp[4], dp[4];
 #pragma unroll
@@ -525,13 +575,7 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
         for (int d = 0; d < 4; ++d)
 #pragma unroll
             for (int c = 0; c < NK; ++c) mma16<T>(dq[d], frag_s<T>(ktt, d * 16 + ql, c, g), frag_acc<T>(dp, c));
-        if (more) {
-            kr.store(nxt, tid);
-            vr.store(nxt + T_, tid);
-            ktr.store(nxt + 2 * T_, tid);
-        }
-        __syncthreads();
-    }
+    });
     if (qok) {
         float *dQ = p.dQ + hq.base(bh) + (int64_t)q * p.q_rs;
 #pragma unroll
