@@ -152,6 +152,10 @@ struct FlashArgs {
     float scale;
     int causal;
 };
+// Decode-shaped BF16 NT GEMM (M <= 16), HBM-bound: kernels_gemv.hip.
+bool gemv_applicable(const GemmArgs &a, bool bf16, bool transA, bool transB);
+it_status launch_gemv(hipStream_t s, const GemmArgs &a);
+
 bool flash_supported(const FlashArgs &p, int elem_bytes, bool backward);
 it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16);
 it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16);

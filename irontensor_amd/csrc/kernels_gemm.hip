@@ -919,6 +919,20 @@ it_status launch_splitk_reduce(hipStream_t s, const GemmArgs &a) {
 it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool transB, GemmArgs a,
                       const char *profile_tag) {
     const bool bf16 = dtype_in == IT_BF16;
+    if (gemv_applicable(a, bf16, transA, transB)) {
+        std::string key;
+        hipEvent_t ev = nullptr;
+        if (ctx->profiling) {
+            char buf[160];
+            std::snprintf(buf, sizeof(buf), "gemv_bf16_NT|%s[%lld,%lld,%lld]x%lld s1", profile_tag ? profile_tag : "",
+                          (long long)a.M, (long long)a.N, (long long)a.K, (long long)a.batch);
+            key = buf;
+            profile_begin(ctx, key, &ev);
+        }
+        const it_status st = launch_gemv(ctx->stream, a);
+        if (ctx->profiling) profile_end(ctx, key, ev);
+        return st;
+    }
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     const Plan plan = choose_plan(a, bf16, cus);
