@@ -76,10 +76,23 @@ it_status it_memcpy_d2d(it_context *ctx, void *dst, const void *src, size_t byte
 /* Zero-fill with a kernel (safe to capture in a graph; replaces Tensor::zeros' CPU memset). */
 it_status it_zero(it_context *ctx, void *dst, size_t bytes);
 
-/* CommandBatch::sync (src/command_batch.rs:191-207). */
+/* CommandBatch::sync (src/command_batch.rs:191-207): waits for all work of the context. */
 it_status it_stream_sync(it_context *ctx);
-/* The HIP stream (hipStream_t) the context launches on, for callers that interoperate. */
+/* The HIP stream (hipStream_t) the context currently launches on, for callers that interoperate. */
 void *it_stream(it_context *ctx);
+
+/*
+ * Overlap of independent work (no counterpart in the reference, whose CommandBatch orders all work
+ * on one queue, src/command_batch.rs:174-390): between it_side_begin and it_side_end, launches go
+ * to a second stream (default priority) that first waits for everything issued so far on the main
+ * stream; the main stream continues concurrently. it_side_join makes the main stream wait for the
+ * side work (it_stream_sync, reads to the host, frees and it_capture_end do so themselves). Each
+ * stream has its own split-K / attention scratch. Used by the training-step driver to run weight
+ * gradients beside the data-gradient chain; graph capture records the fork and join.
+ */
+it_status it_side_begin(it_context *ctx);
+it_status it_side_end(it_context *ctx);
+it_status it_side_join(it_context *ctx);
 /* commit_async / is_async_complete / wait_for_completion (src/command_batch.rs:228-272). */
 it_status it_event_create(it_context *ctx, it_event **out_ev);
 it_status it_event_record(it_context *ctx, it_event *ev);

@@ -108,6 +108,9 @@ _SIGNATURES = {
                                             C.POINTER(AttnLayout), C.POINTER(AttnLayout),
                                             C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "it_side_begin": (c_int, [c_void_p]),
+    "it_side_end": (c_int, [c_void_p]),
+    "it_side_join": (c_int, [c_void_p]),
     "it_capture_begin": (c_int, [c_void_p]),
     "it_capture_end": (c_int, [c_void_p, C.POINTER(c_void_p)]),
     "it_graph_launch": (c_int, [c_void_p, c_void_p]),

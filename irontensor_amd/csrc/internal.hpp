@@ -45,19 +45,26 @@ struct it_context {
     int num_cus = 0;
     int clock_khz = 0;
     char name[256] = {0};
+    // Launches go to `stream`: the main stream, or the side stream between it_side_begin and
+    // it_side_end (independent work, e.g. weight gradients, overlapping the main chain).
     hipStream_t stream = nullptr;
+    hipStream_t main_stream = nullptr, side_stream = nullptr;
+    int cur = 0;                 // 0 = main, 1 = side
+    bool side_pending = false;   // side work not yet joined into the main stream
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
 
-    // Caching allocator: freed blocks are kept per exact size and reused (single stream, so reuse
-    // is stream-ordered and needs no events).
+    // Caching allocator: freed blocks are kept per exact size and reused. Reuse is ordered on the
+    // main stream; a free while side work is pending first makes the main stream wait for it.
     std::map<void *, size_t> live;
     std::multimap<size_t, void *> cache;
     size_t bytes_live = 0;
 
-    // Library-owned scratch (split-K partials; attention recompute buffers), grown on demand.
-    void *scratch = nullptr;
-    size_t scratch_bytes = 0;
-    void *attn_scratch = nullptr;
-    size_t attn_scratch_bytes = 0;
+    // Library-owned scratch (split-K partials; attention recompute buffers), grown on demand, one
+    // set per stream so concurrent main and side launches never share it.
+    void *scratch[2] = {nullptr, nullptr};
+    size_t scratch_bytes[2] = {0, 0};
+    void *attn_scratch[2] = {nullptr, nullptr};
+    size_t attn_scratch_bytes[2] = {0, 0};
 
     // True between it_capture_begin and it_capture_end: nothing may allocate.
     bool capturing = false;
@@ -80,7 +87,12 @@ struct it_graph {
 
 namespace it {
 
-// Grows the context scratch to at least `bytes` (synchronises before freeing the old block).
+// Waits for both streams.
+it_status sync_all(it_context *ctx);
+// Makes the main stream wait for the side stream's pending work.
+it_status join_side(it_context *ctx);
+
+// Grows the current stream's scratch to at least `bytes` (synchronises before freeing the old block).
 it_status ensure_scratch(it_context *ctx, size_t bytes, void **out);
 it_status ensure_attn_scratch(it_context *ctx, size_t bytes, void **out);
 

@@ -30,13 +30,27 @@ it_status fail_hip(hipError_t err, const char *what) {
 
 void clear_error() { g_last_error.clear(); }
 
+it_status sync_all(it_context *ctx) {
+    IT_HIP_TRY(hipStreamSynchronize(ctx->main_stream));
+    IT_HIP_TRY(hipStreamSynchronize(ctx->side_stream));
+    return IT_OK;
+}
+
+it_status join_side(it_context *ctx) {
+    if (!ctx->side_pending) return IT_OK;
+    IT_HIP_TRY(hipEventRecord(ctx->join_ev, ctx->side_stream));
+    IT_HIP_TRY(hipStreamWaitEvent(ctx->main_stream, ctx->join_ev, 0));
+    ctx->side_pending = false;
+    return IT_OK;
+}
+
 static it_status grow(it_context *ctx, void *&buf, size_t &have, size_t bytes, void **out) {
     if (have < bytes && ctx->capturing)
         return fail(IT_ERR_INVALID, "scratch of " + std::to_string(bytes) +
                                         " bytes needed during graph capture: run the work once before capturing");
     if (have < bytes) {
         if (buf) {
-            IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+            if (const it_status st_ = sync_all(ctx); st_ != IT_OK) return st_;
             IT_HIP_TRY(hipFree(buf));
             buf = nullptr;
             have = 0;
@@ -50,11 +64,11 @@ static it_status grow(it_context *ctx, void *&buf, size_t &have, size_t bytes, v
 }
 
 it_status ensure_scratch(it_context *ctx, size_t bytes, void **out) {
-    return grow(ctx, ctx->scratch, ctx->scratch_bytes, bytes, out);
+    return grow(ctx, ctx->scratch[ctx->cur], ctx->scratch_bytes[ctx->cur], bytes, out);
 }
 
 it_status ensure_attn_scratch(it_context *ctx, size_t bytes, void **out) {
-    return grow(ctx, ctx->attn_scratch, ctx->attn_scratch_bytes, bytes, out);
+    return grow(ctx, ctx->attn_scratch[ctx->cur], ctx->attn_scratch_bytes[ctx->cur], bytes, out);
 }
 
 static hipEvent_t pool_event(it_context *ctx) {
@@ -87,7 +101,7 @@ void profile_end(it_context *ctx, const std::string &key, hipEvent_t start) {
 
 static it_status profile_drain(it_context *ctx) {
     if (ctx->pending.empty()) return IT_OK;
-    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (const it_status st_ = sync_all(ctx); st_ != IT_OK) return st_;
     for (auto &r : ctx->pending) {
         float ms = 0.f;
         IT_HIP_TRY(hipEventElapsedTime(&ms, r.start, r.stop));
@@ -149,11 +163,18 @@ it_status it_init(int device, it_context **out_ctx) {
     ctx->clock_khz = prop.clockRate;
     std::snprintf(ctx->name, sizeof(ctx->name), "%s", prop.gcnArchName);
     // Default priority only: streams of mixed priority are avoided on purpose.
-    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    hipError_t e = hipStreamCreateWithFlags(&ctx->main_stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming);
     if (e != hipSuccess) {
+        if (ctx->main_stream) (void)hipStreamDestroy(ctx->main_stream);
+        if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
+        if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
         delete ctx;
-        return it::fail_hip(e, "hipStreamCreateWithFlags");
+        return it::fail_hip(e, "stream/event creation");
     }
+    ctx->stream = ctx->main_stream;
     *out_ctx = ctx;
     it::clear_error();
     return IT_OK;
@@ -162,7 +183,7 @@ it_status it_init(int device, it_context **out_ctx) {
 it_status it_shutdown(it_context *ctx) {
     if (!ctx) return fail(IT_ERR_NULL, "it_shutdown: ctx is NULL");
     (void)hipSetDevice(ctx->device);
-    (void)hipStreamSynchronize(ctx->stream);
+    (void)it::sync_all(ctx);
     for (auto &r : ctx->pending) {
         (void)hipEventDestroy(r.start);
         (void)hipEventDestroy(r.stop);
@@ -170,9 +191,14 @@ it_status it_shutdown(it_context *ctx) {
     for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
     for (auto &kv : ctx->cache) (void)hipFree(kv.second);
     for (auto &kv : ctx->live) (void)hipFree(kv.first);
-    if (ctx->scratch) (void)hipFree(ctx->scratch);
-    if (ctx->attn_scratch) (void)hipFree(ctx->attn_scratch);
-    (void)hipStreamDestroy(ctx->stream);
+    for (int i = 0; i < 2; ++i) {
+        if (ctx->scratch[i]) (void)hipFree(ctx->scratch[i]);
+        if (ctx->attn_scratch[i]) (void)hipFree(ctx->attn_scratch[i]);
+    }
+    (void)hipEventDestroy(ctx->fork_ev);
+    (void)hipEventDestroy(ctx->join_ev);
+    (void)hipStreamDestroy(ctx->main_stream);
+    (void)hipStreamDestroy(ctx->side_stream);
     delete ctx;
     return IT_OK;
 }
@@ -204,7 +230,7 @@ it_status it_malloc(it_context *ctx, size_t bytes, void **out_ptr) {
         hipError_t e = hipMalloc(&p, sz);
         if (e != hipSuccess) {
             // Release the cache once and retry before giving up.
-            (void)hipStreamSynchronize(ctx->stream);
+            (void)it::sync_all(ctx);
             for (auto &kv : ctx->cache) (void)hipFree(kv.second);
             ctx->cache.clear();
             (void)hipGetLastError();
@@ -225,6 +251,8 @@ it_status it_free(it_context *ctx, void *ptr) {
     if (!ptr) return IT_OK;
     auto it = ctx->live.find(ptr);
     if (it == ctx->live.end()) return fail(IT_ERR_INVALID, "it_free: pointer not from it_malloc");
+    // The block may be reused by the next main-stream allocation: order that after pending side work.
+    if (const it_status st_ = it::join_side(ctx); st_ != IT_OK) return st_;
     ctx->bytes_live -= it->second;
     ctx->cache.emplace(it->second, ptr);
     ctx->live.erase(it);
@@ -235,7 +263,7 @@ size_t it_mem_allocated(it_context *ctx) { return ctx ? ctx->bytes_live : 0; }
 
 it_status it_empty_cache(it_context *ctx) {
     if (!ctx) return fail(IT_ERR_NULL, "it_empty_cache: ctx is NULL");
-    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (const it_status st_ = it::sync_all(ctx); st_ != IT_OK) return st_;
     for (auto &kv : ctx->cache) IT_HIP_TRY(hipFree(kv.second));
     ctx->cache.clear();
     return IT_OK;
@@ -253,8 +281,10 @@ it_status it_memcpy_h2d(it_context *ctx, void *dst, const void *src, size_t byte
 it_status it_memcpy_d2h(it_context *ctx, void *dst, const void *src, size_t bytes) {
     if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(IT_ERR_NULL, "it_memcpy_d2h: NULL");
     if (!bytes) return IT_OK;
-    IT_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
-    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    // Results may come from either stream: read after both.
+    if (const it_status st_ = it::join_side(ctx); st_ != IT_OK) return st_;
+    IT_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->main_stream));
+    IT_HIP_TRY(hipStreamSynchronize(ctx->main_stream));
     return IT_OK;
 }
 
@@ -273,8 +303,33 @@ it_status it_zero(it_context *ctx, void *dst, size_t bytes) {
 
 it_status it_stream_sync(it_context *ctx) {
     if (!ctx) return fail(IT_ERR_NULL, "it_stream_sync: ctx is NULL");
-    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (const it_status st_ = it::join_side(ctx); st_ != IT_OK) return st_;
+    return it::sync_all(ctx);
+}
+
+it_status it_side_begin(it_context *ctx) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_side_begin: ctx is NULL");
+    if (ctx->cur != 0) return fail(IT_ERR_INVALID, "it_side_begin: already on the side stream");
+    IT_HIP_TRY(hipEventRecord(ctx->fork_ev, ctx->main_stream));
+    IT_HIP_TRY(hipStreamWaitEvent(ctx->side_stream, ctx->fork_ev, 0));
+    ctx->cur = 1;
+    ctx->stream = ctx->side_stream;
+    ctx->side_pending = true;
     return IT_OK;
+}
+
+it_status it_side_end(it_context *ctx) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_side_end: ctx is NULL");
+    if (ctx->cur != 1) return fail(IT_ERR_INVALID, "it_side_end: not on the side stream");
+    ctx->cur = 0;
+    ctx->stream = ctx->main_stream;
+    return IT_OK;
+}
+
+it_status it_side_join(it_context *ctx) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_side_join: ctx is NULL");
+    if (ctx->cur != 0) return fail(IT_ERR_INVALID, "it_side_join: call it_side_end first");
+    return it::join_side(ctx);
 }
 
 void *it_stream(it_context *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
@@ -327,7 +382,11 @@ it_status it_event_destroy(it_event *ev) {
 it_status it_capture_begin(it_context *ctx) {
     if (!ctx) return fail(IT_ERR_NULL, "it_capture_begin: ctx is NULL");
     if (ctx->capturing) return fail(IT_ERR_INVALID, "it_capture_begin: already capturing");
-    IT_HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    if (ctx->cur != 0) return fail(IT_ERR_INVALID, "it_capture_begin: call it_side_end first");
+    // Side work issued before the capture must not become a dependency of the graph.
+    if (ctx->side_pending) IT_HIP_TRY(hipStreamSynchronize(ctx->side_stream));
+    ctx->side_pending = false;
+    IT_HIP_TRY(hipStreamBeginCapture(ctx->main_stream, hipStreamCaptureModeThreadLocal));
     ctx->capturing = true;
     return IT_OK;
 }
@@ -335,10 +394,17 @@ it_status it_capture_begin(it_context *ctx) {
 it_status it_capture_end(it_context *ctx, it_graph **out_graph) {
     if (!ctx || !out_graph) return fail(IT_ERR_NULL, "it_capture_end: NULL argument");
     if (!ctx->capturing) return fail(IT_ERR_INVALID, "it_capture_end: not capturing");
-    ctx->capturing = false;
     *out_graph = nullptr;
+    if (ctx->cur != 0) {
+        ctx->cur = 0;
+        ctx->stream = ctx->main_stream;
+    }
+    // The side stream rejoins the main stream inside the capture (a forked stream must).
+    const it_status js = it::join_side(ctx);
+    ctx->capturing = false;
     auto *g = new it_graph();
-    hipError_t e = hipStreamEndCapture(ctx->stream, &g->graph);
+    hipError_t e = hipStreamEndCapture(ctx->main_stream, &g->graph);
+    if (js != IT_OK && e == hipSuccess) e = hipErrorInvalidValue;
     if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         if (g->graph) (void)hipGraphDestroy(g->graph);
@@ -351,7 +417,7 @@ it_status it_capture_end(it_context *ctx, it_graph **out_graph) {
 
 it_status it_graph_launch(it_context *ctx, it_graph *graph) {
     if (!ctx || !graph) return fail(IT_ERR_NULL, "it_graph_launch: NULL argument");
-    IT_HIP_TRY(hipGraphLaunch(graph->exec, ctx->stream));
+    IT_HIP_TRY(hipGraphLaunch(graph->exec, ctx->main_stream));
     return IT_OK;
 }
 

@@ -72,7 +72,7 @@ class GemmStep:
 
     def __init__(self, shape: ModelShape, precision: Precision = Precision.FP32,
                  ctx: Optional[Context] = None, seed: int = 1234, fused_attention: Optional[bool] = None,
-                 pooled_data: bool = False, ffn_bias: bool = False):
+                 pooled_data: bool = False, ffn_bias: bool = False, overlap_weight_grads: bool = True):
         if shape.heads * shape.head_dim != shape.hidden:
             raise ValueError("heads * head_dim must equal hidden")
         self.s = shape
@@ -85,6 +85,9 @@ class GemmStep:
         bh = s.batch * s.heads
         self._seed = seed
         self._pooled = pooled_data  # timing-only inputs from synth.pooled_normal (fast at MED sizes)
+        # Weight gradients run on the context's side stream, beside the data-gradient chain; each
+        # is issued right after the main-stream op that produces its upstream gradient.
+        self.overlap = overlap_weight_grads
 
         def w(shape_, std=0.02):
             return self._tensor(shape_, std)
@@ -128,7 +131,10 @@ class GemmStep:
         self.dHh = empty([T, F], Precision.FP32)
         self.dX2 = empty([T, H], Precision.FP32)
         self.dOp = empty([T, H], Precision.FP32)
-        self.dQKV = empty([T, 3 * H], Precision.FP32)
+        # One dQKV per layer: a layer's qkv.dW (side stream) may still read it while the next layer's
+        # attention backward (main stream) writes its own.
+        self.dQKV_layers = [empty([T, 3 * H], Precision.FP32) for _ in range(L)]
+        self.dQKV = self.dQKV_layers[0]
         self.dX = empty([T, H], Precision.FP32)
         self.dWd = [empty([H, F], Precision.FP32) for _ in range(L)]
         self.dWgu = [empty([2 * F, H], Precision.FP32) for _ in range(L)]
@@ -176,6 +182,16 @@ class GemmStep:
             if key not in self._calls:
                 self._calls[key] = (name, A, B, Cout, ta, tb, M, N, K, alpha, epi, a_off, lda)
 
+    def _dw(self, *args, **kw):
+        """A weight-gradient GEMM, on the side stream when overlapping."""
+        if not self.overlap:
+            return self._gemm(*args, **kw)
+        check(self.lib.it_side_begin(self.ctx.handle), "side stream")
+        try:
+            self._gemm(*args, **kw)
+        finally:
+            check(self.lib.it_side_end(self.ctx.handle), "side stream")
+
     def _layouts(self):
         s = self.s
         qkv = _lib.AttnLayout(s.heads, s.seq * 3 * s.hidden, s.head_dim, 3 * s.hidden)
@@ -218,19 +234,19 @@ class GemmStep:
         s, P = self.s, self.prec
         T, H, F = s.tokens, s.hidden, s.ffn
         # down: dHh = dZ.Wd (NN), dWd = dZ^T.Hh (TN)
+        self._dw("down.dW", self.dZ, self.Hh[l], self.dWd[l], True, False, H, F, T)
         self._gemm("down.dX", self.dZ, self.Wd[l], self.dHh, False, False, T, F, H)
-        self._gemm("down.dW", self.dZ, self.Hh[l], self.dWd[l], True, False, H, F, T)
         # gate|up: dX2 = [dG dU].[Wg;Wu] (NN, K = 2F), dWgu = [dG dU]^T.X2 (TN)
+        self._dw("gate_up.dW", self.dGU, self.X2[l], self.dWgu[l], True, False, 2 * F, H, T)
         self._gemm("gate_up.dX", self.dGU, self.Wgu[l], self.dX2, False, False, T, H, 2 * F)
-        self._gemm("gate_up.dW", self.dGU, self.X2[l], self.dWgu[l], True, False, 2 * F, H, T)
         # Wo: dO = dY.Wo (NN), dWo = dY^T.O (TN)
+        self._dw("wo.dW", self.dY, self.Oin[l], self.dWo[l], True, False, H, H, T)
         self._gemm("wo.dX", self.dY, self.Wo[l], self.dOp, False, False, T, H, H)
-        self._gemm("wo.dW", self.dY, self.Oin[l], self.dWo[l], True, False, H, H, T)
         # attention_backward_recompute into the dQKV buffer (f32, same [B,S,3,H,D] layout)
         qkv, o = self._layouts()
         eb = P.byte_size()
         base = self.QKV[l].ptr
-        dbase = self.dQKV.ptr
+        dbase = self.dQKV_layers[l].ptr
         q, k, v = (C.c_void_p(base + i * H * eb) for i in range(3))
         dq, dk, dv = (C.c_void_p(dbase + i * H * 4) for i in range(3))
         if self.fused:
@@ -251,9 +267,9 @@ class GemmStep:
             self.launches += [_Launch(n, attn) for n in ("attn.S", "attn.dV", "attn.dP", "attn.dQ", "attn.dK")]
         # QKV: dX = dQKV.Wqkv (NN), dWqkv = dQKV^T.X (TN). dQKV is f32; in BF16 mode the
         # projection backward reads the seeded BF16 gradient stand-in instead.
-        dqkv = self.dQKV if P is Precision.FP32 else self._dqkv_bf16()
+        dqkv = self.dQKV_layers[l] if P is Precision.FP32 else self._dqkv_bf16()
+        self._dw("qkv.dW", dqkv, self.X[l], self.dWqkv[l], True, False, 3 * H, H, T)
         self._gemm("qkv.dX", dqkv, self.Wqkv[l], self.dX, False, False, T, H, 3 * H)
-        self._gemm("qkv.dW", dqkv, self.X[l], self.dWqkv[l], True, False, 3 * H, H, T)
 
     def _dqkv_bf16(self) -> Tensor:
         if not hasattr(self, "_dqkv16"):
@@ -268,10 +284,12 @@ class GemmStep:
         for l in range(s.layers):
             self.forward_layer(l)
         self._gemm("lm_head", self.Hf, self.E, self.logits, False, True, s.tokens, s.vocab, s.hidden)
-        self._gemm("lm_head.dW", self.dlogits, self.Hf, self.dE, True, False, s.vocab, s.hidden, s.tokens)
+        self._dw("lm_head.dW", self.dlogits, self.Hf, self.dE, True, False, s.vocab, s.hidden, s.tokens)
         self._gemm("lm_head.dX", self.dlogits, self.E, self.dHf, False, False, s.tokens, s.hidden, s.vocab)
         for l in reversed(range(s.layers)):
             self.backward_layer(l)
+        if self.overlap:
+            check(self.lib.it_side_join(self.ctx.handle), "side stream")
         self._record = False
 
     def reissue(self, ta: bool, tb: bool, M: int, N: int, K: int) -> str:
