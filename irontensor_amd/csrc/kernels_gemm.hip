@@ -363,8 +363,10 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
     constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
     using OA = Operand<T, !TA, BM>;
     using OB = Operand<T, TB, BN>;
+    using OBH = Operand<T, TB, BN / 2>;  // DUAL: gate and up halves of the B tile
+    static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
     constexpr int SA = OA::STAGE_BYTES, SB = OB::STAGE_BYTES;
-    constexpr int STAGE = SA + SB * (DUAL ? 2 : 1);
+    constexpr int STAGE = SA + SB;
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -378,7 +380,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
     const T *B = (const T *)p.B + bo * p.sB_out + bi * p.sB_in;
     const T *B2 = DUAL ? (const T *)p.B2 + bo * p.sB_out + bi * p.sB_in : nullptr;
     const int64_t coff = bo * p.sC_out + bi * p.sC_in;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (DUAL ? BN / 2 : BN);
 
     if (p.causal != CAUSAL_NONE && n0 > m0 + BM - 1 + p.causal_offset) {
         // Entire tile is above the diagonal: no products needed.
@@ -398,21 +400,28 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
     const int ntiles = ke > kb ? (int)((ke - kb + BK - 1) / BK) : 0;
 
     f32x4 acc[FM][FN];
-    f32x4 acc2[DUAL ? FM : 1][DUAL ? FN : 1];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (DUAL) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) acc2[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
 
     OA oa;
-    OB ob, ob2;
-    if constexpr (!DUAL) {
+    // SwiGLU (DUAL): the B tile's rows 0..BN/2-1 are gate-weight rows and BN/2..BN-1 the same up-
+    // weight rows, so waves wn = 0 / 1 accumulate gate / up of one BM x BN/2 output tile and the
+    // loop is the ordinary one.
+    std::conditional_t<DUAL, OBH, OB> ob;
+    std::conditional_t<DUAL, OBH, char> ob2;
+    auto gload = [&](int64_t k0) {
+        oa.template load<LM>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
+        ob.template load<LM>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
+        if constexpr (DUAL) ob2.template load<LM>(B2, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
+    };
+    auto gstore = [&](char *st) {
+        oa.store(st, tid);
+        ob.store(st + SA, tid);
+        if constexpr (DUAL) ob2.store(st + SA + OBH::STAGE_BYTES, tid);
+    };
+    {
         // Software-pipelined loop: fragments of k-step 1 are read while the MFMAs of k-step 0
         // issue; the next tile's global loads go out with k-step 0 and land in the other LDS stage
         // during k-step 1; the prefetch after the last tile re-reads it into a dead stage.
@@ -437,10 +446,8 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
             constexpr int VMR = OA::ITERS * OA::LOADS + OB::ITERS * OB::LOADS;
             constexpr int DSW = OA::ITERS * (OA::TRANSPOSE ? 8 : 1) + OB::ITERS * (OB::TRANSPOSE ? 8 : 1);
             constexpr int G = MF < 8 ? MF : 8;
-            oa.template load<LM>(A, p.lda, m0, kb, p.M, ke, p.a_vec_ok, tid);
-            ob.template load<LM>(B, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
-            oa.store(smem, tid);
-            ob.store(smem + SA, tid);
+            gload(kb);
+            gstore(smem);
             __syncthreads();
             frags(fa0, fb0, smem, 0);
             for (int t = 0; t < ntiles; ++t) {
@@ -448,11 +455,9 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
                 char *nxt = smem + ((t + 1) & 1) * STAGE;
                 const int64_t k1 = kb + (int64_t)min(t + 1, last) * BK;
                 frags(fa1, fb1, cur, 1);
-                oa.template load<LM>(A, p.lda, m0, k1, p.M, ke, p.a_vec_ok, tid);
-                ob.template load<LM>(B, p.ldb, n0, k1, p.N, ke, p.b_vec_ok, tid);
+                gload(k1);
                 mmas(fa0, fb0);
-                oa.store(nxt, tid);
-                ob.store(nxt + SA, tid);
+                gstore(nxt);
                 mmas(fa1, fb1);
                 if constexpr (LM != LOAD_CHECKED) {
 #pragma unroll
@@ -471,56 +476,12 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
                 frags(fa0, fb0, nxt, 0);
             }
         }
-    } else {
-        if (ntiles > 0) {
-            oa.template load<LM>(A, p.lda, m0, kb, p.M, ke, p.a_vec_ok, tid);
-            ob.template load<LM>(B, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
-            ob2.template load<LM>(B2, p.ldb, n0, kb, p.N, ke, p.b_vec_ok, tid);
-            oa.store(smem, tid);
-            ob.store(smem + SA, tid);
-            ob2.store(smem + SA + SB, tid);
-            __syncthreads();
-        }
-        for (int t = 0; t < ntiles; ++t) {
-            char *cur = smem + (t & 1) * STAGE;
-            char *nxt = smem + ((t + 1) & 1) * STAGE;
-            const bool more = t + 1 < ntiles;
-            if (more) {
-                const int64_t k = kb + (int64_t)(t + 1) * BK;
-                oa.template load<LM>(A, p.lda, m0, k, p.M, ke, p.a_vec_ok, tid);
-                ob.template load<LM>(B, p.ldb, n0, k, p.N, ke, p.b_vec_ok, tid);
-                ob2.template load<LM>(B2, p.ldb, n0, k, p.N, ke, p.b_vec_ok, tid);
-            }
-#pragma unroll
-            for (int ks = 0; ks < BK / ET<T>::KSTEP; ++ks) {
-                u32x4 af[FM], bfr[FN];
-#pragma unroll
-                for (int i = 0; i < FM; ++i) af[i] = OA::frag(cur, wm * WTM + i * 16, ks, lane);
-#pragma unroll
-                for (int j = 0; j < FN; ++j) bfr[j] = OB::frag(cur + SA, wn * WTN + j * 16, ks, lane);
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j) mma<T>(acc[i][j], af[i], bfr[j]);
-#pragma unroll
-                for (int j = 0; j < FN; ++j) bfr[j] = OB::frag(cur + SA + SB, wn * WTN + j * 16, ks, lane);
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j) mma<T>(acc2[i][j], af[i], bfr[j]);
-            }
-            if (more) {
-                oa.store(nxt, tid);
-                ob.store(nxt + SA, tid);
-                ob2.store(nxt + SA + SB, tid);
-            }
-            __syncthreads();
-        }
     }
 
-    if constexpr (!DUAL) {
+    {
         // Epilogue through LDS: each wave stages half of its tile (WTM x WTN/2 f32) with static
-        // register indices, then finishes it row-major with 4-column vectors.
+        // register indices, then finishes it row-major with 4-column vectors (DUAL: the gate and
+        // up waves of a row half finish their slice together).
         // Lane l of a 16x16 MFMA block holds rows 4*(l/16)+r (r = 0..3), column l%16.
         constexpr int EC = WTN / 2, EP = EC * 4 + 16;
         static_assert(4 * WTM * EP <= 2 * STAGE, "epilogue staging fits in the operand stages");
@@ -539,36 +500,27 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
                         *(float *)(wl + rl * EP + cl * 4) = acc[i][h * (FN / 2) + jj][r];
                     }
             __syncthreads();
-            for (int it = 0; it < WTM * EC / 256; ++it) {
-                const int e = (it * 64 + lane) * 4;
-                const int rl = e / EC, cl = e % EC;
-                const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
-                finish4<true>(p, v, m0 + wm * WTM + rl, n0 + wn * WTN + h * EC + cl, coff, z);
+            if constexpr (DUAL) {
+                const char *gl = smem + (wm * 2) * (WTM * EP), *ul = gl + WTM * EP;
+                const int pt = wn * 64 + lane;
+                for (int it = 0; it < (WTM * EC + 511) / 512; ++it) {
+                    const int e = (it * 128 + pt) * 4;
+                    if (WTM * EC % 512 != 0 && e >= WTM * EC) break;
+                    const int rl = e / EC, cl = e % EC;
+                    finish_swiglu4<true>(p, *(const f32x4 *)(gl + rl * EP + cl * 4),
+                                         *(const f32x4 *)(ul + rl * EP + cl * 4), m0 + wm * WTM + rl,
+                                         n0 + h * EC + cl, coff);
+                }
+            } else {
+                for (int it = 0; it < WTM * EC / 256; ++it) {
+                    const int e = (it * 64 + lane) * 4;
+                    const int rl = e / EC, cl = e % EC;
+                    const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
+                    finish4<true>(p, v, m0 + wm * WTM + rl, n0 + wn * WTN + h * EC + cl, coff, z);
+                }
             }
             __syncthreads();
         }
-    } else {
-        // SwiGLU epilogue per element: gate, up (each with its bias) and silu(gate) * up.
-        const int64_t rbase = m0 + wm * WTM + (lane >> 4) * 4;
-        const int64_t cbase = n0 + wn * WTN + (lane & 15);
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t row = rbase + i * 16 + r, col = cbase + j * 16;
-                    if (row >= p.M || col >= p.N) continue;
-                    const int64_t idx = coff + row * p.ldc + col;
-                    float g = p.alpha * acc[i][j][r], u = p.alpha * acc2[i][j][r];
-                    if (p.has_bias) {  // [gate bias | up bias], N each
-                        g += p.bias[col];
-                        u += p.bias[p.N + col];
-                    }
-                    if (p.G) store_out(p.G, idx, g, p.out_bf16);
-                    if (p.U) store_out(p.U, idx, u, p.out_bf16);
-                    store_out(p.C, idx, silu(g) * u, p.out_bf16);
-                }
     }
 }
 
@@ -839,9 +791,10 @@ struct Plan {
 
 // Picks the tile shape and split-K factor with a cost model fitted to MI355X timings of these
 // kernels (every tile / split choice on the TINY and medium step shapes, the square sweep and the
-// decode shapes: over those 42 shapes its picks take 1.9% longer in total than the fastest
+// decode shapes: over those 42 shapes its picks take 0.5% longer in total than the fastest
 // measured plans):
-//   * a CU runs up to `occ` blocks at once, sharing its MFMA rate;
+//   * a CU runs up to `occ` blocks at once, sharing its MFMA rate (a lone block where two could
+//     run reaches 90% of the tile's efficiency);
 //   * each round of blocks pays a fixed prologue/epilogue cost;
 //   * a k-step costs the larger of its MFMA time (at the tile's steady-state efficiency, times
 //     the blocks sharing the CU) and a memory-latency floor: with one tile of prefetch, a block
@@ -854,11 +807,8 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
         int b, occ;
         double eff;
     };
-    // The dual-B (SwiGLU) form of the 64/128 kernels keeps two B tiles in LDS, which halves its
-    // occupancy, and uses the unpipelined loop: lower efficiencies for it. The 256 kernel's dual
-    // form runs its usual loop.
-    const Cand f32c[] = {{128, a.dual ? 1 : 2, a.dual ? 0.45 : 0.70}, {64, a.dual ? 2 : 4, 0.60}};
-    const Cand b16c[] = {{256, 1, 0.50}, {128, a.dual ? 1 : 2, a.dual ? 0.25 : 0.40}, {64, a.dual ? 2 : 4, 0.15}};
+    const Cand f32c[] = {{128, 2, 0.70}, {64, 4, 0.60}};
+    const Cand b16c[] = {{256, 1, 0.50}, {128, 2, 0.40}, {64, 4, 0.15}};
     const Cand *cands = bf16 ? b16c : f32c;
     const int ncand = bf16 ? 3 : 2;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
@@ -871,8 +821,8 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
     int64_t best_blocks = 0;
     for (int c = 0; c < ncand; ++c) {
         const Cand &cd = cands[c];
-        // The 256 kernel's dual form covers 256 x 128 outputs (its 256 B rows are gate and up).
-        const int bn = cd.b == 256 && a.dual ? 128 : cd.b;
+        // A dual (SwiGLU) tile covers b x b/2 outputs: its b B-tile rows are gate and up halves.
+        const int bn = a.dual ? cd.b / 2 : cd.b;
         const int64_t tiles = cdiv(a.M, cd.b) * cdiv(a.N, bn) * a.batch;
         if (cd.b == 256) {
             const double fill = (double)a.M * a.N * a.batch / ((double)tiles * 256.0 * bn);
@@ -888,7 +838,9 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
             const int64_t conc = std::min<int64_t>(per_cu, cd.occ);
             const int64_t rounds = cdiv(per_cu, cd.occ);
             const int64_t ksteps = std::max<int64_t>(1, cdiv(kps, bk));
-            const double step = (a.dual ? 4.0 : 2.0) * cd.b * bn * bk / (cu_peak * cd.eff);
+            // A lone block on a CU whose tile could run two at once hides less latency.
+            const double eff = conc == 1 && cd.occ > 1 ? 0.9 * cd.eff : cd.eff;
+            const double step = (a.dual ? 4.0 : 2.0) * cd.b * bn * bk / (cu_peak * eff);
             double t = rounds * (round_overhead + ksteps * std::max(conc * step, step_floor));
             if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
             // Near ties (3%) keep the earlier, larger and less split plan, except that between two
