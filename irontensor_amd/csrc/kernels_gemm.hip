@@ -253,12 +253,12 @@ __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf
 
 // Final values of 4 consecutive output columns (the vector form of finish_store), or raw partial
 // sums for split-K. Falls back to element stores at the right edge or for unaligned outputs.
-template <bool EDGE>
+template <bool EDGE, bool FINAL = false>
 __device__ __forceinline__ void finish4(const GemmArgs &p, f32x4 v, int64_t row, int64_t col,
                                         int64_t coff, int64_t z) {
     if (EDGE && (row >= p.M || col >= p.N)) return;
     const bool full = !EDGE || col + 4 <= p.N;
-    if (p.splits > 1) {
+    if (!FINAL && p.splits > 1) {
         float *dst = p.partial + (z * p.M + row) * p.N + col;
         if (full && p.N % 4 == 0) {
             *(f32x4 *)dst = v;
@@ -722,6 +722,22 @@ __global__ __launch_bounds__(256) void splitk_reduce(const GemmArgs p) {
     }
 }
 
+// The same reduction 4 columns per thread (N % 4 == 0): 16-byte partial loads and the vector
+// epilogue. Splits are summed in the same order, so results equal the scalar form's.
+__global__ __launch_bounds__(256) void splitk_reduce4(const GemmArgs p) {
+    const int64_t total = p.batch * p.M * p.N;
+    const int64_t mn = p.M * p.N, total4 = total / 4;
+    for (int64_t e4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e4 < total4;
+         e4 += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t e = e4 * 4;
+        const int64_t b = e / mn, rem = e % mn, row = rem / p.N, col = rem % p.N;
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < p.splits; ++sp) s += *(const f32x4 *)(p.partial + (int64_t)sp * total + e);
+        const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
+        finish4<false, true>(p, s, row, col, bo * p.sC_out + bi * p.sC_in, 0);
+    }
+}
+
 struct TileCfg {
     int bm, bn;
 };
@@ -862,6 +878,12 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
 
 it_status launch_splitk_reduce(hipStream_t s, const GemmArgs &a) {
     const int64_t total = a.batch * a.M * a.N;
+    if (a.N % 4 == 0) {
+        const int64_t blocks = std::min<int64_t>(cdiv(total / 4, 256), 65536);
+        hipLaunchKernelGGL(splitk_reduce4, dim3((unsigned)blocks), dim3(256), 0, s, a);
+        IT_HIP_TRY(hipGetLastError());
+        return IT_OK;
+    }
     const int64_t blocks = std::min<int64_t>(cdiv(total, 256), 65536);
     hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)blocks), dim3(256), 0, s, a);
     IT_HIP_TRY(hipGetLastError());
