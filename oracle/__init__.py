@@ -52,6 +52,17 @@ def load() -> C.CDLL:
     lib.ref_attention_fwd_bhsd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, C.c_float, i, i]
     lib.ref_attention_bwd_bhsd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, C.c_float, i, i]
     lib.ref_default_threads.restype = i
+    f = C.c_float
+    lib.ref_rmsnorm_forward.argtypes = [vp, vp, vp, i64, i64, f]
+    lib.ref_rmsnorm_backward.argtypes = [vp, vp, vp, vp, vp, i64, i64, f]
+    lib.ref_rope.argtypes = [vp, i64, i64, i64, i64, i64, f, i64, i]
+    lib.ref_embedding_forward.argtypes = [vp, vp, vp, i64, i64]
+    lib.ref_embedding_backward.argtypes = [vp, vp, vp, i64, i64, i64]
+    lib.ref_cross_entropy.argtypes = [vp, vp, vp, vp, i64, i64]
+    lib.ref_cross_entropy.restype = f
+    lib.ref_lion.argtypes = [vp, vp, vp, i64, f, f, f, f, f]
+    lib.ref_sum_squares.argtypes = [vp, i64]
+    lib.ref_sum_squares.restype = C.c_double
     _lib = lib
     return lib
 
@@ -193,3 +204,70 @@ def attention_bwd_bhsd(d_o, q, k, v, scale: float, causal: bool, threads=None):
     load().ref_attention_bwd_bhsd(_p(d_o), _p(q), _p(k), _p(v), _p(dq), _p(dk), _p(dv), bh, s, d,
                                   float(scale), int(causal), threads or default_threads())
     return dq, dk, dv
+
+
+# ---------------------------------------------------------------- training-step ops (train_ref.c)
+
+def rmsnorm(x, gamma, eps: float = 1e-5) -> np.ndarray:
+    x, g = _c(x, np.float32), _c(gamma, np.float32)
+    dim = x.shape[-1]
+    y = np.empty_like(x)
+    load().ref_rmsnorm_forward(_p(x), _p(g), _p(y), x.size // dim, dim, float(eps))
+    return y
+
+
+def rmsnorm_backward(dy, x, gamma, eps: float = 1e-5):
+    dy, x, g = _c(dy, np.float32), _c(x, np.float32), _c(gamma, np.float32)
+    dim = x.shape[-1]
+    dx, dg = np.empty_like(x), np.empty(dim, np.float32)
+    load().ref_rmsnorm_backward(_p(dy), _p(x), _p(g), _p(dx), _p(dg), x.size // dim, dim, float(eps))
+    return dx, dg
+
+
+def rope(x, base: float = 10000.0, offset: int = 0, backward: bool = False, heads=None, head_dim=None):
+    """x: [batch, seq, heads, head_dim] (or [batch, seq, cols] with heads*head_dim <= cols and the
+    rotated block at column 0); returns a rotated copy."""
+    y = _c(x, np.float32).copy()
+    if y.ndim == 4:
+        b, s, h, d = y.shape
+        rs = h * d
+    else:
+        b, s, rs = y.shape
+        h, d = heads, head_dim
+    load().ref_rope(_p(y), b, s, h, d, rs, float(base), int(offset), int(backward))
+    return y
+
+
+def embedding(table, ids) -> np.ndarray:
+    t, ids = _c(table, np.float32), _c(ids, np.uint32)
+    out = np.empty((ids.size, t.shape[1]), np.float32)
+    load().ref_embedding_forward(_p(t), _p(ids), _p(out), ids.size, t.shape[1])
+    return out
+
+
+def embedding_backward(dy, ids, vocab: int) -> np.ndarray:
+    dy, ids = _c(dy, np.float32), _c(ids, np.uint32)
+    dw = np.empty((vocab, dy.shape[1]), np.float32)
+    load().ref_embedding_backward(_p(dy), _p(ids), _p(dw), ids.size, dy.shape[1], vocab)
+    return dw
+
+
+def cross_entropy(logits, targets):
+    """Returns (mean_loss, per-row losses, grad_logits)."""
+    x, t = _c(logits, np.float32), _c(targets, np.uint32)
+    rows, vocab = x.shape
+    losses, grad = np.empty(rows, np.float32), np.empty_like(x)
+    mean = load().ref_cross_entropy(_p(x), _p(t), _p(losses), _p(grad), rows, vocab)
+    return float(np.float32(mean)), losses, grad
+
+
+def lion(w, m, g, lr: float, beta1: float, beta2: float, wd: float, scale: float = 1.0):
+    """Returns updated copies (w, m)."""
+    w, m, g = _c(w, np.float32).copy(), _c(m, np.float32).copy(), _c(g, np.float32)
+    load().ref_lion(_p(w), _p(m), _p(g), w.size, float(lr), float(beta1), float(beta2), float(wd), float(scale))
+    return w, m
+
+
+def sum_squares(x) -> float:
+    x = _c(x, np.float32)
+    return float(load().ref_sum_squares(_p(x), x.size))

@@ -118,6 +118,25 @@ void ref_attention_bwd_bhsd(const float *dO, const float *q, const float *k, con
 /* Number of hardware threads the oracle would use by default (sysconf). */
 int ref_default_threads(void);
 
+/* ---- training-step ops around the contractions (train_ref.c) ----
+ * Pinning (tests/test_oracle_train.py): rmsnorm closed forms (constant rows, gamma scaling) and a
+ * float64 restatement; rmsnorm backward by finite differences; RoPE norm preservation,
+ * backward(forward(x)) = x, position 0 identity and the 2x2 rotation by hand; embedding
+ * backward as the transpose of the gather (<dW, W> = <dY, gather(W)>); cross entropy of equal
+ * logits = log(vocab), gradient rows summing to 0, finite differences; Lion sign cases by hand. */
+void ref_rmsnorm_forward(const float *x, const float *gamma, float *y, int64_t rows, int64_t dim, float eps);
+void ref_rmsnorm_backward(const float *dy, const float *x, const float *gamma, float *dx, float *dgamma,
+                          int64_t rows, int64_t dim, float eps);
+void ref_rope(float *x, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim, int64_t row_stride,
+              float base, int64_t offset, int backward);
+void ref_embedding_forward(const float *table, const uint32_t *ids, float *out, int64_t n, int64_t dim);
+void ref_embedding_backward(const float *dy, const uint32_t *ids, float *dw, int64_t n, int64_t dim, int64_t vocab);
+float ref_cross_entropy(const float *logits, const uint32_t *targets, float *losses, float *grad, int64_t rows,
+                        int64_t vocab);
+void ref_lion(float *w, float *m, const float *g, int64_t n, float lr, float beta1, float beta2, float wd,
+              float scale);
+double ref_sum_squares(const float *x, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif
