@@ -248,6 +248,84 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
                                       const void *K, const void *V, const float *O, const float *lse,
                                       float *dQ, float *dK, float *dV);
 
+/* ---------------------------------------------------------------- training-step ops
+ *
+ * The row and elementwise work between the contractions of one training step
+ * (src/train/trainer/train_step.rs:39-460, src/train/forward.rs:79-212, src/train/backward.rs:21-177).
+ * All buffers are device memory, row-major and contiguous unless a stride says otherwise; the
+ * calls are stream-ordered like it_gemm. Reductions run in a fixed order (no float atomics), so
+ * results are bit-for-bit repeatable. IT_BF16 outputs are rounded to nearest even.
+ */
+
+/* RMSNorm with an optional residual add in front. s = x + res (res NULL: s = x), written to
+ * sum_out unless NULL; y = s * (1 / sqrt(mean(s^2) + eps)) * gamma in dtype_y. x, res, sum_out
+ * [rows, dim] f32, gamma [dim] f32.
+ * Replaces rmsnorm (src/ops/norm.rs:31) and the residual add before it
+ * (ops::add, src/ops/elementwise.rs:276, at src/train/forward.rs:155,190). */
+it_status it_rmsnorm_forward(it_context *ctx, it_dtype dtype_y, int64_t rows, int64_t dim, float eps,
+                             const float *x, const float *res, const float *gamma, float *sum_out, void *y);
+
+/* RMSNorm backward with the residual gradient added behind: dx = gres + dRMSNorm/dx . dy
+ * (gres NULL: no add), dgamma[dim] = sum over rows of dy * x / rms (overwritten). dim <= 2048.
+ * Replaces rmsnorm_backward (src/ops/backward/norm.rs:20) and add_tensors
+ * (src/train/backward.rs:73,158). */
+it_status it_rmsnorm_backward(it_context *ctx, int64_t rows, int64_t dim, float eps, const float *dy,
+                              const float *x, const float *gamma, const float *gres, float *dx, float *dgamma);
+
+/* Rotary embedding over rows (b, s) of [batch, seq, heads, head_dim] with row strides (elements):
+ * pairs (2i, 2i+1) of each head rotate by (s + position_offset) / base^(2i/head_dim); backward != 0
+ * applies the inverse (transposed) rotation. src == dst works in place (same dtype and stride);
+ * otherwise copy_cols further columns after heads*head_dim are copied (e.g. V of a fused QKV
+ * gradient changing precision). Replaces rope (src/ops/rope.rs:22) and rope_backward
+ * (src/ops/backward/rope.rs:16). */
+it_status it_rope(it_context *ctx, it_dtype dtype_src, it_dtype dtype_dst, int64_t batch, int64_t seq,
+                  int64_t heads, int64_t head_dim, float base, int64_t position_offset, int backward,
+                  const void *src, int64_t src_row_stride, void *dst, int64_t dst_row_stride, int64_t copy_cols);
+
+/* out[i] = table[ids[i]] ([n, dim]); ids are device uint32. The reference asserts every id is
+ * below vocab on the host (src/ops/embedding.rs:41-49); host mirrors do the same before upload,
+ * and the kernel writes a zero row for an out-of-range id instead of reading out of bounds.
+ * Replaces embedding (src/ops/embedding.rs:21). */
+it_status it_embedding_forward(it_context *ctx, it_dtype dtype_table, it_dtype dtype_out, int64_t n, int64_t dim,
+                               int64_t vocab, const void *table, const uint32_t *ids, void *out);
+/* dw[vocab, dim] = scatter-add of dy rows by id, every element summed in token order (no
+ * atomics); rows no id hits are zero. Replaces embedding_backward (src/ops/backward/embedding.rs:21). */
+it_status it_embedding_backward(it_context *ctx, int64_t n, int64_t dim, int64_t vocab, const float *dy,
+                                const uint32_t *ids, float *dw);
+
+/* Fused softmax cross entropy over logits [rows, vocab] f32 and device uint32 targets:
+ * losses[r] = logsumexp(x_r) - x_r[t_r] (losses NULL: library scratch), grad = (softmax - onehot)
+ * / rows in dtype_grad, *loss_mean (device f32, NULL to skip) = mean of losses. Replaces
+ * cross_entropy_fused (src/ops/backward/loss.rs:248; kernel src/shaders/loss.metal:91-131). */
+it_status it_cross_entropy_fused(it_context *ctx, it_dtype dtype_grad, int64_t rows, int64_t vocab,
+                                 const float *logits, const uint32_t *targets, float *losses, void *grad,
+                                 float *loss_mean);
+
+/* SwiGLU backward: grad_up = g * silu(gate), grad_gate = g * up * silu'(gate), with leading
+ * dimensions so the two results can land in one [rows, 2*cols] gate|up buffer. grad_out f32,
+ * gate/up in dtype_in, results in dtype_out. Replaces swiglu_backward
+ * (src/ops/backward/elementwise.rs:149; src/shaders/backward/elementwise.metal:101-126). */
+it_status it_swiglu_backward(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, int64_t rows, int64_t cols,
+                             const float *grad_out, int64_t ld_grad, const void *gate, const void *up,
+                             int64_t ld_in, void *grad_gate, void *grad_up, int64_t ld_out);
+
+/* Global L2 norm of `count` f32 device tensors (host arrays of pointers and element counts),
+ * summed in double in a fixed order, and the clip factor, written to device out[2] = {norm,
+ * norm > max_norm ? max_norm / norm : 1}. Nothing is read back to the host. Replaces
+ * total_l2_norm_gpu (src/ops/reduction.rs:94) and the clip rule of
+ * src/train/trainer/train_step.rs:405-414. */
+it_status it_grad_norm_clip(it_context *ctx, int count, const float *const *grads, const int64_t *sizes,
+                            float max_norm, float *out);
+
+/* Lion over `count` tensors in one launch per 24: g' = g * (*grad_scale) (NULL: 1);
+ * u = beta2 m + (1-beta2) g'; m = beta1 m + (1-beta1) g'; w -= lr sign(u) + lr wd w, with lr read
+ * from *lr_dev when lr_dev is not NULL (a schedule value updated between graph replays).
+ * Replaces Lion::step (src/optim/lion/optimizer.rs:54-106; src/shaders/lion.metal lion_step_f32)
+ * applied after scale_gradients_inplace (src/train/trainer/train_step.rs:410-414). */
+it_status it_lion_step(it_context *ctx, int count, float *const *weights, float *const *momentum,
+                       const float *const *grads, const int64_t *sizes, float lr, float beta1, float beta2,
+                       float weight_decay, const float *grad_scale, const float *lr_dev);
+
 /* ---------------------------------------------------------------- graphs (launch-bound loops) */
 
 typedef struct it_graph it_graph;

@@ -108,6 +108,21 @@ _SIGNATURES = {
                                             C.POINTER(AttnLayout), C.POINTER(AttnLayout),
                                             C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "it_rmsnorm_forward": (c_int, [c_void_p, c_int, c_i64, c_i64, c_float, c_void_p, c_void_p, c_void_p,
+                                   c_void_p, c_void_p]),
+    "it_rmsnorm_backward": (c_int, [c_void_p, c_i64, c_i64, c_float, c_void_p, c_void_p, c_void_p, c_void_p,
+                                    c_void_p, c_void_p]),
+    "it_rope": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_float, c_i64, c_int,
+                        c_void_p, c_i64, c_void_p, c_i64, c_i64]),
+    "it_embedding_forward": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p]),
+    "it_embedding_backward": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p]),
+    "it_cross_entropy_fused": (c_int, [c_void_p, c_int, c_i64, c_i64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p]),
+    "it_swiglu_backward": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_void_p, c_i64, c_void_p, c_void_p,
+                                   c_i64, c_void_p, c_void_p, c_i64]),
+    "it_grad_norm_clip": (c_int, [c_void_p, c_int, C.POINTER(c_void_p), C.POINTER(c_i64), c_float, c_void_p]),
+    "it_lion_step": (c_int, [c_void_p, c_int, C.POINTER(c_void_p), C.POINTER(c_void_p), C.POINTER(c_void_p),
+                             C.POINTER(c_i64), c_float, c_float, c_float, c_float, c_void_p, c_void_p]),
     "it_side_begin": (c_int, [c_void_p]),
     "it_side_end": (c_int, [c_void_p]),
     "it_side_join": (c_int, [c_void_p]),

@@ -1,0 +1,200 @@
+// C ABI entry points for the training step's ops around the contractions: argument validation with
+// the reference's error cases (assert! on shapes and precisions becomes IT_ERR_*), library-owned
+// scratch for the deterministic reductions, and profiler keys for the step breakdown.
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "internal.hpp"
+
+using it::fail;
+
+namespace {
+
+std::string i64(int64_t v) { return std::to_string((long long)v); }
+
+bool f32_or_bf16(it_dtype d) { return d == IT_F32 || d == IT_BF16; }
+
+// Times one op under the profiler (no-op otherwise).
+struct Prof {
+    it_context *ctx;
+    std::string key;
+    hipEvent_t ev = nullptr;
+    Prof(it_context *c, std::string k) : ctx(c) {
+        if (ctx->profiling) {
+            key = std::move(k);
+            it::profile_begin(ctx, key, &ev);
+        }
+    }
+    it_status done(it_status st) {
+        if (ctx->profiling) it::profile_end(ctx, key, ev);
+        return st;
+    }
+};
+
+const char *sfx(it_dtype d) { return d == IT_BF16 ? "_bf16" : "_f32"; }
+
+}  // namespace
+
+extern "C" {
+
+it_status it_rmsnorm_forward(it_context *ctx, it_dtype dtype_y, int64_t rows, int64_t dim, float eps,
+                             const float *x, const float *res, const float *gamma, float *sum_out, void *y) {
+    if (!ctx) return fail(IT_ERR_NULL, "rmsnorm: ctx is NULL");
+    if (!f32_or_bf16(dtype_y)) return fail(IT_ERR_PRECISION, "rmsnorm: precision mismatch, expected FP32 or BF16");
+    if (rows < 0 || dim < 0) return fail(IT_ERR_INVALID, "rmsnorm: negative size");
+    if (rows == 0 || dim == 0) return IT_OK;
+    if (!x || !gamma || !y) return fail(IT_ERR_NULL, "rmsnorm: NULL buffer");
+    Prof p(ctx, std::string("rmsnorm_fwd") + sfx(dtype_y) + (res ? "_add" : "") + "[" + i64(rows) + "x" + i64(dim) + "]");
+    return p.done(it::launch_rmsnorm_forward(ctx->stream, dtype_y == IT_BF16, rows, dim, eps, x, res, gamma,
+                                             sum_out, y));
+}
+
+it_status it_rmsnorm_backward(it_context *ctx, int64_t rows, int64_t dim, float eps, const float *dy,
+                              const float *x, const float *gamma, const float *gres, float *dx, float *dgamma) {
+    if (!ctx) return fail(IT_ERR_NULL, "rmsnorm_backward: ctx is NULL");
+    if (rows < 0 || dim < 0) return fail(IT_ERR_INVALID, "rmsnorm_backward: negative size");
+    if (dim > 2048)
+        return fail(IT_ERR_DIMS, "rmsnorm_backward: unsupported dimensions, dim must be at most 2048, got " + i64(dim));
+    if (dim == 0) return IT_OK;
+    if (!dgamma || !gamma) return fail(IT_ERR_NULL, "rmsnorm_backward: NULL buffer");
+    if (rows == 0) return it::launch_zero(ctx->stream, dgamma, (size_t)dim * sizeof(float));
+    if (!dy || !x || !dx) return fail(IT_ERR_NULL, "rmsnorm_backward: NULL buffer");
+    void *part = nullptr;
+    if (const it_status st = it::ensure_scratch(ctx, (size_t)it::rmsnorm_backward_scratch_bytes(rows, dim), &part);
+        st != IT_OK)
+        return st;
+    Prof p(ctx, std::string("rmsnorm_bwd") + (gres ? "_add" : "") + "[" + i64(rows) + "x" + i64(dim) + "]");
+    return p.done(it::launch_rmsnorm_backward(ctx->stream, rows, dim, eps, dy, x, gamma, gres, dx, dgamma,
+                                              (float *)part));
+}
+
+it_status it_rope(it_context *ctx, it_dtype dtype_src, it_dtype dtype_dst, int64_t batch, int64_t seq,
+                  int64_t heads, int64_t head_dim, float base, int64_t position_offset, int backward,
+                  const void *src, int64_t src_row_stride, void *dst, int64_t dst_row_stride, int64_t copy_cols) {
+    if (!ctx) return fail(IT_ERR_NULL, "rope: ctx is NULL");
+    if (!f32_or_bf16(dtype_src) || !f32_or_bf16(dtype_dst))
+        return fail(IT_ERR_PRECISION, "rope: precision mismatch, expected FP32 or BF16");
+    if (batch < 0 || seq < 0 || heads < 0 || head_dim < 0 || copy_cols < 0 || position_offset < 0)
+        return fail(IT_ERR_INVALID, "rope: negative size");
+    if (head_dim % 2 != 0) return fail(IT_ERR_SHAPE, "rope: head_dim must be even, got " + i64(head_dim));
+    const int64_t width = heads * head_dim + copy_cols;
+    if (src_row_stride < width || dst_row_stride < width)
+        return fail(IT_ERR_SHAPE, "rope: row stride smaller than the rotated and copied columns");
+    if (batch * seq == 0 || width == 0) return IT_OK;
+    if (!src || !dst) return fail(IT_ERR_NULL, "rope: NULL buffer");
+    if (src == dst && (dtype_src != dtype_dst || src_row_stride != dst_row_stride))
+        return fail(IT_ERR_INVALID, "rope: in place needs the same precision and row stride");
+    if (batch * seq > 0x7fffffff) return fail(IT_ERR_DIMS, "rope: too many rows");
+    Prof p(ctx, std::string(backward ? "rope_bwd" : "rope_fwd") + sfx(dtype_dst) + "[" + i64(batch * seq) + "x" +
+                    i64(heads) + "x" + i64(head_dim) + "]");
+    return p.done(it::launch_rope(ctx->stream, dtype_src == IT_BF16, dtype_dst == IT_BF16, batch, seq, heads,
+                                  head_dim, base, position_offset, backward ? 1 : 0, src, src_row_stride, dst,
+                                  dst_row_stride, src == dst ? 0 : copy_cols));
+}
+
+it_status it_embedding_forward(it_context *ctx, it_dtype dtype_table, it_dtype dtype_out, int64_t n, int64_t dim,
+                               int64_t vocab, const void *table, const uint32_t *ids, void *out) {
+    if (!ctx) return fail(IT_ERR_NULL, "embedding: ctx is NULL");
+    if (!f32_or_bf16(dtype_table) || !f32_or_bf16(dtype_out))
+        return fail(IT_ERR_PRECISION, "embedding: precision mismatch, expected FP32 or BF16");
+    if (n < 0 || dim < 0 || vocab < 0) return fail(IT_ERR_INVALID, "embedding: negative size");
+    if (n == 0 || dim == 0) return IT_OK;
+    if (!table || !ids || !out) return fail(IT_ERR_NULL, "embedding: NULL buffer");
+    Prof p(ctx, std::string("embedding_fwd") + sfx(dtype_out) + "[" + i64(n) + "x" + i64(dim) + "]");
+    return p.done(it::launch_embedding_forward(ctx->stream, dtype_table == IT_BF16, dtype_out == IT_BF16, n, dim,
+                                               vocab, table, ids, out));
+}
+
+it_status it_embedding_backward(it_context *ctx, int64_t n, int64_t dim, int64_t vocab, const float *dy,
+                                const uint32_t *ids, float *dw) {
+    if (!ctx) return fail(IT_ERR_NULL, "embedding_backward: ctx is NULL");
+    if (n < 0 || dim < 0 || vocab < 0) return fail(IT_ERR_INVALID, "embedding_backward: negative size");
+    if (vocab == 0 || dim == 0) return IT_OK;
+    if (!dw) return fail(IT_ERR_NULL, "embedding_backward: NULL buffer");
+    if (n == 0) return it::launch_zero(ctx->stream, dw, (size_t)(vocab * dim) * sizeof(float));
+    if (!dy || !ids) return fail(IT_ERR_NULL, "embedding_backward: NULL buffer");
+    if ((vocab + 15) / 16 > 0x7fffffff) return fail(IT_ERR_DIMS, "embedding_backward: vocabulary too large");
+    Prof p(ctx, "embedding_bwd[" + i64(n) + "x" + i64(dim) + ",V=" + i64(vocab) + "]");
+    return p.done(it::launch_embedding_backward(ctx->stream, n, dim, vocab, dy, ids, dw));
+}
+
+it_status it_cross_entropy_fused(it_context *ctx, it_dtype dtype_grad, int64_t rows, int64_t vocab,
+                                 const float *logits, const uint32_t *targets, float *losses, void *grad,
+                                 float *loss_mean) {
+    if (!ctx) return fail(IT_ERR_NULL, "cross_entropy_fused: ctx is NULL");
+    if (!f32_or_bf16(dtype_grad))
+        return fail(IT_ERR_PRECISION, "cross_entropy_fused: precision mismatch, expected FP32 or BF16");
+    if (rows < 0 || vocab < 0) return fail(IT_ERR_INVALID, "cross_entropy_fused: negative size");
+    if (rows > 0x7fffffff) return fail(IT_ERR_DIMS, "cross_entropy_fused: too many rows");
+    if (rows == 0) {
+        // The reference returns a zero loss for an empty batch.
+        return loss_mean ? it::launch_zero(ctx->stream, loss_mean, sizeof(float)) : IT_OK;
+    }
+    if (vocab == 0) return fail(IT_ERR_SHAPE, "cross_entropy_fused: vocabulary is empty");
+    if (!logits || !targets || !grad) return fail(IT_ERR_NULL, "cross_entropy_fused: NULL buffer");
+    if (!losses) {
+        void *p = nullptr;
+        if (const it_status st = it::ensure_scratch(ctx, (size_t)rows * sizeof(float), &p); st != IT_OK) return st;
+        losses = (float *)p;
+    }
+    const bool vec_ok = vocab % 4 == 0 && (uintptr_t)logits % 16 == 0 &&
+                        (uintptr_t)grad % (dtype_grad == IT_BF16 ? 8 : 16) == 0;
+    Prof p(ctx, std::string("cross_entropy") + sfx(dtype_grad) + "[" + i64(rows) + "x" + i64(vocab) + "]");
+    return p.done(it::launch_cross_entropy(ctx->stream, dtype_grad == IT_BF16, rows, vocab, logits, targets, losses,
+                                           grad, loss_mean, vec_ok));
+}
+
+it_status it_swiglu_backward(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, int64_t rows, int64_t cols,
+                             const float *grad_out, int64_t ld_grad, const void *gate, const void *up,
+                             int64_t ld_in, void *grad_gate, void *grad_up, int64_t ld_out) {
+    if (!ctx) return fail(IT_ERR_NULL, "swiglu_backward: ctx is NULL");
+    if (!f32_or_bf16(dtype_in) || !f32_or_bf16(dtype_out))
+        return fail(IT_ERR_PRECISION, "swiglu_backward: precision mismatch, expected FP32 or BF16");
+    if (rows < 0 || cols < 0) return fail(IT_ERR_INVALID, "swiglu_backward: negative size");
+    if (ld_grad < cols || ld_in < cols || ld_out < cols)
+        return fail(IT_ERR_SHAPE, "swiglu_backward: leading dimension smaller than cols");
+    if (rows == 0 || cols == 0) return IT_OK;
+    if (rows > 0x7fffffff) return fail(IT_ERR_DIMS, "swiglu_backward: too many rows");
+    if (!grad_out || !gate || !up || !grad_gate || !grad_up) return fail(IT_ERR_NULL, "swiglu_backward: NULL buffer");
+    Prof p(ctx, std::string("swiglu_bwd") + sfx(dtype_out) + "[" + i64(rows) + "x" + i64(cols) + "]");
+    return p.done(it::launch_swiglu_backward(ctx->stream, dtype_in == IT_BF16, dtype_out == IT_BF16, rows, cols,
+                                             grad_out, ld_grad, gate, up, ld_in, grad_gate, grad_up, ld_out));
+}
+
+it_status it_grad_norm_clip(it_context *ctx, int count, const float *const *grads, const int64_t *sizes,
+                            float max_norm, float *out) {
+    if (!ctx) return fail(IT_ERR_NULL, "total_l2_norm: ctx is NULL");
+    if (count < 0) return fail(IT_ERR_INVALID, "total_l2_norm: negative count");
+    if (!out) return fail(IT_ERR_NULL, "total_l2_norm: NULL output");
+    if (count > 0 && (!grads || !sizes)) return fail(IT_ERR_NULL, "total_l2_norm: NULL table");
+    for (int i = 0; i < count; ++i) {
+        if (sizes[i] < 0) return fail(IT_ERR_INVALID, "total_l2_norm: negative size");
+        if (sizes[i] > 0 && !grads[i]) return fail(IT_ERR_NULL, "total_l2_norm: NULL buffer");
+    }
+    const int64_t parts = it::grad_norm_partials(count, sizes);
+    void *part = nullptr;
+    if (const it_status st = it::ensure_scratch(ctx, (size_t)(parts > 0 ? parts : 1) * sizeof(double), &part);
+        st != IT_OK)
+        return st;
+    Prof p(ctx, "grad_norm[" + std::to_string(count) + " tensors]");
+    return p.done(it::launch_grad_norm(ctx->stream, count, grads, sizes, max_norm, out, (double *)part));
+}
+
+it_status it_lion_step(it_context *ctx, int count, float *const *weights, float *const *momentum,
+                       const float *const *grads, const int64_t *sizes, float lr, float beta1, float beta2,
+                       float weight_decay, const float *grad_scale, const float *lr_dev) {
+    if (!ctx) return fail(IT_ERR_NULL, "lion: ctx is NULL");
+    if (count < 0) return fail(IT_ERR_INVALID, "lion: negative count");
+    if (count == 0) return IT_OK;
+    if (!weights || !momentum || !grads || !sizes) return fail(IT_ERR_NULL, "lion: NULL table");
+    for (int i = 0; i < count; ++i) {
+        if (sizes[i] < 0) return fail(IT_ERR_INVALID, "lion: negative size");
+        if (sizes[i] > 0 && (!weights[i] || !momentum[i] || !grads[i])) return fail(IT_ERR_NULL, "lion: NULL buffer");
+    }
+    Prof p(ctx, "lion[" + std::to_string(count) + " tensors]");
+    return p.done(it::launch_lion(ctx->stream, count, weights, momentum, grads, sizes, lr, beta1, beta2, weight_decay,
+                                  grad_scale, lr_dev));
+}
+
+}  // extern "C"

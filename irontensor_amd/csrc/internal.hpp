@@ -184,4 +184,30 @@ it_status launch_softmax_backward(hipStream_t s, const float *dY, const void *Y,
                                   int64_t cols, int causal);
 it_status launch_splitk_reduce(hipStream_t s, const GemmArgs &a);
 
+// Training-step ops around the contractions (kernels_train.hip).
+it_status launch_rmsnorm_forward(hipStream_t s, bool y_bf16, int64_t rows, int64_t dim, float eps, const float *x,
+                                 const float *res, const float *gamma, float *sum_out, void *y);
+int64_t rmsnorm_backward_scratch_bytes(int64_t rows, int64_t dim);
+it_status launch_rmsnorm_backward(hipStream_t s, int64_t rows, int64_t dim, float eps, const float *dy,
+                                  const float *x, const float *gamma, const float *gres, float *dx,
+                                  float *dgamma, float *part);
+it_status launch_rope(hipStream_t s, bool src_bf16, bool dst_bf16, int64_t batch, int64_t seq, int64_t heads,
+                      int64_t head_dim, float base, int64_t offset, int backward, const void *src, int64_t src_rs,
+                      void *dst, int64_t dst_rs, int64_t copy_cols);
+it_status launch_embedding_forward(hipStream_t s, bool table_bf16, bool out_bf16, int64_t n, int64_t dim,
+                                   int64_t vocab, const void *table, const uint32_t *ids, void *out);
+it_status launch_embedding_backward(hipStream_t s, int64_t n, int64_t dim, int64_t vocab, const float *dy,
+                                    const uint32_t *ids, float *dw);
+it_status launch_cross_entropy(hipStream_t s, bool grad_bf16, int64_t rows, int64_t vocab, const float *logits,
+                               const uint32_t *targets, float *losses, void *grad, float *loss_mean, bool vec_ok);
+it_status launch_swiglu_backward(hipStream_t s, bool in_bf16, bool out_bf16, int64_t rows, int64_t cols,
+                                 const float *dh, int64_t ld_dh, const void *gate, const void *up, int64_t ld_gu,
+                                 void *dgate, void *dup, int64_t ld_out);
+int64_t grad_norm_partials(int count, const int64_t *n);
+it_status launch_grad_norm(hipStream_t s, int count, const float *const *g, const int64_t *n, float max_norm,
+                           float *out, double *part);
+it_status launch_lion(hipStream_t s, int count, float *const *w, float *const *m, const float *const *g,
+                      const int64_t *n, float lr, float beta1, float beta2, float wd, const float *scale_dev,
+                      const float *lr_dev);
+
 }  // namespace it

@@ -150,3 +150,16 @@ def test_planted_slips_fail(oracle):
     assert not np.allclose(oracle.rope(wrong_sign, backward=False), y, atol=1e-5)  # forward twice != identity
     _, _, grad = oracle.cross_entropy(synth.normal(16, (2, 5)), np.array([1, 4]))
     assert not np.allclose(grad.sum(-1) + 1.0 / 2, 0, atol=1e-7)  # a missing onehot would sum to 1/rows
+
+
+def test_rope_theta_is_the_correctly_rounded_power():
+    """The oracle's theta uses the host powf; the GPU kernel rounds a double-precision power once.
+    They agree when the host powf is correctly rounded at these arguments, which this checks for
+    every pair index of the head sizes in use (a one-ulp theta shows after the position multiply)."""
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.powf.restype, libm.powf.argtypes = ctypes.c_float, [ctypes.c_float, ctypes.c_float]
+    for d in (2, 16, 32, 64, 128, 256):
+        for i in range(d // 2):
+            e = np.float32(np.float32(2 * i) / np.float32(d))
+            assert np.float32(libm.powf(10000.0, float(e))) == np.float32(np.power(10000.0, np.float64(e)))
