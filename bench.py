@@ -204,6 +204,54 @@ def extra_sweep(it, timer) -> dict:
     return out
 
 
+def train_step_figures(it, timer, steps: int, warmup: int) -> dict:
+    """The complete TINY training step (irontensor_amd.train.TrainStep): embedding, 4 layers with
+    RMSNorm, RoPE and fused attention, final norm, LM head, fused cross entropy, the backward pass,
+    the global-norm clip and Lion, graph-replayed. Per-kernel shares from one eager profiled step."""
+    from irontensor_amd.step import TINY
+    from irontensor_amd.train import TrainStep
+    ctx = it.Context.global_()
+    st = TrainStep(TINY, ctx)
+    try:
+        st.step()
+        ctx.sync()
+        loss0 = st.loss_value()
+        st.capture()
+        for _ in range(warmup):
+            st.step()
+        ctx.sync()
+        t0 = time.perf_counter()
+        timer.start()
+        for _ in range(steps):
+            st.step()
+        ev_ms = timer.stop_ms() / steps
+        ctx.sync()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        loss1, gnorm = st.loss_value(), st.grad_norm()
+        st.overlap = False
+        ctx.lib.it_profiler_reset(ctx.handle)
+        ctx.lib.it_profiler_enable(ctx.handle, 1)
+        st.enqueue()
+        stats = profiler_stats(ctx)
+        ctx.lib.it_profiler_enable(ctx.handle, 0)
+    finally:
+        st.close()
+    total = sum(v["total_ms"] for v in stats.values())
+    groups = {}
+    for k, v in stats.items():
+        g = k.split("|")[0].split("[")[0]
+        g = "gemm" if g.startswith("gemm") or g.startswith("gemv") else g
+        groups[g] = groups.get(g, 0.0) + v["total_ms"]
+    return {"ms_per_step": round(wall_ms, 4), "ms_per_step_events": round(ev_ms, 4),
+            "tokens_per_s": round(TINY.tokens / (wall_ms * 1e-3), 0), "steps": steps, "warmup": warmup,
+            "loss_first": round(loss0, 4), "loss_last": round(loss1, 4), "grad_norm_last": round(gnorm, 4),
+            "gemm_tflops_in_step": round(st.gemm_flops() / (wall_ms * 1e-3) / 1e12, 2),
+            "eager_kernel_ms_by_group": {k: round(v, 4) for k, v in sorted(groups.items(), key=lambda kv: -kv[1])},
+            "eager_kernel_ms_total": round(total, 4),
+            "optimizer": "Lion lr 3e-4 betas (0.9, 0.99) wd 0.1, clip 1.0 (src/bin/benchmark.rs:124-129)",
+            "execution": "one hipGraph per step; weight gradients on a second stream; loss, norm and clip stay on the GPU"}
+
+
 def extras(it, timer) -> dict:
     out = {}
     for fn in (extra_config1, extra_attention, extra_sweep, extra_med_step):
@@ -302,6 +350,18 @@ def cpu_baseline(step) -> dict:
     t1 = time.perf_counter()
     oracle.gemm_f32(x1, w1, False, True, threads=1)
     dt1 = time.perf_counter() - t1
+    # the complete training step (embedding .. Lion) on the oracle, once
+    from oracle import train_step as ots
+    L = s.layers
+    prm = {"emb": w((V, H), 40), "E": w((V, H), 41), "final_norm": np.ones(H, np.float32),
+           "attn_norm": [np.ones(H, np.float32)] * L, "ffn_norm": [np.ones(H, np.float32)] * L,
+           "Wqkv": [w((3 * H, H), 42 + l) for l in range(L)], "Wo": [w((H, H), 50 + l) for l in range(L)],
+           "Wgu": [w((2 * F, H), 60 + l) for l in range(L)], "Wd": [w((H, F), 70 + l) for l in range(L)]}
+    mom = [np.zeros_like(x) for x in ots.param_list(prm)]
+    stream = synth.tokens(99, s.batch * (s.seq + 1), V).reshape(s.batch, s.seq + 1)
+    t2 = time.perf_counter()
+    ots.train_step(prm, mom, stream[:, :-1].ravel(), stream[:, 1:].ravel(), s, threads=thr)
+    dt2 = time.perf_counter() - t2
     model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -319,7 +379,11 @@ def cpu_baseline(step) -> dict:
                        f"backward) + 3 LM-head GEMMs, {flops / 1e9:.1f} GFLOP in {dt:.2f} s; oracle/ref.c "
                        f"sequential f32 loop (no FMA contraction), {thr} threads, pooled N(0,1)/N(0,0.02) inputs"),
             "seconds": round(dt, 2),
-            "ms_per_step": round(dt * 1e3, 1)}
+            "ms_per_step": round(dt * 1e3, 1),
+            "train_step_ms": round(dt2 * 1e3, 1),
+            "train_step_sample": ("one complete TINY training step on the oracle (oracle/train_step.py: "
+                                  "embedding, layers, final norm, LM head, cross entropy, backward, clip, "
+                                  f"Lion), {thr} threads for the contractions")}
 
 
 def main() -> int:
@@ -426,6 +490,9 @@ def main() -> int:
         "gemm_kernel_ms_per_step": round(gemm_ms, 4),
         "top_kernels": [{"key": k, "avg_us": round(a * 1e3, 2), "per_step": c} for k, a, c in per_kernel[:8]],
     }
+    log("[bench] complete TINY training step")
+    result["train_step"] = train_step_figures(it, timer, args.steps, args.warmup)
+    log(f"[bench] train step {result['train_step']['ms_per_step']} ms")
     if not args.no_extra:
         log("[bench] extra GEMM figures")
         result["extra"] = extras(it, timer)

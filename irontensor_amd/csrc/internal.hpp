@@ -66,6 +66,10 @@ struct it_context {
     void *attn_scratch[2] = {nullptr, nullptr};
     size_t attn_scratch_bytes[2] = {0, 0};
 
+    // RoPE (cos, sin) tables per (seq, head_dim, base bits, position offset), built on first use
+    // and kept until shutdown (every layer's forward and backward share one).
+    std::map<std::vector<int64_t>, void *> rope_tables;
+
     // True between it_capture_begin and it_capture_end: nothing may allocate.
     bool capturing = false;
 
@@ -191,8 +195,9 @@ int64_t rmsnorm_backward_scratch_bytes(int64_t rows, int64_t dim);
 it_status launch_rmsnorm_backward(hipStream_t s, int64_t rows, int64_t dim, float eps, const float *dy,
                                   const float *x, const float *gamma, const float *gres, float *dx,
                                   float *dgamma, float *part);
+it_status launch_rope_table(hipStream_t s, int64_t seq, int64_t head_dim, float base, int64_t offset, void *table);
 it_status launch_rope(hipStream_t s, bool src_bf16, bool dst_bf16, int64_t batch, int64_t seq, int64_t heads,
-                      int64_t head_dim, float base, int64_t offset, int backward, const void *src, int64_t src_rs,
+                      int64_t head_dim, const void *table, int backward, const void *src, int64_t src_rs,
                       void *dst, int64_t dst_rs, int64_t copy_cols);
 it_status launch_embedding_forward(hipStream_t s, bool table_bf16, bool out_bf16, int64_t n, int64_t dim,
                                    int64_t vocab, const void *table, const uint32_t *ids, void *out);

@@ -64,10 +64,11 @@ unsigned blocks_for(int64_t n, int64_t per_block, int64_t cap = 0x7fffffff) {
 
 // ------------------------------------------------------------------ RMSNorm forward
 
-// One wave per row, lane-strided columns (lane + 64 k): s = x (+ res); sum_out = s;
-// y = s * (1 / sqrt(sum(s^2) / dim + eps)) * gamma. Columns are read twice; the second pass hits
-// the cache (rows are at most a few KB).
-template <typename TY>
+// One wave per row, lane-strided columns (c = lane + 64 k): s = x (+ res); sum_out = s;
+// y = s * (1 / sqrt(sum(s^2) / dim + eps)) * gamma. With MAXK > 0 (dim <= 64 MAXK) the row stays in
+// registers (every load issued before the reduction: one pass over HBM); MAXK == 0 reads the row
+// twice for any dim.
+template <typename TY, int MAXK>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const float *x, const float *res, float *sum_out,
                                                           const float *gamma, TY *y, int64_t rows,
                                                           int64_t dim, float eps) {
@@ -77,64 +78,97 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const float *x, const 
     const float *xr = x + row * dim;
     const float *rr = res ? res + row * dim : nullptr;
     float ss = 0.f;
-    for (int64_t c = lane; c < dim; c += 64) {
-        const float s = rr ? xr[c] + rr[c] : xr[c];
-        if (sum_out) sum_out[row * dim + c] = s;
-        ss += s * s;
-    }
-    ss = wsum(ss);
-    const float rms = sqrtf(ss / (float)dim + eps);
-    const float inv = 1.0f / rms;
-    for (int64_t c = lane; c < dim; c += 64) {
-        const float s = rr ? xr[c] + rr[c] : xr[c];
-        stv<TY>(y, row * dim + c, s * inv * gamma[c]);
+    if constexpr (MAXK > 0) {
+        float sv[MAXK];
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) {
+            const int64_t c = lane + 64 * k;
+            sv[k] = c < dim ? (rr ? xr[c] + rr[c] : xr[c]) : 0.f;
+            ss += sv[k] * sv[k];
+        }
+        ss = wsum(ss);
+        const float rms = sqrtf(ss / (float)dim + eps);
+        const float inv = 1.0f / rms;
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) {
+            const int64_t c = lane + 64 * k;
+            if (c < dim) {
+                if (sum_out) sum_out[row * dim + c] = sv[k];
+                stv<TY>(y, row * dim + c, sv[k] * inv * gamma[c]);
+            }
+        }
+    } else {
+        for (int64_t c = lane; c < dim; c += 64) {
+            const float v = rr ? xr[c] + rr[c] : xr[c];
+            if (sum_out) sum_out[row * dim + c] = v;
+            ss += v * v;
+        }
+        ss = wsum(ss);
+        const float rms = sqrtf(ss / (float)dim + eps);
+        const float inv = 1.0f / rms;
+        for (int64_t c = lane; c < dim; c += 64) {
+            const float v = rr ? xr[c] + rr[c] : xr[c];
+            stv<TY>(y, row * dim + c, v * inv * gamma[c]);
+        }
     }
 }
 
 // ------------------------------------------------------------------ RMSNorm backward
 
-// Rows are split over blocks of RB_ROWS; each wave takes every fourth row of its block. Per row:
-// s = 1/rms, dot = sum(dy * gamma * x), dx = gres + dy * gamma * s - (1/dim) s^3 x dot. Each lane
-// keeps its columns' dgamma partial sum (dy * x * s) in registers over the block's rows; the four
-// waves combine in a fixed order into part[block][dim], which rmsnorm_dgamma_reduce sums over
-// blocks in order.
-constexpr int RB_ROWS = 16;
-
-template <int MAXK>  // columns per lane: dim <= 64 * MAXK
+// Each wave takes RPW consecutive rows and loads all of them before reducing (RPW rows of memory
+// latency overlap); a block's four waves cover 4 RPW rows. Per row: s = 1/rms,
+// dot = sum(dy * gamma * x), dx = gres + dy * gamma * s - (1/dim) s^3 x dot. Each lane keeps its
+// columns' dgamma partial sum (dy * x * s, rows in order) in registers; the four waves combine in a
+// fixed order into part[block][dim], summed over blocks in order by rmsnorm_dgamma_reduce.
+template <int MAXK, int RPW>  // columns per lane (dim <= 64 MAXK), rows per wave
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float *dy, const float *x, const float *gamma,
                                                           const float *gres, float *dx, float *part,
                                                           int64_t rows, int64_t dim, float eps) {
     extern __shared__ float red[];  // [4][dim]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t r0 = (int64_t)blockIdx.x * RB_ROWS;
+    const int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RPW;
     const float n = (float)dim;
-    float acc[MAXK];
+    float gm[MAXK], acc[MAXK];
+    float xv[RPW][MAXK], gv[RPW][MAXK];
 #pragma unroll
-    for (int k = 0; k < MAXK; ++k) acc[k] = 0.f;
-    for (int64_t row = r0 + wave; row < min(rows, r0 + RB_ROWS); row += 4) {
-        const float *xr = x + row * dim, *gr = dy + row * dim;
-        float xv[MAXK], gv[MAXK];
-        float ss = 0.f, dot = 0.f;
+    for (int k = 0; k < MAXK; ++k) {
+        const int64_t c = lane + 64 * k;
+        gm[k] = c < dim ? gamma[c] : 0.f;
+        acc[k] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        const int64_t row = r0 + j;
 #pragma unroll
         for (int k = 0; k < MAXK; ++k) {
             const int64_t c = lane + 64 * k;
-            xv[k] = c < dim ? xr[c] : 0.f;
-            gv[k] = c < dim ? gr[c] : 0.f;
-            ss += xv[k] * xv[k];
-            dot += gv[k] * (c < dim ? gamma[c] : 0.f) * xv[k];
+            const bool ok = row < rows && c < dim;
+            xv[j][k] = ok ? x[row * dim + c] : 0.f;
+            gv[j][k] = ok ? dy[row * dim + c] : 0.f;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        const int64_t row = r0 + j;
+        float ss = 0.f, dot = 0.f;
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) {
+            ss += xv[j][k] * xv[j][k];
+            dot += gv[j][k] * gm[k] * xv[j][k];
         }
         ss = wsum(ss);
         dot = wsum(dot);
+        if (row >= rows) continue;
         const float rms = sqrtf(ss / n + eps);
         const float s = 1.0f / rms, s3 = s * s * s;
 #pragma unroll
         for (int k = 0; k < MAXK; ++k) {
             const int64_t c = lane + 64 * k;
             if (c < dim) {
-                float v = gv[k] * gamma[c] * s - (1.0f / n) * s3 * xv[k] * dot;
+                float v = gv[j][k] * gm[k] * s - (1.0f / n) * s3 * xv[j][k] * dot;
                 if (gres) v = gres[row * dim + c] + v;
                 dx[row * dim + c] = v;
-                acc[k] += gv[k] * xv[k] * s;
+                acc[k] += gv[j][k] * xv[j][k] * s;
             }
         }
     }
@@ -148,29 +182,34 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float *dy, const
         part[(int64_t)blockIdx.x * dim + c] = ((red[c] + red[dim + c]) + red[2 * dim + c]) + red[3 * dim + c];
 }
 
-// dgamma[c] = sum over blocks of part[b][c]: 64 columns per block (lane = column), the four waves
-// take every fourth partial row and combine in a fixed order.
-__global__ __launch_bounds__(256) void rmsnorm_dgamma_reduce(const float *part, float *dgamma, int64_t blocks,
-                                                             int64_t dim) {
-    __shared__ float red[4][64];
+// dgamma[c] = sum over blocks b of part[b][c]: one 1024-thread block per 64 columns (lane =
+// column); wave w sums rows b = w (mod 16) with sixteen loads in flight, then the 16 waves combine
+// in a fixed order.
+__global__ __launch_bounds__(1024) void rmsnorm_dgamma_reduce(const float *part, float *dgamma, int64_t blocks,
+                                                              int64_t dim) {
+    __shared__ float red[16][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t c = (int64_t)blockIdx.x * 64 + lane;
     float s = 0.f;
     if (c < dim) {
         int64_t b = wave;
-        for (; b + 12 < blocks; b += 16) {
-            const float v0 = part[b * dim + c], v1 = part[(b + 4) * dim + c];
-            const float v2 = part[(b + 8) * dim + c], v3 = part[(b + 12) * dim + c];
-            s += v0;
-            s += v1;
-            s += v2;
-            s += v3;
+        for (; b + 15 * 16 < blocks; b += 256) {
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = part[(b + 16 * j) * dim + c];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s += v[j];
         }
-        for (; b < blocks; b += 4) s += part[b * dim + c];
+        for (; b < blocks; b += 16) s += part[b * dim + c];
     }
     red[wave][lane] = s;
     __syncthreads();
-    if (wave == 0 && c < dim) dgamma[c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    if (wave == 0 && c < dim) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) t += red[w][lane];
+        dgamma[c] = t;
+    }
 }
 
 // ------------------------------------------------------------------ RoPE
@@ -189,39 +228,52 @@ __device__ __forceinline__ float rope_theta(float base, int i, int64_t head_dim)
     return 1.0f / (float)pow((double)base, (double)e);
 }
 
-constexpr int ROPE_TABLE = 256;  // pairs per head whose theta is tabulated per block
+// table[s][i] = (cos, sin) of angle (s + offset) * theta_i, for s < seq and i < head_dim / 2.
+__global__ __launch_bounds__(256) void rope_table_kernel(float2 *table, int64_t seq, int64_t head_dim, float base,
+                                                         int64_t offset) {
+    const int64_t half = head_dim / 2;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= seq * half) return;
+    const int64_t s = t / half;
+    const int i = (int)(t % half);
+    const float angle = (float)(s + offset) * rope_theta(base, i, head_dim);
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    table[t] = make_float2(cs, sn);
+}
 
+// One thread per rotated pair (2i, 2i+1) of each head, over rows (b, s) of src at
+// (b * seq + s) * src_rs, with (cos, sin) from the table; the backward applies the transposed
+// rotation. When src and dst differ, copy_cols further columns are copied after the rotated ones
+// (the V block of a fused QKV gradient changing precision).
 template <typename TS, typename TD>
-__global__ __launch_bounds__(256) void rope_kernel(const TS *src, TD *dst, int64_t seq, int64_t heads,
-                                                   int64_t head_dim, int64_t src_rs, int64_t dst_rs,
-                                                   int64_t copy_cols, float base, int64_t offset, int backward) {
-    const int64_t row = blockIdx.x;
-    const int64_t s = row % seq;
-    const int half = (int)(head_dim / 2);
+__global__ __launch_bounds__(256) void rope_kernel(const TS *src, TD *dst, const float2 *table, int64_t rows,
+                                                   int64_t seq, int heads, int half, int64_t src_rs, int64_t dst_rs,
+                                                   int copy_cols, int backward) {
+    const int per_row = heads * half + (copy_cols + 1) / 2;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= rows * per_row) return;
+    const int64_t row = t / per_row;
+    const int j = (int)(t - row * per_row);
     const TS *sp = src + row * src_rs;
     TD *dp = dst + row * dst_rs;
-    __shared__ float theta_s[ROPE_TABLE];
-    if (threadIdx.x < min(half, ROPE_TABLE)) theta_s[threadIdx.x] = rope_theta(base, threadIdx.x, head_dim);
-    __syncthreads();
-    const int64_t pairs = heads * half;
-    for (int64_t j = threadIdx.x; j < pairs; j += 256) {
-        const int i = (int)(j % half);
-        const int64_t c = (j / half) * head_dim + 2 * i;
-        const float theta = i < ROPE_TABLE ? theta_s[i] : rope_theta(base, i, head_dim);
-        const float angle = (float)(s + offset) * theta;
-        float sn, cs;
-        sincosf(angle, &sn, &cs);
+    if (j < heads * half) {
+        const int i = j % half;
+        const int64_t c = 2 * (int64_t)j;  // (j / half) * head_dim + 2 i
+        const float2 cs = table[(row % seq) * half + i];
         const float x0 = ldv<TS>(sp, c), x1 = ldv<TS>(sp, c + 1);
         if (!backward) {
-            stv<TD>(dp, c, x0 * cs - x1 * sn);
-            stv<TD>(dp, c + 1, x0 * sn + x1 * cs);
+            stv<TD>(dp, c, x0 * cs.x - x1 * cs.y);
+            stv<TD>(dp, c + 1, x0 * cs.y + x1 * cs.x);
         } else {
-            stv<TD>(dp, c, x0 * cs + x1 * sn);
-            stv<TD>(dp, c + 1, -x0 * sn + x1 * cs);
+            stv<TD>(dp, c, x0 * cs.x + x1 * cs.y);
+            stv<TD>(dp, c + 1, -x0 * cs.y + x1 * cs.x);
         }
+    } else {
+        const int64_t c0 = 2 * (int64_t)j;
+        const int64_t end = 2 * (int64_t)heads * half + copy_cols;
+        for (int64_t c = c0; c < min(c0 + 2, end); ++c) stv<TD>(dp, c, ldv<TS>(sp, c));
     }
-    const int64_t c0 = heads * head_dim;
-    for (int64_t c = c0 + threadIdx.x; c < c0 + copy_cols; c += 256) stv<TD>(dp, c, ldv<TS>(sp, c));
 }
 
 // ------------------------------------------------------------------ embedding
@@ -241,55 +293,67 @@ __global__ __launch_bounds__(256) void embedding_fwd_kernel(const TW *table, con
 }
 
 // Scatter-add without atomics: block b owns vocabulary rows [EB_ROWS b, EB_ROWS (b+1)). It scans the
-// ids in windows of EB_WIN tokens, compacts the tokens that hit its rows into an index-ordered list
-// in LDS, and each thread adds dy[token][c] into its own columns c of the owned rows, in token
-// order. Every element is therefore summed in index order, as a sequential loop would, and rows no
-// token hits are written as zeros.
+// ids in windows of EB_WIN tokens (each thread loads EB_PER consecutive ids), compacts the tokens
+// that hit its rows into an index-ordered list in LDS with one block-wide prefix sum, and each thread
+// adds dy[token][c] into its own columns c of the owned rows, in token order. Every element is
+// therefore summed in index order, as a sequential loop would, and rows no token hits are written
+// as zeros.
 constexpr int EB_ROWS = 16;
-constexpr int EB_WIN = 2048;
+constexpr int EB_PER = 16;
+constexpr int EB_WIN = 256 * EB_PER;
 
 __global__ __launch_bounds__(256) void embedding_bwd_kernel(const float *dy, const uint32_t *ids, float *dw,
                                                             int64_t n, int64_t dim, int64_t vocab) {
     __shared__ int tok[EB_WIN];
     __shared__ uint8_t hit_row[EB_WIN];
-    __shared__ int wave_cnt[4];
+    __shared__ int wave_tot[4];
     __shared__ int row_cnt[EB_ROWS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t v0 = (int64_t)blockIdx.x * EB_ROWS;
     const int nrows = (int)min((int64_t)EB_ROWS, vocab - v0);
     for (int64_t w0 = 0; w0 < n || w0 == 0; w0 += EB_WIN) {
-        const int64_t wend = min(n, w0 + EB_WIN);
         if (tid < EB_ROWS) row_cnt[tid] = 0;
-        int count = 0;
-        __syncthreads();
-        for (int64_t c0 = w0; c0 < wend; c0 += 256) {
-            const int64_t i = c0 + tid;
-            const uint32_t id = i < wend ? ids[i] : 0xffffffffu;
-            const int64_t r = (int64_t)id - v0;
-            const bool hit = i < wend && r >= 0 && r < nrows;
-            const uint64_t mask = __ballot(hit);
-            const int before = __popcll(mask & ((1ull << lane) - 1ull));
-            if (lane == 0) wave_cnt[wave] = __popcll(mask);
-            __syncthreads();
-            int base = count;
-            for (int w = 0; w < wave; ++w) base += wave_cnt[w];
-            if (hit) {
-                tok[base + before] = (int)(i - w0);
-                hit_row[base + before] = (uint8_t)r;
-                atomicAdd(&row_cnt[r], 1);  // integer count: order-free
-            }
-            count += wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
-            __syncthreads();
+        // this thread's tokens: [w0 + EB_PER tid, w0 + EB_PER (tid + 1)), all loads issued first
+        const int64_t t0 = w0 + (int64_t)EB_PER * tid;
+        int r[EB_PER];
+        int mine = 0;
+#pragma unroll
+        for (int e = 0; e < EB_PER; ++e) {
+            const int64_t i = t0 + e;
+            const int64_t d = i < n ? (int64_t)ids[i] - v0 : -1;
+            r[e] = (d >= 0 && d < nrows) ? (int)d : -1;
+            mine += r[e] >= 0;
         }
-        for (int r = 0; r < nrows; ++r) {
-            const int cnt_r = row_cnt[r];
+        // exclusive prefix of `mine` over the block, in thread order
+        int incl = mine;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        if (lane == 63) wave_tot[wave] = incl;
+        __syncthreads();
+        int base = incl - mine;
+        for (int w = 0; w < wave; ++w) base += wave_tot[w];
+        const int count = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+#pragma unroll
+        for (int e = 0; e < EB_PER; ++e)
+            if (r[e] >= 0) {
+                tok[base] = (int)(t0 + e - w0);
+                hit_row[base] = (uint8_t)r[e];
+                atomicAdd(&row_cnt[r[e]], 1);  // integer count: order-free
+                ++base;
+            }
+        __syncthreads();
+        for (int rr = 0; rr < nrows; ++rr) {
+            const int cnt_r = row_cnt[rr];
             if (w0 > 0 && cnt_r == 0) continue;  // earlier windows already wrote this row
-            float *out = dw + (v0 + r) * dim;
+            float *out = dw + (v0 + rr) * dim;
             for (int64_t c = tid; c < dim; c += 256) {
                 float acc = w0 == 0 ? 0.f : out[c];
                 if (cnt_r)
                     for (int m = 0; m < count; ++m)
-                        if (hit_row[m] == r) acc += dy[(w0 + tok[m]) * dim + c];
+                        if (hit_row[m] == rr) acc += dy[(w0 + tok[m]) * dim + c];
                 out[c] = acc;
             }
         }
@@ -377,12 +441,21 @@ __global__ __launch_bounds__(256) void ce_kernel(const float *logits, const uint
     if (tid == 0) losses[row] = (int64_t)t < vocab ? -x[t] + (mx + logf(sum)) : NAN;
 }
 
-// Mean of `n` values in a fixed order (one block): per-thread strided sums, then a tree.
+// Mean of `n` values in a fixed order (one block): per-thread sums of a strided slice (eight loads
+// in flight), then a tree.
 __global__ __launch_bounds__(256) void mean_kernel(const float *v, int64_t n, float *out) {
     __shared__ float red[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float s = 0.f;
-    for (int64_t i = tid; i < n; i += 256) s += v[i];
+    int64_t i = tid;
+    for (; i + 7 * 256 < n; i += 8 * 256) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = v[i + 256 * j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += t[j];
+    }
+    for (; i < n; i += 256) s += v[i];
     s = wsum(s);
     if (lane == 0) red[wave] = s;
     __syncthreads();
@@ -392,20 +465,62 @@ __global__ __launch_bounds__(256) void mean_kernel(const float *v, int64_t n, fl
 // ------------------------------------------------------------------ SwiGLU backward
 
 // grad_up = dh * silu(g); grad_gate = dh * u * sig(g) (1 + g (1 - sig(g))), sig(g) = 1 / (1 + exp(-g)).
-// One block per row.
-template <typename TI, typename TO>
+// One block per row; VEC consecutive columns per thread (VEC = 4 when every row start is aligned
+// for 16-byte f32 / 8-byte bf16 accesses and cols % 4 == 0).
+__device__ __forceinline__ void swiglu_grad(float go, float g, float u, float &dg, float &du) {
+    const float sig = 1.0f / (1.0f + expf(-g));
+    const float silu = g * sig;
+    du = go * silu;
+    const float d_silu = sig * (1.0f + g * (1.0f - sig));
+    dg = go * u * d_silu;
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4 ld4(const T *p) {
+    if constexpr (sizeof(T) == 4) {
+        return *(const f32x4 *)p;
+    } else {
+        const u32x2 h = *(const u32x2 *)p;
+        return f32x4{__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u), __uint_as_float(h[1] << 16),
+                     __uint_as_float(h[1] & 0xffff0000u)};
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void st4(T *p, f32x4 v) {
+    if constexpr (sizeof(T) == 4)
+        *(f32x4 *)p = v;
+    else
+        *(u32x2 *)p = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+}
+
+template <typename TI, typename TO, int VEC>
 __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const float *dh, int64_t ld_dh, const TI *gate,
                                                          const TI *up, int64_t ld_gu, TO *dgate, TO *dup,
                                                          int64_t ld_out, int64_t cols) {
     const int64_t r = blockIdx.x;
-    for (int64_t c = threadIdx.x; c < cols; c += 256) {
-        const float g = ldv<TI>(gate, r * ld_gu + c), u = ldv<TI>(up, r * ld_gu + c);
-        const float go = dh[r * ld_dh + c];
-        const float sig = 1.0f / (1.0f + expf(-g));
-        const float silu = g * sig;
-        stv<TO>(dup, r * ld_out + c, go * silu);
-        const float d_silu = sig * (1.0f + g * (1.0f - sig));
-        stv<TO>(dgate, r * ld_out + c, go * u * d_silu);
+    if constexpr (VEC == 4) {
+        for (int64_t c = 4 * (int64_t)threadIdx.x; c < cols; c += 1024) {
+            const f32x4 go = *(const f32x4 *)(dh + r * ld_dh + c);
+            const f32x4 g = ld4<TI>(gate + r * ld_gu + c), u = ld4<TI>(up + r * ld_gu + c);
+            f32x4 dg, du;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float a, b;
+                swiglu_grad(go[q], g[q], u[q], a, b);
+                dg[q] = a;
+                du[q] = b;
+            }
+            st4<TO>(dgate + r * ld_out + c, dg);
+            st4<TO>(dup + r * ld_out + c, du);
+        }
+    } else {
+        for (int64_t c = threadIdx.x; c < cols; c += 256) {
+            float dg, du;
+            swiglu_grad(dh[r * ld_dh + c], ldv<TI>(gate, r * ld_gu + c), ldv<TI>(up, r * ld_gu + c), dg, du);
+            stv<TO>(dup, r * ld_out + c, du);
+            stv<TO>(dgate, r * ld_out + c, dg);
+        }
     }
 }
 
@@ -431,6 +546,7 @@ __device__ __forceinline__ int table_find(const TensorTable &t, int64_t b) {
 }
 
 // Sum of squares in double: each block sums its MT_ELEMS-element chunk of one tensor into part[slot].
+// 16-byte loads (four in flight per thread) where the tensor is 16-byte aligned; elementwise otherwise.
 __global__ __launch_bounds__(256) void sumsq_kernel(const TensorTable t, double *part) {
     __shared__ double red[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -440,9 +556,19 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const TensorTable t, double 
     const int64_t e1 = min(t.n[i], e0 + MT_ELEMS);
     const float *g = t.g[i];
     double s = 0.0;
-    for (int64_t e = e0 + tid; e < e1; e += 256) {
-        const double v = (double)g[e];
-        s += v * v;
+    if ((uintptr_t)g % 16 == 0 && e1 - e0 == MT_ELEMS) {
+        f32x4 v[MT_ELEMS / 1024];
+#pragma unroll
+        for (int k = 0; k < MT_ELEMS / 1024; ++k) v[k] = *(const f32x4 *)(g + e0 + 4 * (tid + 256 * k));
+#pragma unroll
+        for (int k = 0; k < MT_ELEMS / 1024; ++k)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s += (double)v[k][q] * (double)v[k][q];
+    } else {
+        for (int64_t e = e0 + tid; e < e1; e += 256) {
+            const double v = (double)g[e];
+            s += v * v;
+        }
     }
     s = wsum(s);
     if (lane == 0) red[wave] = s;
@@ -469,10 +595,20 @@ __global__ __launch_bounds__(256) void norm_finish_kernel(const double *part, in
 
 // Lion, per element: g' = g * scale; u = beta2 m + (1 - beta2) g'; m = beta1 m + (1 - beta1) g';
 // w = w - lr sign(u) - lr wd w. scale and lr come from device memory when given (a clip factor
-// computed on the GPU, a schedule value updated between graph replays).
+// computed on the GPU, a schedule value updated between graph replays). 16-byte accesses where all
+// three buffers are 16-byte aligned and the chunk is whole.
+__device__ __forceinline__ void lion_elem(float &w, float &m, float g, float rate, float beta1, float beta2,
+                                          float wd, float scale) {
+#pragma clang fp contract(off)  // separate roundings, as the reference's expression is written
+    const float gi = g * scale;
+    const float u = beta2 * m + (1.0f - beta2) * gi;
+    const float dir = u > 0.f ? 1.f : (u < 0.f ? -1.f : 0.f);
+    m = beta1 * m + (1.0f - beta1) * gi;
+    w = w - rate * dir - rate * wd * w;
+}
+
 __global__ __launch_bounds__(256) void lion_kernel(const TensorTable t, float lr, float beta1, float beta2,
                                                    float wd, const float *scale_dev, const float *lr_dev) {
-#pragma clang fp contract(off)  // separate roundings, as the reference's expression is written
     const int64_t b = blockIdx.x;
     const int i = table_find(t, b);
     const int64_t e0 = (b - t.first_block[i]) * MT_ELEMS;
@@ -481,13 +617,37 @@ __global__ __launch_bounds__(256) void lion_kernel(const TensorTable t, float lr
     const float rate = lr_dev ? lr_dev[0] : lr;
     float *w = t.w[i], *m = t.m[i];
     const float *g = t.g[i];
-    for (int64_t e = e0 + threadIdx.x; e < e1; e += 256) {
-        const float gi = g[e] * scale;
-        const float mi = m[e], wi = w[e];
-        const float u = beta2 * mi + (1.0f - beta2) * gi;
-        const float dir = u > 0.f ? 1.f : (u < 0.f ? -1.f : 0.f);
-        m[e] = beta1 * mi + (1.0f - beta1) * gi;
-        w[e] = wi - rate * dir - rate * wd * wi;
+    const bool vec = ((uintptr_t)w | (uintptr_t)m | (uintptr_t)g) % 16 == 0 && e1 - e0 == MT_ELEMS;
+    if (vec) {
+        constexpr int NV = MT_ELEMS / 1024;
+        f32x4 wv[NV], mv[NV], gv[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int64_t e = e0 + 4 * (threadIdx.x + 256 * k);
+            wv[k] = *(const f32x4 *)(w + e);
+            mv[k] = *(const f32x4 *)(m + e);
+            gv[k] = *(const f32x4 *)(g + e);
+        }
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int64_t e = e0 + 4 * (threadIdx.x + 256 * k);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float wq = wv[k][q], mq = mv[k][q];
+                lion_elem(wq, mq, gv[k][q], rate, beta1, beta2, wd, scale);
+                wv[k][q] = wq;
+                mv[k][q] = mq;
+            }
+            *(f32x4 *)(w + e) = wv[k];
+            *(f32x4 *)(m + e) = mv[k];
+        }
+    } else {
+        for (int64_t e = e0 + threadIdx.x; e < e1; e += 256) {
+            float wi = w[e], mi = m[e];
+            lion_elem(wi, mi, g[e], rate, beta1, beta2, wd, scale);
+            m[e] = mi;
+            w[e] = wi;
+        }
     }
 }
 
@@ -498,48 +658,81 @@ __global__ __launch_bounds__(256) void lion_kernel(const TensorTable t, float lr
 it_status launch_rmsnorm_forward(hipStream_t s, bool y_bf16, int64_t rows, int64_t dim, float eps, const float *x,
                                  const float *res, const float *gamma, float *sum_out, void *y) {
     const unsigned grid = blocks_for(rows, 4);
-    if (y_bf16)
-        hipLaunchKernelGGL(rmsnorm_fwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, x, res, sum_out, gamma,
-                           (uint16_t *)y, rows, dim, eps);
-    else
-        hipLaunchKernelGGL(rmsnorm_fwd_kernel<float>, dim3(grid), dim3(256), 0, s, x, res, sum_out, gamma,
-                           (float *)y, rows, dim, eps);
+#define IT_RMSF(TY, K)                                                                                         \
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<TY, K>), dim3(grid), dim3(256), 0, s, x, res, sum_out, gamma, (TY *)y, \
+                       rows, dim, eps)
+#define IT_RMSF_K(TY)          \
+    if (dim <= 256)            \
+        IT_RMSF(TY, 4);        \
+    else if (dim <= 1024)      \
+        IT_RMSF(TY, 16);       \
+    else if (dim <= 2048)      \
+        IT_RMSF(TY, 32);       \
+    else                       \
+        IT_RMSF(TY, 0);
+    if (y_bf16) {
+        IT_RMSF_K(uint16_t)
+    } else {
+        IT_RMSF_K(float)
+    }
+#undef IT_RMSF_K
+#undef IT_RMSF
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
 }
 
+// Rows per block of the backward kernel: 4 waves x rows per wave.
+static int64_t rmsnorm_bwd_rows_per_block(int64_t dim) { return dim <= 256 ? 16 : 4; }
+
 int64_t rmsnorm_backward_scratch_bytes(int64_t rows, int64_t dim) {
-    return ((rows + RB_ROWS - 1) / RB_ROWS) * dim * (int64_t)sizeof(float);
+    const int64_t rpb = rmsnorm_bwd_rows_per_block(dim);
+    return ((rows + rpb - 1) / rpb) * dim * (int64_t)sizeof(float);
 }
 
 it_status launch_rmsnorm_backward(hipStream_t s, int64_t rows, int64_t dim, float eps, const float *dy,
                                   const float *x, const float *gamma, const float *gres, float *dx,
                                   float *dgamma, float *part) {
-    const int64_t blocks = (rows + RB_ROWS - 1) / RB_ROWS;
+    const int64_t rpb = rmsnorm_bwd_rows_per_block(dim);
+    const int64_t blocks = (rows + rpb - 1) / rpb;
+    if (blocks > 0x7fffffff) return fail(IT_ERR_DIMS, "rmsnorm_backward: too many rows");
     const size_t lds = 4 * (size_t)dim * sizeof(float);
     if (dim <= 256)
-        hipLaunchKernelGGL(rmsnorm_bwd_kernel<4>, dim3((unsigned)blocks), dim3(256), lds, s, dy, x, gamma, gres, dx,
-                           part, rows, dim, eps);
+        hipLaunchKernelGGL((rmsnorm_bwd_kernel<4, 4>), dim3((unsigned)blocks), dim3(256), lds, s, dy, x, gamma, gres,
+                           dx, part, rows, dim, eps);
     else if (dim <= 1024)
-        hipLaunchKernelGGL(rmsnorm_bwd_kernel<16>, dim3((unsigned)blocks), dim3(256), lds, s, dy, x, gamma, gres,
-                           dx, part, rows, dim, eps);
+        hipLaunchKernelGGL((rmsnorm_bwd_kernel<16, 1>), dim3((unsigned)blocks), dim3(256), lds, s, dy, x, gamma,
+                           gres, dx, part, rows, dim, eps);
     else
-        hipLaunchKernelGGL(rmsnorm_bwd_kernel<32>, dim3((unsigned)blocks), dim3(256), lds, s, dy, x, gamma, gres,
-                           dx, part, rows, dim, eps);
+        hipLaunchKernelGGL((rmsnorm_bwd_kernel<32, 1>), dim3((unsigned)blocks), dim3(256), lds, s, dy, x, gamma,
+                           gres, dx, part, rows, dim, eps);
     IT_HIP_TRY(hipGetLastError());
-    hipLaunchKernelGGL(rmsnorm_dgamma_reduce, dim3(blocks_for(dim, 64)), dim3(256), 0, s, part, dgamma, blocks,
-                       dim);
+    hipLaunchKernelGGL(rmsnorm_dgamma_reduce, dim3(blocks_for(dim, 64)), dim3(1024), 0, s, part, dgamma, blocks, dim);
+    IT_HIP_TRY(hipGetLastError());
+    return IT_OK;
+}
+
+it_status launch_rope_table(hipStream_t s, int64_t seq, int64_t head_dim, float base, int64_t offset, void *table) {
+    const int64_t n = seq * (head_dim / 2);
+    if (n == 0) return IT_OK;
+    hipLaunchKernelGGL(rope_table_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, (float2 *)table, seq, head_dim,
+                       base, offset);
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
 }
 
 it_status launch_rope(hipStream_t s, bool src_bf16, bool dst_bf16, int64_t batch, int64_t seq, int64_t heads,
-                      int64_t head_dim, float base, int64_t offset, int backward, const void *src, int64_t src_rs,
+                      int64_t head_dim, const void *table, int backward, const void *src, int64_t src_rs,
                       void *dst, int64_t dst_rs, int64_t copy_cols) {
-    const dim3 grid((unsigned)(batch * seq));
-#define IT_ROPE(TS, TD)                                                                                        \
-    hipLaunchKernelGGL((rope_kernel<TS, TD>), grid, dim3(256), 0, s, (const TS *)src, (TD *)dst, seq, heads,   \
-                       head_dim, src_rs, dst_rs, copy_cols, base, offset, backward)
+    const int64_t rows = batch * seq;
+    const int half = (int)(head_dim / 2);
+    if (heads * half > 0x3fffffff || copy_cols > 0x3fffffff) return fail(IT_ERR_DIMS, "rope: rows too wide");
+    const int64_t per_row = heads * half + (copy_cols + 1) / 2;
+    const int64_t blocks = (rows * per_row + 255) / 256;
+    if (blocks > 0x7fffffff) return fail(IT_ERR_DIMS, "rope: too many elements");
+    if (blocks == 0) return IT_OK;
+#define IT_ROPE(TS, TD)                                                                                         \
+    hipLaunchKernelGGL((rope_kernel<TS, TD>), dim3((unsigned)blocks), dim3(256), 0, s, (const TS *)src, (TD *)dst, \
+                       (const float2 *)table, rows, seq, (int)heads, half, src_rs, dst_rs, (int)copy_cols, backward)
     if (!src_bf16 && !dst_bf16)
         IT_ROPE(float, float);
     else if (!src_bf16 && dst_bf16)
@@ -615,17 +808,26 @@ it_status launch_swiglu_backward(hipStream_t s, bool in_bf16, bool out_bf16, int
                                  const float *dh, int64_t ld_dh, const void *gate, const void *up, int64_t ld_gu,
                                  void *dgate, void *dup, int64_t ld_out) {
     const dim3 grid((unsigned)rows);
-#define IT_SWB(TI, TO)                                                                                          \
-    hipLaunchKernelGGL((swiglu_bwd_kernel<TI, TO>), grid, dim3(256), 0, s, dh, ld_dh, (const TI *)gate,         \
-                       (const TI *)up, ld_gu, (TO *)dgate, (TO *)dup, ld_out, cols)
-    if (!in_bf16 && !out_bf16)
-        IT_SWB(float, float);
-    else if (!in_bf16 && out_bf16)
-        IT_SWB(float, uint16_t);
-    else if (in_bf16 && out_bf16)
-        IT_SWB(uint16_t, uint16_t);
-    else
-        IT_SWB(uint16_t, float);
+    const uintptr_t ia = in_bf16 ? 8 : 16, oa = out_bf16 ? 8 : 16;
+    const bool vec = cols % 4 == 0 && ld_dh % 4 == 0 && ld_gu % 4 == 0 && ld_out % 4 == 0 && (uintptr_t)dh % 16 == 0 &&
+                     (uintptr_t)gate % ia == 0 && (uintptr_t)up % ia == 0 && (uintptr_t)dgate % oa == 0 &&
+                     (uintptr_t)dup % oa == 0;
+#define IT_SWB(TI, TO)                                                                                           \
+    if (vec)                                                                                                     \
+        hipLaunchKernelGGL((swiglu_bwd_kernel<TI, TO, 4>), grid, dim3(256), 0, s, dh, ld_dh, (const TI *)gate,   \
+                           (const TI *)up, ld_gu, (TO *)dgate, (TO *)dup, ld_out, cols);                         \
+    else                                                                                                         \
+        hipLaunchKernelGGL((swiglu_bwd_kernel<TI, TO, 1>), grid, dim3(256), 0, s, dh, ld_dh, (const TI *)gate,   \
+                           (const TI *)up, ld_gu, (TO *)dgate, (TO *)dup, ld_out, cols);
+    if (!in_bf16 && !out_bf16) {
+        IT_SWB(float, float)
+    } else if (!in_bf16 && out_bf16) {
+        IT_SWB(float, uint16_t)
+    } else if (in_bf16 && out_bf16) {
+        IT_SWB(uint16_t, uint16_t)
+    } else {
+        IT_SWB(uint16_t, float)
+    }
 #undef IT_SWB
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;

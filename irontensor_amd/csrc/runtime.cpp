@@ -191,6 +191,7 @@ it_status it_shutdown(it_context *ctx) {
     for (auto e : ctx->event_pool) (void)hipEventDestroy(e);
     for (auto &kv : ctx->cache) (void)hipFree(kv.second);
     for (auto &kv : ctx->live) (void)hipFree(kv.first);
+    for (auto &kv : ctx->rope_tables) (void)hipFree(kv.second);
     for (int i = 0; i < 2; ++i) {
         if (ctx->scratch[i]) (void)hipFree(ctx->scratch[i]);
         if (ctx->attn_scratch[i]) (void)hipFree(ctx->attn_scratch[i]);
