@@ -309,59 +309,63 @@ def kernel_only(it, ctx, step, iters: int) -> int:
 
 
 def cpu_baseline(step) -> dict:
-    """The oracle's sequential f32 loop (the reference's CPU matmul), row-parallel over host cores,
-    over one whole TINY step: every layer's forward and backward GEMMs at the step's real shapes
-    (the fused QKV and gate|up weights as single GEMMs, as on the GPU), the attention forward and
-    backward per layer, and the three LM-head GEMMs. Config 1 is also timed on one thread."""
+    """One complete TINY training step on the oracle (oracle/train_step.py: embedding, layers, final
+    norm, LM head, cross entropy, backward, clip, Lion) on host cores; its contractions are the
+    reference's sequential f32 loop (oracle/ref.c), row-parallel over all host threads. `value` is
+    the contractions' FLOPs over the time spent in them (timed call by call inside the step);
+    `train_step_ms` is the whole step. Config 1 is also timed on one thread."""
     import oracle
+    from oracle import train_step as ots
     from irontensor_amd import synth
     s = step.s
-    T, H, F, V = s.tokens, s.hidden, s.ffn, s.vocab
+    H, F, V, L = s.hidden, s.ffn, s.vocab, s.layers
     thr = oracle.default_threads()
     w = lambda sh, seed: synth.pooled_normal(seed, sh, std=0.02)  # noqa: E731
-    a = lambda sh, seed: synth.pooled_normal(seed, sh)  # noqa: E731
-    X, X2, Hh, O = a((T, H), 1), a((T, H), 2), a((T, F), 3), a((T, H), 4)
-    Wqkv, Wo, Wgu, Wd, E = w((3 * H, H), 5), w((H, H), 6), w((2 * F, H), 7), w((H, F), 8), w((V, H), 9)
-    dZ, dGU, dY, dQKV = a((T, H), 10), a((T, 2 * F), 11), a((T, H), 12), a((T, 3 * H), 13)
-    Hf, dlog = a((T, H), 14), a((T, V), 15)
-    layer = [
-        (X, Wqkv, False, True), (O, Wo, False, True), (X2, Wgu, False, True), (Hh, Wd, False, True),
-        (dZ, Wd, False, False), (dZ, Hh, True, False), (dGU, Wgu, False, False), (dGU, X2, True, False),
-        (dY, Wo, False, False), (dY, O, True, False), (dQKV, Wqkv, False, False), (dQKV, X, True, False),
-    ]
-    lm = [(Hf, E, False, True), (dlog, Hf, True, False), (dlog, E, False, False)]
-    bh = s.batch * s.heads
-    q, k, v, do = (a((bh, s.seq, s.head_dim), 20 + i) for i in range(4))
-    flops = 0.0
-    t0 = time.perf_counter()
-    for _ in range(s.layers):
-        for A, B, ta, tb in layer:
-            oracle.gemm_f32(A, B, ta, tb, threads=thr)
-            flops += 2.0 * A.shape[0] * A.shape[1] * (B.shape[0] if tb else B.shape[1])
-        oracle.attention_fwd_bhsd(q, k, v, 0.125, True, threads=thr)
-        oracle.attention_bwd_bhsd(do, q, k, v, 0.125, True, threads=thr)
-        flops += 7 * 2.0 * bh * s.seq * s.seq * s.head_dim
-    for A, B, ta, tb in lm:
-        oracle.gemm_f32(A, B, ta, tb, threads=thr)
-        flops += 2.0 * A.shape[0] * A.shape[1] * (B.shape[0] if tb else B.shape[1])
-    dt = time.perf_counter() - t0
-    # config 1 on one thread, for the per-core figure
-    x1, w1 = a((4096, 256), 30), w((768, 256), 31)
-    t1 = time.perf_counter()
-    oracle.gemm_f32(x1, w1, False, True, threads=1)
-    dt1 = time.perf_counter() - t1
-    # the complete training step (embedding .. Lion) on the oracle, once
-    from oracle import train_step as ots
-    L = s.layers
+    acc = {"t": 0.0, "flops": 0.0}
+
+    def timed(fn, flops_of):
+        def run(*a, **k):
+            t = time.perf_counter()
+            out = fn(*a, **k)
+            acc["t"] += time.perf_counter() - t
+            acc["flops"] += flops_of(*a, **k)
+            return out
+        return run
+
+    def gemm_flops(a, b, trans_a=False, trans_b=False, threads=None):
+        m, kk = (a.shape[1], a.shape[0]) if trans_a else a.shape
+        n = b.shape[0] if trans_b else b.shape[1]
+        return 2.0 * m * n * kk
+
+    def attn_flops(n_gemms):
+        def f(*a, **k):
+            q = a[1] if n_gemms == 5 else a[0]
+            bh, sq, d = q.shape
+            return n_gemms * 2.0 * bh * sq * sq * d
+        return f
+
     prm = {"emb": w((V, H), 40), "E": w((V, H), 41), "final_norm": np.ones(H, np.float32),
            "attn_norm": [np.ones(H, np.float32)] * L, "ffn_norm": [np.ones(H, np.float32)] * L,
            "Wqkv": [w((3 * H, H), 42 + l) for l in range(L)], "Wo": [w((H, H), 50 + l) for l in range(L)],
            "Wgu": [w((2 * F, H), 60 + l) for l in range(L)], "Wd": [w((H, F), 70 + l) for l in range(L)]}
     mom = [np.zeros_like(x) for x in ots.param_list(prm)]
     stream = synth.tokens(99, s.batch * (s.seq + 1), V).reshape(s.batch, s.seq + 1)
-    t2 = time.perf_counter()
-    ots.train_step(prm, mom, stream[:, :-1].ravel(), stream[:, 1:].ravel(), s, threads=thr)
-    dt2 = time.perf_counter() - t2
+    saved = (ots.gemm_f32, ots.attention_fwd_bhsd, ots.attention_bwd_bhsd)
+    ots.gemm_f32 = timed(saved[0], gemm_flops)
+    ots.attention_fwd_bhsd = timed(saved[1], attn_flops(2))
+    ots.attention_bwd_bhsd = timed(saved[2], attn_flops(5))
+    try:
+        t0 = time.perf_counter()
+        ots.train_step(prm, mom, stream[:, :-1].ravel(), stream[:, 1:].ravel(), s, threads=thr)
+        dt = time.perf_counter() - t0
+    finally:
+        ots.gemm_f32, ots.attention_fwd_bhsd, ots.attention_bwd_bhsd = saved
+    # config 1 on one thread, for the per-core figure
+    a = lambda sh, seed: synth.pooled_normal(seed, sh)  # noqa: E731
+    x1, w1 = a((4096, 256), 30), w((768, 256), 31)
+    t1 = time.perf_counter()
+    oracle.gemm_f32(x1, w1, False, True, threads=1)
+    dt1 = time.perf_counter() - t1
     model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -370,20 +374,18 @@ def cpu_baseline(step) -> dict:
                 break
     except OSError:
         pass
-    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": thr,
+    return {"value": round(acc["flops"] / acc["t"] / 1e12, 5), "unit": "TFLOP/s", "cores": thr,
             "host_cpus": os.cpu_count(), "cpu_model": model,
             "config1_one_thread_ms": round(dt1 * 1e3, 1),
             "config1_one_thread_gflops": round(2 * 4096 * 768 * 256 / dt1 / 1e9, 3),
             "kind": "port",
-            "sample": (f"one whole TINY step: {s.layers} layers x (12 linear GEMMs + attention forward and "
-                       f"backward) + 3 LM-head GEMMs, {flops / 1e9:.1f} GFLOP in {dt:.2f} s; oracle/ref.c "
-                       f"sequential f32 loop (no FMA contraction), {thr} threads, pooled N(0,1)/N(0,0.02) inputs"),
+            "sample": (f"one complete TINY training step on the oracle: {acc['flops'] / 1e9:.1f} GFLOP of "
+                       f"contractions (linear GEMMs, attention forward and backward, LM head) in "
+                       f"{acc['t']:.2f} s of a {dt:.2f} s step; oracle/ref.c sequential f32 loop (no FMA "
+                       f"contraction), {thr} threads"),
             "seconds": round(dt, 2),
-            "ms_per_step": round(dt * 1e3, 1),
-            "train_step_ms": round(dt2 * 1e3, 1),
-            "train_step_sample": ("one complete TINY training step on the oracle (oracle/train_step.py: "
-                                  "embedding, layers, final norm, LM head, cross entropy, backward, clip, "
-                                  f"Lion), {thr} threads for the contractions")}
+            "contraction_seconds": round(acc["t"], 2),
+            "train_step_ms": round(dt * 1e3, 1)}
 
 
 def main() -> int:
@@ -395,6 +397,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip the extra GEMM figures")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only a calibration copy and the dominant kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--train-only", action="store_true",
+                    help="run only the complete TINY training step, graph-replayed (for kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -413,6 +417,9 @@ def main() -> int:
     ctx = it.Context.global_()
     info = ctx.info()
     log(f"[bench] device {info}")
+    if args.train_only:
+        print(json.dumps({"train_step": train_step_figures(it, Timer(ctx), args.steps, args.warmup)}), flush=True)
+        return 0
     step = GemmStep(TINY, it.Precision.FP32, ctx)
     step.enqueue()                      # eager once: records the launch list, sizes scratch
     ctx.sync()

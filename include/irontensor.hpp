@@ -16,6 +16,7 @@
 #include <cstdint>
 #include <cstring>
 #include <memory>
+#include <limits>
 #include <numeric>
 #include <sstream>
 #include <stdexcept>
@@ -552,5 +553,176 @@ inline AttentionGrads flash_attention_backward(const Tensor &grad_output, const 
           "attention_backward");
     return g;
 }
+
+// ------------------------------------------------------------------ training-step ops
+
+namespace detail {
+inline size_t last_dim(const Tensor &t) { return t.shape().empty() ? 1 : t.shape().back(); }
+// Host index check as the reference asserts it (src/ops/embedding.rs:41-49), then upload as uint32.
+inline Tensor upload_ids(const std::vector<uint32_t> &ids, size_t bound) {
+    for (size_t i = 0; i < ids.size(); ++i)
+        if (ids[i] >= bound)
+            throw Panic("Index " + std::to_string(ids[i]) + " at position " + std::to_string(i) +
+                        " is out of bounds for vocab_size " + std::to_string(bound));
+    Tensor t = Tensor::empty({ids.size()}, Precision::FP32);  // raw 32-bit words
+    if (!ids.empty()) check(it_memcpy_h2d(Context::global().handle(), t.data(), ids.data(), ids.size() * 4), "upload ids");
+    return t;
+}
+}  // namespace detail
+
+// rmsnorm (src/ops/norm.rs:31): y = x / sqrt(mean(x^2) + eps) * gamma over the last dimension.
+inline Tensor rmsnorm(const Tensor &input, const Tensor &gamma, float eps) {
+    if (!input.is_f32()) throw PrecisionMismatch("rmsnorm", "FP32", precision_name(input.precision()));
+    const size_t dim = detail::last_dim(input);
+    detail::require(gamma.numel() == dim, "gamma length must equal the last dimension");
+    Tensor y = Tensor::empty(input.shape(), Precision::FP32);
+    check(it_rmsnorm_forward(Context::global().handle(), IT_F32, (int64_t)(input.numel() / (dim ? dim : 1)),
+                             (int64_t)dim, eps, (const float *)input.data(), nullptr, (const float *)gamma.data(),
+                             nullptr, y.data()),
+          "rmsnorm");
+    return y;
+}
+
+// rmsnorm_backward (src/ops/backward/norm.rs:20) -> (grad_input, grad_gamma).
+inline std::pair<Tensor, Tensor> rmsnorm_backward(const Tensor &grad_output, const Tensor &input, const Tensor &gamma,
+                                                  float eps) {
+    detail::require(grad_output.shape() == input.shape(), "grad_output and input shapes differ");
+    const size_t dim = detail::last_dim(input);
+    Tensor dx = Tensor::empty(input.shape(), Precision::FP32), dg = Tensor::empty({dim}, Precision::FP32);
+    check(it_rmsnorm_backward(Context::global().handle(), (int64_t)(input.numel() / (dim ? dim : 1)), (int64_t)dim, eps,
+                              (const float *)grad_output.data(), (const float *)input.data(),
+                              (const float *)gamma.data(), nullptr, (float *)dx.data(), (float *)dg.data()),
+          "rmsnorm_backward");
+    return {dx, dg};
+}
+
+namespace detail {
+inline Tensor rope(const Tensor &x, float base, size_t offset, int backward) {
+    const auto &s = x.shape();
+    require(s.size() == 4, "rope expects [batch, seq, heads, head_dim]");
+    Tensor out = Tensor::empty(s, x.precision());
+    const int64_t w = (int64_t)(s[2] * s[3]);
+    check(it_rope(Context::global().handle(), (it_dtype)x.precision(), (it_dtype)x.precision(), (int64_t)s[0],
+                  (int64_t)s[1], (int64_t)s[2], (int64_t)s[3], base, (int64_t)offset, backward, x.data(), w,
+                  out.data(), w, 0),
+          backward ? "rope_backward" : "rope");
+    return out;
+}
+}  // namespace detail
+
+// rope (src/ops/rope.rs:22) and rope_backward (src/ops/backward/rope.rs:16).
+inline Tensor rope(const Tensor &input, float base, size_t position_offset) {
+    return detail::rope(input, base, position_offset, 0);
+}
+inline Tensor rope_backward(const Tensor &grad_output, float base, size_t position_offset) {
+    return detail::rope(grad_output, base, position_offset, 1);
+}
+
+// embedding (src/ops/embedding.rs:21): rows of weights [vocab, dim] by index, FP32 out.
+inline Tensor embedding(const Tensor &weights, const std::vector<uint32_t> &indices) {
+    detail::require(weights.shape().size() == 2, "Weights must be 2D [vocab_size, embed_dim]");
+    const size_t vocab = weights.shape()[0], dim = weights.shape()[1];
+    Tensor ids = detail::upload_ids(indices, vocab);
+    Tensor out = Tensor::empty({indices.size(), dim}, Precision::FP32);
+    check(it_embedding_forward(Context::global().handle(), (it_dtype)weights.precision(), IT_F32,
+                               (int64_t)indices.size(), (int64_t)dim, (int64_t)vocab, weights.data(),
+                               (const uint32_t *)ids.data(), out.data()),
+          "embedding");
+    return out;
+}
+
+// embedding_backward (src/ops/backward/embedding.rs:21): deterministic scatter-add.
+inline Tensor embedding_backward(const Tensor &grad_output, const std::vector<uint32_t> &indices, size_t vocab_size) {
+    detail::require(grad_output.is_f32(), "assertion `left == right` failed: embedding_backward requires FP32");
+    detail::require(grad_output.shape().size() == 2, "grad_output must be 2D");
+    const size_t n = grad_output.shape()[0], dim = grad_output.shape()[1];
+    detail::require(indices.size() == n, "assertion `left == right` failed: indices length");
+    Tensor ids = detail::upload_ids(indices, vocab_size);
+    Tensor dw = Tensor::empty({vocab_size, dim}, Precision::FP32);
+    check(it_embedding_backward(Context::global().handle(), (int64_t)n, (int64_t)dim, (int64_t)vocab_size,
+                                (const float *)grad_output.data(), (const uint32_t *)ids.data(), (float *)dw.data()),
+          "embedding_backward");
+    return dw;
+}
+
+// cross_entropy_fused (src/ops/backward/loss.rs:248) -> (mean loss, losses [rows], grad [rows, vocab]).
+struct CrossEntropy {
+    float loss;
+    Tensor losses, grad;
+};
+inline CrossEntropy cross_entropy_fused(const Tensor &logits, const std::vector<uint32_t> &targets) {
+    detail::require(logits.is_f32(), "assertion `left == right` failed: cross_entropy_fused requires FP32");
+    detail::require(logits.shape().size() == 2, "logits must be 2D");
+    const size_t rows = logits.shape()[0], vocab = logits.shape()[1];
+    detail::require(targets.size() == rows, "assertion `left == right` failed: targets length");
+    CrossEntropy r{0.f, Tensor::zeros({rows}, Precision::FP32), Tensor::zeros({rows, vocab}, Precision::FP32)};
+    if (rows == 0) return r;
+    Tensor t = detail::upload_ids(targets, vocab);
+    Tensor mean = Tensor::empty({1}, Precision::FP32);
+    check(it_cross_entropy_fused(Context::global().handle(), IT_F32, (int64_t)rows, (int64_t)vocab,
+                                 (const float *)logits.data(), (const uint32_t *)t.data(), (float *)r.losses.data(),
+                                 r.grad.data(), (float *)mean.data()),
+          "cross_entropy_fused");
+    r.loss = mean.as_f32_slice()[0];
+    return r;
+}
+
+// swiglu_backward (src/ops/backward/elementwise.rs:149) -> (grad_gate, grad_up).
+inline std::pair<Tensor, Tensor> swiglu_backward(const Tensor &grad_output, const Tensor &gate, const Tensor &up) {
+    detail::require(grad_output.shape() == gate.shape() && gate.shape() == up.shape(), "swiglu_backward: shapes differ");
+    const size_t cols = detail::last_dim(gate), rows = gate.numel() / (cols ? cols : 1);
+    Tensor gg = Tensor::empty(gate.shape(), Precision::FP32), gu = Tensor::empty(gate.shape(), Precision::FP32);
+    check(it_swiglu_backward(Context::global().handle(), (it_dtype)gate.precision(), IT_F32, (int64_t)rows,
+                             (int64_t)cols, (const float *)grad_output.data(), (int64_t)cols, gate.data(), up.data(),
+                             (int64_t)cols, gg.data(), gu.data(), (int64_t)cols),
+          "swiglu_backward");
+    return {gg, gu};
+}
+
+// total_l2_norm_gpu (src/ops/reduction.rs:94): sqrt of the summed squares of all tensors.
+inline float total_l2_norm_gpu(const std::vector<const Tensor *> &tensors) {
+    if (tensors.empty()) return 0.f;
+    std::vector<const float *> p;
+    std::vector<int64_t> n;
+    for (const Tensor *t : tensors) {
+        p.push_back((const float *)t->data());
+        n.push_back((int64_t)t->numel());
+    }
+    Tensor out = Tensor::empty({2}, Precision::FP32);
+    check(it_grad_norm_clip(Context::global().handle(), (int)p.size(), p.data(), n.data(),
+                            std::numeric_limits<float>::infinity(), (float *)out.data()),
+          "total_l2_norm_gpu");
+    return out.as_f32_slice()[0];
+}
+
+// Lion (src/optim/lion/optimizer.rs:32-106; LionConfig defaults src/optim/lion/config.rs:91-99).
+struct LionConfig {
+    float lr = 1e-4f, beta1 = 0.9f, beta2 = 0.99f, weight_decay = 0.f;
+};
+struct ParamState {
+    Tensor momentum;
+    explicit ParamState(const Tensor &weights) : momentum(Tensor::zeros(weights.shape(), Precision::FP32)) {}
+};
+class Lion {
+  public:
+    explicit Lion(LionConfig c) : c_(c) {}
+    static Lion with_lr(float lr) { return Lion(LionConfig{lr}); }
+    float lr() const { return c_.lr; }
+    void set_lr(float lr) { c_.lr = lr; }
+    // Updates weights and state.momentum in place.
+    void step(const Tensor &weights, const Tensor &gradients, ParamState &state) const {
+        detail::require(weights.is_f32() && gradients.is_f32(), "lion: FP32 weights and gradients");
+        detail::require(weights.numel() == gradients.numel(), "lion: weights and gradients differ in size");
+        float *w = (float *)weights.data(), *m = (float *)state.momentum.data();
+        const float *g = (const float *)gradients.data();
+        const int64_t n = (int64_t)weights.numel();
+        check(it_lion_step(Context::global().handle(), 1, &w, &m, &g, &n, c_.lr, c_.beta1, c_.beta2, c_.weight_decay,
+                           nullptr, nullptr),
+              "lion");
+    }
+
+  private:
+    LionConfig c_;
+};
 
 }  // namespace irontensor

@@ -245,6 +245,57 @@ static void gpu_tests() {
         CHECK(c.as_f32_slice()[0] == 64.0f);
         CHECK(gpu_memory_allocated() > 0);
     });
+    run("rmsnorm_closed_forms", [] {  // src/ops/norm.rs:31
+        Tensor x = Tensor::from_f32_slice(std::vector<float>(3 * 8, 2.0f), {3, 8});
+        Tensor g = Tensor::from_f32_slice({1, 2, 3, 4, 5, 6, 7, 8}, {8});
+        std::vector<float> y = rmsnorm(x, g, 0.f).as_f32_slice();
+        for (int r = 0; r < 3; ++r)
+            for (int c = 0; c < 8; ++c) CHECK(std::fabs(y[r * 8 + c] - (c + 1)) < 1e-6f);
+        auto [dx, dg] = rmsnorm_backward(Tensor::zeros({3, 8}, Precision::FP32), x, g, 1e-5f);
+        for (float v : dx.as_f32_slice()) CHECK(v == 0.f);
+        for (float v : dg.as_f32_slice()) CHECK(v == 0.f);
+    });
+    run("rope_inverse_and_position_zero", [] {  // src/ops/rope.rs:22, src/ops/backward/rope.rs:16
+        std::vector<float> h(2 * 5 * 2 * 8);
+        for (size_t i = 0; i < h.size(); ++i) h[i] = std::sin(0.37f * (float)i);
+        Tensor x = Tensor::from_f32_slice(h, {2, 5, 2, 8});
+        std::vector<float> y = rope(x, 10000.f, 0).as_f32_slice();
+        std::vector<float> back = rope_backward(rope(x, 10000.f, 0), 10000.f, 0).as_f32_slice();
+        for (size_t i = 0; i < h.size(); ++i) CHECK(std::fabs(back[i] - h[i]) < 1e-5f);
+        for (int b = 0; b < 2; ++b)
+            for (int i = 0; i < 16; ++i) CHECK(y[b * 80 + i] == h[b * 80 + i]);  // position 0 unrotated
+    });
+    run("embedding_gather_scatter", [] {  // src/ops/embedding.rs:21, src/ops/backward/embedding.rs:21
+        Tensor w = Tensor::from_f32_slice({0, 1, 10, 11, 20, 21}, {3, 2});
+        std::vector<float> e = embedding(w, {2, 0, 2}).as_f32_slice();
+        CHECK((e == std::vector<float>{20, 21, 0, 1, 20, 21}));
+        Tensor dy = Tensor::from_f32_slice({1, 2, 3, 4, 5, 6}, {3, 2});
+        CHECK((embedding_backward(dy, {2, 0, 2}, 3).as_f32_slice() == std::vector<float>{3, 4, 0, 0, 6, 8}));
+        expect_throw<Panic>([&] { embedding(w, {3}); });
+    });
+    run("cross_entropy_uniform_logits", [] {  // src/ops/backward/loss.rs:248
+        CrossEntropy ce = cross_entropy_fused(Tensor::zeros({4, 10}, Precision::FP32), {0, 3, 9, 5});
+        CHECK(std::fabs(ce.loss - std::log(10.f)) < 1e-6f);
+        std::vector<float> g = ce.grad.as_f32_slice();
+        CHECK(std::fabs(g[0] - (0.1f - 1.f) / 4.f) < 1e-7f && std::fabs(g[1] - 0.1f / 4.f) < 1e-7f);
+    });
+    run("swiglu_backward_at_zero", [] {  // src/shaders/backward/elementwise.metal:101-126
+        Tensor one = Tensor::from_f32_slice({1, 1}, {1, 2}), zero = Tensor::zeros({1, 2}, Precision::FP32);
+        auto [gg, gu] = swiglu_backward(one, zero, one);
+        for (float v : gg.as_f32_slice()) CHECK(v == 0.5f);  // sig(0) * (1 + 0) * up
+        for (float v : gu.as_f32_slice()) CHECK(v == 0.f);   // silu(0)
+    });
+    run("l2_norm_and_lion", [] {  // src/ops/reduction.rs:94, src/shaders/lion.metal
+        Tensor a = Tensor::from_f32_slice({3, 0}, {2}), b = Tensor::from_f32_slice({4}, {1});
+        CHECK(total_l2_norm_gpu({&a, &b}) == 5.f);
+        Tensor w = Tensor::from_f32_slice({1.f, -2.f}, {2}), g = Tensor::from_f32_slice({1.f, -1.f}, {2});
+        ParamState st(w);
+        Lion opt(LionConfig{0.5f, 0.9f, 0.99f, 0.f});
+        opt.step(w, g, st);
+        CHECK((w.as_f32_slice() == std::vector<float>{0.5f, -1.5f}));
+        std::vector<float> m = st.momentum.as_f32_slice();
+        CHECK(std::fabs(m[0] - 0.1f) < 1e-7f && std::fabs(m[1] + 0.1f) < 1e-7f);
+    });
 }
 
 int main(int argc, char **argv) {
