@@ -252,9 +252,75 @@ def train_step_figures(it, timer, steps: int, warmup: int) -> dict:
             "execution": "one hipGraph per step; weight gradients on a second stream; loss, norm and clip stay on the GPU"}
 
 
+def extra_fusions(it, timer, iters: int = 10) -> dict:
+    """The reference's GEMM prologue/epilogue fusions against the unfused ops, at the TINY step's
+    shapes: RMSNorm -> Q|K|V projection ([4096, 256] -> 768) and the LM head with cross entropy
+    ([4096, 256] x [16384, 256]^T, loss + grad_hidden + grad_weight), one vocabulary chunk (the
+    default 256 MiB budget) and four (64 MiB)."""
+    from irontensor_amd import synth, train_ops as T
+    P = it.Precision
+    out = {}
+
+    def run(fn):
+        fn()
+        it.Context.global_().sync()
+        timer.start()
+        for _ in range(iters):
+            fn()
+        return timer.stop_ms() / iters
+
+    x = it.Tensor.from_f32_slice(synth.pooled_normal(1, (4096, 256)), [4096, 256])
+    g = it.Tensor.from_f32_slice(1 + synth.pooled_normal(2, (256,), std=0.1), [256])
+    w = it.Tensor.from_f32_slice(synth.pooled_normal(3, (768, 256), std=0.02), [768, 256])
+    xn = it.Tensor.empty([4096, 256])
+    y = it.Tensor.empty([4096, 768])
+    lib, h = it.Context.global_().lib, it.Context.global_().handle
+
+    def unfused():
+        lib.it_rmsnorm_forward(h, 0, 4096, 256, 1e-5, C.c_void_p(x.ptr), None, C.c_void_p(g.ptr), None,
+                               C.c_void_p(xn.ptr))
+        it.gemm(xn, w, trans_b=True, out=y)
+
+    def fused():
+        lib.it_fused_rmsnorm_linear(h, 4096, 256, 768, 1e-5, C.c_void_p(x.ptr), C.c_void_p(g.ptr), C.c_void_p(w.ptr),
+                                    C.c_void_p(y.ptr))
+
+    out["rmsnorm_qkv_4096x256x768"] = {"unfused_us": round(run(unfused) * 1e3, 2), "fused_us": round(run(fused) * 1e3, 2)}
+    hs = it.Tensor.from_f32_slice(synth.pooled_normal(4, (4096, 256)), [4096, 256])
+    E = it.Tensor.from_f32_slice(synth.pooled_normal(5, (16384, 256), std=0.02), [16384, 256])
+    tg = synth.tokens(6, 4096, 16384)
+    t32 = it.Tensor.from_f32_slice(tg.astype(np.int32).view(np.float32), [4096])
+    tu = T.upload_ids(tg, 16384)
+    logits, dlog = it.Tensor.empty([4096, 16384]), it.Tensor.empty([4096, 16384])
+    dh, dw, mean = it.Tensor.empty([4096, 256]), it.Tensor.empty([16384, 256]), it.Tensor.empty([1])
+
+    def lm_unfused():
+        it.gemm(hs, E, trans_b=True, out=logits)
+        lib.it_cross_entropy_fused(h, 0, 4096, 16384, C.c_void_p(logits.ptr), C.c_void_p(tu.ptr), None,
+                                   C.c_void_p(dlog.ptr), C.c_void_p(mean.ptr))
+        it.gemm(dlog, hs, trans_a=True, out=dw)
+        it.gemm(dlog, E, out=dh)
+
+    def lm_fused(budget):
+        def f():
+            lib.it_fused_linear_cross_entropy(h, 4096, 256, 16384, C.c_void_p(hs.ptr), C.c_void_p(E.ptr),
+                                              C.c_void_p(t32.ptr), None, C.c_void_p(mean.ptr), C.c_void_p(dh.ptr),
+                                              C.c_void_p(dw.ptr), budget)
+        return f
+
+    out["lm_head_ce_4096x256x16384"] = {
+        "unfused_us": round(run(lm_unfused) * 1e3, 1),
+        "fused_1chunk_us": round(run(lm_fused(256 << 20)) * 1e3, 1),
+        "fused_4chunks_us": round(run(lm_fused(64 << 20)) * 1e3, 1),
+        "logits_bytes_unfused": 2 * 4096 * 16384 * 4, "logits_bytes_fused_4chunks": 4096 * 4096 * 4,
+        "note": "unfused: logits GEMM, cross entropy, dW and dX GEMMs (logits and dlogits buffers); fused: "
+                "chunk GEMM + stats, gradient in place, dW/dX GEMMs per chunk (chunks but the last one recomputed)"}
+    return {"fusions": out}
+
+
 def extras(it, timer) -> dict:
     out = {}
-    for fn in (extra_config1, extra_attention, extra_sweep, extra_med_step):
+    for fn in (extra_config1, extra_attention, extra_fusions, extra_sweep, extra_med_step):
         log(f"[bench] extra: {fn.__name__}")
         out.update(fn(it, timer))
     return out

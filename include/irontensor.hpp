@@ -725,4 +725,55 @@ class Lion {
     LionConfig c_;
 };
 
+// fused_rmsnorm_linear (src/ops/fused_rmsnorm_linear.rs:73-205): rmsnorm(input, gamma, eps) . weight^T
+// without the normalized intermediate.
+inline Tensor fused_rmsnorm_linear(const Tensor &input, const Tensor &gamma, const Tensor &weight, float eps) {
+    detail::require(input.is_f32(), "assertion `left == right` failed: Input must be FP32");
+    detail::require(input.shape().size() == 2, "Input must be 2D [batch_seq, hidden_dim]");
+    detail::require(weight.shape().size() == 2, "Weight must be 2D [out_features, hidden_dim]");
+    const size_t rows = input.shape()[0], hidden = input.shape()[1], out_f = weight.shape()[0];
+    detail::require(weight.shape()[1] == hidden, "Hidden dimensions must match");
+    detail::require(gamma.shape() == std::vector<size_t>{hidden}, "Gamma must have shape [hidden_dim]");
+    Tensor out = Tensor::empty({rows, out_f}, Precision::FP32);
+    check(it_fused_rmsnorm_linear(Context::global().handle(), (int64_t)rows, (int64_t)hidden, (int64_t)out_f, eps,
+                                  (const float *)input.data(), (const float *)gamma.data(),
+                                  (const float *)weight.data(), (float *)out.data()),
+          "fused_rmsnorm_linear");
+    return out;
+}
+
+// fused_linear_cross_entropy (src/ops/fused_linear_cross_entropy.rs:79-242): (mean loss, grad_hidden,
+// grad_weight) without the [rows, vocab] logits; targets < 0 or >= vocab (-100) are ignored;
+// grad_weight unscaled as in the reference. forward_only (:246-374) leaves grad_weight empty.
+struct FusedLinearCE {
+    float loss;
+    Tensor grad_hidden;
+    std::shared_ptr<Tensor> grad_weight;
+};
+inline FusedLinearCE fused_linear_cross_entropy(const Tensor &hidden, const Tensor &weight,
+                                                const std::vector<int32_t> &targets, bool forward_only = false,
+                                                int64_t chunk_bytes = 0) {
+    detail::require(hidden.is_f32() && weight.is_f32(), "assertion `left == right` failed: FP32 required");
+    detail::require(hidden.shape().size() == 2, "hidden must be 2D [batch*seq, hidden_dim]");
+    detail::require(weight.shape().size() == 2, "weight must be 2D [vocab_size, hidden_dim]");
+    const size_t rows = hidden.shape()[0], hd = hidden.shape()[1], vocab = weight.shape()[0];
+    detail::require(weight.shape()[1] == hd, "weight hidden_dim must match hidden");
+    detail::require(targets.size() == rows, "targets length must match batch*seq");
+    detail::require(hd <= 256, "hidden_dim must be <= 256 for this kernel");
+    FusedLinearCE r{0.f, Tensor::zeros({rows, hd}, Precision::FP32), nullptr};
+    if (!forward_only) r.grad_weight = std::make_shared<Tensor>(Tensor::zeros({vocab, hd}, Precision::FP32));
+    Tensor t = Tensor::empty({targets.size()}, Precision::FP32);  // raw int32 words
+    if (!targets.empty())
+        check(it_memcpy_h2d(Context::global().handle(), t.data(), targets.data(), targets.size() * 4), "upload targets");
+    Tensor mean = Tensor::zeros({1}, Precision::FP32);
+    check(it_fused_linear_cross_entropy(Context::global().handle(), (int64_t)rows, (int64_t)hd, (int64_t)vocab,
+                                        (const float *)hidden.data(), (const float *)weight.data(),
+                                        (const int32_t *)t.data(), nullptr, (float *)mean.data(),
+                                        (float *)r.grad_hidden.data(),
+                                        r.grad_weight ? (float *)r.grad_weight->data() : nullptr, chunk_bytes),
+          "fused_linear_cross_entropy");
+    r.loss = mean.as_f32_slice()[0];
+    return r;
+}
+
 }  // namespace irontensor

@@ -265,6 +265,31 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
 it_status it_rmsnorm_forward(it_context *ctx, it_dtype dtype_y, int64_t rows, int64_t dim, float eps,
                              const float *x, const float *res, const float *gamma, float *sum_out, void *y);
 
+/* Fused RMSNorm + projection: out[r, o] = (sum_j (x[r,j] * gamma[j]) * W[o,j]) / sqrt(mean(x_r^2) + eps),
+ * FP32; input [rows, hidden], gamma [hidden], weight [out_features, hidden] (the Linear layout),
+ * out [rows, out_features]. The normalized activations are never written: gamma scales the A tile
+ * on its way into the MFMA GEMM and 1/rms (one value per row, library scratch) scales the result.
+ * Replaces fused_rmsnorm_linear (src/ops/fused_rmsnorm_linear.rs:73-205; kernel
+ * src/shaders/fused_rmsnorm_linear.metal:42-114). */
+it_status it_fused_rmsnorm_linear(it_context *ctx, int64_t rows, int64_t hidden, int64_t out_features, float eps,
+                                  const float *input, const float *gamma, const float *weight, float *out);
+
+/* Fused linear + cross entropy without the [rows, vocab] logits: logits = H.W^T are produced in
+ * vocabulary chunks of at most chunk_bytes (<= 0: 256 MiB) by the MFMA GEMM, reduced to per-row
+ * (max, sum exp), combined into the log-sum-exp; then each chunk (recomputed unless it is the last
+ * one) becomes softmax - onehot in place and feeds grad_weight[v0:v0+n] = chunk^T.H and
+ * grad_hidden += chunk.W[v0:v0+n]. H [rows, hidden] and W [vocab, hidden] FP32; targets device
+ * int32, any value outside [0, vocab) (the reference's -100) ignored. Outputs: *loss_mean (device)
+ * = mean loss over valid rows; losses [rows] (NULL: scratch); grad_hidden (NULL: forward only) =
+ * gradient of the mean loss (scaled by 1 / valid count); grad_weight (NULL: skipped) UNSCALED, as
+ * the reference's weight-gradient kernel leaves it (src/shaders/fused_linear_cross_entropy.metal:
+ * 119-185). Deterministic (chunk order fixed). Replaces fused_linear_cross_entropy and
+ * fused_linear_cross_entropy_forward_only (src/ops/fused_linear_cross_entropy.rs:79-242, :246-374). */
+it_status it_fused_linear_cross_entropy(it_context *ctx, int64_t rows, int64_t hidden, int64_t vocab,
+                                        const float *hidden_states, const float *weight, const int32_t *targets,
+                                        float *losses, float *loss_mean, float *grad_hidden, float *grad_weight,
+                                        int64_t chunk_bytes);
+
 /* RMSNorm backward with the residual gradient added behind: dx = gres + dRMSNorm/dx . dy
  * (gres NULL: no add), dgamma[dim] = sum over rows of dy * x / rms (overwritten). dim <= 2048.
  * Replaces rmsnorm_backward (src/ops/backward/norm.rs:20) and add_tensors

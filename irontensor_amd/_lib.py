@@ -123,6 +123,10 @@ _SIGNATURES = {
     "it_grad_norm_clip": (c_int, [c_void_p, c_int, C.POINTER(c_void_p), C.POINTER(c_i64), c_float, c_void_p]),
     "it_lion_step": (c_int, [c_void_p, c_int, C.POINTER(c_void_p), C.POINTER(c_void_p), C.POINTER(c_void_p),
                              C.POINTER(c_i64), c_float, c_float, c_float, c_float, c_void_p, c_void_p]),
+    "it_fused_rmsnorm_linear": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_float, c_void_p, c_void_p, c_void_p,
+                                        c_void_p]),
+    "it_fused_linear_cross_entropy": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p,
+                                              c_void_p, c_void_p, c_void_p, c_void_p, c_i64]),
     "it_side_begin": (c_int, [c_void_p]),
     "it_side_end": (c_int, [c_void_p]),
     "it_side_join": (c_int, [c_void_p]),

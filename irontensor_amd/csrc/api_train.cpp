@@ -2,6 +2,7 @@
 // the reference's error cases (assert! on shapes and precisions becomes IT_ERR_*), library-owned
 // scratch for the deterministic reductions, and profiler keys for the step breakdown.
 #include <cstdint>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -68,6 +69,163 @@ it_status it_rmsnorm_backward(it_context *ctx, int64_t rows, int64_t dim, float 
     Prof p(ctx, std::string("rmsnorm_bwd") + (gres ? "_add" : "") + "[" + i64(rows) + "x" + i64(dim) + "]");
     return p.done(it::launch_rmsnorm_backward(ctx->stream, rows, dim, eps, dy, x, gamma, gres, dx, dgamma,
                                               (float *)part));
+}
+
+it_status it_fused_rmsnorm_linear(it_context *ctx, int64_t rows, int64_t hidden, int64_t out_features, float eps,
+                                  const float *input, const float *gamma, const float *weight, float *out) {
+    if (!ctx) return fail(IT_ERR_NULL, "fused_rmsnorm_linear: ctx is NULL");
+    if (rows < 0 || hidden < 0 || out_features < 0) return fail(IT_ERR_INVALID, "fused_rmsnorm_linear: negative size");
+    if (rows == 0 || out_features == 0) return IT_OK;
+    if (!out) return fail(IT_ERR_NULL, "fused_rmsnorm_linear: NULL buffer");
+    if (hidden == 0) return it::launch_zero(ctx->stream, out, (size_t)(rows * out_features) * sizeof(float));
+    if (!input || !gamma || !weight) return fail(IT_ERR_NULL, "fused_rmsnorm_linear: NULL buffer");
+    it::GemmArgs a{};
+    a.A = input;
+    a.B = weight;
+    a.C = out;
+    a.M = rows;
+    a.N = out_features;
+    a.K = hidden;
+    a.lda = hidden;
+    a.ldb = hidden;
+    a.ldc = out_features;
+    a.batch_inner = 1;
+    a.batch = 1;
+    a.alpha = 1.f;
+    a.a_vec_ok = (uintptr_t)input % 16 == 0 && hidden % 4 == 0;
+    a.b_vec_ok = (uintptr_t)weight % 16 == 0 && hidden % 4 == 0;
+    a.c_vec_ok = (uintptr_t)out % 16 == 0 && out_features % 4 == 0;
+    a.a_kscale = gamma;  // the kernel also sums each row's squares and applies 1/rms in its epilogue
+    a.rms_eps = eps;
+    a.no_split = 1;
+    return it::launch_gemm(ctx, IT_F32, false, true, a, "");
+}
+
+namespace {
+
+// One FP32 GEMM of the chunked fused linear + cross entropy (C = op(A).op(B) + beta C).
+it_status flce_gemm(it_context *ctx, bool ta, bool tb, int64_t M, int64_t N, int64_t K, const float *A, int64_t lda,
+                    const float *B, int64_t ldb, float *C, int64_t ldc, float beta) {
+    it::GemmArgs a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.batch_inner = 1;
+    a.batch = 1;
+    a.alpha = 1.f;
+    a.beta = beta;
+    a.a_vec_ok = (uintptr_t)A % 16 == 0 && lda % 4 == 0;
+    a.b_vec_ok = (uintptr_t)B % 16 == 0 && ldb % 4 == 0;
+    a.c_vec_ok = (uintptr_t)C % 16 == 0 && ldc % 4 == 0;
+    return it::launch_gemm(ctx, IT_F32, ta, tb, a, "flce");
+}
+
+size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+}  // namespace
+
+it_status it_fused_linear_cross_entropy(it_context *ctx, int64_t rows, int64_t hidden, int64_t vocab,
+                                        const float *hidden_states, const float *weight, const int32_t *targets,
+                                        float *losses, float *loss_mean, float *grad_hidden, float *grad_weight,
+                                        int64_t chunk_bytes) {
+    if (!ctx) return fail(IT_ERR_NULL, "fused_linear_cross_entropy: ctx is NULL");
+    if (rows < 0 || hidden < 0 || vocab < 0) return fail(IT_ERR_INVALID, "fused_linear_cross_entropy: negative size");
+    if (!loss_mean) return fail(IT_ERR_NULL, "fused_linear_cross_entropy: loss_mean is NULL");
+    if (rows == 0 || vocab == 0 || hidden == 0) {
+        // Nothing to average: zero loss and gradients (the reference returns zeros for an empty batch).
+        if (const it_status st = it::launch_zero(ctx->stream, loss_mean, sizeof(float)); st != IT_OK) return st;
+        if (losses && rows > 0)
+            if (const it_status st = it::launch_zero(ctx->stream, losses, (size_t)rows * 4); st != IT_OK) return st;
+        if (grad_hidden && rows * hidden > 0)
+            if (const it_status st = it::launch_zero(ctx->stream, grad_hidden, (size_t)(rows * hidden) * 4); st != IT_OK)
+                return st;
+        if (grad_weight && vocab * hidden > 0)
+            if (const it_status st = it::launch_zero(ctx->stream, grad_weight, (size_t)(vocab * hidden) * 4);
+                st != IT_OK)
+                return st;
+        return IT_OK;
+    }
+    if (!hidden_states || !weight || !targets) return fail(IT_ERR_NULL, "fused_linear_cross_entropy: NULL buffer");
+    if (grad_weight && !grad_hidden)
+        return fail(IT_ERR_INVALID, "fused_linear_cross_entropy: grad_weight needs grad_hidden");
+    if (rows > 0x7fffffff) return fail(IT_ERR_DIMS, "fused_linear_cross_entropy: too many rows");
+    // Vocabulary chunk: as many columns as fit the budget (default 256 MiB of logits), a multiple of
+    // 128 (whole GEMM tiles) unless the vocabulary is smaller.
+    const int64_t budget = chunk_bytes > 0 ? chunk_bytes : (int64_t)256 << 20;
+    int64_t vc = budget / (rows * 4);
+    vc = vc >= vocab ? vocab : std::max<int64_t>(128, vc / 128 * 128);
+    if (vc > vocab) vc = vocab;
+    const int64_t nchunks = (vocab + vc - 1) / vc;
+    const size_t chunk_sz = up256((size_t)(rows * vc) * 4), stats_sz = up256((size_t)(rows * nchunks) * 8);
+    const size_t row_sz = up256((size_t)rows * 4);
+    void *ws = nullptr;
+    if (const it_status st = it::ensure_attn_scratch(ctx, chunk_sz + stats_sz + 4 * row_sz + 256, &ws); st != IT_OK)
+        return st;
+    char *w8 = (char *)ws;
+    float *chunk = (float *)w8;
+    void *stats = w8 + chunk_sz;
+    float *tlogit = (float *)(w8 + chunk_sz + stats_sz);
+    float *lse = (float *)(w8 + chunk_sz + stats_sz + row_sz);
+    float *loss_rows = losses ? losses : (float *)(w8 + chunk_sz + stats_sz + 2 * row_sz);
+    float *scale = (float *)(w8 + chunk_sz + stats_sz + 3 * row_sz);
+    auto v0_of = [&](int64_t c) { return c * vc; };
+    auto vc_of = [&](int64_t c) { return std::min(vc, vocab - c * vc); };
+    // Pass 1: logits chunk by chunk -> per-row (max, sum exp) and the target logit.
+    for (int64_t c = 0; c < nchunks; ++c) {
+        const int64_t v0 = v0_of(c), n = vc_of(c);
+        if (const it_status st = flce_gemm(ctx, false, true, rows, n, hidden, hidden_states, hidden,
+                                           weight + v0 * hidden, hidden, chunk, vc, 0.f);
+            st != IT_OK)
+            return st;
+        Prof p(ctx, "flce_stats[" + i64(rows) + "x" + i64(n) + "]");
+        if (const it_status st = p.done(it::launch_flce_chunk_stats(ctx->stream, chunk, vc, rows, n, v0, targets, vocab,
+                                                                    stats, nchunks, c, tlogit));
+            st != IT_OK)
+            return st;
+    }
+    {
+        Prof p(ctx, "flce_combine[" + i64(rows) + "x" + i64(nchunks) + "]");
+        if (const it_status st = p.done(it::launch_flce_combine(ctx->stream, stats, nchunks, tlogit, targets, vocab,
+                                                                rows, lse, loss_rows, loss_mean, scale));
+            st != IT_OK)
+            return st;
+    }
+    if (!grad_hidden) return IT_OK;
+    // Pass 2, last chunk first (still in the buffer), then the others recomputed: the gradient
+    // softmax - onehot in place, dW rows of the chunk (unscaled, as the reference), dH accumulated in
+    // this fixed chunk order and scaled by 1 / valid count at the end.
+    for (int64_t c = nchunks - 1; c >= 0; --c) {
+        const int64_t v0 = v0_of(c), n = vc_of(c);
+        if (c != nchunks - 1)
+            if (const it_status st = flce_gemm(ctx, false, true, rows, n, hidden, hidden_states, hidden,
+                                               weight + v0 * hidden, hidden, chunk, vc, 0.f);
+                st != IT_OK)
+                return st;
+        {
+            Prof p(ctx, "flce_grad[" + i64(rows) + "x" + i64(n) + "]");
+            if (const it_status st =
+                    p.done(it::launch_flce_chunk_grad(ctx->stream, chunk, vc, rows, n, v0, targets, vocab, lse));
+                st != IT_OK)
+                return st;
+        }
+        if (grad_weight)
+            if (const it_status st = flce_gemm(ctx, true, false, n, hidden, rows, chunk, vc, hidden_states, hidden,
+                                               grad_weight + v0 * hidden, hidden, 0.f);
+                st != IT_OK)
+                return st;
+        if (const it_status st = flce_gemm(ctx, false, false, rows, hidden, n, chunk, vc, weight + v0 * hidden, hidden,
+                                           grad_hidden, hidden, c == nchunks - 1 ? 0.f : 1.f);
+            st != IT_OK)
+            return st;
+    }
+    Prof p(ctx, "flce_scale[" + i64(rows) + "x" + i64(hidden) + "]");
+    return p.done(it::launch_scale_by_device(ctx->stream, grad_hidden, rows * hidden, scale));
 }
 
 it_status it_rope(it_context *ctx, it_dtype dtype_src, it_dtype dtype_dst, int64_t batch, int64_t seq,

@@ -127,6 +127,14 @@ struct GemmArgs {
     void *U;  // SwiGLU up pre-activation (optional)
     const float *bias;
     float *partial;  // split-K partial sums [splits][batch][M][N] (f32)
+    // Fused RMSNorm in front of the GEMM (FP32, A not transposed, one k split): op(A)[m,k] is
+    // multiplied by a_kscale[k] on its way into LDS, the kernel sums the squares of each A row as
+    // the tiles stream through, and the epilogue scales row m by 1 / sqrt(sum / K + rms_eps).
+    // row_scale (optional, any GEMM): result row m multiplied by row_scale[m].
+    const float *a_kscale;
+    const float *row_scale;
+    float rms_eps;
+    int no_split;  // the planner must not split K
 
     int64_t M, N, K;
     int64_t lda, ldb, ldc;
@@ -208,6 +216,15 @@ it_status launch_cross_entropy(hipStream_t s, bool grad_bf16, int64_t rows, int6
 it_status launch_swiglu_backward(hipStream_t s, bool in_bf16, bool out_bf16, int64_t rows, int64_t cols,
                                  const float *dh, int64_t ld_dh, const void *gate, const void *up, int64_t ld_gu,
                                  void *dgate, void *dup, int64_t ld_out);
+it_status launch_flce_chunk_stats(hipStream_t s, const float *x, int64_t ld, int64_t rows, int64_t vc, int64_t v0,
+                                  const int32_t *targets, int64_t vocab, void *stats, int64_t nchunks, int64_t chunk,
+                                  float *tlogit);
+it_status launch_flce_combine(hipStream_t s, const void *stats, int64_t nchunks, const float *tlogit,
+                              const int32_t *targets, int64_t vocab, int64_t rows, float *lse, float *losses,
+                              float *mean_out, float *scale_out);
+it_status launch_flce_chunk_grad(hipStream_t s, float *x, int64_t ld, int64_t rows, int64_t vc, int64_t v0,
+                                 const int32_t *targets, int64_t vocab, const float *lse);
+it_status launch_scale_by_device(hipStream_t s, float *x, int64_t n, const float *scale);
 int64_t grad_norm_partials(int count, const int64_t *n);
 it_status launch_grad_norm(hipStream_t s, int count, const float *const *g, const int64_t *n, float max_norm,
                            float *out, double *part);

@@ -161,6 +161,53 @@ struct Operand {
         }
     }
 
+    // Per-k scale of a k-contiguous FP32 tile (the RMSNorm gamma of a fused norm + projection):
+    // load_kscale fetches s[k] for this thread's elements with the tile's own loads, apply_kscale
+    // multiplies the loaded elements before they go to LDS (elements at k >= klim are zeros).
+    f32x4 kscale[ITERS];
+
+    __device__ __forceinline__ void load_kscale(const float *s, int64_t k0, int64_t klim, int tid) {
+        static_assert(KCONTIG && sizeof(T) == 4, "k scaling applies to k-contiguous FP32 tiles");
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int item = tid + it * NTHREADS;
+            if (ITEMS % NTHREADS != 0 && item >= ITEMS) continue;
+            const int64_t gk = k0 + (item % (BK / VEC)) * VEC;
+            if (gk + 4 <= klim && (uintptr_t)(s + gk) % 16 == 0) {
+                kscale[it] = *(const f32x4 *)(s + gk);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kscale[it][e] = gk + e < klim ? s[gk + e] : 0.f;
+            }
+        }
+    }
+
+    // Adds the squares of this thread's loaded elements to ss[it] (the rows of a thread's items are
+    // the same in every k-tile).
+    __device__ __forceinline__ void add_squares(float (&ss)[ITERS], int tid) const {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int item = tid + it * NTHREADS;
+            if (ITEMS % NTHREADS != 0 && item >= ITEMS) continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float v = __uint_as_float(reg[it][0][e]);
+                ss[it] += v * v;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void apply_kscale(int tid) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int item = tid + it * NTHREADS;
+            if (ITEMS % NTHREADS != 0 && item >= ITEMS) continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                reg[it][0][e] = __float_as_uint(__uint_as_float(reg[it][0][e]) * kscale[it][e]);
+        }
+    }
+
     __device__ __forceinline__ void store(char *lds, int tid) const {
 #pragma unroll
         for (int it = 0; it < ITERS; ++it) {
@@ -243,6 +290,7 @@ __device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int 
 __device__ __forceinline__ void finish_store(const GemmArgs &p, void *C, int64_t idx, float acc,
                                              int64_t row, int64_t col) {
     float v = p.alpha * acc;
+    if (p.row_scale) v *= p.row_scale[row];
     if (p.beta != 0.f) v += p.beta * load_out(C, idx, p.out_bf16);
     if (p.has_bias) v += p.bias[col];
     if (p.causal != CAUSAL_NONE && col > row + p.causal_offset) v = -INFINITY;
@@ -272,6 +320,7 @@ __device__ __forceinline__ void finish4(const GemmArgs &p, f32x4 v, int64_t row,
     const int64_t idx = coff + row * p.ldc + col;
     if (full && p.c_vec_ok) {
         v *= p.alpha;
+        if (p.row_scale) v *= p.row_scale[row];
         if (p.beta != 0.f) {
             f32x4 old;
             if (p.out_bf16) {
@@ -356,7 +405,7 @@ namespace sg {
 constexpr int MFMA = 0x008, VMEM_READ = 0x020, DS_READ = 0x100, DS_WRITE = 0x200;
 }
 
-template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL, int LM>
+template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL, int LM, bool KS = false>
 __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
     static_assert(WM * WN == 4, "4 waves per block");
     constexpr int BK = ET<T>::BK;
@@ -413,10 +462,19 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
     std::conditional_t<DUAL, OBH, char> ob2;
     auto gload = [&](int64_t k0) {
         oa.template load<LM>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
+        if constexpr (KS) oa.load_kscale(p.a_kscale, k0, ke, tid);
         ob.template load<LM>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
         if constexpr (DUAL) ob2.template load<LM>(B2, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
     };
-    auto gstore = [&](char *st) {
+    // KS: per-thread partial sums of squares of its A rows, over the k-tiles written to LDS.
+    float ssq[KS ? OA::ITERS : 1];
+#pragma unroll
+    for (int i = 0; i < (KS ? OA::ITERS : 1); ++i) ssq[i] = 0.f;
+    auto gstore = [&](char *st, bool fresh = true) {
+        if constexpr (KS) {
+            if (fresh) oa.add_squares(ssq, tid);
+            oa.apply_kscale(tid);
+        }
         oa.store(st, tid);
         ob.store(st + SA, tid);
         if constexpr (DUAL) ob2.store(st + SA + OBH::STAGE_BYTES, tid);
@@ -457,7 +515,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
                 frags(fa1, fb1, cur, 1);
                 gload(k1);
                 mmas(fa0, fb0);
-                gstore(nxt);
+                gstore(nxt, t + 1 < ntiles);
                 mmas(fa1, fb1);
                 if constexpr (LM != LOAD_CHECKED) {
 #pragma unroll
@@ -474,6 +532,24 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
                 }
                 __syncthreads();
                 frags(fa0, fb0, nxt, 0);
+            }
+        }
+    }
+
+    // KS: row sums of squares -> 1/rms per block row (the 8 threads of a row are 8 consecutive lanes).
+    __shared__ float row_inv[KS ? BM : 1];
+    if constexpr (KS) {
+        constexpr int PER_ROW = BK / ET<T>::VEC;
+        static_assert(PER_ROW == 8 && NTHREADS % PER_ROW == 0, "row partials sit in 8 consecutive lanes");
+#pragma unroll
+        for (int it = 0; it < OA::ITERS; ++it) {
+            float v = ssq[it];
+#pragma unroll
+            for (int o = 1; o < PER_ROW; o <<= 1) v += __shfl_xor(v, o, 64);
+            const int item = tid + it * NTHREADS;
+            if ((OA::ITEMS % NTHREADS == 0 || item < OA::ITEMS) && tid % PER_ROW == 0) {
+                const float rms = sqrtf(v / (float)p.K + p.rms_eps);
+                row_inv[item / PER_ROW] = 1.0f / rms;
             }
         }
     }
@@ -515,7 +591,8 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
                 for (int it = 0; it < WTM * EC / 256; ++it) {
                     const int e = (it * 64 + lane) * 4;
                     const int rl = e / EC, cl = e % EC;
-                    const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
+                    f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
+                    if constexpr (KS) v *= row_inv[wm * WTM + rl];
                     finish4<true>(p, v, m0 + wm * WTM + rl, n0 + wn * WTN + h * EC + cl, coff, z);
                 }
             }
@@ -765,12 +842,12 @@ hipError_t launch_bf16_256(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipSt
     return hipGetLastError();
 }
 
-template <typename T, bool TA, bool TB, bool DUAL, int LM>
+template <typename T, bool TA, bool TB, bool DUAL, int LM, bool KS = false>
 void launch_cfg_lm(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
     if (cfg.bm == 128)
-        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 128, 128, 2, 2, DUAL, LM>), grid, dim3(NTHREADS), 0, s, a);
+        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 128, 128, 2, 2, DUAL, LM, KS>), grid, dim3(NTHREADS), 0, s, a);
     else
-        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 64, 64, 2, 2, DUAL, LM>), grid, dim3(NTHREADS), 0, s, a);
+        hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 64, 64, 2, 2, DUAL, LM, KS>), grid, dim3(NTHREADS), 0, s, a);
 }
 
 // Branch-free masked loads need aligned 16-byte vectors that never straddle an edge.
@@ -792,6 +869,15 @@ hipError_t launch_cfg(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStrea
 template <typename T>
 hipError_t launch_typed(bool ta, bool tb, bool dual, const TileCfg &cfg, const GemmArgs &a, dim3 grid,
                         hipStream_t s) {
+    if constexpr (sizeof(T) == 4) {
+        if (a.a_kscale) {  // fused RMSNorm + projection: X.W^T only (checked by the caller)
+            if (vectors_exact<T>(a, false, true))
+                launch_cfg_lm<T, false, true, false, LOAD_MASKED, true>(cfg, a, grid, s);
+            else
+                launch_cfg_lm<T, false, true, false, LOAD_CHECKED, true>(cfg, a, grid, s);
+            return hipGetLastError();
+        }
+    }
     if (dual) return launch_cfg<T, false, true, true>(cfg, a, grid, s);
     if (!ta && !tb) return launch_cfg<T, false, false, false>(cfg, a, grid, s);
     if (!ta && tb) return launch_cfg<T, false, true, false>(cfg, a, grid, s);
@@ -831,7 +917,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
     const double cu_peak = (bf16 ? 2.5e15 : 157.3e12) / 256.0;  // FLOP/s per CU
     const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = 4e12;
     const double step_floor = bf16 ? 1.0e-6 : 0.5e-6;
-    const bool can_split = !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL;
+    const bool can_split = !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.no_split;
     Plan best{64, 64, 1};
     double best_t = 1e30;
     int64_t best_blocks = 0;
@@ -938,9 +1024,9 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     hipEvent_t ev = nullptr;
     if (ctx->profiling) {
         char buf[192];
-        std::snprintf(buf, sizeof(buf), "gemm_%s_%c%c_%dx%d%s%s|%s[%lld,%lld,%lld]x%lld s%d",
+        std::snprintf(buf, sizeof(buf), "gemm_%s_%c%c_%dx%d%s%s%s|%s[%lld,%lld,%lld]x%lld s%d",
                       bf16 ? "bf16" : "f32", transA ? 'T' : 'N', transB ? 'T' : 'N', cfg.bm, cfg.bn,
-                      a.dual ? "_swiglu" : "", a.causal || a.kmode ? "_causal" : "",
+                      a.dual ? "_swiglu" : "", a.causal || a.kmode ? "_causal" : "", a.a_kscale ? "_rmsnorm" : "",
                       profile_tag ? profile_tag : "", (long long)a.M, (long long)a.N,
                       (long long)a.K, (long long)a.batch, splits);
         key = buf;

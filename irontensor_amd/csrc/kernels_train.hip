@@ -462,6 +462,105 @@ __global__ __launch_bounds__(256) void mean_kernel(const float *v, int64_t n, fl
     if (tid == 0) out[0] = (((red[0] + red[1]) + red[2]) + red[3]) / (float)n;
 }
 
+// ------------------------------------------------------------------ fused linear + cross entropy
+
+// The logits are produced one vocabulary chunk [rows, vc] at a time by the GEMM; these kernels
+// reduce a chunk to per-row (max, sum exp(x - max)) and the target's logit, combine the chunks into
+// the row log-sum-exp and loss, and turn a (recomputed) chunk into the unscaled gradient
+// softmax - onehot in place. A target outside [0, vocab) marks an ignored row.
+__device__ __forceinline__ bool target_ok(int32_t t, int64_t vocab) { return t >= 0 && (int64_t)t < vocab; }
+
+__global__ __launch_bounds__(256) void flce_chunk_stats(const float *x, int64_t ld, int64_t vc, int64_t v0,
+                                                        const int32_t *targets, int64_t vocab, float2 *stats,
+                                                        int64_t nchunks, int64_t chunk, float *tlogit) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t row = blockIdx.x;
+    const float *xr = x + row * ld;
+    float mx = -INFINITY;
+    for (int64_t c = tid; c < vc; c += 256) mx = fmaxf(mx, xr[c]);
+    mx = wmax(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float sum = 0.f;
+    for (int64_t c = tid; c < vc; c += 256) sum += expf(xr[c] - mx);
+    sum = wsum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        stats[row * nchunks + chunk] = make_float2(mx, ((red[0] + red[1]) + red[2]) + red[3]);
+        const int32_t t = targets[row];
+        if (target_ok(t, vocab) && (int64_t)t >= v0 && (int64_t)t < v0 + vc) tlogit[row] = xr[t - v0];
+    }
+}
+
+// One block: per row lse = M + log(sum_c s_c exp(m_c - M)) and loss = lse - logit[target] (0 when
+// ignored); then the valid count, the mean loss and 1 / count, in a fixed order.
+__global__ __launch_bounds__(1024) void flce_combine(const float2 *stats, int64_t nchunks, const float *tlogit,
+                                                     const int32_t *targets, int64_t vocab, int64_t rows,
+                                                     float *lse, float *losses, float *mean_out, float *scale_out) {
+    __shared__ float rs[16];
+    __shared__ int rc[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float tot = 0.f;
+    int cnt = 0;
+    for (int64_t r = tid; r < rows; r += 1024) {
+        const float2 *st = stats + r * nchunks;
+        float m = -INFINITY;
+        for (int64_t c = 0; c < nchunks; ++c) m = fmaxf(m, st[c].x);
+        float s = 0.f;
+        for (int64_t c = 0; c < nchunks; ++c) s += st[c].y * expf(st[c].x - m);
+        const float l = m + logf(s);
+        lse[r] = l;
+        if (target_ok(targets[r], vocab)) {
+            losses[r] = l - tlogit[r];
+            tot += losses[r];
+            ++cnt;
+        } else {
+            losses[r] = 0.f;
+        }
+    }
+    tot = wsum(tot);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+    if (lane == 0) {
+        rs[wave] = tot;
+        rc[wave] = cnt;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float t = 0.f;
+        int n = 0;
+        for (int w = 0; w < 16; ++w) {
+            t += rs[w];
+            n += rc[w];
+        }
+        mean_out[0] = n > 0 ? t / (float)n : 0.f;
+        scale_out[0] = n > 0 ? 1.0f / (float)n : 0.f;
+    }
+}
+
+// In place over a chunk: x <- exp(x - lse[row]) - [v0 + c == target] for valid rows, 0 otherwise.
+__global__ __launch_bounds__(256) void flce_chunk_grad(float *x, int64_t ld, int64_t vc, int64_t v0,
+                                                       const int32_t *targets, int64_t vocab, const float *lse) {
+    const int64_t row = blockIdx.x;
+    float *xr = x + row * ld;
+    const int32_t t = targets[row];
+    const bool ok = target_ok(t, vocab);
+    const float l = lse[row];
+    for (int64_t c = threadIdx.x; c < vc; c += 256)
+        xr[c] = ok ? expf(xr[c] - l) - ((int64_t)t == v0 + c ? 1.0f : 0.0f) : 0.f;
+}
+
+// x[i] *= s[0] (the 1 / valid-count scale of grad_hidden, known only on the device).
+__global__ __launch_bounds__(256) void scale_by_device_kernel(float *x, int64_t n, const float *s) {
+    const float f = s[0];
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] *= f;
+}
+
 // ------------------------------------------------------------------ SwiGLU backward
 
 // grad_up = dh * silu(g); grad_gate = dh * u * sig(g) (1 + g (1 - sig(g))), sig(g) = 1 / (1 + exp(-g)).
@@ -801,6 +900,37 @@ it_status launch_cross_entropy(hipStream_t s, bool grad_bf16, int64_t rows, int6
         hipLaunchKernelGGL(mean_kernel, dim3(1), dim3(256), 0, s, losses, rows, loss_mean);
         IT_HIP_TRY(hipGetLastError());
     }
+    return IT_OK;
+}
+
+it_status launch_flce_chunk_stats(hipStream_t s, const float *x, int64_t ld, int64_t rows, int64_t vc, int64_t v0,
+                                  const int32_t *targets, int64_t vocab, void *stats, int64_t nchunks, int64_t chunk,
+                                  float *tlogit) {
+    hipLaunchKernelGGL(flce_chunk_stats, dim3((unsigned)rows), dim3(256), 0, s, x, ld, vc, v0, targets, vocab,
+                       (float2 *)stats, nchunks, chunk, tlogit);
+    IT_HIP_TRY(hipGetLastError());
+    return IT_OK;
+}
+
+it_status launch_flce_combine(hipStream_t s, const void *stats, int64_t nchunks, const float *tlogit,
+                              const int32_t *targets, int64_t vocab, int64_t rows, float *lse, float *losses,
+                              float *mean_out, float *scale_out) {
+    hipLaunchKernelGGL(flce_combine, dim3(1), dim3(1024), 0, s, (const float2 *)stats, nchunks, tlogit, targets, vocab,
+                       rows, lse, losses, mean_out, scale_out);
+    IT_HIP_TRY(hipGetLastError());
+    return IT_OK;
+}
+
+it_status launch_flce_chunk_grad(hipStream_t s, float *x, int64_t ld, int64_t rows, int64_t vc, int64_t v0,
+                                 const int32_t *targets, int64_t vocab, const float *lse) {
+    hipLaunchKernelGGL(flce_chunk_grad, dim3((unsigned)rows), dim3(256), 0, s, x, ld, vc, v0, targets, vocab, lse);
+    IT_HIP_TRY(hipGetLastError());
+    return IT_OK;
+}
+
+it_status launch_scale_by_device(hipStream_t s, float *x, int64_t n, const float *scale) {
+    hipLaunchKernelGGL(scale_by_device_kernel, dim3(blocks_for(n, 256 * 4, 65536)), dim3(256), 0, s, x, n, scale);
+    IT_HIP_TRY(hipGetLastError());
     return IT_OK;
 }
 

@@ -88,6 +88,65 @@ def rmsnorm_backward(grad_output: Tensor, input: Tensor, gamma: Tensor, eps: flo
     return dx, dg
 
 
+def fused_rmsnorm_linear(input: Tensor, gamma: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """fused_rmsnorm_linear (src/ops/fused_rmsnorm_linear.rs:73-205): rmsnorm(input, gamma, eps) @ weight^T
+    without writing the normalized input. input [rows, hidden], weight [out_features, hidden], FP32."""
+    for t in (input, gamma, weight):
+        _need_f32(t, "fused_rmsnorm_linear")
+    if len(input.shape()) != 2:
+        raise Panic("Input must be 2D [batch_seq, hidden_dim]")
+    if len(weight.shape()) != 2:
+        raise Panic("Weight must be 2D [out_features, hidden_dim]")
+    rows, hidden = input.shape()
+    out_features, wh = weight.shape()
+    if wh != hidden:
+        raise Panic(f"Hidden dimensions must match: input has {hidden}, weight has {wh}")
+    if gamma.shape() != [hidden]:
+        raise Panic("Gamma must have shape [hidden_dim]")
+    out = Tensor.empty([rows, out_features], _P.FP32, input.ctx)
+    check(input.ctx.lib.it_fused_rmsnorm_linear(input.ctx.handle, rows, hidden, out_features, float(eps), _vp(input),
+                                                _vp(gamma), _vp(weight), _vp(out)), "fused_rmsnorm_linear")
+    return out
+
+
+def _i32(targets) -> Tuple[np.ndarray, Optional[Tensor]]:
+    t = np.ascontiguousarray(np.asarray(targets, dtype=np.int32).ravel())
+    return t, (Tensor.from_f32_slice(t.view(np.float32), [t.size]) if t.size else None)
+
+
+def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, targets, *, chunk_bytes: int = 0,
+                               forward_only: bool = False):
+    """fused_linear_cross_entropy (src/ops/fused_linear_cross_entropy.rs:79-242) -> (mean loss,
+    grad_hidden, grad_weight); with forward_only, fused_linear_cross_entropy_forward_only (:246-374)
+    -> (mean loss, grad_hidden). targets are i32; values outside [0, vocab) (-100) are ignored. The
+    [rows, vocab] logits are never materialised (chunks of at most chunk_bytes, default 256 MiB).
+    grad_weight is unscaled, as the reference's kernel leaves it."""
+    _need_f32(hidden, "fused_linear_cross_entropy")
+    _need_f32(weight, "fused_linear_cross_entropy")
+    if len(hidden.shape()) != 2:
+        raise Panic("hidden must be 2D [batch*seq, hidden_dim]")
+    if len(weight.shape()) != 2:
+        raise Panic("weight must be 2D [vocab_size, hidden_dim]")
+    rows, hd = hidden.shape()
+    vocab = weight.shape()[0]
+    if weight.shape()[1] != hd:
+        raise Panic("weight hidden_dim must match hidden")
+    t_host, t = _i32(targets)
+    if t_host.size != rows:
+        raise Panic("targets length must match batch*seq")
+    if hd > 256:
+        raise Panic("hidden_dim must be <= 256 for this kernel")
+    ctx = hidden.ctx
+    gh = Tensor.zeros([rows, hd], _P.FP32, ctx)
+    gw = None if forward_only else Tensor.zeros([vocab, hd], _P.FP32, ctx)
+    mean = Tensor.zeros([1], _P.FP32, ctx)
+    check(ctx.lib.it_fused_linear_cross_entropy(ctx.handle, rows, hd, vocab, _vp(hidden), _vp(weight), _vp(t), None,
+                                                _vp(mean), _vp(gh), _vp(gw), int(chunk_bytes)),
+          "fused_linear_cross_entropy")
+    loss = float(mean.as_f32_slice()[0])
+    return (loss, gh) if forward_only else (loss, gh, gw)
+
+
 def _rope(x: Tensor, base: float, position_offset: int, backward: bool, name: str) -> Tensor:
     shape = x.shape()
     if len(shape) != 4:

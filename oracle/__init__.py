@@ -63,6 +63,9 @@ def load() -> C.CDLL:
     lib.ref_lion.argtypes = [vp, vp, vp, i64, f, f, f, f, f]
     lib.ref_sum_squares.argtypes = [vp, i64]
     lib.ref_sum_squares.restype = C.c_double
+    lib.ref_fused_rmsnorm_linear.argtypes = [vp, vp, vp, vp, i64, i64, i64, f]
+    lib.ref_fused_linear_cross_entropy.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64]
+    lib.ref_fused_linear_cross_entropy.restype = C.c_float
     _lib = lib
     return lib
 
@@ -271,3 +274,25 @@ def lion(w, m, g, lr: float, beta1: float, beta2: float, wd: float, scale: float
 def sum_squares(x) -> float:
     x = _c(x, np.float32)
     return float(load().ref_sum_squares(_p(x), x.size))
+
+
+def fused_rmsnorm_linear(x, gamma, w, eps: float = 1e-5) -> np.ndarray:
+    x, g, w = _c(x, np.float32), _c(gamma, np.float32), _c(w, np.float32)
+    rows, hidden = x.shape
+    out = np.empty((rows, w.shape[0]), np.float32)
+    load().ref_fused_rmsnorm_linear(_p(x), _p(g), _p(w), _p(out), rows, hidden, w.shape[0], float(eps))
+    return out
+
+
+def fused_linear_cross_entropy(hidden, weight, targets, with_weight_grad: bool = True):
+    """Returns (mean loss over valid targets, per-row losses, grad_hidden, grad_weight or None).
+    targets are int32; values outside [0, vocab) (-100 by convention) are ignored."""
+    h, w = _c(hidden, np.float32), _c(weight, np.float32)
+    t = _c(targets, np.int32)
+    rows, hd = h.shape
+    vocab = w.shape[0]
+    losses, gh = np.empty(rows, np.float32), np.empty_like(h)
+    gw = np.empty_like(w) if with_weight_grad else None
+    mean = load().ref_fused_linear_cross_entropy(_p(h), _p(w), _p(t), _p(losses), _p(gh),
+                                                 _p(gw) if gw is not None else None, rows, hd, vocab)
+    return float(np.float32(mean)), losses, gh, gw

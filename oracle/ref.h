@@ -136,6 +136,11 @@ float ref_cross_entropy(const float *logits, const uint32_t *targets, float *los
 void ref_lion(float *w, float *m, const float *g, int64_t n, float lr, float beta1, float beta2, float wd,
               float scale);
 double ref_sum_squares(const float *x, int64_t n);
+float ref_fused_linear_cross_entropy(const float *hidden, const float *weight, const int32_t *targets, float *losses,
+                                     float *grad_hidden, float *grad_weight, int64_t rows, int64_t hidden_dim,
+                                     int64_t vocab);
+void ref_fused_rmsnorm_linear(const float *x, const float *gamma, const float *w, float *out, int64_t rows,
+                              int64_t hidden, int64_t out_features, float eps);
 
 #ifdef __cplusplus
 }

@@ -131,3 +131,99 @@ double ref_sum_squares(const float *x, int64_t n) {
     for (int64_t i = 0; i < n; ++i) s += (double)x[i] * (double)x[i];
     return s;
 }
+
+/* Fused RMSNorm + projection, src/shaders/fused_rmsnorm_linear.metal:42-114: per row, sum of squares
+ * in index order, inv = 1 / sqrt(sum/n + eps); out[o] = (sum_j (x_j * gamma_j) * W[o][j], j in order)
+ * * inv. (The reference's own test compares against rmsnorm then matmul,
+ * src/ops/fused_rmsnorm_linear.rs:214-245; the same value up to rounding.) */
+void ref_fused_rmsnorm_linear(const float *x, const float *gamma, const float *w, float *out, int64_t rows,
+                              int64_t hidden, int64_t out_features, float eps) {
+    float *xg = (float *)malloc(sizeof(float) * (size_t)(hidden > 0 ? hidden : 1));
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * hidden;
+        float ss = 0.0f;
+        for (int64_t j = 0; j < hidden; ++j) {
+            ss += xr[j] * xr[j];
+            xg[j] = xr[j] * gamma[j];
+        }
+        const float rms = sqrtf(ss / (float)hidden + eps);
+        const float inv = 1.0f / rms;
+        for (int64_t o = 0; o < out_features; ++o) {
+            const float *wo = w + o * hidden;
+            float sum = 0.0f;
+            for (int64_t j = 0; j < hidden; ++j) sum += xg[j] * wo[j];
+            out[r * out_features + o] = sum * inv;
+        }
+    }
+    free(xg);
+}
+
+/* Fused linear + cross entropy, src/shaders/fused_linear_cross_entropy.metal:189-280 (per token:
+ * logits h.w_v in index order, max, sum of exp(logit - max), lse = max + log(sum), loss = lse -
+ * logit[target], grad_h = (-w_target + sum_v exp(logit_v - lse) w_v) * grad_scale) and :119-185
+ * (grad_weight[v][d] = sum over valid tokens in order of (p_tv - [v == target_t]) h_td, with no
+ * grad_scale: the reference leaves the weight gradient unscaled). Targets outside [0, vocab) (-100
+ * by convention) are ignored: zero loss and zero grad_h; grad_scale = 1 / valid count
+ * (src/ops/fused_linear_cross_entropy.rs:131-133). Returns the mean loss over valid rows (summed in
+ * row order, src/ops/fused_linear_cross_entropy.rs:196-208). grad_weight may be NULL. */
+static float dot_seq(const float *a, const float *b, int64_t n) {
+    float s = 0.0f;
+    for (int64_t d = 0; d < n; ++d) s += a[d] * b[d];
+    return s;
+}
+
+float ref_fused_linear_cross_entropy(const float *hidden, const float *weight, const int32_t *targets, float *losses,
+                                     float *grad_hidden, float *grad_weight, int64_t rows, int64_t hd,
+                                     int64_t vocab) {
+    int64_t valid = 0;
+    for (int64_t t = 0; t < rows; ++t) valid += targets[t] >= 0 && targets[t] < vocab;
+    const float scale = valid > 0 ? 1.0f / (float)valid : 0.0f;
+    float *lse = (float *)malloc(sizeof(float) * (size_t)(rows > 0 ? rows : 1));
+    float total = 0.0f;
+    for (int64_t t = 0; t < rows; ++t) {
+        const float *h = hidden + t * hd;
+        float *gh = grad_hidden + t * hd;
+        const int32_t tg = targets[t];
+        if (tg < 0 || tg >= vocab) {
+            losses[t] = 0.0f;
+            for (int64_t d = 0; d < hd; ++d) gh[d] = 0.0f;
+            lse[t] = 0.0f;
+            continue;
+        }
+        float mx = -INFINITY;
+        for (int64_t v = 0; v < vocab; ++v) mx = fmaxf(mx, dot_seq(h, weight + v * hd, hd));
+        float sum = 0.0f, tl = 0.0f;
+        for (int64_t v = 0; v < vocab; ++v) {
+            const float lg = dot_seq(h, weight + v * hd, hd);
+            sum += expf(lg - mx);
+            if (v == tg) tl = lg;
+        }
+        lse[t] = mx + logf(sum);
+        losses[t] = lse[t] - tl;
+        total += losses[t];
+        for (int64_t d = 0; d < hd; ++d) gh[d] = -weight[(int64_t)tg * hd + d];
+        for (int64_t v = 0; v < vocab; ++v) {
+            const float *w = weight + v * hd;
+            const float prob = expf(dot_seq(h, w, hd) - lse[t]);
+            for (int64_t d = 0; d < hd; ++d) gh[d] += prob * w[d];
+        }
+        for (int64_t d = 0; d < hd; ++d) gh[d] *= scale;
+    }
+    if (grad_weight) {
+        /* each grad_weight[v][d] sums its tokens in order, as the reference's per-(v, d) loop does */
+        for (int64_t v = 0; v < vocab; ++v) {
+            float *gw = grad_weight + v * hd;
+            for (int64_t d = 0; d < hd; ++d) gw[d] = 0.0f;
+            for (int64_t t = 0; t < rows; ++t) {
+                const int32_t tg = targets[t];
+                if (tg < 0 || tg >= vocab) continue;
+                const float *h = hidden + t * hd;
+                float gl = expf(dot_seq(h, weight + v * hd, hd) - lse[t]);
+                if (tg == v) gl -= 1.0f;
+                for (int64_t d = 0; d < hd; ++d) gw[d] += gl * h[d];
+            }
+        }
+    }
+    free(lse);
+    return valid > 0 ? total / (float)valid : 0.0f;
+}

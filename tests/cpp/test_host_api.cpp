@@ -285,6 +285,27 @@ static void gpu_tests() {
         for (float v : gg.as_f32_slice()) CHECK(v == 0.5f);  // sig(0) * (1 + 0) * up
         for (float v : gu.as_f32_slice()) CHECK(v == 0.f);   // silu(0)
     });
+    run("fused_rmsnorm_linear_matches_separate", [] {  // src/ops/fused_rmsnorm_linear.rs:279-316
+        std::vector<float> x(8 * 128), g(128), w(64 * 128);
+        for (size_t i = 0; i < x.size(); ++i) x[i] = ((float)(i % 100) - 50.f) * 0.01f;
+        for (size_t i = 0; i < g.size(); ++i) g[i] = 1.f + std::sin((float)i) * 0.1f;
+        for (size_t i = 0; i < w.size(); ++i) w[i] = ((float)(i % 200) - 100.f) * 0.001f;
+        Tensor tx = Tensor::from_f32_slice(x, {8, 128}), tg = Tensor::from_f32_slice(g, {128});
+        Tensor tw = Tensor::from_f32_slice(w, {64, 128});
+        std::vector<float> fused = fused_rmsnorm_linear(tx, tg, tw, 1e-5f).as_f32_slice();
+        std::vector<float> sep = matmul_mps_nt(rmsnorm(tx, tg, 1e-5f), tw).as_f32_slice();
+        for (size_t i = 0; i < fused.size(); ++i) CHECK(std::fabs(fused[i] - sep[i]) < 1e-4f);
+    });
+    run("fused_linear_cross_entropy_ignore_index", [] {  // src/ops/fused_linear_cross_entropy.rs:454-490
+        std::vector<float> h(4 * 16), w(32 * 16);
+        for (size_t i = 0; i < h.size(); ++i) h[i] = std::sin((float)i * 0.1f);
+        for (size_t i = 0; i < w.size(); ++i) w[i] = std::cos((float)i * 0.05f);
+        FusedLinearCE r = fused_linear_cross_entropy(Tensor::from_f32_slice(h, {4, 16}),
+                                                     Tensor::from_f32_slice(w, {32, 16}), {5, -100, 10, -100});
+        CHECK(r.loss > 0.f);
+        std::vector<float> gh = r.grad_hidden.as_f32_slice();
+        for (int d = 0; d < 16; ++d) CHECK(gh[16 + d] == 0.f && gh[48 + d] == 0.f);
+    });
     run("l2_norm_and_lion", [] {  // src/ops/reduction.rs:94, src/shaders/lion.metal
         Tensor a = Tensor::from_f32_slice({3, 0}, {2}), b = Tensor::from_f32_slice({4}, {1});
         CHECK(total_l2_norm_gpu({&a, &b}) == 5.f);

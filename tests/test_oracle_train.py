@@ -163,3 +163,73 @@ def test_rope_theta_is_the_correctly_rounded_power():
         for i in range(d // 2):
             e = np.float32(np.float32(2 * i) / np.float32(d))
             assert np.float32(libm.powf(10000.0, float(e))) == np.float32(np.power(10000.0, np.float64(e)))
+
+
+# ---------------------------------------------------------------- fused RMSNorm + projection
+
+def test_fused_rmsnorm_linear_oracle(oracle):
+    """Against rmsnorm then x.W^T in float64, the reference's own test data
+    (src/ops/fused_rmsnorm_linear.rs:244-276, tolerance 1e-3 there) and two planted slips."""
+    rows, hidden, out_f = 4, 64, 32
+    x = ((np.arange(rows * hidden) % 100) - 50.0).astype(np.float32).reshape(rows, hidden) * np.float32(0.01)
+    g = (1.0 + np.sin(np.arange(hidden, dtype=np.float64)) * 0.1).astype(np.float32)
+    w = ((np.arange(out_f * hidden) % 200) - 100.0).astype(np.float32).reshape(out_f, hidden) * np.float32(0.001)
+    got = oracle.fused_rmsnorm_linear(x, g, w, 1e-5)
+    x64 = x.astype(np.float64)
+    ref = (x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + 1e-5) * g) @ w.astype(np.float64).T
+    assert np.max(np.abs(got - ref)) <= 1e-6 * np.max(np.abs(ref)) + 1e-7
+    assert np.max(np.abs(got - ref)) < 1e-3
+    no_gamma = (x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + 1e-5)) @ w.astype(np.float64).T
+    assert np.max(np.abs(no_gamma - got)) > 1e-3
+    no_inv = (x64 * g) @ w.astype(np.float64).T
+    assert np.max(np.abs(no_inv - got)) > 1e-3
+
+
+# ---------------------------------------------------------------- fused linear + cross entropy
+
+def _flce_f64(h, w, t):
+    h64, w64 = h.astype(np.float64), w.astype(np.float64)
+    logits = h64 @ w64.T
+    valid = (t >= 0) & (t < w.shape[0])
+    m = logits.max(1, keepdims=True)
+    lse = (m + np.log(np.exp(logits - m).sum(1, keepdims=True)))[:, 0]
+    loss = np.where(valid, lse - logits[np.arange(len(t)), np.where(valid, t, 0)], 0.0)
+    p = np.exp(logits - lse[:, None])
+    p[np.arange(len(t))[valid], t[valid]] -= 1.0
+    p[~valid] = 0.0
+    n = max(int(valid.sum()), 1)
+    return loss.sum() / n, loss, (p @ w64) / n, p.T @ h64
+
+
+def test_fused_linear_cross_entropy_oracle(oracle):
+    """Against the float64 composition logits -> cross entropy -> products, with ignored rows; the
+    gradients against finite differences of the mean loss (grad_weight is the unscaled sum, so it
+    is grad of the mean times the valid count); the reference's own comparison case
+    (src/ops/fused_linear_cross_entropy.rs:389-451, tolerance 1e-3 there)."""
+    h = synth.normal(30, (12, 16), std=0.7)
+    w = synth.normal(31, (40, 16), std=0.5)
+    t = synth.tokens(32, 12, 40).astype(np.int32)
+    t[[2, 7]] = -100
+    mean, losses, gh, gw = oracle.fused_linear_cross_entropy(h, w, t)
+    rm, rl, rgh, rgw = _flce_f64(h, w, t)
+    assert abs(mean - rm) <= 1e-6 * abs(rm)
+    assert np.allclose(losses, rl, rtol=1e-5, atol=1e-6)
+    assert np.allclose(gh, rgh, rtol=1e-4, atol=1e-6) and np.allclose(gw, rgw, rtol=1e-4, atol=1e-6)
+    assert not gh[[2, 7]].any()
+
+    def f_h(hh):
+        return _flce_f64(hh, w, t)[0]
+
+    def f_w(ww):
+        return _flce_f64(h, ww, t)[0]
+
+    n_valid = int(((t >= 0) & (t < 40)).sum())
+    assert np.allclose(gh, _fd(f_h, h.astype(np.float64), 1e-4), rtol=1e-3, atol=1e-6)
+    assert np.allclose(gw / n_valid, _fd(f_w, w.astype(np.float64), 1e-4), rtol=1e-3, atol=1e-6)
+    # the reference's case: hidden sin(0.01 i) * 0.5, weight cos(0.02 i) * 0.3, targets 7i mod 64
+    h2 = (np.sin(np.arange(8 * 32) * 0.01) * 0.5).astype(np.float32).reshape(8, 32)
+    w2 = (np.cos(np.arange(64 * 32) * 0.02) * 0.3).astype(np.float32).reshape(64, 32)
+    t2 = ((np.arange(8) * 7) % 64).astype(np.int32)
+    m2, _, gh2, _ = oracle.fused_linear_cross_entropy(h2, w2, t2)
+    sm, _, sgrad = oracle.cross_entropy(oracle.gemm_f32(h2, w2, trans_b=True), t2.astype(np.uint32))
+    assert abs(m2 - sm) < 1e-3 and np.max(np.abs(gh2 - oracle.gemm_f32(sgrad, w2))) < 1e-3
