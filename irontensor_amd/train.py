@@ -347,6 +347,72 @@ class TrainStep:
         per_layer_bwd = 2 * 2.0 * T * H * (3 * H + H + 2 * F + F) + 5 * attn
         return L * (per_layer_fwd + per_layer_bwd) + 3 * 2.0 * T * H * V
 
+    # ---------------------------------------------------------------- checkpoints (IRON v2)
+    def _named(self, tensors: List[Tensor]):
+        """(embed, final_norm, E, layers) in the reference's names, from params-ordered tensors."""
+        s = self.s
+        H, F = s.hidden, s.ffn
+        arrs = [t.numpy() for t in tensors]
+        layers = []
+        for l in range(s.layers):
+            an, fn, qkv, wo, gu, wd = arrs[3 + 6 * l: 9 + 6 * l]
+            layers.append({"wq": qkv[:H], "wk": qkv[H:2 * H], "wv": qkv[2 * H:], "wo": wo, "w_gate": gu[:F],
+                           "w_up": gu[F:], "w_down": wd, "attn_norm": an, "ffn_norm": fn})
+        return arrs[0], arrs[1], arrs[2], layers
+
+    def save_checkpoint(self, path, step: int = 0, epoch: int = 0, best_val_loss: float = float("inf"),
+                        with_optimizer: bool = True) -> None:
+        """Writes the parameters (and the Lion momenta) as an IRON v2 file: Q|K|V and gate|up are
+        split back into the reference's wq, wk, wv and w_gate, w_up; the untied LM head goes into the
+        extension block (irontensor_amd.checkpoint)."""
+        from . import checkpoint as ck
+        s = self.s
+        cfg = ck.ModelConfig(s.vocab, s.hidden, s.layers, s.heads, s.heads, s.ffn, self.eps, self.rope_base, s.seq,
+                             False, 0)
+        emb, fnorm, E, layers = self._named(self.params)
+        w = ck.Weights(emb, layers, fnorm, E)
+        opt = None
+        if with_optimizer:
+            m_emb, m_fn, m_E, m_layers = self._named(self.momentum)
+            opt = ck.OptimizerState(m_emb, m_layers, m_fn, m_E)
+        ck.save_model_weights(path, w, ck.Checkpoint(cfg, step, epoch, best_val_loss, self.lr, with_optimizer), opt)
+
+    def load_checkpoint(self, path):
+        """Loads an IRON v2 file written for this shape into the parameters (and momenta when the
+        file has them; zeros otherwise). Returns the Checkpoint metadata."""
+        from . import checkpoint as ck
+        w, meta, opt = ck.load_model_weights(path)
+        s, c = self.s, meta.config
+        if (c.vocab_size, c.hidden_dim, c.num_layers, c.num_heads, c.intermediate_dim) != \
+                (s.vocab, s.hidden, s.layers, s.heads, s.ffn) or c.num_kv_heads != c.num_heads:
+            raise ValueError(f"checkpoint config {c} does not match the step's shape {s}")
+        out = w.output_weight if w.output_weight is not None else w.embed_tokens
+
+        def flat(embed, final_norm, output, layers):
+            arrs = [embed, final_norm, output]
+            for L in layers:
+                arrs += [L["attn_norm"], L["ffn_norm"], np.concatenate([L["wq"], L["wk"], L["wv"]]), L["wo"],
+                         np.concatenate([L["w_gate"], L["w_up"]]), L["w_down"]]
+            return arrs
+
+        def upload(dst: List[Tensor], arrs):
+            for t, a in zip(dst, arrs):
+                a = np.ascontiguousarray(a, np.float32)
+                if list(a.shape) != t.shape():
+                    raise ValueError(f"checkpoint tensor of shape {list(a.shape)} where {t.shape()} is expected")
+                check(self.lib.it_memcpy_h2d(self.h, C.c_void_p(t.ptr), a.ctypes.data_as(C.c_void_p), a.nbytes),
+                      "load checkpoint")
+
+        upload(self.params, flat(w.embed_tokens, w.final_norm, out, w.layers))
+        if opt is not None:
+            o_out = opt.output_weight if opt.output_weight is not None else np.zeros_like(out)
+            upload(self.momentum, flat(opt.embed, opt.final_norm, o_out, opt.layers))
+        else:
+            for m in self.momentum:
+                check(self.lib.it_zero(self.h, C.c_void_p(m.ptr), m.byte_size()), "zero momentum")
+        self.set_lr(meta.learning_rate)
+        return meta
+
     def close(self) -> None:
         if self.graph is not None:
             self.lib.it_graph_destroy(self.graph)
