@@ -107,14 +107,27 @@ it_status it_event_destroy(it_event *ev);
 #define IT_EPI_BIAS 0x1u        /* C[m,n] += bias[n]            (Linear bias, src/nn/linear.rs:8-18) */
 #define IT_EPI_SWIGLU 0x2u      /* dual-B: C = silu(op(A).op(B)) * (op(A).op(B2)) (ffn, elementwise.metal:100-115) */
 #define IT_EPI_CAUSAL 0x4u      /* C[m,n] = -inf where n > m + causal_offset (attention.metal:186-207) */
+#define IT_EPI_ROPE 0x8u        /* rotary embedding of columns n < rope_cols (src/ops/rope.rs:22) */
+#define IT_EPI_SWIGLU_BWD 0x10u /* SwiGLU backward of the product (src/ops/backward/elementwise.rs:149) */
 
 typedef struct it_epilogue {
     uint32_t flags;
     const float *bias;      /* IT_EPI_BIAS: [N] f32; with IT_EPI_SWIGLU [2N]: gate bias, then up bias */
     const void *B2;         /* IT_EPI_SWIGLU: up-projection weight, same dtype/layout/ldb/strideB as B */
-    void *gate_out;         /* IT_EPI_SWIGLU (optional): pre-activation gate, out dtype, ldc/strideC */
-    void *up_out;           /* IT_EPI_SWIGLU (optional): pre-activation up, out dtype, ldc/strideC */
+    void *gate_out;         /* IT_EPI_SWIGLU (optional): pre-activation gate, out dtype, ldc/strideC;
+                               IT_EPI_SWIGLU_BWD (input): the forward's gate [M, N], out dtype, ld N */
+    void *up_out;           /* IT_EPI_SWIGLU (optional): pre-activation up, likewise;
+                               IT_EPI_SWIGLU_BWD (input): the forward's up [M, N], out dtype, ld N */
     int64_t causal_offset;  /* IT_EPI_CAUSAL: mask columns n > m + causal_offset */
+    /* IT_EPI_ROPE: row m is position (m % rope_seq) + rope_offset of its sequence; columns
+     * n < rope_cols form heads of rope_head_dim (even) whose pairs (2i, 2i+1) rotate by
+     * position / rope_base^(2i / rope_head_dim), as it_rope does. Needs N % 4 == 0 and a 16-byte
+     * aligned C with ldc % 4 == 0 (the rotation works on 4-column vectors). */
+    float rope_base;
+    int64_t rope_seq;
+    int64_t rope_head_dim;
+    int64_t rope_cols;
+    int64_t rope_offset;
 } it_epilogue;
 
 /*
@@ -128,6 +141,9 @@ typedef struct it_epilogue {
  * :278-290, :390-402, :519-537) and every Metal GEMM kernel (src/shaders/gemm.metal,
  * src/shaders/backward/gemm.metal, src/shaders/bf16_ops.metal:25-122).
  * epi may be NULL. beta != 0 is not combined with IT_EPI_SWIGLU or IT_EPI_CAUSAL.
+ * IT_EPI_SWIGLU_BWD: the product is dL/dh of h = silu(gate) * up; C (ldc >= 2N) receives
+ * dgate in columns [0, N) and dup in [N, 2N) of each row (the [T, 2F] gate|up gradient the
+ * projection's backward reads); combines with no other flag, beta == 0.
  */
 it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_op transB,
                   int64_t M, int64_t N, int64_t K, float alpha,

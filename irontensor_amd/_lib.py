@@ -29,6 +29,8 @@ IT_OP_N, IT_OP_T = 0, 1
 IT_EPI_BIAS = 0x1
 IT_EPI_SWIGLU = 0x2
 IT_EPI_CAUSAL = 0x4
+IT_EPI_ROPE = 0x8
+IT_EPI_SWIGLU_BWD = 0x10
 
 c_void_p = C.c_void_p
 c_i64 = C.c_int64
@@ -44,6 +46,11 @@ class Epilogue(C.Structure):
         ("gate_out", c_void_p),
         ("up_out", c_void_p),
         ("causal_offset", c_i64),
+        ("rope_base", c_float),
+        ("rope_seq", c_i64),
+        ("rope_head_dim", c_i64),
+        ("rope_cols", c_i64),
+        ("rope_offset", c_i64),
     ]
 
 

@@ -58,14 +58,16 @@ it_status it_gemm_check(it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_
         return fail(IT_ERR_INVALID, "matmul: lda " + i64(lda) + " < " + i64(min_lda));
     if (ldb < (min_ldb > 1 ? min_ldb : 1))
         return fail(IT_ERR_INVALID, "matmul: ldb " + i64(ldb) + " < " + i64(min_ldb));
-    if (ldc < (N > 1 ? N : 1)) return fail(IT_ERR_INVALID, "matmul: ldc " + i64(ldc) + " < " + i64(N));
+    const bool swb = epi && (epi->flags & IT_EPI_SWIGLU_BWD);
+    const int64_t min_ldc = swb ? 2 * N : N;
+    if (ldc < (min_ldc > 1 ? min_ldc : 1)) return fail(IT_ERR_INVALID, "matmul: ldc " + i64(ldc) + " < " + i64(min_ldc));
     if (strideA < 0 || strideB < 0 || strideC < 0)
         return fail(IT_ERR_INVALID, "matmul: negative batch stride");
     const bool has_out = M > 0 && N > 0 && batch > 0;
     if (has_out && !C) return fail(IT_ERR_NULL, "matmul: C is NULL");
     if (has_out && K > 0 && (!A || !B)) return fail(IT_ERR_NULL, "matmul: A or B is NULL");
     if (epi) {
-        const uint32_t known = IT_EPI_BIAS | IT_EPI_SWIGLU | IT_EPI_CAUSAL;
+        const uint32_t known = IT_EPI_BIAS | IT_EPI_SWIGLU | IT_EPI_CAUSAL | IT_EPI_ROPE | IT_EPI_SWIGLU_BWD;
         if (epi->flags & ~known) return fail(IT_ERR_INVALID, "matmul: unknown epilogue flags");
         if ((epi->flags & IT_EPI_BIAS) && !epi->bias)
             return fail(IT_ERR_NULL, "matmul: bias epilogue without a bias pointer");
@@ -79,6 +81,24 @@ it_status it_gemm_check(it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_
         }
         if ((epi->flags & (IT_EPI_SWIGLU | IT_EPI_CAUSAL)) && beta != 0.f)
             return fail(IT_ERR_INVALID, "matmul: beta != 0 cannot be combined with SwiGLU or causal");
+        if (epi->flags & IT_EPI_SWIGLU_BWD) {
+            if (epi->flags != IT_EPI_SWIGLU_BWD)
+                return fail(IT_ERR_INVALID, "matmul: the SwiGLU-backward epilogue combines with no other flag");
+            if (beta != 0.f) return fail(IT_ERR_INVALID, "matmul: beta != 0 cannot be combined with SwiGLU backward");
+            if (has_out && (!epi->gate_out || !epi->up_out))
+                return fail(IT_ERR_NULL, "matmul: SwiGLU-backward epilogue without gate or up");
+            if (batch > 1) return fail(IT_ERR_INVALID, "matmul: SwiGLU backward is a single (unbatched) product");
+        }
+        if (epi->flags & IT_EPI_ROPE) {
+            if (epi->flags & (IT_EPI_SWIGLU | IT_EPI_CAUSAL))
+                return fail(IT_ERR_INVALID, "matmul: RoPE cannot be combined with SwiGLU or causal");
+            if (epi->rope_head_dim <= 0 || epi->rope_head_dim % 2 != 0 || epi->rope_seq <= 0 ||
+                epi->rope_cols < 0 || epi->rope_cols > N || epi->rope_cols % epi->rope_head_dim != 0 ||
+                epi->rope_offset < 0)
+                return fail(IT_ERR_INVALID, "matmul: bad RoPE parameters");
+            if (N % 4 != 0 || ldc % 4 != 0 || (C && (uintptr_t)C % 16 != 0))
+                return fail(IT_ERR_DIMS, "matmul: RoPE epilogue needs N % 4 == 0 and a 16-byte aligned C with ldc % 4 == 0");
+        }
     }
     return IT_OK;
 }
@@ -133,6 +153,24 @@ it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op 
         if (epi->flags & IT_EPI_CAUSAL) {
             a.causal = it::CAUSAL_WRITE;
             a.causal_offset = epi->causal_offset;
+        }
+        if (epi->flags & IT_EPI_SWIGLU_BWD) {
+            a.swiglu_bwd = 1;
+            a.G = epi->gate_out;
+            a.U = epi->up_out;
+            const uintptr_t al = a.out_bf16 ? 8 : 16;
+            a.c_vec_ok = a.c_vec_ok && N % 4 == 0 && (uintptr_t)a.G % al == 0 && (uintptr_t)a.U % al == 0;
+        }
+        if (epi->flags & IT_EPI_ROPE) {
+            const void *table = nullptr;
+            if (const it_status rs = it::rope_table(ctx, epi->rope_seq, epi->rope_head_dim, epi->rope_base,
+                                                    epi->rope_offset, &table);
+                rs != IT_OK)
+                return rs;
+            a.rope_table = (const float2 *)table;
+            a.rope_seq = epi->rope_seq;
+            a.rope_half = (int)(epi->rope_head_dim / 2);
+            a.rope_cols = epi->rope_cols;
         }
     }
     return it::launch_gemm(ctx, dtype_in, transA == IT_OP_T, transB == IT_OP_T, a, "");

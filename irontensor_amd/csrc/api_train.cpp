@@ -38,6 +38,34 @@ const char *sfx(it_dtype d) { return d == IT_BF16 ? "_bf16" : "_f32"; }
 
 }  // namespace
 
+namespace it {
+
+// (cos, sin) per (position, pair): built once per parameter set on the calling stream, kept in the
+// context, and shared by every later call (a graph replay reuses it unchanged).
+it_status rope_table(it_context *ctx, int64_t seq, int64_t head_dim, float base, int64_t offset, const void **out) {
+    uint32_t base_bits;
+    std::memcpy(&base_bits, &base, sizeof base_bits);
+    const std::vector<int64_t> key{seq, head_dim, (int64_t)base_bits, offset};
+    auto found = ctx->rope_tables.find(key);
+    if (found != ctx->rope_tables.end()) {
+        *out = found->second;
+        return IT_OK;
+    }
+    if (ctx->capturing)
+        return fail(IT_ERR_INVALID, "rope: first use of these parameters during graph capture: "
+                                    "run the work once before capturing");
+    void *table = nullptr;
+    IT_HIP_TRY(hipMalloc(&table, (size_t)(seq * (head_dim / 2)) * 2 * sizeof(float)));
+    ctx->rope_tables[key] = table;
+    if (const it_status st = launch_rope_table(ctx->stream, seq, head_dim, base, offset, table); st != IT_OK) return st;
+    // Ready before any stream uses it (later calls may come from the other stream).
+    IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    *out = table;
+    return IT_OK;
+}
+
+}  // namespace it
+
 extern "C" {
 
 it_status it_rmsnorm_forward(it_context *ctx, it_dtype dtype_y, int64_t rows, int64_t dim, float eps,
@@ -246,29 +274,10 @@ it_status it_rope(it_context *ctx, it_dtype dtype_src, it_dtype dtype_dst, int64
         return fail(IT_ERR_INVALID, "rope: in place needs the same precision and row stride");
     if (batch * seq > 0x7fffffff) return fail(IT_ERR_DIMS, "rope: too many rows");
     if (seq * (head_dim / 2) > 0x7fffffff) return fail(IT_ERR_DIMS, "rope: table too large");
-    // (cos, sin) per (position, pair): built once per parameter set on the calling stream, kept in
-    // the context, and shared by every later call (a graph replay reuses it unchanged).
-    uint32_t base_bits;
-    std::memcpy(&base_bits, &base, sizeof base_bits);
-    const std::vector<int64_t> key{seq, head_dim, (int64_t)base_bits, position_offset};
-    void *table = nullptr;
-    if (head_dim > 0) {
-        auto found = ctx->rope_tables.find(key);
-        if (found != ctx->rope_tables.end()) {
-            table = found->second;
-        } else {
-            if (ctx->capturing)
-                return fail(IT_ERR_INVALID, "rope: first use of these parameters during graph capture: "
-                                            "run the work once before capturing");
-            IT_HIP_TRY(hipMalloc(&table, (size_t)(seq * (head_dim / 2)) * 2 * sizeof(float)));
-            ctx->rope_tables[key] = table;
-            if (const it_status st = it::launch_rope_table(ctx->stream, seq, head_dim, base, position_offset, table);
-                st != IT_OK)
-                return st;
-            // Ready before any stream uses it (later calls may come from the other stream).
-            IT_HIP_TRY(hipStreamSynchronize(ctx->stream));
-        }
-    }
+    const void *table = nullptr;
+    if (head_dim > 0)
+        if (const it_status st = it::rope_table(ctx, seq, head_dim, base, position_offset, &table); st != IT_OK)
+            return st;
     Prof p(ctx, std::string(backward ? "rope_bwd" : "rope_fwd") + sfx(dtype_dst) + "[" + i64(batch * seq) + "x" +
                     i64(heads) + "x" + i64(head_dim) + "]");
     return p.done(it::launch_rope(ctx->stream, dtype_src == IT_BF16, dtype_dst == IT_BF16, batch, seq, heads,

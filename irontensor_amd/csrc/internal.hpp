@@ -135,6 +135,14 @@ struct GemmArgs {
     const float *row_scale;
     float rms_eps;
     int no_split;  // the planner must not split K
+    // RoPE on the result (epilogue, 4-column vectors): columns < rope_cols rotate pairwise (2i,
+    // 2i+1 of each head of 2 rope_half columns) by rope_table[(row % rope_seq) * rope_half + i].
+    const float2 *rope_table;
+    int64_t rope_seq, rope_cols;
+    int rope_half;
+    // SwiGLU backward (epilogue): the product is dL/dh; with the forward's gate G and up U ([M, N],
+    // ld N) it writes dgate to C[row, col] and dup to C[row, N + col].
+    int swiglu_bwd;
 
     int64_t M, N, K;
     int64_t lda, ldb, ldc;
@@ -204,6 +212,8 @@ it_status launch_rmsnorm_backward(hipStream_t s, int64_t rows, int64_t dim, floa
                                   const float *x, const float *gamma, const float *gres, float *dx,
                                   float *dgamma, float *part);
 it_status launch_rope_table(hipStream_t s, int64_t seq, int64_t head_dim, float base, int64_t offset, void *table);
+// The context's (cos, sin) table for these parameters, built on first use (not during capture).
+it_status rope_table(it_context *ctx, int64_t seq, int64_t head_dim, float base, int64_t offset, const void **out);
 it_status launch_rope(hipStream_t s, bool src_bf16, bool dst_bf16, int64_t batch, int64_t seq, int64_t heads,
                       int64_t head_dim, const void *table, int backward, const void *src, int64_t src_rs,
                       void *dst, int64_t dst_rs, int64_t copy_cols);

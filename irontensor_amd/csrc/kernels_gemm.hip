@@ -287,9 +287,23 @@ __device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int 
 
 // Final value of one output element (alpha, beta, bias, causal), shared by the GEMM epilogue and
 // the split-K reduction.
+__device__ __forceinline__ float silu_grad(float go, float g, float u, float &du) {
+    const float sig = 1.0f / (1.0f + expf(-g));
+    du = go * (g * sig);
+    return go * u * (sig * (1.0f + g * (1.0f - sig)));
+}
+
 __device__ __forceinline__ void finish_store(const GemmArgs &p, void *C, int64_t idx, float acc,
                                              int64_t row, int64_t col) {
     float v = p.alpha * acc;
+    if (p.swiglu_bwd) {  // dgate at idx, dup N columns later (C rows hold [dgate | dup])
+        const int64_t gi = row * p.N + col;
+        float du;
+        const float dg = silu_grad(v, load_out(p.G, gi, p.out_bf16), load_out(p.U, gi, p.out_bf16), du);
+        store_out(C, idx, dg, p.out_bf16);
+        store_out(C, idx + p.N, du, p.out_bf16);
+        return;
+    }
     if (p.row_scale) v *= p.row_scale[row];
     if (p.beta != 0.f) v += p.beta * load_out(C, idx, p.out_bf16);
     if (p.has_bias) v += p.bias[col];
@@ -320,6 +334,34 @@ __device__ __forceinline__ void finish4(const GemmArgs &p, f32x4 v, int64_t row,
     const int64_t idx = coff + row * p.ldc + col;
     if (full && p.c_vec_ok) {
         v *= p.alpha;
+        if (p.swiglu_bwd) {
+            const int64_t gi = row * p.N + col;
+            f32x4 g, u, dg, du;
+            if (p.out_bf16) {
+                const u32x2 gh = *(const u32x2 *)((const uint16_t *)p.G + gi), uh = *(const u32x2 *)((const uint16_t *)p.U + gi);
+                g = f32x4{__uint_as_float(gh[0] << 16), __uint_as_float(gh[0] & 0xffff0000u),
+                          __uint_as_float(gh[1] << 16), __uint_as_float(gh[1] & 0xffff0000u)};
+                u = f32x4{__uint_as_float(uh[0] << 16), __uint_as_float(uh[0] & 0xffff0000u),
+                          __uint_as_float(uh[1] << 16), __uint_as_float(uh[1] & 0xffff0000u)};
+            } else {
+                g = *(const f32x4 *)((const float *)p.G + gi);
+                u = *(const f32x4 *)((const float *)p.U + gi);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float b;
+                dg[e] = silu_grad(v[e], g[e], u[e], b);
+                du[e] = b;
+            }
+            if (p.out_bf16) {
+                *(u32x2 *)((uint16_t *)p.C + idx) = u32x2{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
+                *(u32x2 *)((uint16_t *)p.C + idx + p.N) = u32x2{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
+            } else {
+                *(f32x4 *)((float *)p.C + idx) = dg;
+                *(f32x4 *)((float *)p.C + idx + p.N) = du;
+            }
+            return;
+        }
         if (p.row_scale) v *= p.row_scale[row];
         if (p.beta != 0.f) {
             f32x4 old;
@@ -335,6 +377,18 @@ __device__ __forceinline__ void finish4(const GemmArgs &p, f32x4 v, int64_t row,
         if (p.has_bias) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] += p.bias[col + e];
+        }
+        if (p.rope_table && col < p.rope_cols) {
+            // col % 4 == 0 and heads have an even width, so both pairs (0,1), (2,3) lie in this vector.
+            const float2 *tr = p.rope_table + (row % p.rope_seq) * p.rope_half;
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                if (col + e >= p.rope_cols) break;
+                const float2 cs = tr[((col + e) % (2 * p.rope_half)) / 2];
+                const float x0 = v[e], x1 = v[e + 1];
+                v[e] = x0 * cs.x - x1 * cs.y;
+                v[e + 1] = x0 * cs.y + x1 * cs.x;
+            }
         }
         if (p.causal != CAUSAL_NONE) {
 #pragma unroll

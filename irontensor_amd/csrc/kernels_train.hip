@@ -115,8 +115,8 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const float *x, const 
 
 // ------------------------------------------------------------------ RMSNorm backward
 
-// Each wave takes RPW consecutive rows and loads all of them before reducing (RPW rows of memory
-// latency overlap); a block's four waves cover 4 RPW rows. Per row: s = 1/rms,
+// Each wave takes RPW consecutive rows and loads all of them (x, dy and the residual gradient)
+// before reducing (RPW rows of memory latency overlap); a block's four waves cover 4 RPW rows. Per row: s = 1/rms,
 // dot = sum(dy * gamma * x), dx = gres + dy * gamma * s - (1/dim) s^3 x dot. Each lane keeps its
 // columns' dgamma partial sum (dy * x * s, rows in order) in registers; the four waves combine in a
 // fixed order into part[block][dim], summed over blocks in order by rmsnorm_dgamma_reduce.
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float *dy, const
     const int64_t r0 = ((int64_t)blockIdx.x * 4 + wave) * RPW;
     const float n = (float)dim;
     float gm[MAXK], acc[MAXK];
-    float xv[RPW][MAXK], gv[RPW][MAXK];
+    float xv[RPW][MAXK], gv[RPW][MAXK], rv[RPW][MAXK];
 #pragma unroll
     for (int k = 0; k < MAXK; ++k) {
         const int64_t c = lane + 64 * k;
@@ -145,6 +145,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float *dy, const
             const bool ok = row < rows && c < dim;
             xv[j][k] = ok ? x[row * dim + c] : 0.f;
             gv[j][k] = ok ? dy[row * dim + c] : 0.f;
+            rv[j][k] = ok && gres ? gres[row * dim + c] : 0.f;  // in flight with x and dy
         }
     }
 #pragma unroll
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float *dy, const
             const int64_t c = lane + 64 * k;
             if (c < dim) {
                 float v = gv[j][k] * gm[k] * s - (1.0f / n) * s3 * xv[j][k] * dot;
-                if (gres) v = gres[row * dim + c] + v;
+                if (gres) v = rv[j][k] + v;
                 dx[row * dim + c] = v;
                 acc[k] += gv[j][k] * xv[j][k] * s;
             }

@@ -8,11 +8,12 @@ attention kernels), and the row/elementwise ops of kernels_train.hip. The MI355X
 
   * residual adds are fused into the RMSNorm that follows them (forward) and the RMSNorm backward
     that precedes them (backward), so no standalone add kernel runs;
-  * Q|K|V is one NT GEMM into a [T, 3H] buffer; RoPE rotates Q and K in place there, attention
-    reads heads from it by stride, and its backward writes dQ|dK|dV into one [T, 3H] buffer that
-    RoPE's backward rotates in place and one NN GEMM consumes;
-  * gate and up are one dual-B GEMM with the SwiGLU epilogue; their backward is one SwiGLU-backward
-    kernel writing a [T, 2F] buffer read by one NN and one TN GEMM;
+  * Q|K|V is one NT GEMM into a [T, 3H] buffer with RoPE applied to Q and K in its epilogue;
+    attention reads heads from it by stride, and its backward writes dQ|dK|dV into one [T, 3H]
+    buffer that RoPE's backward rotates in place and one NN GEMM consumes;
+  * gate and up are one dual-B GEMM with the SwiGLU epilogue; the down projection's dX GEMM runs
+    the SwiGLU backward in its epilogue, writing the [T, 2F] gate|up gradient read by one NN and
+    one TN GEMM (dL/dh is never stored);
   * weight-gradient GEMMs run on the side stream beside the data-gradient chain; every buffer they
     read is per layer, so the main stream never overwrites one before the side stream has read it;
   * the gradient norm, the clip factor and the learning rate stay on the device (Lion reads them
@@ -134,7 +135,6 @@ class TrainStep:
         self.gpost = [empty([T, H]) for _ in range(L)]
         self.dGU = [empty([T, 2 * F]) for _ in range(L)]
         self.dQKV = [empty([T, 3 * H]) for _ in range(L)]
-        self.dHh = empty([T, F])
         self.dX2 = empty([T, H])
         self.dOp = empty([T, H])
         self.dXn = empty([T, H])
@@ -215,8 +215,10 @@ class TrainStep:
         s = self.s
         T, H, F = s.tokens, s.hidden, s.ffn
         L = s.layers
-        self._gemm("qkv", self.xn[l], self.Wqkv[l], self.QKV[l], False, True, T, 3 * H, H)
-        self._rope(self.QKV[l], False)
+        # Q|K|V projection with RoPE applied to the Q and K columns in the GEMM's epilogue
+        rope = _lib.Epilogue(flags=_lib.IT_EPI_ROPE, rope_base=self.rope_base, rope_seq=s.seq,
+                             rope_head_dim=s.head_dim, rope_cols=2 * H, rope_offset=0)
+        self._gemm("qkv", self.xn[l], self.Wqkv[l], self.QKV[l], False, True, T, 3 * H, H, epi=rope)
         qkv, o = self._layouts()
         q, k, v = (C.c_void_p(self.QKV[l].ptr + i * H * 4) for i in range(3))
         scale = 1.0 / math.sqrt(s.head_dim)
@@ -249,10 +251,9 @@ class TrainStep:
         g = self.g_out[l + 1]
         # FFN: down projection, SwiGLU, gate|up projection, ffn norm (+ residual)
         self._dw("down.dW", g, self.Hh[l], self.dWd[l], True, False, H, F, T)
-        self._gemm("down.dX", g, self.Wd[l], self.dHh, False, False, T, F, H)
-        check(self.lib.it_swiglu_backward(self.h, 0, 0, T, F, C.c_void_p(self.dHh.ptr), F, C.c_void_p(self.G[l].ptr),
-                                          C.c_void_p(self.U[l].ptr), F, C.c_void_p(self.dGU[l].ptr),
-                                          C.c_void_p(self.dGU[l].ptr + F * 4), 2 * F), "swiglu_backward")
+        # dL/dh = g.Wd goes straight through the SwiGLU backward in the GEMM's epilogue into dGate|dUp
+        swb = _lib.Epilogue(flags=_lib.IT_EPI_SWIGLU_BWD, gate_out=self.G[l].ptr, up_out=self.U[l].ptr)
+        self._gemm("down.dX+swiglu_bwd", g, self.Wd[l], self.dGU[l], False, False, T, F, H, epi=swb)
         self._dw("gate_up.dW", self.dGU[l], self.x2[l], self.dWgu[l], True, False, 2 * F, H, T)
         self._gemm("gate_up.dX", self.dGU[l], self.Wgu[l], self.dX2, False, False, T, H, 2 * F)
         self._norm_bwd(self.dX2, self.post[l], self.ffn_norm[l], g, self.gpost[l], self.d_ffn_norm[l])

@@ -229,3 +229,61 @@ def test_lion_bit_exact(it, oracle):
         rw, rm = oracle.lion(w, m, g, 3e-4, 0.9, 0.99, 0.1, scale=0.25)
         assert np.array_equal(dw.numpy(), rw)
         assert np.array_equal(st.momentum.numpy(), rm)
+
+
+# ---------------------------------------------------------------- GEMM epilogues of the step
+
+def _epi_gemm(it, A, B, Cout, ta, tb, M, N, K, epi):
+    ctx = it.Context.global_()
+    st = ctx.lib.it_gemm(ctx.handle, int(A.precision()), int(Cout.precision()), int(ta), int(tb), M, N, K, 1.0,
+                         C.c_void_p(A.ptr), A.shape()[-1], 0, C.c_void_p(B.ptr), B.shape()[-1], 0, 0.0,
+                         C.c_void_p(Cout.ptr), Cout.shape()[-1], 0, 1, C.byref(epi))
+    assert st == 0, it._lib.last_error() if hasattr(it, "_lib") else st
+
+
+@pytest.mark.parametrize("T,H,heads,K", [(4096, 256, 4, 256), (256, 128, 2, 1000), (64, 128, 2, 4096)])
+def test_gemm_rope_epilogue(it, oracle, T, H, heads, K):
+    """Q|K|V projection with RoPE in the epilogue == projection then it_rope (the large-K case
+    takes split-K, so the rotation runs in the reduction's epilogue)."""
+    from irontensor_amd import _lib
+    print(f"[case] rope epilogue T={T} H={H} K={K}", flush=True)
+    seq, d = 64, H // heads
+    x, w = synth.normal(30, (T, K)), synth.normal(31, (3 * H, K), std=0.05)
+    X, W = _t(it, x), _t(it, w)
+    got = it.Tensor.empty([T, 3 * H])
+    epi = _lib.Epilogue(flags=_lib.IT_EPI_ROPE, rope_base=10000.0, rope_seq=seq, rope_head_dim=d, rope_cols=2 * H)
+    _epi_gemm(it, X, W, got, False, True, T, 3 * H, K, epi)
+    ref = it.linear_forward(X, W)
+    ctx = it.Context.global_()
+    assert ctx.lib.it_rope(ctx.handle, 0, 0, T // seq, seq, 2 * heads, d, 10000.0, 0, 0, C.c_void_p(ref.ptr), 3 * H,
+                           C.c_void_p(ref.ptr), 3 * H, 0) == 0
+    assert normwise_rel(got.numpy(), ref.numpy()) <= 1e-6
+    # against the oracle: projection, then RoPE on Q and K
+    proj = oracle.gemm_f32(x, w, trans_b=True).reshape(T // seq, seq, 3 * H)
+    want = oracle.rope(proj, heads=2 * heads, head_dim=d).reshape(T, 3 * H)
+    assert normwise_rel(got.numpy(), want) <= FP32_TOL
+
+
+@pytest.mark.parametrize("prec,T,F,K", [("f32", 4096, 688, 256), ("f32", 100, 50, 64), ("bf16", 512, 688, 256)])
+def test_gemm_swiglu_backward_epilogue(it, oracle, prec, T, F, K):
+    """dL/dh = g.Wd with the SwiGLU backward in the epilogue == the product, then swiglu_backward
+    (F = 50 takes the element-wise path: no 4-column vectors)."""
+    from irontensor_amd import _lib, train_ops as Tops
+    print(f"[case] swiglu-backward epilogue {prec} T={T} F={F} K={K}", flush=True)
+    P = it.Precision
+    g_, w_ = synth.normal(32, (T, K)), synth.normal(33, (K, F), std=0.05)
+    gate, up = synth.normal(34, (T, F)), synth.normal(35, (T, F))
+    mk = (lambda a: it.Tensor.from_f32_as_bf16(a, list(a.shape))) if prec == "bf16" else (lambda a: _t(it, a))
+    G_, W_, GA, UP = mk(g_), mk(w_), mk(gate), mk(up)
+    out = it.Tensor.empty([T, 2 * F], P.BF16 if prec == "bf16" else P.FP32)
+    epi = _lib.Epilogue(flags=_lib.IT_EPI_SWIGLU_BWD, gate_out=GA.ptr, up_out=UP.ptr)
+    _epi_gemm(it, G_, W_, out, False, False, T, F, K, epi)
+    dh = it.gemm(G_, W_, out_precision=P.FP32).numpy()
+    rg, ru = oracle.swiglu_backward(dh, GA.numpy(), UP.numpy())
+    o = out.numpy()
+    tol = FP32_TOL if prec == "f32" else 1e-2
+    metric = normwise_rel if prec == "f32" else frob_rel
+    assert metric(o[:, :F], rg) <= tol and metric(o[:, F:], ru) <= tol
+    if prec == "f32":
+        gg, gu = Tops.swiglu_backward(_t(it, dh), GA, UP)
+        assert normwise_rel(o[:, :F], gg.numpy()) <= 1e-6 and normwise_rel(o[:, F:], gu.numpy()) <= 1e-6
