@@ -608,11 +608,17 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
             if constexpr (PF == 1) {
                 for (int t = 0; t < ntiles; ++t) tile(t, 0, 0);
             } else {
-                // set (t+1) % 2 holds tile t+1; tile t+2 goes into set t % 2 once it is in LDS
-                for (int t = 0; t < ntiles; t += 2) {
-                    tile(t, 0, 1);
-                    if (t + 1 < ntiles) tile(t + 1, 1, 0);
+                // Tile u's registers are set u % PF: tile t writes set (t+1) % PF to LDS and
+                // reloads set t % PF (written to LDS during tile t-1) with tile t+PF.
+                // Whole groups of PF tiles in a branch-free body, then the remaining tiles.
+                int t = 0;
+                for (; t + PF <= ntiles; t += PF) {
+#pragma unroll
+                    for (int q = 0; q < PF; ++q) tile(t + q, q, (q + 1) % PF);
                 }
+#pragma unroll
+                for (int q = 0; q + 1 < PF; ++q)
+                    if (t + q < ntiles) tile(t + q, q, (q + 1) % PF);
             }
         }
     }
@@ -944,7 +950,9 @@ bool vectors_exact(const GemmArgs &a, bool ta, bool tb) {
 
 template <typename T, bool TA, bool TB, bool DUAL>
 hipError_t launch_cfg(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
-    if (vectors_exact<T>(a, TA, TB))
+    if (tiles_exact(a, cfg.bm, DUAL ? cfg.bn / 2 : cfg.bn, ET<T>::BK))
+        launch_cfg_lm<T, TA, TB, DUAL, LOAD_EXACT>(cfg, a, grid, s);
+    else if (vectors_exact<T>(a, TA, TB))
         launch_cfg_lm<T, TA, TB, DUAL, LOAD_MASKED>(cfg, a, grid, s);
     else
         launch_cfg_lm<T, TA, TB, DUAL, LOAD_CHECKED>(cfg, a, grid, s);
