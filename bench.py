@@ -171,14 +171,12 @@ def extra_med_step(it, timer, steps=5, warmup=2) -> dict:
         "top_kernels": [{"key": k, "ms_per_step": round(v["total_ms"], 3), "calls": v["calls"]} for k, v in top]}}
 
 
-def extra_sweep(it, timer) -> dict:
-    """Config 5: BF16 square GEMMs n^3, n in {1024 .. 16384}, NN/NT/TN, BF16 out; and the decode
-    shapes M in {1, 4, 16}, K 4096, N 11008 (HBM-bound: weight bytes / time against 8 TB/s).
-    Operands from synth.pooled_normal (N(0,1))."""
+def bf16_square(it, timer, sizes) -> dict:
+    """BF16 n^3 GEMMs, NN/NT/TN, BF16 out, `iters` timed launches each ((n, iters) in `sizes`)."""
     from irontensor_amd import synth
     P = it.Precision
     out = {}
-    for n, iters in ((1024, 50), (2048, 20), (4096, 10), (8192, 4), (16384, 2)):
+    for n, iters in sizes:
         a = _bf16(it, synth.pooled_normal(3, (n, n)))
         b = _bf16(it, synth.pooled_normal(4, (n, n)))
         c = it.Tensor.empty([n, n], P.BF16)
@@ -188,6 +186,16 @@ def extra_sweep(it, timer) -> dict:
             out[f"bf16_square_{n}_{lay}"] = {"ms": round(ms, 4), "tflops": round(tf, 1),
                                              "frac_bf16_peak": round(tf / PEAK_TFLOPS["bf16"], 4)}
         del a, b, c
+    return out
+
+
+def extra_sweep(it, timer) -> dict:
+    """Config 5: BF16 square GEMMs n^3, n in {1024 .. 16384}, NN/NT/TN, BF16 out; and the decode
+    shapes M in {1, 4, 16}, K 4096, N 11008 (HBM-bound: weight bytes / time against 8 TB/s).
+    Operands from synth.pooled_normal (N(0,1))."""
+    from irontensor_amd import synth
+    P = it.Precision
+    out = bf16_square(it, timer, ((1024, 50), (2048, 20), (4096, 10), (8192, 4), (16384, 2)))
     k, n = 4096, 11008
     w_nk = _bf16(it, synth.pooled_normal(5, (n, k)))
     w_kn = _bf16(it, synth.pooled_normal(7, (k, n)))
@@ -465,6 +473,8 @@ def main() -> int:
                     help="run only a calibration copy and the dominant kernel (for rocprofv3 --pmc)")
     ap.add_argument("--train-only", action="store_true",
                     help="run only the complete TINY training step, graph-replayed (for kernel traces)")
+    ap.add_argument("--bf16-square", action="store_true",
+                    help="run only the BF16 4096^3 and 8192^3 GEMMs, NN/NT/TN (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -483,6 +493,10 @@ def main() -> int:
     ctx = it.Context.global_()
     info = ctx.info()
     log(f"[bench] device {info}")
+    if args.bf16_square:
+        print(json.dumps(bf16_square(it, Timer(ctx), ((4096, args.steps), (8192, max(1, args.steps // 4))))),
+              flush=True)
+        return 0
     if args.train_only:
         print(json.dumps({"train_step": train_step_figures(it, Timer(ctx), args.steps, args.warmup)}), flush=True)
         return 0
