@@ -667,6 +667,29 @@ inline CrossEntropy cross_entropy_fused(const Tensor &logits, const std::vector<
     return r;
 }
 
+// The loss half of cross_entropy_fused -> (mean loss, losses [rows], stats [rows, 2] = {max,
+// 1 / sum exp(x - max)}); a GEMM with IT_EPI_XENT_A rebuilds the gradient from the stats.
+struct CrossEntropyStats {
+    float loss;
+    Tensor losses, stats;
+};
+inline CrossEntropyStats cross_entropy_stats(const Tensor &logits, const std::vector<uint32_t> &targets) {
+    detail::require(logits.is_f32(), "assertion `left == right` failed: cross_entropy_stats requires FP32");
+    detail::require(logits.shape().size() == 2, "logits must be 2D");
+    const size_t rows = logits.shape()[0], vocab = logits.shape()[1];
+    detail::require(targets.size() == rows, "assertion `left == right` failed: targets length");
+    CrossEntropyStats r{0.f, Tensor::zeros({rows}, Precision::FP32), Tensor::zeros({rows, 2}, Precision::FP32)};
+    if (rows == 0) return r;
+    Tensor t = detail::upload_ids(targets, vocab);
+    Tensor mean = Tensor::empty({1}, Precision::FP32);
+    check(it_cross_entropy_stats(Context::global().handle(), (int64_t)rows, (int64_t)vocab,
+                                 (const float *)logits.data(), (const uint32_t *)t.data(), (float *)r.losses.data(),
+                                 (float *)r.stats.data(), (float *)mean.data()),
+          "cross_entropy_stats");
+    r.loss = mean.as_f32_slice()[0];
+    return r;
+}
+
 // swiglu_backward (src/ops/backward/elementwise.rs:149) -> (grad_gate, grad_up).
 inline std::pair<Tensor, Tensor> swiglu_backward(const Tensor &grad_output, const Tensor &gate, const Tensor &up) {
     detail::require(grad_output.shape() == gate.shape() && gate.shape() == up.shape(), "swiglu_backward: shapes differ");

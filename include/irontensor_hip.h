@@ -109,6 +109,7 @@ it_status it_event_destroy(it_event *ev);
 #define IT_EPI_CAUSAL 0x4u      /* C[m,n] = -inf where n > m + causal_offset (attention.metal:186-207) */
 #define IT_EPI_ROPE 0x8u        /* rotary embedding of columns n < rope_cols (src/ops/rope.rs:22) */
 #define IT_EPI_SWIGLU_BWD 0x10u /* SwiGLU backward of the product (src/ops/backward/elementwise.rs:149) */
+#define IT_EPI_XENT_A 0x20u     /* A = logits read as their cross-entropy gradient (src/ops/backward/loss.rs:248) */
 
 typedef struct it_epilogue {
     uint32_t flags;
@@ -128,6 +129,16 @@ typedef struct it_epilogue {
     int64_t rope_head_dim;
     int64_t rope_cols;
     int64_t rope_offset;
+    /* IT_EPI_XENT_A (dtype_in IT_F32, transB == IT_OP_N, batch 1, no other flag): A holds FP32
+     * logits [tokens, classes] and enters the product as the gradient it_cross_entropy_fused would
+     * have written: element x of token t and class c as
+     * (exp(x - xent_stats[2t]) * xent_stats[2t+1] - (c == xent_targets[t])) * xent_scale, with
+     * {max, 1/sum} per token from it_cross_entropy_stats and xent_scale = 1/tokens for the mean
+     * loss. transA == IT_OP_N: rows of op(A) are tokens (dL/dh = G.E); IT_OP_T: op(A) = A^T and k is
+     * the token (dL/dE = G^T.h). The gradient tensor is never stored. */
+    const float *xent_stats;
+    const uint32_t *xent_targets;
+    float xent_scale;
 } it_epilogue;
 
 /*
@@ -333,6 +344,13 @@ it_status it_embedding_forward(it_context *ctx, it_dtype dtype_table, it_dtype d
  * atomics); rows no id hits are zero. Replaces embedding_backward (src/ops/backward/embedding.rs:21). */
 it_status it_embedding_backward(it_context *ctx, int64_t n, int64_t dim, int64_t vocab, const float *dy,
                                 const uint32_t *ids, float *dw);
+
+/* The forward half of it_cross_entropy_fused: losses (NULL: library scratch) and *loss_mean as
+ * there, plus stats[2r] = max_c x_r[c] and stats[2r+1] = 1 / sum_c exp(x_r[c] - max) (8-byte
+ * aligned); no gradient is written. A GEMM with IT_EPI_XENT_A rebuilds the gradient from these.
+ * Replaces the loss half of cross_entropy_fused (src/ops/backward/loss.rs:248). */
+it_status it_cross_entropy_stats(it_context *ctx, int64_t rows, int64_t vocab, const float *logits,
+                                 const uint32_t *targets, float *losses, float *stats, float *loss_mean);
 
 /* Fused softmax cross entropy over logits [rows, vocab] f32 and device uint32 targets:
  * losses[r] = logsumexp(x_r) - x_r[t_r] (losses NULL: library scratch), grad = (softmax - onehot)

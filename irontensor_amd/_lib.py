@@ -31,6 +31,7 @@ IT_EPI_SWIGLU = 0x2
 IT_EPI_CAUSAL = 0x4
 IT_EPI_ROPE = 0x8
 IT_EPI_SWIGLU_BWD = 0x10
+IT_EPI_XENT_A = 0x20
 
 c_void_p = C.c_void_p
 c_i64 = C.c_int64
@@ -51,6 +52,9 @@ class Epilogue(C.Structure):
         ("rope_head_dim", c_i64),
         ("rope_cols", c_i64),
         ("rope_offset", c_i64),
+        ("xent_stats", c_void_p),
+        ("xent_targets", c_void_p),
+        ("xent_scale", c_float),
     ]
 
 
@@ -125,6 +129,7 @@ _SIGNATURES = {
     "it_embedding_backward": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p]),
     "it_cross_entropy_fused": (c_int, [c_void_p, c_int, c_i64, c_i64, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p]),
+    "it_cross_entropy_stats": (c_int, [c_void_p, c_i64, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "it_swiglu_backward": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_void_p, c_i64, c_void_p, c_void_p,
                                    c_i64, c_void_p, c_void_p, c_i64]),
     "it_grad_norm_clip": (c_int, [c_void_p, c_int, C.POINTER(c_void_p), C.POINTER(c_i64), c_float, c_void_p]),

@@ -67,7 +67,8 @@ it_status it_gemm_check(it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_
     if (has_out && !C) return fail(IT_ERR_NULL, "matmul: C is NULL");
     if (has_out && K > 0 && (!A || !B)) return fail(IT_ERR_NULL, "matmul: A or B is NULL");
     if (epi) {
-        const uint32_t known = IT_EPI_BIAS | IT_EPI_SWIGLU | IT_EPI_CAUSAL | IT_EPI_ROPE | IT_EPI_SWIGLU_BWD;
+        const uint32_t known =
+            IT_EPI_BIAS | IT_EPI_SWIGLU | IT_EPI_CAUSAL | IT_EPI_ROPE | IT_EPI_SWIGLU_BWD | IT_EPI_XENT_A;
         if (epi->flags & ~known) return fail(IT_ERR_INVALID, "matmul: unknown epilogue flags");
         if ((epi->flags & IT_EPI_BIAS) && !epi->bias)
             return fail(IT_ERR_NULL, "matmul: bias epilogue without a bias pointer");
@@ -88,6 +89,18 @@ it_status it_gemm_check(it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_
             if (has_out && (!epi->gate_out || !epi->up_out))
                 return fail(IT_ERR_NULL, "matmul: SwiGLU-backward epilogue without gate or up");
             if (batch > 1) return fail(IT_ERR_INVALID, "matmul: SwiGLU backward is a single (unbatched) product");
+        }
+        if (epi->flags & IT_EPI_XENT_A) {
+            if (epi->flags != IT_EPI_XENT_A)
+                return fail(IT_ERR_INVALID, "matmul: the cross-entropy operand combines with no other flag");
+            if (dtype_in != IT_F32)
+                return fail(IT_ERR_PRECISION, "matmul: the cross-entropy operand needs FP32 inputs");
+            if (transB != IT_OP_N) return fail(IT_ERR_INVALID, "matmul: the cross-entropy operand needs transB=N");
+            if (batch > 1) return fail(IT_ERR_INVALID, "matmul: the cross-entropy operand is a single (unbatched) product");
+            if (has_out && K > 0 && (!epi->xent_stats || !epi->xent_targets))
+                return fail(IT_ERR_NULL, "matmul: cross-entropy operand without stats or targets");
+            if ((uintptr_t)epi->xent_stats % 8 != 0)
+                return fail(IT_ERR_INVALID, "matmul: cross-entropy stats must be 8-byte aligned");
         }
         if (epi->flags & IT_EPI_ROPE) {
             if (epi->flags & (IT_EPI_SWIGLU | IT_EPI_CAUSAL))
@@ -160,6 +173,11 @@ it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op 
             a.U = epi->up_out;
             const uintptr_t al = a.out_bf16 ? 8 : 16;
             a.c_vec_ok = a.c_vec_ok && N % 4 == 0 && (uintptr_t)a.G % al == 0 && (uintptr_t)a.U % al == 0;
+        }
+        if (epi->flags & IT_EPI_XENT_A) {
+            a.xent_stats = (const float2 *)epi->xent_stats;
+            a.xent_tgt = epi->xent_targets;
+            a.xent_scale = epi->xent_scale;
         }
         if (epi->flags & IT_EPI_ROPE) {
             const void *table = nullptr;

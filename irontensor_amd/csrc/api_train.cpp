@@ -334,7 +334,27 @@ it_status it_cross_entropy_fused(it_context *ctx, it_dtype dtype_grad, int64_t r
                         (uintptr_t)grad % (dtype_grad == IT_BF16 ? 8 : 16) == 0;
     Prof p(ctx, std::string("cross_entropy") + sfx(dtype_grad) + "[" + i64(rows) + "x" + i64(vocab) + "]");
     return p.done(it::launch_cross_entropy(ctx->stream, dtype_grad == IT_BF16, rows, vocab, logits, targets, losses,
-                                           grad, loss_mean, vec_ok));
+                                           grad, nullptr, loss_mean, vec_ok));
+}
+
+it_status it_cross_entropy_stats(it_context *ctx, int64_t rows, int64_t vocab, const float *logits,
+                                 const uint32_t *targets, float *losses, float *stats, float *loss_mean) {
+    if (!ctx) return fail(IT_ERR_NULL, "cross_entropy_stats: ctx is NULL");
+    if (rows < 0 || vocab < 0) return fail(IT_ERR_INVALID, "cross_entropy_stats: negative size");
+    if (rows > 0x7fffffff) return fail(IT_ERR_DIMS, "cross_entropy_stats: too many rows");
+    if (rows == 0) return loss_mean ? it::launch_zero(ctx->stream, loss_mean, sizeof(float)) : IT_OK;
+    if (vocab == 0) return fail(IT_ERR_SHAPE, "cross_entropy_stats: vocabulary is empty");
+    if (!logits || !targets || !stats) return fail(IT_ERR_NULL, "cross_entropy_stats: NULL buffer");
+    if ((uintptr_t)stats % 8 != 0) return fail(IT_ERR_INVALID, "cross_entropy_stats: stats must be 8-byte aligned");
+    if (!losses) {
+        void *p = nullptr;
+        if (const it_status st = it::ensure_scratch(ctx, (size_t)rows * sizeof(float), &p); st != IT_OK) return st;
+        losses = (float *)p;
+    }
+    const bool vec_ok = vocab % 4 == 0 && (uintptr_t)logits % 16 == 0;
+    Prof p(ctx, "cross_entropy_stats[" + i64(rows) + "x" + i64(vocab) + "]");
+    return p.done(it::launch_cross_entropy(ctx->stream, false, rows, vocab, logits, targets, losses, nullptr, stats,
+                                           loss_mean, vec_ok));
 }
 
 it_status it_swiglu_backward(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, int64_t rows, int64_t cols,

@@ -143,6 +143,13 @@ struct GemmArgs {
     // SwiGLU backward (epilogue): the product is dL/dh; with the forward's gate G and up U ([M, N],
     // ld N) it writes dgate to C[row, col] and dup to C[row, N + col].
     int swiglu_bwd;
+    // Softmax cross-entropy gradient in place of A (FP32, B not transposed): A holds logits
+    // [tokens, classes]; op(A) rows are tokens (A not transposed) or k is the token (transposed).
+    // Element x of token t, class c enters the product as
+    // (exp(x - xent_stats[t].x) * xent_stats[t].y - (c == xent_tgt[t])) * xent_scale.
+    const float2 *xent_stats;
+    const uint32_t *xent_tgt;
+    float xent_scale;
 
     int64_t M, N, K;
     int64_t lda, ldb, ldc;
@@ -222,7 +229,8 @@ it_status launch_embedding_forward(hipStream_t s, bool table_bf16, bool out_bf16
 it_status launch_embedding_backward(hipStream_t s, int64_t n, int64_t dim, int64_t vocab, const float *dy,
                                     const uint32_t *ids, float *dw);
 it_status launch_cross_entropy(hipStream_t s, bool grad_bf16, int64_t rows, int64_t vocab, const float *logits,
-                               const uint32_t *targets, float *losses, void *grad, float *loss_mean, bool vec_ok);
+                               const uint32_t *targets, float *losses, void *grad, float *stats, float *loss_mean,
+                               bool vec_ok);
 it_status launch_swiglu_backward(hipStream_t s, bool in_bf16, bool out_bf16, int64_t rows, int64_t cols,
                                  const float *dh, int64_t ld_dh, const void *gate, const void *up, int64_t ld_gu,
                                  void *dgate, void *dup, int64_t ld_out);

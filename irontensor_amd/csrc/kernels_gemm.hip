@@ -208,6 +208,54 @@ struct Operand {
         }
     }
 
+    // Softmax cross-entropy gradient of FP32 logits (the A operand of dL/dh = G.E or dL/dE =
+    // G^T.h): load_xent fetches, with the tile, each item's token statistics {max, 1/sum} and
+    // target (rows are tokens when k-contiguous, k is the token otherwise); apply_xent turns the
+    // loaded logits into (exp(x - max) / sum - onehot) * scale, and elements outside the product
+    // (tokens or classes past the limits) into zeros.
+    float2 xs[ITERS];
+    uint32_t xt[ITERS];
+    int64_t xk0;
+
+    __device__ __forceinline__ void load_xent(const float2 *st, const uint32_t *tg, int64_t r0, int64_t k0,
+                                              int64_t rlim, int64_t klim, int tid) {
+        static_assert(sizeof(T) == 4, "cross-entropy gradients are FP32");
+        xk0 = k0;
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int item = tid + it * NTHREADS;
+            if (ITEMS % NTHREADS != 0 && item >= ITEMS) continue;
+            const int64_t tok = KCONTIG ? r0 + item / (BK / VEC) : k0 + item / (ROWS / VEC);
+            const bool ok = tok < (KCONTIG ? rlim : klim);
+            xs[it] = ok ? st[tok] : float2{INFINITY, 0.f};
+            xt[it] = ok ? tg[tok] : 0xffffffffu;
+        }
+    }
+
+    // exp(x - max) as 2^((x - max) log2 e) on the hardware unit: a few VALU operations per element,
+    // since every element of the A tile goes through it (relative error about 1e-6 for a logit 20
+    // below the row max, where the probability itself is below 1e-8).
+    template <bool CHECK>
+    __device__ __forceinline__ void apply_xent(int64_t r0, int64_t rlim, int64_t klim, float scale, int tid) {
+        constexpr float LOG2E = 1.4426950408889634f;
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int item = tid + it * NTHREADS;
+            if (ITEMS % NTHREADS != 0 && item >= ITEMS) continue;
+            const int64_t c0 = KCONTIG ? xk0 + (item % (BK / VEC)) * VEC : r0 + (item % (ROWS / VEC)) * VEC;
+            const int64_t clim = KCONTIG ? klim : rlim;
+            const float mx = xs[it].x, ps = xs[it].y * scale;
+            const int32_t tc = (int32_t)(xt[it] - (uint32_t)c0);  // target's offset in this vector
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x = __uint_as_float(reg[it][0][e]);
+                float g = __builtin_amdgcn_exp2f((x - mx) * LOG2E) * ps - (tc == e ? scale : 0.f);
+                if constexpr (CHECK) g = c0 + e < clim ? g : 0.f;
+                reg[it][0][e] = __float_as_uint(g);
+            }
+        }
+    }
+
     __device__ __forceinline__ void store(char *lds, int tid) const {
 #pragma unroll
         for (int it = 0; it < ITERS; ++it) {
@@ -459,7 +507,8 @@ namespace sg {
 constexpr int MFMA = 0x008, VMEM_READ = 0x020, DS_READ = 0x100, DS_WRITE = 0x200;
 }
 
-template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL, int LM, bool KS = false, int PF = 1>
+template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL, int LM, bool KS = false, int PF = 1,
+          bool XF = false>
 __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
     static_assert(WM * WN == 4, "4 waves per block");
     constexpr int BK = ET<T>::BK;
@@ -521,6 +570,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
             if (q == set) {
                 oa[q].template load<LM>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
                 if constexpr (KS) oa[q].load_kscale(p.a_kscale, k0, ke, tid);
+                if constexpr (XF) oa[q].load_xent(p.xent_stats, p.xent_tgt, m0, k0, p.M, ke, tid);
                 ob[q].template load<LM>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
                 if constexpr (DUAL) ob2[q].template load<LM>(B2, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
             }
@@ -537,6 +587,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
                     if (fresh) oa[q].add_squares(ssq, tid);
                     oa[q].apply_kscale(tid);
                 }
+                if constexpr (XF) oa[q].template apply_xent<LM != LOAD_EXACT>(m0, p.M, ke, p.xent_scale, tid);
                 oa[q].store(st, tid);
                 ob[q].store(st + SA, tid);
                 if constexpr (DUAL) ob2[q].store(st + SA + OBH::STAGE_BYTES, tid);
@@ -959,10 +1010,33 @@ hipError_t launch_cfg(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStrea
     return hipGetLastError();
 }
 
+// Cross-entropy gradient operand (FP32, B not transposed; checked by the caller).
+template <bool TA, int LM>
+void launch_xent_lm(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
+    if (cfg.bm == 128)
+        hipLaunchKernelGGL((gemm_mfma<float, TA, false, 128, 128, 2, 2, false, LM, false, 1, true>), grid,
+                           dim3(NTHREADS), 0, s, a);
+    else
+        hipLaunchKernelGGL((gemm_mfma<float, TA, false, 64, 64, 2, 2, false, LM, false, 2, true>), grid,
+                           dim3(NTHREADS), 0, s, a);
+}
+
+template <bool TA>
+hipError_t launch_xent(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
+    if (tiles_exact(a, cfg.bm, cfg.bn, ET<float>::BK))
+        launch_xent_lm<TA, LOAD_EXACT>(cfg, a, grid, s);
+    else if (vectors_exact<float>(a, TA, false))
+        launch_xent_lm<TA, LOAD_MASKED>(cfg, a, grid, s);
+    else
+        launch_xent_lm<TA, LOAD_CHECKED>(cfg, a, grid, s);
+    return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_typed(bool ta, bool tb, bool dual, const TileCfg &cfg, const GemmArgs &a, dim3 grid,
                         hipStream_t s) {
     if constexpr (sizeof(T) == 4) {
+        if (a.xent_stats) return ta ? launch_xent<true>(cfg, a, grid, s) : launch_xent<false>(cfg, a, grid, s);
         if (a.a_kscale) {  // fused RMSNorm + projection: X.W^T only (checked by the caller)
             if (vectors_exact<T>(a, false, true))
                 launch_cfg_lm<T, false, true, false, LOAD_MASKED, true>(cfg, a, grid, s);
@@ -1119,7 +1193,7 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
         char buf[192];
         std::snprintf(buf, sizeof(buf), "gemm_%s_%c%c_%dx%d%s%s%s|%s[%lld,%lld,%lld]x%lld s%d",
                       bf16 ? "bf16" : "f32", transA ? 'T' : 'N', transB ? 'T' : 'N', cfg.bm, cfg.bn,
-                      a.dual ? "_swiglu" : "", a.causal || a.kmode ? "_causal" : "", a.a_kscale ? "_rmsnorm" : "",
+                      a.dual ? "_swiglu" : "", a.causal || a.kmode ? "_causal" : "", a.a_kscale ? "_rmsnorm" : a.xent_stats ? "_xent" : "",
                       profile_tag ? profile_tag : "", (long long)a.M, (long long)a.N,
                       (long long)a.K, (long long)a.batch, splits);
         key = buf;

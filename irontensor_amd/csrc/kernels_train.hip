@@ -371,7 +371,8 @@ __global__ __launch_bounds__(256) void embedding_bwd_kernel(const float *dy, con
 // loss = -x[t] + (max + log(sum exp(x - max))); grad = (exp(x - max) / sum - onehot) * grad_scale.
 template <int NPT, typename TG>
 __global__ __launch_bounds__(256) void ce_kernel(const float *logits, const uint32_t *targets, float *losses,
-                                                 TG *grad, int64_t rows, int64_t vocab, float grad_scale) {
+                                                 TG *grad, float2 *stats, int64_t rows, int64_t vocab,
+                                                 float grad_scale) {
     __shared__ float red[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t row = blockIdx.x;
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(256) void ce_kernel(const float *logits, const uint
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const int64_t e = 4 * ((int64_t)tid + 256 * k);
-            if (e < vocab) {
+            if (!stats && e < vocab) {
                 f32x4 o;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) o[q] = (v[k][q] * inv - ((uint64_t)(e + q) == t ? 1.0f : 0.0f)) * grad_scale;
@@ -436,10 +437,14 @@ __global__ __launch_bounds__(256) void ce_kernel(const float *logits, const uint
         for (int64_t e = tid; e < vocab; e += 256) sum += expf(x[e] - mx);
         sum = block_sum(sum);
         const float inv = 1.0f / sum;
-        for (int64_t e = tid; e < vocab; e += 256)
+        for (int64_t e = tid; !stats && e < vocab; e += 256)
             stv<TG>(g, e, (expf(x[e] - mx) * inv - ((uint64_t)e == t ? 1.0f : 0.0f)) * grad_scale);
     }
-    if (tid == 0) losses[row] = (int64_t)t < vocab ? -x[t] + (mx + logf(sum)) : NAN;
+    if (tid == 0) {
+        losses[row] = (int64_t)t < vocab ? -x[t] + (mx + logf(sum)) : NAN;
+        // Stats mode: the row's max and 1 / sum, from which a GEMM rebuilds the gradient.
+        if (stats) stats[row] = float2{mx, 1.0f / sum};
+    }
 }
 
 // Mean of `n` values in a fixed order (one block): per-thread sums of a strided slice (eight loads
@@ -874,12 +879,13 @@ it_status launch_embedding_backward(hipStream_t s, int64_t n, int64_t dim, int64
 }
 
 it_status launch_cross_entropy(hipStream_t s, bool grad_bf16, int64_t rows, int64_t vocab, const float *logits,
-                               const uint32_t *targets, float *losses, void *grad, float *loss_mean,
+                               const uint32_t *targets, float *losses, void *grad, float *stats, float *loss_mean,
                                bool vec_ok) {
     const float gs = 1.0f / (float)rows;
     const dim3 grid((unsigned)rows), block(256);
-#define IT_CE(NPT, TG)                                                                                         \
-    hipLaunchKernelGGL((ce_kernel<NPT, TG>), grid, block, 0, s, logits, targets, losses, (TG *)grad, rows, vocab, gs)
+#define IT_CE(NPT, TG)                                                                                    \
+    hipLaunchKernelGGL((ce_kernel<NPT, TG>), grid, block, 0, s, logits, targets, losses, (TG *)grad,       \
+                       (float2 *)stats, rows, vocab, gs)
 #define IT_CE_T(NPT)            \
     if (grad_bf16)              \
         IT_CE(NPT, uint16_t);   \

@@ -14,6 +14,11 @@ attention kernels), and the row/elementwise ops of kernels_train.hip. The MI355X
   * gate and up are one dual-B GEMM with the SwiGLU epilogue; the down projection's dX GEMM runs
     the SwiGLU backward in its epilogue, writing the [T, 2F] gate|up gradient read by one NN and
     one TN GEMM (dL/dh is never stored);
+  * cross entropy writes the [T, V] logit gradient once and the two LM-head backward GEMMs read it;
+    with xent_operand=True it writes only the loss and each row's {max, 1/sum}, and both GEMMs
+    rebuild the gradient from the logits on their way into LDS (IT_EPI_XENT_A): 268 MB less at
+    TINY, but slower (the rebuild runs once per output tile column: cross entropy 111 -> 43 us,
+    the dX and dW GEMMs 298 -> 418 and 287 -> 342 us on MI355X), so it is off by default;
   * weight-gradient GEMMs run on the side stream beside the data-gradient chain; every buffer they
     read is per layer, so the main stream never overwrites one before the side stream has read it;
   * the gradient norm, the clip factor and the learning rate stay on the device (Lion reads them
@@ -45,7 +50,8 @@ class TrainStep:
     def __init__(self, shape: ModelShape = TINY, ctx: Optional[Context] = None, seed: int = 1234,
                  lr: float = 3e-4, beta1: float = 0.9, beta2: float = 0.99, weight_decay: float = 0.1,
                  max_grad_norm: float = 1.0, eps: float = 1e-5, rope_base: float = 10000.0,
-                 overlap_weight_grads: bool = True, fused_attention: Optional[bool] = None):
+                 overlap_weight_grads: bool = True, fused_attention: Optional[bool] = None,
+                 xent_operand: bool = False):
         s = shape
         if s.heads * s.head_dim != s.hidden:
             raise ValueError("heads * head_dim must equal hidden")
@@ -58,6 +64,7 @@ class TrainStep:
         self.max_grad_norm = float(max_grad_norm)
         self.overlap = overlap_weight_grads
         self.fused = (s.head_dim == 64) if fused_attention is None else bool(fused_attention)
+        self.xent_operand = bool(xent_operand)
         self.graph = None
         self._seed = seed
         T, H, F, V, L = s.tokens, s.hidden, s.ffn, s.vocab, s.layers
@@ -123,7 +130,10 @@ class TrainStep:
         self.Z = empty([T, H])   # FFN output, likewise
         self.Hf = empty([T, H])
         self.logits = empty([T, V])
-        self.dlogits = empty([T, V])
+        if self.xent_operand:
+            self.ce_stats = empty([T, 2])   # per token {max, 1 / sum exp(x - max)}
+        else:
+            self.dlogits = empty([T, V])
         if self.fused:
             self.lse = [empty([bh, s.seq]) for _ in range(L)]
         else:
@@ -292,12 +302,23 @@ class TrainStep:
         for l in range(L):
             self._forward_layer(l)
         self._gemm("lm_head", self.Hf, self.E, self.logits, False, True, T, V, H)
-        check(self.lib.it_cross_entropy_fused(self.h, 0, T, V, C.c_void_p(self.logits.ptr),
-                                              C.c_void_p(self.targets.ptr), C.c_void_p(self.losses.ptr),
-                                              C.c_void_p(self.dlogits.ptr), C.c_void_p(self.loss.ptr)),
-              "cross_entropy_fused")
-        self._dw("lm_head.dW", self.dlogits, self.Hf, self.dE, True, False, V, H, T)
-        self._gemm("lm_head.dX", self.dlogits, self.E, self.dHf, False, False, T, H, V)
+        if self.xent_operand:
+            check(self.lib.it_cross_entropy_stats(self.h, T, V, C.c_void_p(self.logits.ptr),
+                                                  C.c_void_p(self.targets.ptr), C.c_void_p(self.losses.ptr),
+                                                  C.c_void_p(self.ce_stats.ptr), C.c_void_p(self.loss.ptr)),
+                  "cross_entropy_stats")
+            xent = _lib.Epilogue(flags=_lib.IT_EPI_XENT_A, xent_stats=self.ce_stats.ptr,
+                                 xent_targets=self.targets.ptr,
+                                 xent_scale=float(np.float32(1.0) / np.float32(T)))
+            self._dw("lm_head.dW", self.logits, self.Hf, self.dE, True, False, V, H, T, epi=xent)
+            self._gemm("lm_head.dX", self.logits, self.E, self.dHf, False, False, T, H, V, epi=xent)
+        else:
+            check(self.lib.it_cross_entropy_fused(self.h, 0, T, V, C.c_void_p(self.logits.ptr),
+                                                  C.c_void_p(self.targets.ptr), C.c_void_p(self.losses.ptr),
+                                                  C.c_void_p(self.dlogits.ptr), C.c_void_p(self.loss.ptr)),
+                  "cross_entropy_fused")
+            self._dw("lm_head.dW", self.dlogits, self.Hf, self.dE, True, False, V, H, T)
+            self._gemm("lm_head.dX", self.dlogits, self.E, self.dHf, False, False, T, H, V)
         self._norm_bwd(self.dHf, self.xin[L], self.final_norm, None, self.g_out[L], self.d_final_norm)
         for l in reversed(range(L)):
             self._backward_layer(l)

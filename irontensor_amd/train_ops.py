@@ -219,6 +219,28 @@ def cross_entropy_fused(logits: Tensor, targets) -> Tuple[float, Tensor, Tensor]
     return float(mean.as_f32_slice()[0]), losses, grad
 
 
+def cross_entropy_stats(logits: Tensor, targets) -> Tuple[float, Tensor, Tensor]:
+    """The loss half of cross_entropy_fused (src/ops/backward/loss.rs:248) -> (mean loss, losses [rows],
+    stats [rows, 2] = {max, 1 / sum exp(x - max)}); a GEMM with the IT_EPI_XENT_A operand rebuilds the
+    gradient from the stats."""
+    _need_f32(logits, "cross_entropy_stats")
+    shape = logits.shape()
+    if len(shape) != 2:
+        raise Panic("logits must be 2D")
+    rows, vocab = shape
+    t_host, t = _ids(targets, vocab, "vocab_size")
+    if t_host.size != rows:
+        raise Panic(f"assertion `left == right` failed\n  left: {t_host.size}\n right: {rows}")
+    losses = Tensor.zeros([rows], _P.FP32, logits.ctx)
+    stats = Tensor.zeros([rows, 2], _P.FP32, logits.ctx)
+    if rows == 0:
+        return 0.0, losses, stats
+    mean = Tensor.empty([1], _P.FP32, logits.ctx)
+    check(logits.ctx.lib.it_cross_entropy_stats(logits.ctx.handle, rows, vocab, _vp(logits), _vp(t), _vp(losses),
+                                                _vp(stats), _vp(mean)), "cross_entropy_stats")
+    return float(mean.as_f32_slice()[0]), losses, stats
+
+
 def swiglu_backward(grad_output: Tensor, gate: Tensor, up: Tensor) -> Tuple[Tensor, Tensor]:
     """swiglu_backward (src/ops/backward/elementwise.rs:149) -> (grad_gate, grad_up)."""
     _need_f32(grad_output, "swiglu_backward")

@@ -287,3 +287,58 @@ def test_gemm_swiglu_backward_epilogue(it, oracle, prec, T, F, K):
     if prec == "f32":
         gg, gu = Tops.swiglu_backward(_t(it, dh), GA, UP)
         assert normwise_rel(o[:, :F], gg.numpy()) <= 1e-6 and normwise_rel(o[:, F:], gu.numpy()) <= 1e-6
+
+
+# ---------------------------------------------------------------- cross-entropy operand
+
+@pytest.mark.parametrize("rows,vocab", [(64, 16384), (33, 1001), (4096, 16384)])
+def test_cross_entropy_stats(it, rows, vocab):
+    """Loss half of the fused cross entropy: the same losses as cross_entropy_fused, and per row
+    {max, 1/sum exp(x - max)} against float64."""
+    from irontensor_amd import train_ops as T
+    print(f"[case] cross_entropy_stats rows={rows} vocab={vocab}", flush=True)
+    logits = synth.normal(40, (rows, vocab), std=3.0)
+    t = synth.tokens(41, rows, vocab)
+    mean, losses, stats = T.cross_entropy_stats(_t(it, logits), t)
+    fmean, flosses, _ = T.cross_entropy_fused(_t(it, logits), t)
+    assert np.array_equal(losses.numpy(), flosses.numpy()) and mean == fmean
+    st = stats.numpy()
+    x = logits.astype(np.float64)
+    mx = x.max(1)
+    assert np.array_equal(st[:, 0], mx.astype(np.float32))
+    inv = 1.0 / np.exp(x - mx[:, None]).sum(1)
+    assert np.max(np.abs(st[:, 1] / inv - 1.0)) <= 1e-5
+
+
+@pytest.mark.parametrize("T,V,H", [(4096, 16384, 256), (300, 1001, 72), (256, 4096, 64), (96, 4100, 256)])
+def test_gemm_cross_entropy_operand(it, oracle, T, V, H):
+    """dL/dh = G.E and dL/dE = G^T.h with G rebuilt from the logits inside the GEMMs (IT_EPI_XENT_A)
+    == the same GEMMs over the gradient cross_entropy_fused stores (ragged shapes take the masked
+    and bounds-checked loads; the TINY shape's dh takes split-K)."""
+    from irontensor_amd import _lib, train_ops as Tops
+    print(f"[case] cross-entropy operand T={T} V={V} H={H}", flush=True)
+    logits = synth.normal(42, (T, V), std=3.0)
+    h, e = synth.normal(43, (T, H)), synth.normal(44, (V, H), std=0.02)
+    t = synth.tokens(45, T, V)
+    Lg, Hh, E = _t(it, logits), _t(it, h), _t(it, e)
+    _, _, stats = Tops.cross_entropy_stats(Lg, t)
+    _, _, grad = Tops.cross_entropy_fused(Lg, t)
+    tg = Tops.upload_ids(t, V)
+    epi = _lib.Epilogue(flags=_lib.IT_EPI_XENT_A, xent_stats=stats.ptr, xent_targets=tg.ptr,
+                        xent_scale=float(np.float32(1.0) / np.float32(T)))
+    dh, de = it.Tensor.empty([T, H]), it.Tensor.empty([V, H])
+    _epi_gemm(it, Lg, E, dh, False, False, T, H, V, epi)
+    _epi_gemm(it, Lg, Hh, de, True, False, V, H, T, epi)
+    ref_dh = it.gemm(grad, E).numpy()
+    ref_de = it.gemm(grad, Hh, trans_a=True).numpy()
+    # the rebuilt gradient is the stored one element for element, so the products agree to rounding
+    assert normwise_rel(dh.numpy(), ref_dh) <= 1e-6
+    assert normwise_rel(de.numpy(), ref_de) <= 1e-6
+    # and against float64: (softmax - onehot) / T contracted with E and h
+    x = logits.astype(np.float64)
+    p = np.exp(x - x.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    p[np.arange(T), t] -= 1.0
+    p /= T
+    assert normwise_rel(dh.numpy(), p @ e.astype(np.float64)) <= FP32_TOL
+    assert normwise_rel(de.numpy(), p.T @ h.astype(np.float64)) <= FP32_TOL

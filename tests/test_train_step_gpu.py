@@ -30,12 +30,14 @@ def _oracle_params(st):
     return p
 
 
-@pytest.mark.parametrize("fused", [True, False])
-def test_train_step_matches_oracle(it, oracle, fused):
+@pytest.mark.parametrize("fused,xent", [(True, False), (False, False), (True, True)])
+def test_train_step_matches_oracle(it, oracle, fused, xent):
+    """xent: the LM-head backward GEMMs rebuild the cross-entropy gradient from the logits
+    (IT_EPI_XENT_A) instead of reading a stored gradient."""
     from irontensor_amd.train import TrainStep
     from oracle import train_step as ts
-    print(f"[case] train step vs oracle, fused attention={fused}", flush=True)
-    st = TrainStep(SMALL64, seed=5, fused_attention=fused, max_grad_norm=1e-3)
+    print(f"[case] train step vs oracle, fused attention={fused}, xent operand={xent}", flush=True)
+    st = TrainStep(SMALL64, seed=5, fused_attention=fused, max_grad_norm=1e-3, xent_operand=xent)
     p0 = _oracle_params(st)
     m0 = [m.numpy() for m in st.momentum]
     st.step()
@@ -71,6 +73,21 @@ def test_train_step_graph_and_side_stream_bit_identical(it):
         assert np.array_equal(x.numpy(), y.numpy())
     assert a.loss_value() == b.loss_value()
     b.close()
+
+
+def test_train_step_xent_operand_matches_stored_gradient(it):
+    """TINY: one step with the cross-entropy operand against one with the stored gradient: the
+    same loss, and gradients equal to rounding (the rebuilt gradient is the stored one element for
+    element; only the GEMMs' summation order can differ)."""
+    from irontensor_amd.train import TrainStep
+    a = TrainStep(TINY, seed=13, xent_operand=False)
+    b = TrainStep(TINY, seed=13, xent_operand=True)
+    a.step()
+    b.step()
+    it.Context.global_().sync()
+    assert a.loss_value() == b.loss_value()
+    for i, (x, y) in enumerate(zip(a.grads, b.grads)):
+        assert normwise_rel(y.numpy(), x.numpy()) <= 1e-6, i
 
 
 def test_train_step_tiny_loss_decreases(it):
