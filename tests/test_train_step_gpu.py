@@ -75,6 +75,23 @@ def test_train_step_graph_and_side_stream_bit_identical(it):
     b.close()
 
 
+def test_train_step_dw_fork_modes_bit_identical(it):
+    """Weight gradients forked to the side stream per GEMM or per layer: the same parameters after
+    two graph-replayed steps, bit for bit."""
+    from irontensor_amd.train import TrainStep
+    a = TrainStep(TINY, seed=17, dw_fork="gemm")
+    b = TrainStep(TINY, seed=17, dw_fork="layer")
+    for st in (a, b):
+        st.step()
+        st.capture()
+        st.step()
+    it.Context.global_().sync()
+    for x, y in zip(a.params, b.params):
+        assert np.array_equal(x.numpy(), y.numpy())
+    a.close()
+    b.close()
+
+
 def test_train_step_xent_operand_matches_stored_gradient(it):
     """TINY: one step with the cross-entropy operand against one with the stored gradient: the
     same loss, and gradients equal to rounding (the rebuilt gradient is the stored one element for
