@@ -248,6 +248,17 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 
+// Work order across the whole grid. Workgroups are dispatched in linear order (x fastest), and a
+// causal row or column block's cost grows with its index, so block (x, y) takes tile
+// lin / heads-count of head lin % heads-count, lin = y * gridDim.x + x: the first wave of
+// workgroups holds the costliest tile of every head, the last the cheapest (longest-first
+// scheduling), and a head's tiles stay on one XCD when the head count is a multiple of 8.
+__device__ __forceinline__ void grid_tile(int &tile, int64_t &bh) {
+    const int64_t lin = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    tile = (int)(lin / gridDim.y);
+    bh = lin % gridDim.y;
+}
+
 // ------------------------------------------------------------------ forward
 
 template <typename T>
@@ -258,10 +269,11 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
-    // Causal blocks are enumerated heaviest first (the last query block sees every key block), so
-    // the long blocks start early and the short ones fill the tail.
-    const int qb = p.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    const int64_t bh = blockIdx.y;
+    // Causal: the last query block sees every key block, so query blocks go out last-first.
+    int qb;
+    int64_t bh;
+    grid_tile(qb, bh);
+    if (p.causal) qb = (int)gridDim.x - 1 - qb;
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
     const T *Q = (const T *)p.Q + hq.base(bh);
@@ -397,8 +409,10 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
-    const int kb = blockIdx.x;
-    const int64_t bh = blockIdx.y;
+    // Causal: key block 0 is seen by every query block, so key blocks go out first-first.
+    int kb;
+    int64_t bh;
+    grid_tile(kb, bh);
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         hd{p.heads, p.do_bs, p.do_hs, p.do_rs};
     const T *Q = (const T *)p.Q + hq.base(bh);
@@ -506,8 +520,10 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 15, g = lane >> 4;
-    const int qb = p.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;  // heaviest first
-    const int64_t bh = blockIdx.y;
+    int qb;
+    int64_t bh;
+    grid_tile(qb, bh);
+    if (p.causal) qb = (int)gridDim.x - 1 - qb;  // heaviest first
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         hd{p.heads, p.do_bs, p.do_hs, p.do_rs};
     const T *Q = (const T *)p.Q + hq.base(bh);
