@@ -85,9 +85,13 @@ class GemmStep:
         bh = s.batch * s.heads
         self._seed = seed
         self._pooled = pooled_data  # timing-only inputs from synth.pooled_normal (fast at MED sizes)
-        # Weight gradients run on the context's side stream, beside the data-gradient chain; each
-        # is issued right after the main-stream op that produces its upstream gradient.
+        # Weight gradients run on the context's side stream, beside the data-gradient chain. A
+        # layer's four are issued together, once its last upstream gradient (dQKV) is ready: each
+        # fork of the side stream idles the GPU for microseconds inside the graph, so one fork per
+        # layer beats one per GEMM (dw_fork = "gemm").
         self.overlap = overlap_weight_grads
+        self.dw_fork = "layer"
+        self._dw_queue = None
 
         def w(shape_, std=0.02):
             return self._tensor(shape_, std)
@@ -183,12 +187,27 @@ class GemmStep:
                 self._calls[key] = (name, A, B, Cout, ta, tb, M, N, K, alpha, epi, a_off, lda)
 
     def _dw(self, *args, **kw):
-        """A weight-gradient GEMM, on the side stream when overlapping."""
+        """A weight-gradient GEMM, on the side stream when overlapping (queued for the layer's
+        single fork when one is open)."""
         if not self.overlap:
             return self._gemm(*args, **kw)
+        if self._dw_queue is not None:
+            self._dw_queue.append((args, kw))
+            return None
         check(self.lib.it_side_begin(self.ctx.handle), "side stream")
         try:
             self._gemm(*args, **kw)
+        finally:
+            check(self.lib.it_side_end(self.ctx.handle), "side stream")
+
+    def _dw_flush(self):
+        q, self._dw_queue = self._dw_queue, None
+        if not q:
+            return
+        check(self.lib.it_side_begin(self.ctx.handle), "side stream")
+        try:
+            for args, kw in q:
+                self._gemm(*args, **kw)
         finally:
             check(self.lib.it_side_end(self.ctx.handle), "side stream")
 
@@ -233,6 +252,8 @@ class GemmStep:
     def backward_layer(self, l: int) -> None:
         s, P = self.s, self.prec
         T, H, F = s.tokens, s.hidden, s.ffn
+        if self.overlap and self.dw_fork == "layer":
+            self._dw_queue = []
         # down: dHh = dZ.Wd (NN), dWd = dZ^T.Hh (TN)
         self._dw("down.dW", self.dZ, self.Hh[l], self.dWd[l], True, False, H, F, T)
         self._gemm("down.dX", self.dZ, self.Wd[l], self.dHh, False, False, T, F, H)
@@ -269,6 +290,7 @@ class GemmStep:
         # projection backward reads the seeded BF16 gradient stand-in instead.
         dqkv = self.dQKV_layers[l] if P is Precision.FP32 else self._dqkv_bf16()
         self._dw("qkv.dW", dqkv, self.X[l], self.dWqkv[l], True, False, 3 * H, H, T)
+        self._dw_flush()
         self._gemm("qkv.dX", dqkv, self.Wqkv[l], self.dX, False, False, T, H, 3 * H)
 
     def _dqkv_bf16(self) -> Tensor:
