@@ -306,6 +306,26 @@ def test_bf16_decode_shapes(it, oracle, m, ta, tb):
     assert frob_rel(c.numpy(), oracle.gemm_f32(a, b, bool(ta), bool(tb))) <= BF16_FROB_TOL
 
 
+@pytest.mark.parametrize("m,k,n,ta", [(2, 1000, 1000, 0), (7, 4160, 512, 1), (13, 64, 8, 0), (16, 333, 2056, 1),
+                                      (1, 70, 1032, 1)])
+def test_bf16_decode_kn_ragged(it, m, k, n, ta):
+    """Decode-sized products with the weight stored [K, N] (the tiled GEMM's bounds-checked and
+    split-K paths): ragged M, K and column counts, exact small integers against a float64 product,
+    plus alpha, beta and bias in the epilogue."""
+    _log(f"[decode kn] m={m} k={k} n={n} ta={ta}")
+    a = synth.small_ints(210 + m, (k, m) if ta else (m, k), -8, 8)
+    b = synth.small_ints(211, (k, n), -8, 8)
+    A, B = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    c = it.gemm(A, B, trans_a=bool(ta), out_precision=it.Precision.FP32)
+    exact = op(a, ta).astype(np.float64) @ b.astype(np.float64)
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    bias = synth.small_ints(212, (n,), -4, 4)
+    c0 = synth.small_ints(213, (m, n), -4, 4)
+    out = it.Tensor.from_f32_slice(c0, [m, n])
+    it.gemm(A, B, trans_a=bool(ta), alpha=2.0, beta=1.0, out=out, bias=it.Tensor.from_f32_slice(bias, [n]))
+    assert np.array_equal(out.numpy(), (2.0 * exact + c0 + bias).astype(np.float32))
+
+
 @pytest.mark.parametrize("n", [2048, 4096])
 def test_bf16_square_freivalds(it, n):
     """Full-size property check (the oracle would take minutes): (A.B).x == A.(B.x) in float64 for
