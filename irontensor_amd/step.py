@@ -301,6 +301,7 @@ class GemmStep:
     def enqueue(self) -> None:
         """Issues one full step on the context stream."""
         s = self.s
+        self._dw_queue = None  # a step interrupted mid-layer leaves no queued weight gradients
         if self._record:
             self.launches = []
         for l in range(s.layers):

@@ -321,6 +321,7 @@ class TrainStep:
     def enqueue(self) -> None:
         """Issues one full step (forward, loss, backward, clip, Lion) on the context's stream."""
         s = self.s
+        self._dw_queue = None  # a step interrupted mid-layer leaves no queued weight gradients
         T, H, V, L = s.tokens, s.hidden, s.vocab, s.layers
         check(self.lib.it_embedding_forward(self.h, 0, 0, T, H, V, C.c_void_p(self.emb.ptr), C.c_void_p(self.ids.ptr),
                                             C.c_void_p(self.xin[0].ptr)), "embedding")
