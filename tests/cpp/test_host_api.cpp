@@ -279,6 +279,12 @@ static void gpu_tests() {
         std::vector<float> g = ce.grad.as_f32_slice();
         CHECK(std::fabs(g[0] - (0.1f - 1.f) / 4.f) < 1e-7f && std::fabs(g[1] - 0.1f / 4.f) < 1e-7f);
     });
+    run("cross_entropy_stats_uniform_logits", [] {  // the loss half of src/ops/backward/loss.rs:248
+        CrossEntropyStats ce = cross_entropy_stats(Tensor::zeros({4, 10}, Precision::FP32), {0, 3, 9, 5});
+        CHECK(std::fabs(ce.loss - std::log(10.f)) < 1e-6f);
+        std::vector<float> st = ce.stats.as_f32_slice();  // {max, 1/sum} per row: {0, 1/10}
+        for (int r = 0; r < 4; ++r) CHECK(st[2 * r] == 0.f && std::fabs(st[2 * r + 1] - 0.1f) < 1e-7f);
+    });
     run("swiglu_backward_at_zero", [] {  // src/shaders/backward/elementwise.metal:101-126
         Tensor one = Tensor::from_f32_slice({1, 1}, {1, 2}), zero = Tensor::zeros({1, 2}, Precision::FP32);
         auto [gg, gu] = swiglu_backward(one, zero, one);
