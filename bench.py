@@ -172,7 +172,8 @@ def extra_med_step(it, timer, steps=5, warmup=2) -> dict:
 
 
 def bf16_square(it, timer, sizes) -> dict:
-    """BF16 n^3 GEMMs, NN/NT/TN, BF16 out, `iters` timed launches each ((n, iters) in `sizes`)."""
+    """BF16 n^3 GEMMs, NN/NT/TN, BF16 out: the median of three batches of `iters` timed launches
+    each ((n, iters) in `sizes`); single batches moved by up to 15% with the clock."""
     from irontensor_amd import synth
     P = it.Precision
     out = {}
@@ -181,7 +182,7 @@ def bf16_square(it, timer, sizes) -> dict:
         b = _bf16(it, synth.pooled_normal(4, (n, n)))
         c = it.Tensor.empty([n, n], P.BF16)
         for lay, (ta, tb) in (("NN", (False, False)), ("NT", (False, True)), ("TN", (True, False))):
-            ms = time_gemm(it, timer, a, b, c, ta, tb, iters, warm=2)
+            ms = sorted(time_gemm(it, timer, a, b, c, ta, tb, iters, warm=2) for _ in range(3))[1]
             tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
             out[f"bf16_square_{n}_{lay}"] = {"ms": round(ms, 4), "tflops": round(tf, 1),
                                              "frac_bf16_peak": round(tf / PEAK_TFLOPS["bf16"], 4)}
@@ -195,7 +196,7 @@ def extra_sweep(it, timer) -> dict:
     Operands from synth.pooled_normal (N(0,1))."""
     from irontensor_amd import synth
     P = it.Precision
-    out = bf16_square(it, timer, ((1024, 50), (2048, 20), (4096, 10), (8192, 4), (16384, 2)))
+    out = bf16_square(it, timer, ((1024, 50), (2048, 30), (4096, 20), (8192, 8), (16384, 3)))
     k, n = 4096, 11008
     w_nk = _bf16(it, synth.pooled_normal(5, (n, k)))
     w_kn = _bf16(it, synth.pooled_normal(7, (k, n)))
