@@ -372,32 +372,6 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
 
 // ------------------------------------------------------------------ backward
 
-// dlt[bh][q] = sum_d dO[q][d] * O[q][d] (= rowsum(dP * P)). 16 lanes per row, 4 columns each,
-// so a row's dO and O are read as contiguous 16-lane segments.
-template <typename T>
-__global__ __launch_bounds__(NTH) void flash_dlt(const FlashArgs p) {
-    const int64_t row = (int64_t)blockIdx.x * (NTH / 16) + threadIdx.x / 16;
-    const int part = threadIdx.x % 16;
-    float acc = 0.f;
-    if (row < p.bh * p.sq) {
-        const int64_t bh = row / p.sq, q = row % p.sq;
-        const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
-        const T *dO = (const T *)p.dO + hd.base(bh) + q * p.do_rs + part * 4;
-        const f32x4 o = *(const f32x4 *)(p.O + ho.base(bh) + q * p.o_rs + part * 4);
-        f32x4 g;
-        if constexpr (sizeof(T) == 4) {
-            g = *(const f32x4 *)dO;
-        } else {
-            const u32x2 h = *(const u32x2 *)dO;
-            g = f32x4{__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u),
-                      __uint_as_float(h[1] << 16), __uint_as_float(h[1] & 0xffff0000u)};
-        }
-        acc = g[0] * o[0] + g[1] * o[1] + g[2] * o[2] + g[3] * o[3];
-    }
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 16);
-    if (part == 0 && row < p.bh * p.sq) p.dlt[row] = acc;
-}
 
 // dK, dV for 64 keys per block (16 per wave), looping over the query blocks that see them.
 template <typename T>
@@ -533,7 +507,7 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
     const int q = qb * TR + wave * 16 + ql;
     const bool qok = q < p.sq;
     const float c2 = p.scale * LOG2E;
-    const float lse2 = qok ? p.lse[bh * p.sq + q] * LOG2E : 0.f, dl = qok ? p.dlt[bh * p.sq + q] : 0.f;
+    const float lse2 = qok ? p.lse[bh * p.sq + q] * LOG2E : 0.f;
 
     u32x4 qf[NC], of[NC];
 #pragma unroll
@@ -542,6 +516,36 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
         const u32x4 b = ld16(dO + (qok ? (int64_t)q * p.do_rs + c * FE<T>::KC + g * FE<T>::VEC : 0));
         qf[c] = qok ? a : u32x4{0u, 0u, 0u, 0u};
         of[c] = qok ? b : u32x4{0u, 0u, 0u, 0u};
+    }
+    // dlt[q] = rowsum(dO * O) for this block's queries, from the dO fragments just loaded: the 4
+    // lanes of a query hold 16 of its 64 columns each. Written for the dK/dV kernel, which runs
+    // after this one.
+    float dl = 0.f;
+    {
+        const Head ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
+        const float *Orow = p.O + ho.base(bh) + (qok ? (int64_t)q * p.o_rs : 0);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            constexpr int V = FE<T>::VEC;
+            const int d0 = c * FE<T>::KC + g * V;
+#pragma unroll
+            for (int h = 0; h < V; h += 4) {
+                const f32x4 o = qok ? *(const f32x4 *)(Orow + d0 + h) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float gv;
+                    if constexpr (sizeof(T) == 4)
+                        gv = __uint_as_float(of[c][h + e]);
+                    else
+                        gv = __uint_as_float((h + e) & 1 ? of[c][(h + e) >> 1] & 0xffff0000u
+                                                         : of[c][(h + e) >> 1] << 16);
+                    dl += gv * o[e];
+                }
+            }
+        }
+        dl += __shfl_xor(dl, 16, 64);
+        dl += __shfl_xor(dl, 32, 64);
+        if (g == 0 && qok) p.dlt[bh * p.sq + q] = dl;
     }
     f32x4 dq[4];
 #pragma unroll
@@ -632,19 +636,13 @@ it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16) {
     const int64_t qblocks = (p.sq + TR - 1) / TR, kblocks = (p.skv + TR - 1) / TR;
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || p.bh > 65535)
         return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
-    const int64_t rows = p.bh * p.sq;
-    const int64_t dlt_rows_per_block = NTH / 16;
-    if ((rows + dlt_rows_per_block - 1) / dlt_rows_per_block > 0x7fffffff)
-        return fail(IT_ERR_DIMS, "flash attention backward: too many rows");
-    const unsigned dlt_blocks = (unsigned)((rows + dlt_rows_per_block - 1) / dlt_rows_per_block);
+    // dQ first: it also computes dlt = rowsum(dO * O) for its queries, which dK/dV reads.
     if (bf16) {
-        hipLaunchKernelGGL(flash_dlt<uint16_t>, dim3(dlt_blocks), dim3(NTH), 0, s, p);
-        hipLaunchKernelGGL(flash_bwd_dkdv<uint16_t>, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
         hipLaunchKernelGGL(flash_bwd_dq<uint16_t>, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+        hipLaunchKernelGGL(flash_bwd_dkdv<uint16_t>, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
     } else {
-        hipLaunchKernelGGL(flash_dlt<float>, dim3(dlt_blocks), dim3(NTH), 0, s, p);
-        hipLaunchKernelGGL(flash_bwd_dkdv<float>, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
         hipLaunchKernelGGL(flash_bwd_dq<float>, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+        hipLaunchKernelGGL(flash_bwd_dkdv<float>, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
     }
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
