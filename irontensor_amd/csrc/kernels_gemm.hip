@@ -1084,8 +1084,10 @@ struct Plan {
 
 // Picks the tile shape and split-K factor with a cost model fitted to MI355X timings of these
 // kernels (every tile / split choice on the TINY and medium step shapes, the square sweep and the
-// decode shapes: over those 42 shapes its picks take 0.5% longer in total than the fastest
-// measured plans):
+// decode shapes, each timed with cold caches as inside a training step; the BF16 efficiencies
+// were refitted after the kernel changes since the first fit: over the 32 BF16 shapes its picks
+// take 0.2% longer in total than the fastest measured plans, against 3.3% with the first fit,
+// whose 128x128 efficiency kept the medium step's long-K data gradients off the 256x256 tile):
 //   * a CU runs up to `occ` blocks at once, sharing its MFMA rate (a lone block where two could
 //     run reaches 90% of the tile's efficiency);
 //   * each round of blocks pays a fixed prologue/epilogue cost;
@@ -1101,7 +1103,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
         double eff;
     };
     const Cand f32c[] = {{128, 2, 0.70}, {64, 4, 0.60}};
-    const Cand b16c[] = {{256, 1, 0.50}, {128, 2, 0.40}, {64, 4, 0.15}};
+    const Cand b16c[] = {{256, 1, 0.40}, {128, 2, 0.20}, {64, 4, 0.20}};
     const Cand *cands = bf16 ? b16c : f32c;
     const int ncand = bf16 ? 3 : 2;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
