@@ -1083,11 +1083,15 @@ struct Plan {
 };
 
 // Picks the tile shape and split-K factor with a cost model fitted to MI355X timings of these
-// kernels (every tile / split choice on the TINY and medium step shapes, the square sweep and the
-// decode shapes, each timed with cold caches as inside a training step; the BF16 efficiencies
-// were refitted after the kernel changes since the first fit: over the 32 BF16 shapes its picks
-// take 0.2% longer in total than the fastest measured plans, against 3.3% with the first fit,
-// whose 128x128 efficiency kept the medium step's long-K data gradients off the 256x256 tile):
+// kernels: every tile / split choice on the TINY and medium step shapes, the square sweep and the
+// decode shapes. The efficiencies were refitted after later kernel changes, on sweeps that time
+// each plan with caches flushed (and, for FP32, also warm):
+//   * BF16, 32 shapes: the picks take 0.2% longer in total than the fastest measured plans
+//     (3.3% with the first fit, whose 128x128 efficiency kept the medium step's long-K data
+//     gradients off the 256x256 tile);
+//   * FP32, the 14 plain TINY step shapes: 0.6% longer (2.9% with the first fit, which put the
+//     LM-head GEMMs on 128x128 tiles where the prefetching 64x64 tile is now 5-8% faster).
+// The model:
 //   * a CU runs up to `occ` blocks at once, sharing its MFMA rate (a lone block where two could
 //     run reaches 90% of the tile's efficiency);
 //   * each round of blocks pays a fixed prologue/epilogue cost;
@@ -1102,7 +1106,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
         int b, occ;
         double eff;
     };
-    const Cand f32c[] = {{128, 2, 0.70}, {64, 4, 0.60}};
+    const Cand f32c[] = {{128, 2, 0.50}, {64, 4, 0.60}};
     const Cand b16c[] = {{256, 1, 0.40}, {128, 2, 0.20}, {64, 4, 0.20}};
     const Cand *cands = bf16 ? b16c : f32c;
     const int ncand = bf16 ? 3 : 2;
