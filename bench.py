@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import hashlib
 import json
 import os
 import re
@@ -89,6 +90,12 @@ def _bf16(it, x):
     return it.Tensor.from_f32_as_bf16(x, list(x.shape))
 
 
+def _dev(it, seed, shape, std=1.0, prec=None):
+    """Seeded N(0, std^2) device tensor (synth.normal's stream, drawn on the GPU)."""
+    from irontensor_amd import synth
+    return synth.normal_tensor(seed, list(shape), std=std, precision=prec if prec is not None else it.Precision.FP32)
+
+
 def extra_config1(it, timer) -> dict:
     """Config 1: the FP32 QKV projection Y = X.W^T, X [4096,256], W [768,256]."""
     from irontensor_amd import synth
@@ -108,7 +115,7 @@ def extra_attention(it, timer) -> dict:
     useful fraction is (S+1)/(2S)."""
     from irontensor_amd import synth
     b, h, s, d = 16, 8, 1024, 64
-    q, k, v, do = (_bf16(it, synth.pooled_normal(30 + i, (b, h, s, d))) for i in range(4))
+    q, k, v, do = (_dev(it, 30 + i, (b, h, s, d), prec=it.Precision.BF16) for i in range(4))
     ctx = it.Context.global_()
 
     def run(fn, iters):
@@ -140,10 +147,12 @@ def extra_attention(it, timer) -> dict:
 def extra_med_step(it, timer, steps=5, warmup=2) -> dict:
     """Config 4: the medium BF16 step (12 layers, hidden 1024, 16 x 64 heads, SwiGLU FFN 2816 with
     the fused bias + SwiGLU epilogue, vocab 32768, batch 8 x seq 1024): every contraction forward
-    and backward, graph-replayed like the TINY step. Inputs from synth.pooled_normal."""
+    and backward, graph-replayed like the TINY step (weight gradients on the second stream), and the
+    same step on one stream. Per-kernel times come from one eager step on one stream (with the
+    weight gradients overlapped, a kernel's events would also time its neighbour)."""
     from irontensor_amd.step import MEDIUM, GemmStep
     ctx = it.Context.global_()
-    step = GemmStep(MEDIUM, it.Precision.BF16, ctx, pooled_data=True, ffn_bias=True)
+    step = GemmStep(MEDIUM, it.Precision.BF16, ctx, ffn_bias=True)
     try:
         step.enqueue()
         ctx.sync()
@@ -156,6 +165,17 @@ def extra_med_step(it, timer, steps=5, warmup=2) -> dict:
         for _ in range(steps):
             step.replay()
         ms = timer.stop_ms() / steps
+        step.close()
+        step.overlap = False
+        step.enqueue()
+        step.capture()
+        for _ in range(warmup):
+            step.replay()
+        ctx.sync()
+        timer.start()
+        for _ in range(steps):
+            step.replay()
+        ms1 = timer.stop_ms() / steps
         ctx.lib.it_profiler_reset(ctx.handle)
         ctx.lib.it_profiler_enable(ctx.handle, 1)
         step.enqueue()
@@ -163,11 +183,13 @@ def extra_med_step(it, timer, steps=5, warmup=2) -> dict:
         ctx.lib.it_profiler_enable(ctx.handle, 0)
     finally:
         step.close()
-    top = sorted(stats.items(), key=lambda kv: -kv[1]["total_ms"])[:6]
+    top = sorted(stats.items(), key=lambda kv: -kv[1]["total_ms"])[:10]
     tf = flops / (ms * 1e-3) / 1e12
     return {"config4_bf16_medium_step": {
-        "ms_per_step": round(ms, 3), "gflop_per_step": round(flops / 1e9, 1), "tflops": round(tf, 1),
+        "ms_per_step": round(ms, 3), "ms_per_step_single_stream": round(ms1, 3),
+        "gflop_per_step": round(flops / 1e9, 1), "tflops": round(tf, 1),
         "frac_bf16_peak": round(tf / PEAK_TFLOPS["bf16"], 4), "steps": steps,
+        "eager_single_stream_kernel_ms": round(sum(v["total_ms"] for v in stats.values()), 3),
         "top_kernels": [{"key": k, "ms_per_step": round(v["total_ms"], 3), "calls": v["calls"]} for k, v in top]}}
 
 
@@ -178,8 +200,8 @@ def bf16_square(it, timer, sizes) -> dict:
     P = it.Precision
     out = {}
     for n, iters in sizes:
-        a = _bf16(it, synth.pooled_normal(3, (n, n)))
-        b = _bf16(it, synth.pooled_normal(4, (n, n)))
+        a = _dev(it, 3, (n, n), prec=P.BF16)
+        b = _dev(it, 4, (n, n), prec=P.BF16)
         c = it.Tensor.empty([n, n], P.BF16)
         for lay, (ta, tb) in (("NN", (False, False)), ("NT", (False, True)), ("TN", (True, False))):
             ms = sorted(time_gemm(it, timer, a, b, c, ta, tb, iters, warm=2) for _ in range(3))[1]
@@ -192,25 +214,38 @@ def bf16_square(it, timer, sizes) -> dict:
 
 def extra_sweep(it, timer) -> dict:
     """Config 5: BF16 square GEMMs n^3, n in {1024 .. 16384}, NN/NT/TN, BF16 out; and the decode
-    shapes M in {1, 4, 16}, K 4096, N 11008 (HBM-bound: weight bytes / time against 8 TB/s).
-    Operands from synth.pooled_normal (N(0,1))."""
-    from irontensor_amd import synth
+    shapes M in {1, 4, 16}, K 4096, N 11008 (HBM-bound: bytes / time against 8 TB/s). The decode
+    timing rotates over DECODE_COPIES distinct weight copies (8 x 90 MB, more than the 256 MB
+    Infinity Cache), so every call streams its weight from HBM. Operands are seeded N(0,1)."""
     P = it.Precision
     out = bf16_square(it, timer, ((1024, 50), (2048, 30), (4096, 20), (8192, 8), (16384, 3)))
     k, n = 4096, 11008
-    w_nk = _bf16(it, synth.pooled_normal(5, (n, k)))
-    w_kn = _bf16(it, synth.pooled_normal(7, (k, n)))
+    copies = DECODE_COPIES
+    w_nk = [_dev(it, 500 + c, (n, k), prec=P.BF16) for c in range(copies)]
+    w_kn = [_dev(it, 600 + c, (k, n), prec=P.BF16) for c in range(copies)]
+    ctx = it.Context.global_()
     for m in (1, 4, 16):
-        xa = _bf16(it, synth.pooled_normal(6, (m, k)))
-        xt = _bf16(it, synth.pooled_normal(8, (k, m)))
+        xa = _dev(it, 6, (m, k), prec=P.BF16)
+        xt = _dev(it, 8, (k, m), prec=P.BF16)
         yo = it.Tensor.empty([m, n], P.BF16)
-        for lay, (A, B, ta, tb) in (("NT", (xa, w_nk, False, True)), ("NN", (xa, w_kn, False, False)),
-                                    ("TN", (xt, w_kn, True, False))):
-            ms = time_gemm(it, timer, A, B, yo, ta, tb, 20)
+        for lay, (A, Bs, ta, tb) in (("NT", (xa, w_nk, False, True)), ("NN", (xa, w_kn, False, False)),
+                                     ("TN", (xt, w_kn, True, False))):
+            for c in range(copies):
+                it.gemm(A, Bs[c], trans_a=ta, trans_b=tb, out=yo)
+            ctx.sync()
+            iters = 4 * copies
+            timer.start()
+            for i in range(iters):
+                it.gemm(A, Bs[i % copies], trans_a=ta, trans_b=tb, out=yo)
+            ms = timer.stop_ms() / iters
             gbs = (n * k * 2 + m * k * 2 + m * n * 2) / (ms * 1e-3) / 1e9
             out[f"bf16_decode_m{m}_k4096_n11008_{lay}"] = {"ms": round(ms, 5), "GBps": round(gbs, 1),
-                                                           "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+                                                           "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                                                           "weights": f"{copies} copies rotated (cold in L2/MALL)"}
     return out
+
+
+DECODE_COPIES = 8
 
 
 def train_step_figures(it, timer, steps: int, warmup: int) -> dict:
@@ -278,9 +313,9 @@ def extra_fusions(it, timer, iters: int = 10) -> dict:
             fn()
         return timer.stop_ms() / iters
 
-    x = it.Tensor.from_f32_slice(synth.pooled_normal(1, (4096, 256)), [4096, 256])
-    g = it.Tensor.from_f32_slice(1 + synth.pooled_normal(2, (256,), std=0.1), [256])
-    w = it.Tensor.from_f32_slice(synth.pooled_normal(3, (768, 256), std=0.02), [768, 256])
+    x = _dev(it, 1, (4096, 256))
+    g = it.Tensor.from_f32_slice(1 + synth.normal(2, (256,), std=0.1), [256])
+    w = _dev(it, 3, (768, 256), std=0.02)
     xn = it.Tensor.empty([4096, 256])
     y = it.Tensor.empty([4096, 768])
     lib, h = it.Context.global_().lib, it.Context.global_().handle
@@ -295,8 +330,8 @@ def extra_fusions(it, timer, iters: int = 10) -> dict:
                                     C.c_void_p(y.ptr))
 
     out["rmsnorm_qkv_4096x256x768"] = {"unfused_us": round(run(unfused) * 1e3, 2), "fused_us": round(run(fused) * 1e3, 2)}
-    hs = it.Tensor.from_f32_slice(synth.pooled_normal(4, (4096, 256)), [4096, 256])
-    E = it.Tensor.from_f32_slice(synth.pooled_normal(5, (16384, 256), std=0.02), [16384, 256])
+    hs = _dev(it, 4, (4096, 256))
+    E = _dev(it, 5, (16384, 256), std=0.02)
     tg = synth.tokens(6, 4096, 16384)
     t32 = it.Tensor.from_f32_slice(tg.astype(np.int32).view(np.float32), [4096])
     tu = T.upload_ids(tg, 16384)
@@ -356,7 +391,7 @@ def kernel_only(it, ctx, step, iters: int) -> int:
     the order of the groups with their profiler keys, to map dispatches back to keys."""
     from irontensor_amd import synth
     n = 1 << 26  # 256 MiB read, 128 MiB written
-    src = it.Tensor.from_f32_slice(synth.pooled_normal(9, (n,)), [n])
+    src = _dev(it, 9, (n,))
     dst = it.Tensor.empty([n], it.Precision.BF16)
     ctx.sync()
     for _ in range(5):
@@ -395,7 +430,7 @@ def cpu_baseline(step) -> dict:
     s = step.s
     H, F, V, L = s.hidden, s.ffn, s.vocab, s.layers
     thr = oracle.default_threads()
-    w = lambda sh, seed: synth.pooled_normal(seed, sh, std=0.02)  # noqa: E731
+    w = lambda sh, seed: synth.normal(seed, sh, std=0.02)  # noqa: E731
     acc = {"t": 0.0, "flops": 0.0}
 
     def timed(fn, flops_of):
@@ -436,7 +471,7 @@ def cpu_baseline(step) -> dict:
     finally:
         ots.gemm_f32, ots.attention_fwd_bhsd, ots.attention_bwd_bhsd = saved
     # config 1 on one thread, for the per-core figure
-    a = lambda sh, seed: synth.pooled_normal(seed, sh)  # noqa: E731
+    a = lambda sh, seed: synth.normal(seed, sh)  # noqa: E731
     x1, w1 = a((4096, 256), 30), w((768, 256), 31)
     t1 = time.perf_counter()
     oracle.gemm_f32(x1, w1, False, True, threads=1)
@@ -484,6 +519,10 @@ def main() -> int:
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: launched with WORLD_SIZE > 1; this build runs on one GPU only", file=sys.stderr)
         return 2
+    if os.environ.get("IRONTENSOR_LIB"):
+        print("bench.py: IRONTENSOR_LIB is set; the bench times only the in-tree library "
+              "(irontensor_amd/libirontensor_hip.so), unset it", file=sys.stderr)
+        return 2
 
     import irontensor_amd as it
     from irontensor_amd.step import TINY, GemmStep
@@ -494,6 +533,11 @@ def main() -> int:
     ctx = it.Context.global_()
     info = ctx.info()
     log(f"[bench] device {info}")
+    from irontensor_amd import _lib
+    lib_path = Path(_lib.LIB_PATH).resolve()
+    lib_info = {"path": str(lib_path.relative_to(ROOT)) if lib_path.is_relative_to(ROOT) else str(lib_path),
+                "sha256": hashlib.sha256(lib_path.read_bytes()).hexdigest()}
+    log(f"[bench] library {lib_info}")
     if args.bf16_square:
         print(json.dumps(bf16_square(it, Timer(ctx), ((4096, args.steps), (8192, max(1, args.steps // 4))))),
               flush=True)
@@ -533,6 +577,20 @@ def main() -> int:
         step.enqueue()
     stats = profiler_stats(ctx)
     ctx.lib.it_profiler_enable(ctx.handle, 0)
+    # The same step on one stream (no side-stream fork), graph-replayed and timed the same way.
+    step.close()
+    step.enqueue()
+    step.capture()
+    for _ in range(args.warmup):
+        step.replay()
+    ctx.sync()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        step.replay()
+    ctx.sync()
+    ms_single = (time.perf_counter() - t1) * 1e3 / args.steps
+    log(f"[bench] single-stream replay {ms_single:.3f} ms/step")
+    step.close()
     step.overlap = True
     gemm_ms = sum(v["total_ms"] for v in stats.values()) / args.steps
     dom_key, dom = max(stats.items(), key=lambda kv: kv[1]["total_ms"])
@@ -543,6 +601,11 @@ def main() -> int:
         f"{achieved:.1f} TFLOP/s; sum of GEMM launches {gemm_ms:.3f} ms/step")
     per_kernel = sorted(((k, v["total_ms"] / v["calls"], v["calls"] // args.steps) for k, v in stats.items()),
                         key=lambda x: -x[1] * x[2])
+    s_ = TINY
+    attn_unit = 2.0 * s_.batch * s_.heads * s_.seq * s_.seq * s_.head_dim
+    attn_flops = sum(x.flops for x in step.launches if x.name.startswith("attn."))
+    attn_skipped = attn_flops * (1.0 - (s_.seq + 1) / (2.0 * s_.seq))
+    assert abs(attn_flops - 7 * s_.layers * attn_unit) < 1.0
 
     result = {
         "metric": "GEMM TFLOP/s (% of MFMA peak) + TINY train-step ms, FP32 and BF16, 1 GPU",
@@ -563,7 +626,14 @@ def main() -> int:
             "tied_lm_head": False, "batch": 16, "seq": 256, "gflop_per_step": round(total_flops / 1e9, 2),
             "gemm_launches": len(step.launches), "execution": "hipGraph replay; weight gradients on a second stream",
             "frac_fp32_mfma_peak": round(total_flops / (ms_per_step * 1e-3) / 1e12 / PEAK_TFLOPS["f32"], 4),
+            "ms_per_step_single_stream": round(ms_single, 4),
+            "tflops_single_stream": round(total_flops / (ms_single * 1e-3) / 1e12, 3),
+            "attention_gflop_dense_equiv": round(attn_flops / 1e9, 2),
+            "attention_gflop_skipped_by_causal": round(attn_skipped / 1e9, 2),
+            "note_flops": "value counts attention as dense-equivalent GEMMs (BASELINE's definition); the causal "
+                          "kernels skip the masked half, attention_gflop_skipped_by_causal of gflop_per_step",
         },
+        "library": lib_info,
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 2),

@@ -554,6 +554,30 @@ inline AttentionGrads flash_attention_backward(const Tensor &grad_output, const 
     return g;
 }
 
+// transpose_3d_gpu (src/ops/attention.rs:395-449; re-exported at src/ops/mod.rs:21):
+// [batch, m, n] -> [batch, n, m], FP32, into a new tensor; panics on a size mismatch.
+inline Tensor transpose_3d_gpu(const Tensor &t, size_t batch, size_t m, size_t n) {
+    detail::require(t.numel() == batch * m * n, "assertion `left == right` failed: Tensor size mismatch");
+    detail::require(t.is_f32(), "transpose_3d_gpu requires an FP32 tensor");
+    Tensor out = Tensor::empty({batch, n, m}, Precision::FP32);
+    check(it_transpose_3d(Context::global().handle(), (const float *)t.data(), (float *)out.data(), (int64_t)batch,
+                          (int64_t)m, (int64_t)n),
+          "transpose_3d_gpu");
+    return out;
+}
+
+// causal_mask_3d_gpu (src/ops/attention.rs:455-517; re-exported at src/ops/mod.rs:21):
+// [batch, seq, seq] with columns > row set to -inf, into a new FP32 tensor.
+inline Tensor causal_mask_3d_gpu(const Tensor &t, size_t batch, size_t seq_len) {
+    detail::require(t.numel() == batch * seq_len * seq_len, "assertion `left == right` failed: Tensor size mismatch");
+    detail::require(t.is_f32(), "causal_mask_3d_gpu requires an FP32 tensor");
+    Tensor out = Tensor::empty({batch, seq_len, seq_len}, Precision::FP32);
+    check(it_causal_mask_3d(Context::global().handle(), (const float *)t.data(), (float *)out.data(),
+                            (int64_t)batch, (int64_t)seq_len),
+          "causal_mask_3d_gpu");
+    return out;
+}
+
 // ------------------------------------------------------------------ training-step ops
 
 namespace detail {

@@ -197,6 +197,22 @@ it_status it_softmax_backward(it_context *ctx, const float *dY, const void *Y, i
                               int64_t cols, int causal);
 
 /*
+ * transpose_3d_gpu (src/ops/attention.rs:395-449, kernel transpose_3d_f32 in
+ * src/shaders/attention.metal:163-182; re-exported at src/ops/mod.rs:21):
+ * out[b, j, i] = in[b, i, j] for in [batch, m, n] f32 and out [batch, n, m] f32. The output must
+ * not overlap the input (the reference always writes a new tensor). HBM-bound: 8 bytes per element.
+ */
+it_status it_transpose_3d(it_context *ctx, const float *in, float *out, int64_t batch, int64_t m, int64_t n);
+
+/*
+ * causal_mask_3d_gpu (src/ops/attention.rs:455-517, kernel causal_mask_3d_f32 in
+ * src/shaders/attention.metal:186-207; re-exported at src/ops/mod.rs:21):
+ * out[b, r, c] = c > r ? -inf : in[b, r, c] over [batch, seq, seq] f32. in == out masks in place;
+ * masked elements are written without being read.
+ */
+it_status it_causal_mask_3d(it_context *ctx, const float *in, float *out, int64_t batch, int64_t seq);
+
+/*
  * Per-head operand layout: element (bh, s, d) lives at
  *   (bh / heads) * batch_stride + (bh % heads) * head_stride + s * row_stride + d.
  * [B,H,S,D] contiguous: heads = 1, batch_stride = S*D, head_stride = 0, row_stride = D.
@@ -384,6 +400,21 @@ it_status it_grad_norm_clip(it_context *ctx, int count, const float *const *grad
 it_status it_lion_step(it_context *ctx, int count, float *const *weights, float *const *momentum,
                        const float *const *grads, const int64_t *sizes, float lr, float beta1, float beta2,
                        float weight_decay, const float *grad_scale, const float *lr_dev);
+
+/* ---------------------------------------------------------------- synthetic inputs */
+
+/*
+ * Seeded N(0, std_dev^2) fill for benchmark and test inputs; no counterpart in the reference,
+ * whose benchmark draws unseeded host values (src/bin/benchmark.rs:110-113). dst[e] (e < n) is
+ * normal number offset + e of `seed`: SplitMix64 output i = mix(seed + (i + 1) * 0x9E3779B97F4A7C15),
+ * uniforms from its top 53 bits, (bits + 0.5) / 2^53, and Box-Muller over consecutive uniform
+ * pairs (number 2p = r cos(2 pi u_{2p+1}), 2p + 1 = r sin(2 pi u_{2p+1}), r = sqrt(-2 ln u_{2p}))
+ * in float64, times std_dev, rounded to FP32 (then RNE to BF16 for IT_BF16). The same stream as
+ * the Python package's synth.normal; results agree bit for bit except where the device's float64
+ * log/sin/cos and the host libm's differ by an ulp and that ulp moves the FP32 rounding.
+ */
+it_status it_fill_normal(it_context *ctx, it_dtype dtype, uint64_t seed, int64_t offset, int64_t n,
+                         double std_dev, void *dst);
 
 /* ---------------------------------------------------------------- graphs (launch-bound loops) */
 

@@ -11,6 +11,7 @@ from .ops import (Linear, attention, attention_backward_recompute, attention_for
                   flash_attention_forward_bhsd, gemm, linear, linear_backward, linear_forward, matmul,
                   matmul_backward, matmul_backward_a, matmul_backward_b, matmul_bf16,
                   matmul_bf16_batched, matmul_custom, matmul_mps, matmul_mps_nt, matmul_mps_tn,
-                  matmul_tn, softmax_backward, softmax_rows, swiglu_up, to_bf16_gpu, to_f32_gpu)
+                  matmul_tn, softmax_backward, softmax_rows, swiglu_up, to_bf16_gpu, to_f32_gpu,
+                  causal_mask_3d_gpu, transpose_3d_gpu)
 
 __all__ = [name for name in dir() if not name.startswith("_")]

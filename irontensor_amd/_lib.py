@@ -139,6 +139,9 @@ _SIGNATURES = {
                                         c_void_p]),
     "it_fused_linear_cross_entropy": (c_int, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p,
                                               c_void_p, c_void_p, c_void_p, c_void_p, c_i64]),
+    "it_transpose_3d": (c_int, [c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64]),
+    "it_causal_mask_3d": (c_int, [c_void_p, c_void_p, c_void_p, c_i64, c_i64]),
+    "it_fill_normal": (c_int, [c_void_p, c_int, C.c_uint64, c_i64, c_i64, C.c_double, c_void_p]),
     "it_side_begin": (c_int, [c_void_p]),
     "it_side_end": (c_int, [c_void_p]),
     "it_side_join": (c_int, [c_void_p]),

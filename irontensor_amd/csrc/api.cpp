@@ -237,6 +237,40 @@ it_status it_softmax_backward(it_context *ctx, const float *dY, const void *Y, i
                                        dtype_dx == IT_BF16, batch, rows, cols, causal != 0);
 }
 
+it_status it_transpose_3d(it_context *ctx, const float *in, float *out, int64_t batch, int64_t m, int64_t n) {
+    if (!ctx) return fail(IT_ERR_NULL, "transpose_3d_gpu: ctx is NULL");
+    if (batch < 0 || m < 0 || n < 0) return fail(IT_ERR_INVALID, "transpose_3d_gpu: negative size");
+    if (batch == 0 || m == 0 || n == 0) return IT_OK;
+    if (!in || !out) return fail(IT_ERR_NULL, "transpose_3d_gpu: NULL buffer");
+    const uintptr_t bytes = (uintptr_t)(batch * m * n) * sizeof(float);
+    if ((uintptr_t)in < (uintptr_t)out + bytes && (uintptr_t)out < (uintptr_t)in + bytes)
+        return fail(IT_ERR_INVALID, "transpose_3d_gpu: output overlaps the input");
+    return it::launch_transpose_3d(ctx->stream, in, out, batch, m, n);
+}
+
+it_status it_causal_mask_3d(it_context *ctx, const float *in, float *out, int64_t batch, int64_t seq) {
+    if (!ctx) return fail(IT_ERR_NULL, "causal_mask_3d_gpu: ctx is NULL");
+    if (batch < 0 || seq < 0) return fail(IT_ERR_INVALID, "causal_mask_3d_gpu: negative size");
+    if (batch == 0 || seq == 0) return IT_OK;
+    if (!in || !out) return fail(IT_ERR_NULL, "causal_mask_3d_gpu: NULL buffer");
+    const uintptr_t bytes = (uintptr_t)(batch * seq * seq) * sizeof(float);
+    if (in != out && (uintptr_t)in < (uintptr_t)out + bytes && (uintptr_t)out < (uintptr_t)in + bytes)
+        return fail(IT_ERR_INVALID, "causal_mask_3d_gpu: output partially overlaps the input");
+    return it::launch_causal_mask_3d(ctx->stream, in, out, batch, seq);
+}
+
+it_status it_fill_normal(it_context *ctx, it_dtype dtype, uint64_t seed, int64_t offset, int64_t n,
+                         double std_dev, void *dst) {
+    if (!ctx) return fail(IT_ERR_NULL, "fill_normal: ctx is NULL");
+    if (dtype != IT_F32 && dtype != IT_BF16)
+        return fail(IT_ERR_PRECISION, std::string("fill_normal: precision mismatch, expected FP32 or BF16, got ") +
+                                          dtype_name(dtype));
+    if (n < 0 || offset < 0) return fail(IT_ERR_INVALID, "fill_normal: negative size or offset");
+    if (n == 0) return IT_OK;
+    if (!dst) return fail(IT_ERR_NULL, "fill_normal: dst is NULL");
+    return it::launch_fill_normal(ctx->stream, dtype == IT_BF16, dst, seed, offset, n, std_dev);
+}
+
 }  // extern "C"
 
 // ------------------------------------------------------------------ attention compositions

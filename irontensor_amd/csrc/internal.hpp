@@ -210,6 +210,10 @@ it_status launch_softmax_backward(hipStream_t s, const float *dY, const void *Y,
                                   void *dX, int dx_bf16, int64_t batch, int64_t rows,
                                   int64_t cols, int causal);
 it_status launch_splitk_reduce(hipStream_t s, const GemmArgs &a);
+it_status launch_transpose_3d(hipStream_t s, const float *in, float *out, int64_t batch, int64_t m, int64_t n);
+it_status launch_causal_mask_3d(hipStream_t s, const float *in, float *out, int64_t batch, int64_t seq);
+it_status launch_fill_normal(hipStream_t s, bool bf16, void *dst, uint64_t seed, int64_t offset, int64_t n,
+                             double std_dev);
 
 // Training-step ops around the contractions (kernels_train.hip).
 it_status launch_rmsnorm_forward(hipStream_t s, bool y_bf16, int64_t rows, int64_t dim, float eps, const float *x,

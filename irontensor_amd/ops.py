@@ -512,6 +512,32 @@ def flash_attention_backward(grad_output: Tensor, q: Tensor, k: Tensor, v: Tenso
     return dq, dk, dv
 
 
+def transpose_3d_gpu(t: Tensor, batch: int, m: int, n: int) -> Tensor:
+    """src/ops/attention.rs:395-449 (re-exported at src/ops/mod.rs:21): [batch, m, n] -> [batch, n, m],
+    FP32, into a new tensor; panics unless t holds batch*m*n elements. The reference reads any
+    tensor's buffer as f32; this mirror panics on a BF16 tensor instead of misreading it."""
+    if t.numel() != batch * m * n:
+        raise Panic("assertion `left == right` failed: Tensor size mismatch")
+    if t.precision() is not _P.FP32:
+        raise Panic("transpose_3d_gpu requires an FP32 tensor")
+    out = Tensor.empty([batch, n, m], _P.FP32, t.ctx)
+    check(t.ctx.lib.it_transpose_3d(t.ctx.handle, _vp(t), _vp(out), batch, m, n), "transpose_3d_gpu")
+    return out
+
+
+def causal_mask_3d_gpu(t: Tensor, batch: int, seq_len: int) -> Tensor:
+    """src/ops/attention.rs:455-517 (re-exported at src/ops/mod.rs:21): [batch, seq, seq] scores with
+    every column > row set to -inf, into a new FP32 tensor; panics unless t holds batch*seq*seq
+    elements (a BF16 tensor panics too, where the reference would misread it as f32)."""
+    if t.numel() != batch * seq_len * seq_len:
+        raise Panic("assertion `left == right` failed: Tensor size mismatch")
+    if t.precision() is not _P.FP32:
+        raise Panic("causal_mask_3d_gpu requires an FP32 tensor")
+    out = Tensor.empty([batch, seq_len, seq_len], _P.FP32, t.ctx)
+    check(t.ctx.lib.it_causal_mask_3d(t.ctx.handle, _vp(t), _vp(out), batch, seq_len), "causal_mask_3d_gpu")
+    return out
+
+
 def softmax_rows(s: Tensor, causal: bool = False, out_precision: Precision = _P.FP32) -> Tensor:
     """Row softmax of an FP32 [.., rows, cols] tensor (src/shaders/softmax.metal), causal-aware."""
     shape = s.shape()

@@ -20,7 +20,8 @@ src/train/forward.rs:79-212, src/train/backward.rs:21-177) for every contraction
 The elementwise work between contractions (RMSNorm, RoPE, residual adds, SwiGLU backward, cross
 entropy) is outside this path: each layer's normalised inputs and each upstream gradient are
 seeded N(0,1) buffers standing where those ops would write, so every GEMM runs at its real shape
-on realistic data. Weights are N(0, 0.02).
+on realistic data. Weights are N(0, 0.02); all seeded inputs are drawn on the device
+(synth.normal_tensor), the same stream as the host's synth.normal.
 """
 from __future__ import annotations
 
@@ -72,7 +73,7 @@ class GemmStep:
 
     def __init__(self, shape: ModelShape, precision: Precision = Precision.FP32,
                  ctx: Optional[Context] = None, seed: int = 1234, fused_attention: Optional[bool] = None,
-                 pooled_data: bool = False, ffn_bias: bool = False, overlap_weight_grads: bool = True):
+                 ffn_bias: bool = False, overlap_weight_grads: bool = True):
         if shape.heads * shape.head_dim != shape.hidden:
             raise ValueError("heads * head_dim must equal hidden")
         self.s = shape
@@ -84,7 +85,10 @@ class GemmStep:
         T, H, F, V, L = s.tokens, s.hidden, s.ffn, s.vocab, s.layers
         bh = s.batch * s.heads
         self._seed = seed
-        self._pooled = pooled_data  # timing-only inputs from synth.pooled_normal (fast at MED sizes)
+        # Seeded inputs are generated on the device (synth.normal_tensor: the stream of synth.normal);
+        # seed_of maps each one's device address to (seed, std), so a check can regenerate any
+        # element on the host (synth.normal_at).
+        self.seed_of: dict = {}
         # Weight gradients run on the context's side stream, beside the data-gradient chain. A
         # layer's four are issued together, once its last upstream gradient (dQKV) is ready: each
         # fork of the side stream idles the GPU for microseconds inside the graph, so one fork per
@@ -161,11 +165,9 @@ class GemmStep:
     # ---------------------------------------------------------------- helpers
     def _tensor(self, shape_, std) -> Tensor:
         self._seed += 1
-        gen = synth.pooled_normal if self._pooled else synth.normal
-        data = gen(self._seed, shape_, std=std)
-        if self.prec is Precision.BF16:
-            return Tensor.from_f32_as_bf16(data, shape_, self.ctx)
-        return Tensor.from_f32_slice(data, shape_, self.ctx)
+        t = synth.normal_tensor(self._seed, shape_, std=std, precision=self.prec, ctx=self.ctx)
+        self.seed_of[t.ptr] = (self._seed, std)
+        return t
 
     def _gemm(self, name, A: Tensor, B: Tensor, Cout: Tensor, ta: bool, tb: bool, M, N, K,
               alpha=1.0, epi: Optional[_lib.Epilogue] = None, a_off=0, lda=None):

@@ -48,6 +48,44 @@ def normal(seed: int, shape, std: float = 1.0, mean: float = 0.0) -> np.ndarray:
     return vals.astype(np.float32).reshape(shape)
 
 
+def normal_at(seed: int, index, std: float = 1.0) -> np.ndarray:
+    """float32 values of normal(seed, ...) at the given flat element indices (any shape), without
+    generating the rest: element i is the cos (i even) or sin (i odd) half of pair i // 2."""
+    idx = np.asarray(index, dtype=np.int64)
+    pair = idx // 2
+    u1 = _uniform_at(seed, 2 * pair)
+    u2 = _uniform_at(seed, 2 * pair + 1)
+    r = np.sqrt(-2.0 * np.log(u1))
+    ang = 2.0 * np.pi * u2
+    z = np.where(idx % 2 == 0, r * np.cos(ang), r * np.sin(ang))
+    return (z * std + 0.0).astype(np.float32)
+
+
+def _uniform_at(seed: int, i) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed & 0xFFFFFFFFFFFFFFFF) + (np.asarray(i, dtype=np.uint64) + np.uint64(1)) * _GOLDEN
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        z = z ^ (z >> np.uint64(31))
+    return ((z >> np.uint64(11)).astype(np.float64) + 0.5) * (1.0 / 9007199254740992.0)
+
+
+def normal_tensor(seed: int, shape, std: float = 1.0, precision=None, ctx=None):
+    """Device tensor holding normal(seed, shape, std) (BF16: rounded to nearest even), generated on
+    the GPU by it_fill_normal -- the same stream as `normal`, for sizes the host makes slowly."""
+    from ctypes import c_void_p
+
+    from .errors import check
+    from .tensor import Precision, Tensor
+
+    prec = Precision.FP32 if precision is None else Precision(precision)
+    t = Tensor.empty(list(shape), prec, ctx)
+    if t.numel():
+        check(t.ctx.lib.it_fill_normal(t.ctx.handle, int(prec), seed & 0xFFFFFFFFFFFFFFFF, 0, t.numel(),
+                                       float(std), c_void_p(t.ptr)), "fill_normal")
+    return t
+
+
 def tokens(seed: int, n: int, vocab: int) -> np.ndarray:
     """n token ids uniform over [0, vocab) (uint32), by multiply-shift of the 64-bit outputs."""
     bits = splitmix64(seed, n) >> np.uint64(32)

@@ -52,6 +52,8 @@ def load() -> C.CDLL:
     lib.ref_attention_fwd_bhsd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, C.c_float, i, i]
     lib.ref_attention_bwd_bhsd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, C.c_float, i, i]
     lib.ref_default_threads.restype = i
+    lib.ref_transpose_3d.argtypes = [vp, vp, i64, i64, i64]
+    lib.ref_causal_mask_3d.argtypes = [vp, vp, i64, i64]
     f = C.c_float
     lib.ref_rmsnorm_forward.argtypes = [vp, vp, vp, i64, i64, f]
     lib.ref_rmsnorm_backward.argtypes = [vp, vp, vp, vp, vp, i64, i64, f]
@@ -207,6 +209,24 @@ def attention_bwd_bhsd(d_o, q, k, v, scale: float, causal: bool, threads=None):
     load().ref_attention_bwd_bhsd(_p(d_o), _p(q), _p(k), _p(v), _p(dq), _p(dk), _p(dv), bh, s, d,
                                   float(scale), int(causal), threads or default_threads())
     return dq, dk, dv
+
+
+def transpose_3d(x, batch: int, m: int, n: int) -> np.ndarray:
+    """[batch, m, n] -> [batch, n, m] (transpose_3d_f32, src/shaders/attention.metal:163-182)."""
+    x = _c(x, np.float32)
+    assert x.size == batch * m * n
+    out = np.empty((batch, n, m), np.float32)
+    load().ref_transpose_3d(_p(x), _p(out), batch, m, n)
+    return out
+
+
+def causal_mask_3d(x, batch: int, seq: int) -> np.ndarray:
+    """columns > row set to -inf over [batch, seq, seq] (causal_mask_3d_f32, attention.metal:186-207)."""
+    x = _c(x, np.float32)
+    assert x.size == batch * seq * seq
+    out = np.empty((batch, seq, seq), np.float32)
+    load().ref_causal_mask_3d(_p(x), _p(out), batch, seq)
+    return out
 
 
 # ---------------------------------------------------------------- training-step ops (train_ref.c)

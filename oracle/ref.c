@@ -354,3 +354,22 @@ void ref_attention_bwd_bhsd(const float *dO, const float *q, const float *k, con
     free(dP);
     free(dS);
 }
+
+/* ------------------------------------------------------------------ attention helpers */
+
+void ref_transpose_3d(const float *in, float *out, int64_t batch, int64_t m, int64_t n) {
+    /* src/shaders/attention.metal:169-181: one output element per (b, j, i). */
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t j = 0; j < n; ++j)
+            for (int64_t i = 0; i < m; ++i) out[b * n * m + j * m + i] = in[b * m * n + i * n + j];
+}
+
+void ref_causal_mask_3d(const float *in, float *out, int64_t batch, int64_t seq) {
+    /* src/shaders/attention.metal:193-206 */
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t r = 0; r < seq; ++r)
+            for (int64_t c = 0; c < seq; ++c) {
+                const int64_t idx = b * seq * seq + r * seq + c;
+                out[idx] = c > r ? -INFINITY : in[idx];
+            }
+}

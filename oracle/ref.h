@@ -142,6 +142,17 @@ float ref_fused_linear_cross_entropy(const float *hidden, const float *weight, c
 void ref_fused_rmsnorm_linear(const float *x, const float *gamma, const float *w, float *out, int64_t rows,
                               int64_t hidden, int64_t out_features, float eps);
 
+/* transpose_3d_f32 (src/shaders/attention.metal:163-182, called by transpose_3d_gpu,
+ * src/ops/attention.rs:395-449): out[b][j][i] = in[b][i][j], in [batch][m][n].
+ * Pinned by: numpy swapaxes on random data, involution (two transposes give the input back). */
+void ref_transpose_3d(const float *in, float *out, int64_t batch, int64_t m, int64_t n);
+
+/* causal_mask_3d_f32 (src/shaders/attention.metal:186-207, called by causal_mask_3d_gpu,
+ * src/ops/attention.rs:455-517): out = col > row ? -inf : in over [batch][seq][seq].
+ * Pinned by: numpy triu mask; the softmax of a masked constant row is 1/(row+1) on the
+ * allowed columns (the causal prefix mean); a planted off-by-one (col >= row) is rejected. */
+void ref_causal_mask_3d(const float *in, float *out, int64_t batch, int64_t seq);
+
 #ifdef __cplusplus
 }
 #endif

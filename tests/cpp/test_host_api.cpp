@@ -222,6 +222,30 @@ static void gpu_tests() {
         for (const Tensor *r : {&g.dq, &g.dk, &g.dv})
             for (float f : r->as_f32_slice()) CHECK(f == 0.0f);
     });
+    run("transpose_3d_gpu", [] {  // src/ops/attention.rs:395-449, ragged tiles
+        const size_t b = 3, m = 70, n = 130;
+        std::vector<float> x(b * m * n);
+        for (size_t i = 0; i < x.size(); ++i) x[i] = (float)i;
+        auto t = transpose_3d_gpu(Tensor::from_f32_slice(x, {b, m, n}), b, m, n);
+        CHECK((t.shape() == std::vector<size_t>{b, n, m}));
+        auto y = t.as_f32_slice();
+        for (size_t z = 0; z < b; ++z)
+            for (size_t i = 0; i < m; ++i)
+                for (size_t j = 0; j < n; ++j) CHECK(y[(z * n + j) * m + i] == x[(z * m + i) * n + j]);
+        expect_throw<Panic>([&] { transpose_3d_gpu(Tensor::from_f32_slice(x, {b, m, n}), b, m, n + 1); });
+    });
+    run("causal_mask_3d_gpu", [] {  // src/ops/attention.rs:455-517
+        const size_t b = 2, s = 37;
+        std::vector<float> x(b * s * s);
+        for (size_t i = 0; i < x.size(); ++i) x[i] = (float)(i % 101) - 50.f;
+        auto y = causal_mask_3d_gpu(Tensor::from_f32_slice(x, {b, s, s}), b, s).as_f32_slice();
+        for (size_t z = 0; z < b; ++z)
+            for (size_t r = 0; r < s; ++r)
+                for (size_t c = 0; c < s; ++c) {
+                    const size_t i = (z * s + r) * s + c;
+                    CHECK(c > r ? (std::isinf(y[i]) && y[i] < 0) : y[i] == x[i]);
+                }
+    });
     run("typed_errors", [] {  // src/ops/mps_gemm.rs:45-108
         Tensor f = Tensor::zeros({2, 3}, Precision::FP32), g = Tensor::zeros({4, 5}, Precision::FP32);
         CHECK(expect_throw<InnerDimensionMismatch>([&] { matmul(f, g); }).find("A=[2, 3], B=[4, 5]") != std::string::npos);

@@ -33,3 +33,21 @@ def frob_rel(x, ref) -> float:
 
 def op(a, trans):
     return np.swapaxes(a, -1, -2) if trans else a
+
+
+# A BF16 output is the round-to-nearest-even of an FP32 sum, and RNE moves a value by at most half a
+# BF16 ulp, 2^-8 of its magnitude. Against the oracle's FP32 sum on the same operands, a BF16 output
+# may therefore differ by 2^-8 |ref| plus the summation-order difference of the FP32 sums, which is
+# held to the FP32 contract (FP32_TOL of the largest reference magnitude).
+BF16_HALF_ULP = 2.0 ** -8
+
+
+def bf16_out_excess(x, ref) -> float:
+    """max over elements of (|x - ref| - 2^-8 |ref|) / max|ref|: <= FP32_TOL when x is a BF16
+    rounding of an FP32 result that meets the FP32 contract against ref."""
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if not ref.size:
+        return 0.0
+    denom = np.max(np.abs(ref)) or 1.0
+    return float(np.max(np.abs(x - ref) - BF16_HALF_ULP * np.abs(ref)) / denom)

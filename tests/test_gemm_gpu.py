@@ -326,24 +326,62 @@ def test_bf16_decode_kn_ragged(it, m, k, n, ta):
     assert np.array_equal(out.numpy(), (2.0 * exact + c0 + bias).astype(np.float32))
 
 
-@pytest.mark.parametrize("n", [2048, 4096])
-def test_bf16_square_freivalds(it, n):
-    """Full-size property check (the oracle would take minutes): (A.B).x == A.(B.x) in float64 for
-    random x, on the BF16-rounded operands (Freivalds); error relative to |A|.(|B|.|x|)."""
-    _log(f"[freivalds] n={n}")
-    a = synth.normal(90, (n, n))
-    b = synth.normal(91, (n, n))
-    ta, tb = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
-    a64 = it.bf16_to_f32(ta.as_bf16_slice()).reshape(n, n).astype(np.float64)
-    b64 = it.bf16_to_f32(tb.as_bf16_slice()).reshape(n, n).astype(np.float64)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_bf16_square_1024_against_oracle(it, oracle, ta, tb):
+    """BASELINE config 5a at n = 1024 in the NN, NT and TN layouts, whole output against the oracle:
+    normwise 1e-5 against its FP32 sums of the same BF16 operands, relative Frobenius 1e-2 against
+    its f32 loop on the unrounded N(0,1) inputs."""
+    n = 1024
+    _log(f"[square 1024] ta={ta} tb={tb}")
+    a = synth.normal(95, (n, n))
+    b = synth.normal(96, (n, n))
+    a16, b16 = oracle.f32_to_bf16(a), oracle.f32_to_bf16(b)
+    c = it.gemm(it.Tensor.from_bf16_slice(a16, a.shape), it.Tensor.from_bf16_slice(b16, b.shape),
+                trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    assert normwise_rel(c, oracle.gemm_bf16(a16, b16, bool(ta), bool(tb))) <= FP32_TOL
+    assert frob_rel(c, oracle.gemm_f32(a, b, bool(ta), bool(tb))) <= BF16_FROB_TOL
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("n", [2048, 4096, 8192, 16384])
+def test_bf16_square_full_size(it, n, ta, tb):
+    """BASELINE config 5a at full size, NN / NT / TN (the oracle's loop would take minutes to hours):
+    * Freivalds: (op(A).op(B)).x == op(A).(op(B).x) in float64 for a random x, on the BF16 operands,
+      error relative to |op(A)|.(|op(B)|.|x|) below 1e-5;
+    * 64+ sampled full output rows against a float64 product of the same BF16 operands (normwise
+      1e-5) and of the unrounded seeded N(0,1) inputs regenerated on the host (Frobenius 1e-2).
+    The operands are drawn on the device (synth.normal_tensor, the stream of synth.normal)."""
+    from tests.stepcheck import sample_rows
+    _log(f"[square full] n={n} ta={ta} tb={tb}")
+    seed_a, seed_b = 90 + n, 91 + n
+    A = synth.normal_tensor(seed_a, (n, n), precision=it.Precision.BF16)
+    B = synth.normal_tensor(seed_b, (n, n), precision=it.Precision.BF16)
+    c = it.gemm(A, B, trans_a=bool(ta), trans_b=bool(tb)).numpy()
+    a64 = it.bf16_to_f32(A.as_bf16_slice()).reshape(n, n).astype(np.float64)
+    b64 = it.bf16_to_f32(B.as_bf16_slice()).reshape(n, n).astype(np.float64)
+    opa = a64.T if ta else a64
+    opb = b64.T if tb else b64
     x = synth.normal(92, (n,)).astype(np.float64)
-    for trans_b in (False, True):
-        c = it.gemm(ta, tb, trans_b=trans_b).numpy().astype(np.float64)
-        bb = b64.T if trans_b else b64
-        lhs = c @ x
-        rhs = a64 @ (bb @ x)
-        scale = np.abs(a64) @ (np.abs(bb) @ np.abs(x))
-        assert np.max(np.abs(lhs - rhs) / scale) < 1e-5, trans_b
+    lhs = c.astype(np.float64) @ x
+    rhs = opa @ (opb @ x)
+    scale = np.abs(opa) @ (np.abs(opb) @ np.abs(x))
+    fv = float(np.max(np.abs(lhs - rhs) / scale))
+    rows = sample_rows(n, 64, seed=n + 3 * ta + tb)
+    ref_same = opa[rows] @ opb
+    e_same = normwise_rel(c[rows], ref_same)
+    _log(f"[square full] n={n} ta={ta} tb={tb}: freivalds {fv:.2e}, rows same-operand {e_same:.2e}")
+    assert fv < 1e-5
+    assert e_same <= FP32_TOL
+    if n <= 8192:
+        # unrounded inputs (host generation of n^2 normals; 16384^2 would take most of a minute):
+        # element (i, j) of the stored matrix is normal number i * n + j of its seed
+        ia = (np.arange(n)[:, None] * n + rows[None, :]) if ta else (rows[:, None] * n + np.arange(n)[None, :])
+        a_rows = synth.normal_at(seed_a, ia).astype(np.float64)
+        a_rows = a_rows.T if ta else a_rows
+        b32 = synth.normal(seed_b, (n, n)).astype(np.float64)
+        e_frob = frob_rel(c[rows], a_rows @ (b32.T if tb else b32))
+        _log(f"[square full] n={n}: frob vs unrounded {e_frob:.2e}")
+        assert e_frob <= BF16_FROB_TOL
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])

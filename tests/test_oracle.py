@@ -351,3 +351,31 @@ def test_planted_mistakes_are_caught(oracle):
     assert np.max(np.abs(o_bad - o_good)) > 1e-3
     o_oracle, _ = oracle.attention_fwd_bhsd(q, kk, v, 0.5, True)
     assert np.max(np.abs(o_oracle - o_good)) < 1e-5
+
+
+# ------------------------------------------------------------------ attention helpers (transpose, mask)
+
+@pytest.mark.parametrize("batch,m,n", [(1, 1, 1), (2, 3, 5), (3, 70, 130), (4, 64, 64)])
+def test_transpose_3d_matches_numpy_and_is_an_involution(oracle, batch, m, n):
+    x = synth.normal(70 + m, (batch, m, n))
+    t = oracle.transpose_3d(x, batch, m, n)
+    assert np.array_equal(t, np.swapaxes(x, 1, 2))
+    assert np.array_equal(oracle.transpose_3d(t, batch, n, m), x)
+
+
+def test_causal_mask_3d_matches_triu_and_gives_prefix_means(oracle):
+    b, s = 3, 17
+    x = synth.normal(75, (b, s, s))
+    y = oracle.causal_mask_3d(x, b, s)
+    upper = np.triu(np.ones((s, s), bool), 1)
+    assert np.all(np.isneginf(y[:, upper]))
+    assert np.array_equal(y[:, ~upper], x[:, ~upper])
+    # a masked constant score row softmaxes to 1/(row+1) on the allowed columns, so P.V is the
+    # running mean of V's rows
+    p = oracle.softmax_rows(oracle.causal_mask_3d(np.zeros((1, s, s), np.float32), 1, s)[0])
+    v = synth.normal(76, (s, 4)).astype(np.float64)
+    means = np.cumsum(v, 0) / np.arange(1, s + 1)[:, None]
+    assert np.max(np.abs(p @ v - means)) < 1e-6
+    # a mask that also hides the diagonal (c >= r) is caught by the same checks
+    bad = np.where(np.triu(np.ones((s, s), bool), 0), -np.inf, x[0])
+    assert not np.array_equal(bad, y[0])

@@ -8,6 +8,7 @@ import pytest
 
 from irontensor_amd.step import TINY, GemmStep
 from tests.numerics import FP32_TOL, normwise_rel
+from tests.stepcheck import StepChecker
 
 pytestmark = pytest.mark.gpu
 
@@ -44,6 +45,16 @@ def test_step_layer0_against_oracle(it, oracle, step):
     got = _heads(step.dQKV.numpy(), s)
     for name, g, r in zip("QKV", got, refs):
         assert normwise_rel(g, r) <= FP32_TOL, name
+
+
+def test_step_lm_head_gemms_against_oracle(it, oracle, step):
+    """The three LM-head GEMMs at [4096,16384,256] (forward NT, dE TN, dHf NN) in the plans the
+    step uses, on 64+ sampled output rows against the oracle's FP32 loop (normwise 1e-5)."""
+    s = step.s
+    T, H, V = s.tokens, s.hidden, s.vocab
+    chk = StepChecker(it, oracle, step, rows=64, log=lambda m: print(m, flush=True))
+    for key in ((False, True, T, V, H), (True, False, V, H, T), (False, False, T, H, V)):
+        chk.check_call(key)
 
 
 def test_step_graph_replay_matches_eager(it, step):
