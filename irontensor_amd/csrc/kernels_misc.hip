@@ -218,10 +218,14 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(void *dst, uint64_t se
             const int64_t e = 2 * p + h - offset;
             if (e < 0 || e >= n) continue;
             const float v = (float)__dadd_rn(__dmul_rn(z[h], std_dev), 0.0);
-            if (BF16)
-                ((uint16_t *)dst)[e] = f32_to_bf16_rne(v);
-            else
+            if (BF16) {
+                // RNE from the FP32 bits (the values are finite): written on the bits so that the
+                // compiler cannot fold the two roundings into one float64 -> BF16 conversion.
+                const uint32_t b = __float_as_uint(v);
+                ((uint16_t *)dst)[e] = (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+            } else {
                 ((float *)dst)[e] = v;
+            }
         }
     }
 }
