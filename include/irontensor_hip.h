@@ -291,6 +291,29 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
                                       const void *K, const void *V, const float *O, const float *lse,
                                       float *dQ, float *dK, float *dV);
 
+/*
+ * it_flash_attention_backward without any device allocation. No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same arguments, kernels and results as it_flash_attention_backward, except:
+ *   - O and lse (the forward's outputs) are required, since the forward is not recomputed
+ *     (IT_ERR_NULL otherwise);
+ *   - its one workspace, rowsum(dO * O) per query row (4 bytes per row), lives in a static device
+ *     array of IT_NOALLOC_SCRATCH_BYTES (4 MiB) that each GPU the library runs on holds until the
+ *     process ends, so bh * seq may be at most 1048576 rows (IT_ERR_DIMS otherwise, before any
+ *     device work);
+ *   - every call on a GPU shares that GPU's array: calls that overlap on one GPU (other streams or
+ *     contexts) race. The array keeps the last call's values and needs no clearing: each call
+ *     writes every row before it reads it.
+ * Calls no hipMalloc, hipFree or other allocating routine, and no profiler hooks.
+ */
+#define IT_NOALLOC_SCRATCH_BYTES (4u << 20)
+it_status it_flash_attention_backward_noalloc(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
+                                              int64_t head_dim, float scale, int causal,
+                                              const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                              const it_attn_layout *o_layout, const void *dO, const void *Q,
+                                              const void *K, const void *V, const float *O, const float *lse,
+                                              float *dQ, float *dK, float *dV);
+
 /* ---------------------------------------------------------------- training-step ops
  *
  * The row and elementwise work between the contractions of one training step

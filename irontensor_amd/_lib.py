@@ -119,6 +119,11 @@ _SIGNATURES = {
                                             C.POINTER(AttnLayout), C.POINTER(AttnLayout),
                                             C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "it_flash_attention_backward_noalloc": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_float, c_int,
+                                                    C.POINTER(AttnLayout), C.POINTER(AttnLayout),
+                                                    C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
+                                                    c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                    c_void_p]),
     "it_rmsnorm_forward": (c_int, [c_void_p, c_int, c_i64, c_i64, c_float, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_void_p]),
     "it_rmsnorm_backward": (c_int, [c_void_p, c_i64, c_i64, c_float, c_void_p, c_void_p, c_void_p, c_void_p,

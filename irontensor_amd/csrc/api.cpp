@@ -560,6 +560,53 @@ it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh
     return st;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Validates a fused-backward call and fills its kernel arguments (everything but O, lse and dlt).
+// *empty is set when there is nothing to compute.
+it_status flash_bwd_args(const char *op, it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
+                         int64_t head_dim, float scale, int causal, const it_attn_layout *q_layout,
+                         const it_attn_layout *kv_layout, const it_attn_layout *o_layout, const void *dO,
+                         const void *Q, const void *K, const void *V, const float *O, const float *lse, float *dQ,
+                         float *dK, float *dV, AttnGeom *g, it::FlashArgs *f, bool *empty) {
+    *empty = false;
+    it_status st = check_attention(op, ctx, dtype, bh, seq, seq, head_dim, q_layout, kv_layout, o_layout, g);
+    if (st != IT_OK) return st;
+    if (head_dim != 64)
+        return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, head_dim must be 64, got " +
+                                     i64(head_dim));
+    if ((O == nullptr) != (lse == nullptr))
+        return fail(IT_ERR_INVALID, std::string(op) + ": pass both O and lse, or neither");
+    if (bh == 0 || seq == 0) {
+        *empty = true;
+        return IT_OK;
+    }
+    if (!dO || !Q || !K || !V || !dQ || !dK || !dV) return fail(IT_ERR_NULL, std::string(op) + ": NULL buffer");
+    *f = flash_args(*g, scale, causal);
+    f->Q = Q;
+    f->K = K;
+    f->V = V;
+    f->dO = dO;
+    f->dQ = dQ;
+    f->dK = dK;
+    f->dV = dV;
+    const int eb = dtype == IT_BF16 ? 2 : 4;
+    if (!it::flash_supported(*f, eb, true))
+        return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, operands must be 16-byte "
+                                                   "aligned with strides that are multiples of 16 bytes");
+    if (O && ((uintptr_t)O % 16 != 0 || g->o_lay.batch_stride % 4 || g->o_lay.head_stride % 4 ||
+              g->o_lay.row_stride % 4))
+        return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, O must be 16-byte aligned "
+                                                   "with strides that are multiples of 4");
+    return IT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
                                       int64_t head_dim, float scale, int causal,
                                       const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
@@ -567,33 +614,11 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
                                       const void *K, const void *V, const float *O, const float *lse,
                                       float *dQ, float *dK, float *dV) {
     AttnGeom g;
-    it_status st = check_attention("flash_attention_backward", ctx, dtype, bh, seq, seq, head_dim, q_layout,
-                                   kv_layout, o_layout, &g);
-    if (st != IT_OK) return st;
-    if (head_dim != 64)
-        return fail(IT_ERR_DIMS, "flash_attention_backward: unsupported dimensions, head_dim must be 64, got " +
-                                     i64(head_dim));
-    if ((O == nullptr) != (lse == nullptr))
-        return fail(IT_ERR_INVALID, "flash_attention_backward: pass both O and lse, or neither");
-    if (bh == 0 || seq == 0) return IT_OK;
-    if (!dO || !Q || !K || !V || !dQ || !dK || !dV)
-        return fail(IT_ERR_NULL, "flash_attention_backward: NULL buffer");
-    it::FlashArgs f = flash_args(g, scale, causal);
-    f.Q = Q;
-    f.K = K;
-    f.V = V;
-    f.dO = dO;
-    f.dQ = dQ;
-    f.dK = dK;
-    f.dV = dV;
-    const int eb = dtype == IT_BF16 ? 2 : 4;
-    if (!it::flash_supported(f, eb, true))
-        return fail(IT_ERR_DIMS, "flash_attention_backward: unsupported dimensions, operands must be 16-byte "
-                                 "aligned with strides that are multiples of 16 bytes");
-    if (O && ((uintptr_t)O % 16 != 0 || g.o_lay.batch_stride % 4 || g.o_lay.head_stride % 4 ||
-              g.o_lay.row_stride % 4))
-        return fail(IT_ERR_DIMS, "flash_attention_backward: unsupported dimensions, O must be 16-byte aligned "
-                                 "with strides that are multiples of 4");
+    it::FlashArgs f;
+    bool empty = false;
+    it_status st = flash_bwd_args("flash_attention_backward", ctx, dtype, bh, seq, head_dim, scale, causal,
+                                  q_layout, kv_layout, o_layout, dO, Q, K, V, O, lse, dQ, dK, dV, &g, &f, &empty);
+    if (st != IT_OK || empty) return st;
     const size_t rows = (size_t)bh * (size_t)seq;
     // Workspace: when the forward is recomputed, O [rows, 64] and lse [rows]; then dlt [rows].
     const size_t bytes = rows * 4 * (O ? 1 : 64 + 2);
@@ -622,6 +647,36 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
     if (st == IT_OK) st = it::launch_flash_bwd(ctx->stream, f, bf16);
     if (ctx->profiling) it::profile_end(ctx, key, ev);
     return st;
+}
+
+it_status it_flash_attention_backward_noalloc(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
+                                              int64_t head_dim, float scale, int causal,
+                                              const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                              const it_attn_layout *o_layout, const void *dO, const void *Q,
+                                              const void *K, const void *V, const float *O, const float *lse,
+                                              float *dQ, float *dK, float *dV) {
+    const char *op = "flash_attention_backward_noalloc";
+    // The static workspace holds rowsum(dO * O) for at most max_rows query rows; checked first, so a
+    // call it cannot hold is refused before anything else is looked at.
+    const int64_t max_rows = (int64_t)(IT_NOALLOC_SCRATCH_BYTES / sizeof(float));
+    if (bh > 0 && seq > 0 && bh > max_rows / seq)
+        return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, bh * seq = " + i64(bh) + " * " +
+                                     i64(seq) + " query rows exceed the " + i64(max_rows) +
+                                     " rows of the static workspace");
+    if (ctx && (!O || !lse))
+        return fail(IT_ERR_NULL, std::string(op) + ": O and lse are required (the forward is not recomputed)");
+    AttnGeom g;
+    it::FlashArgs f;
+    bool empty = false;
+    it_status st = flash_bwd_args(op, ctx, dtype, bh, seq, head_dim, scale, causal, q_layout, kv_layout, o_layout,
+                                  dO, Q, K, V, O, lse, dQ, dK, dV, &g, &f, &empty);
+    if (st != IT_OK || empty) return st;
+    void *ws = it::noalloc_scratch(ctx->device);
+    if (!ws) return fail(IT_ERR_NO_DEVICE, std::string(op) + ": no static workspace on device " + i64(ctx->device));
+    f.O = const_cast<float *>(O);
+    f.lse = const_cast<float *>(lse);
+    f.dlt = (float *)ws;  // every row the dK/dV kernel reads is written first by the dQ kernel
+    return it::launch_flash_bwd(ctx->stream, f, dtype == IT_BF16);
 }
 
 }  // extern "C"

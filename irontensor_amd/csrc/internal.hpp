@@ -196,6 +196,11 @@ bool gemv_applicable(const GemmArgs &a, bool bf16, bool transA, bool transB);
 it_status launch_gemv(hipStream_t s, const GemmArgs &a);
 
 bool flash_supported(const FlashArgs &p, int elem_bytes, bool backward);
+// The static device workspace of the no-allocation entry points (noalloc.hip): noalloc_init looks
+// up this device's copy (called by it_init with the device current); noalloc_scratch returns its
+// device address, or NULL before that.
+it_status noalloc_init(int device);
+void *noalloc_scratch(int device);
 it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16);
 it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16);
 

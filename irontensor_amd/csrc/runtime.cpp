@@ -155,6 +155,7 @@ it_status it_init(int device, it_context **out_ctx) {
         return fail(IT_ERR_NO_DEVICE, "it_init: device ordinal " + std::to_string(device) +
                                           " out of range (" + std::to_string(n) + " devices)");
     IT_HIP_TRY(hipSetDevice(device));
+    if (const it_status st = it::noalloc_init(device); st != IT_OK) return st;
     hipDeviceProp_t prop;
     IT_HIP_TRY(hipGetDeviceProperties(&prop, device));
     auto *ctx = new it_context();

@@ -176,3 +176,21 @@ def test_error_display_formats():
     assert str(it.InnerDimensionMismatch("op", [1, 2], [3, 4])) == "op: inner dimensions don't match, A=[1, 2], B=[3, 4]"
     assert str(it.EmptyTensor("op")) == "op: empty tensor not supported"
     assert str(it.InvalidValue("op", "bad")) == "op: bad"
+
+
+def test_noalloc_backward_refuses_sizes_beyond_its_static_workspace():
+    """it_flash_attention_backward_noalloc keeps rowsum(dO * O) in a 4 MiB static device array:
+    more than 1048576 query rows (bh * seq) are refused on the host, before the context or any
+    buffer is looked at (so no device is needed here)."""
+    lib = _lib.load()
+    lay = _lib.AttnLayout(1, 0, 0, 64)
+    ptrs = [C.c_void_p(256)] * 9
+
+    def call(bh, seq):
+        return lib.it_flash_attention_backward_noalloc(None, _lib.IT_BF16, bh, seq, 64, C.c_float(0.125), 1,
+                                                       C.byref(lay), None, None, *ptrs)
+
+    assert call(1025, 1024) == _lib.IT_ERR_DIMS
+    assert "static workspace" in _lib.last_error()
+    assert call(1, 1048577) == _lib.IT_ERR_DIMS
+    assert call(1024, 1024) == _lib.IT_ERR_NULL  # within the limit: the NULL context is the next refusal
