@@ -947,6 +947,230 @@ void gemm_bf16_256(const GemmArgs p) {
     }
 }
 
+// BF16 256x256x64 GEMM with direct global -> LDS loads (buffer_load_dwordx4 ... lds): the wave never
+// holds operand tiles in registers and issues no LDS writes of its own, so a k-tile costs it 16
+// load instructions (their offsets fixed for the whole k loop, the k position in the scalar offset)
+// besides its fragment reads and 64 MFMAs (v_mfma_f32_32x32x16_bf16, 128x128 per wave). Two stages
+// in two LDS objects (so the compiler can see that loads into one never alias reads of the other);
+// the loads of tile t+2 are issued right after the barrier that ends the reads of tile t's stage,
+// so they have a whole k-tile to land before the wait that precedes the next barrier.
+//
+// Each operand's stage (32 KB) is laid out by its global layout:
+//   k-contiguous (A not transposed, B transposed): [256 rows][64 k], 128-byte rows, the 16-byte
+//     chunk c of row r at position c ^ ((r >> 1) & 7); a load instruction fills 8 rows (lane L:
+//     row L / 8, position L % 8); a fragment (32 rows x 8 k) is one ds_read_b128 per lane, the 16
+//     lanes served together hitting 16 distinct 16-byte bank groups.
+//   mn-contiguous (A transposed, B not): [64 k][256 rows], 512-byte k-rows, chunk c of k-row q at
+//     position c ^ (4 (q & 3)); a load instruction fills 2 k-rows (lane L: k-row L / 32, position
+//     L % 32); a fragment is two ds_read_tr16_b64 per lane, each giving a 16-lane group a 16 x 4
+//     (rows x k) block transposed: lane j of the group points at the 4 rows 4 (j % 4) .. +3 of
+//     k-row j / 4 and receives 4 consecutive k of row j. The 32 lanes served together hit 16
+//     distinct 16-byte bank groups.
+// Whole tiles only (M, N multiples of 256, K of 64); no k limits or masked epilogues.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dtl_rsrc(const void *base, int64_t bytes) {
+    const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
+
+template <bool KCONTIG>
+struct DtlOperand {
+    static constexpr int ROWS = 256, BK = 64;
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t voff[8];
+    uint32_t kstride;  // bytes per k of the global operand (2 for k-contiguous, 2 ld otherwise)
+
+    // base: element (row 0, k kb) of this block; krange: k extent of this block's split.
+    __device__ __forceinline__ void init(const uint16_t *base, int64_t ld, int64_t krange, int wave, int lane) {
+        if constexpr (KCONTIG) {
+            rsrc = dtl_rsrc(base, (int64_t)ROWS * ld * 2);
+            kstride = 2;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int r = 8 * (8 * wave + j) + (lane >> 3);
+                const int c = (lane & 7) ^ ((r >> 1) & 7);
+                voff[j] = (uint32_t)((r * ld + c * 8) * 2);
+            }
+        } else {
+            rsrc = dtl_rsrc(base, krange * ld * 2);
+            kstride = (uint32_t)(ld * 2);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int q = 2 * (8 * wave + j) + (lane >> 5);
+                const int c = (lane & 31) ^ (4 * (q & 3));
+                voff[j] = (uint32_t)((q * ld + c * 8) * 2);
+            }
+        }
+    }
+
+    // The k-tile starting kk elements into the split, into `stage`.
+    __device__ __forceinline__ void issue(char *stage, int64_t kk, int wave) const {
+        const uint32_t soff = (uint32_t)(kk * kstride);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(stage + (8 * wave + j) * 1024), 16, voff[j],
+                                                     soff, 0, 0);
+    }
+
+    // Fragment (rows row .. row + 31, k 16 ks .. +15) of a 32x32x16 MFMA operand: lane l holds row
+    // row + l % 32 at k 16 ks + 8 (l / 32) .. +7.
+    __device__ __forceinline__ static u32x4 frag(const char *st, int row, int ks, int lane) {
+        if constexpr (KCONTIG) {
+            const int fr = lane & 31;
+            const int y = (lane >> 5) ^ ((fr >> 1) & 7);
+            return *(const u32x4 *)(st + (row + fr) * 128 + (((2 * ks) ^ y) * 16));
+        } else {
+            const int g = lane >> 4, j = lane & 15;
+            const int n = row + 16 * (g & 1);           // first row of this group's 16
+            const int q = 16 * ks + 8 * (g >> 1) + (j >> 2);  // k-row of this lane's chunk
+            const int cbyte = n * 2 + 8 * (j & 3);       // byte of the chunk within the k-row
+            const int off = (((cbyte >> 4) ^ (4 * (q & 3))) << 4) + (cbyte & 15);
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(st + q * 512 + off));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(st + (q + 4) * 512 + off));
+            u32x4 v;
+            v[0] = (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+            v[1] = (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+            v[2] = (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+            v[3] = (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+            return v;
+        }
+    }
+};
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_dtl(const GemmArgs p) {
+    using T = uint16_t;
+    constexpr int BM = 256, BN = 256, BK = 64, WT = 128, F = 4;
+    constexpr int TILE = BM * BK * 2;  // bytes of one operand in one stage (32 KB)
+    constexpr int STAGE = 2 * TILE;
+    using OA = DtlOperand<!TA>;
+    using OB = DtlOperand<TB>;
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int64_t z = blockIdx.y;
+    const int64_t b = z % p.batch, split = z / p.batch;
+    const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t coff = bo * p.sC_out + bi * p.sC_in;
+    const int64_t kb = split * p.k_per_split;
+    const int64_t ke = min(p.K, kb + p.k_per_split);
+    const int ntiles = ke > kb ? (int)((ke - kb) / BK) : 0;
+
+    const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    f32x16 acc[F][F];
+#pragma unroll
+    for (int i = 0; i < F; ++i)
+#pragma unroll
+        for (int j = 0; j < F; ++j) acc[i][j] = zero;
+
+    if (ntiles > 0) {
+        const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in + (TA ? kb * p.lda + m0 : m0 * p.lda + kb);
+        const T *B = (const T *)p.B + bo * p.sB_out + bi * p.sB_in + (TB ? n0 * p.ldb + kb : kb * p.ldb + n0);
+        OA oa;
+        OB ob;
+        oa.init(A, p.lda, ke - kb, wave, lane);
+        ob.init(B, p.ldb, ke - kb, wave, lane);
+        const int last = ntiles - 1;
+        auto issue = [&](int t, char *stage) {
+            const int64_t kk = (int64_t)min(t, last) * BK;
+            oa.issue(stage, kk, wave);
+            ob.issue(stage + TILE, kk, wave);
+        };
+        u32x4 fa0[F], fb0[F], fa1[F], fb1[F];
+        auto frags = [&](u32x4 (&fa)[F], u32x4 (&fb)[F], const char *st, int ks) {
+#pragma unroll
+            for (int i = 0; i < F; ++i) fa[i] = OA::frag(st, wm * WT + i * 32, ks, lane);
+#pragma unroll
+            for (int j = 0; j < F; ++j) fb[j] = OB::frag(st + TILE, wn * WT + j * 32, ks, lane);
+        };
+        auto mfma16 = [&](const u32x4 (&fa)[F], const u32x4 (&fb)[F]) {
+#pragma unroll
+            for (int i = 0; i < F; ++i)
+#pragma unroll
+                for (int j = 0; j < F; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8, fa[i]), __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
+        };
+        // DS reads per MFMA pair (a fragment set is 8 fragments, an mn-contiguous one two reads).
+        constexpr int DSR = (4 * (TA ? 2 : 1) + 4 * (TB ? 1 : 2) + 7) / 8;
+        // Tile t from `cur` (its k-step 0 fragments already in fa0/fb0); tile t+1 is streaming into
+        // `nxt`; the loads of tile t+2 go into `cur` once every wave has passed the barrier.
+        auto body = [&](char *cur, char *nxt, int t) {
+            frags(fa1, fb1, cur, 1);
+            mfma16(fa0, fb0);
+            frags(fa0, fb0, cur, 2);
+            mfma16(fa1, fb1);
+            frags(fa1, fb1, cur, 3);
+            mfma16(fa0, fb0);
+            // k-steps 0..2, each step's MFMAs interleaved with the next step's fragment reads.
+#pragma unroll
+            for (int g = 0; g < 24; ++g) {
+                __builtin_amdgcn_sched_group_barrier(sg::DS_READ, DSR, 0);
+                __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
+            }
+            __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile t+1 landed, `cur` read
+            __syncthreads();
+            issue(t + 2, cur);
+            // k-step 3 with the next tile's first fragment reads and the loads of tile t+2.
+            frags(fa0, fb0, nxt, 0);
+            mfma16(fa1, fb1);
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                __builtin_amdgcn_sched_group_barrier(sg::DS_READ, DSR, 0);
+                __builtin_amdgcn_sched_group_barrier(sg::VMEM_READ, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
+            }
+        };
+        issue(0, st0);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        __syncthreads();
+        issue(1, st1);
+        frags(fa0, fb0, st0, 0);
+        int t = 0;
+        for (; t + 1 < ntiles; t += 2) {
+            body(st0, st1, t);
+            body(st1, st0, t + 1);
+        }
+        if (t < ntiles) body(st0, st1, t);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads into dead stages have landed
+    }
+    __syncthreads();
+
+    // Epilogue through LDS, as gemm_bf16_256's (waves 0-1 stage in st0, waves 2-3 in st1).
+    constexpr int EC = 32, EP = EC * 4 + 16;
+    static_assert(2 * WT * EP <= STAGE, "epilogue staging fits in the operand stages");
+    char *wl = (wave < 2 ? st0 : st1) + (wave & 1) * (WT * EP);
+#pragma unroll
+    for (int h = 0; h < F; ++h) {
+#pragma unroll
+        for (int i = 0; i < F; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rl = i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                const int cl = lane & 31;
+                *(float *)(wl + rl * EP + cl * 4) = acc[i][h][r];
+            }
+        __syncthreads();
+        for (int it = 0; it < WT * EC / 256; ++it) {
+            const int e = (it * 64 + lane) * 4;
+            const int rl = e / EC, cl = e % EC;
+            const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
+            finish4<false>(p, v, m0 + wm * WT + rl, n0 + wn * WT + h * EC + cl, coff, z);
+        }
+        __syncthreads();
+    }
+}
+
 // Deterministic split-K reduction: partial sums are added in split order.
 __global__ __launch_bounds__(256) void splitk_reduce(const GemmArgs p) {
     const int64_t total = p.batch * p.M * p.N;
@@ -996,7 +1220,26 @@ bool tiles_exact(const GemmArgs &a, int bm, int bn, int bk) {
            a.a_vec_ok && a.b_vec_ok;
 }
 
+
+// The direct-to-LDS kernel takes whole tiles without epilogue masks or k limits, and 32-bit buffer
+// offsets: a k-contiguous operand's 256 rows, or an mn-contiguous operand's k range, within 2 GiB.
+bool dtl_applicable(bool ta, bool tb, const GemmArgs &a) {
+    auto fits = [&](bool kcontig, int64_t ld) {
+        return kcontig ? ld * 2 * 256 < (1ll << 31) : a.k_per_split * ld * 2 < (1ll << 31);
+    };
+    return !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.swiglu_bwd && !a.xent_stats &&
+           !a.a_kscale && tiles_exact(a, 256, 256, ET<uint16_t>::BK) && fits(!ta, a.lda) && fits(tb, a.ldb) &&
+           a.K * 2 < (1ll << 31);
+}
+
 hipError_t launch_bf16_256(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipStream_t s) {
+    if (dtl_applicable(ta, tb, a)) {
+        if (!ta && tb) hipLaunchKernelGGL((gemm_bf16_dtl<false, true>), grid, dim3(NTHREADS), 0, s, a);
+        else if (!ta && !tb) hipLaunchKernelGGL((gemm_bf16_dtl<false, false>), grid, dim3(NTHREADS), 0, s, a);
+        else if (ta && !tb) hipLaunchKernelGGL((gemm_bf16_dtl<true, false>), grid, dim3(NTHREADS), 0, s, a);
+        else hipLaunchKernelGGL((gemm_bf16_dtl<true, true>), grid, dim3(NTHREADS), 0, s, a);
+        return hipGetLastError();
+    }
     if (tiles_exact(a, 256, a.dual ? 128 : 256, ET<uint16_t>::BK))
         launch_bf16_256_e<false>(ta, tb, a, grid, s);
     else
@@ -1221,8 +1464,9 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     hipEvent_t ev = nullptr;
     if (ctx->profiling) {
         char buf[192];
-        std::snprintf(buf, sizeof(buf), "gemm_%s_%c%c_%dx%d%s%s%s|%s[%lld,%lld,%lld]x%lld s%d",
+        std::snprintf(buf, sizeof(buf), "gemm_%s_%c%c_%dx%d%s%s%s%s|%s[%lld,%lld,%lld]x%lld s%d",
                       bf16 ? "bf16" : "f32", transA ? 'T' : 'N', transB ? 'T' : 'N', cfg.bm, cfg.bn,
+                      cfg.bm == 256 && dtl_applicable(transA, transB, a) ? "_dtl" : "",
                       a.dual ? "_swiglu" : "", a.causal || a.kmode ? "_causal" : "", a.a_kscale ? "_rmsnorm" : a.xent_stats ? "_xent" : "",
                       profile_tag ? profile_tag : "", (long long)a.M, (long long)a.N,
                       (long long)a.K, (long long)a.batch, splits);
