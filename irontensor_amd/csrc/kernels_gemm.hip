@@ -983,16 +983,19 @@ struct DtlOperand {
     uint32_t voff[8];
     uint32_t kstride;  // bytes per k of the global operand (2 for k-contiguous, 2 ld otherwise)
 
-    // base: element (row 0, k kb) of this block; krange: k extent of this block's split.
-    __device__ __forceinline__ void init(const uint16_t *base, int64_t ld, int64_t krange, int wave, int lane) {
+    // base: element (row 0, k kb) of this block; krange: k extent of this block's split. A
+    // k-contiguous operand may take the rows from `row_shift` on from a second matrix (the up
+    // weight of the SwiGLU dual form: this wave's rows are then rows r - row_shift of `base`).
+    __device__ __forceinline__ void init(const uint16_t *base, int64_t ld, int64_t krange, int wave, int lane,
+                                         int row_shift = 0) {
         if constexpr (KCONTIG) {
-            rsrc = dtl_rsrc(base, (int64_t)ROWS * ld * 2);
+            rsrc = dtl_rsrc(base, (int64_t)(ROWS - row_shift) * ld * 2);
             kstride = 2;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int r = 8 * (8 * wave + j) + (lane >> 3);
                 const int c = (lane & 7) ^ ((r >> 1) & 7);
-                voff[j] = (uint32_t)((r * ld + c * 8) * 2);
+                voff[j] = (uint32_t)(((r - row_shift) * ld + c * 8) * 2);
             }
         } else {
             rsrc = dtl_rsrc(base, krange * ld * 2);
@@ -1040,9 +1043,13 @@ struct DtlOperand {
     }
 };
 
-template <bool TA, bool TB>
+template <bool TA, bool TB, bool DUAL = false>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_dtl(const GemmArgs p) {
+    // DUAL (SwiGLU, Y = X.W^T only): the B stage's rows 0..127 are 128 gate-weight rows (loaded
+    // by waves 0-1) and rows 128..255 the same rows of the up weight (waves 2-3), so waves wn = 0
+    // accumulate gate and wn = 1 up for one 256 x 128 output tile; the epilogue pairs them.
+    static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
     using T = uint16_t;
     constexpr int BM = 256, BN = 256, BK = 64, WT = 128, F = 4;
     constexpr int TILE = BM * BK * 2;  // bytes of one operand in one stage (32 KB)
@@ -1060,7 +1067,7 @@ void gemm_bf16_dtl(const GemmArgs p) {
     const int64_t z = blockIdx.y;
     const int64_t b = z % p.batch, split = z / p.batch;
     const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (DUAL ? BN / 2 : BN);
     const int64_t coff = bo * p.sC_out + bi * p.sC_in;
     const int64_t kb = split * p.k_per_split;
     const int64_t ke = min(p.K, kb + p.k_per_split);
@@ -1075,11 +1082,12 @@ void gemm_bf16_dtl(const GemmArgs p) {
 
     if (ntiles > 0) {
         const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in + (TA ? kb * p.lda + m0 : m0 * p.lda + kb);
-        const T *B = (const T *)p.B + bo * p.sB_out + bi * p.sB_in + (TB ? n0 * p.ldb + kb : kb * p.ldb + n0);
+        const T *Bm = (const T *)(DUAL && wave >= 2 ? p.B2 : p.B);
+        const T *B = Bm + bo * p.sB_out + bi * p.sB_in + (TB ? n0 * p.ldb + kb : kb * p.ldb + n0);
         OA oa;
         OB ob;
         oa.init(A, p.lda, ke - kb, wave, lane);
-        ob.init(B, p.ldb, ke - kb, wave, lane);
+        ob.init(B, p.ldb, ke - kb, wave, lane, DUAL && wave >= 2 ? BN / 2 : 0);
         const int last = ntiles - 1;
         auto issue = [&](int t, char *stage) {
             const int64_t kk = (int64_t)min(t, last) * BK;
@@ -1161,11 +1169,24 @@ void gemm_bf16_dtl(const GemmArgs p) {
                 *(float *)(wl + rl * EP + cl * 4) = acc[i][h][r];
             }
         __syncthreads();
-        for (int it = 0; it < WT * EC / 256; ++it) {
-            const int e = (it * 64 + lane) * 4;
-            const int rl = e / EC, cl = e % EC;
-            const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
-            finish4<false>(p, v, m0 + wm * WT + rl, n0 + wn * WT + h * EC + cl, coff, z);
+        if constexpr (DUAL) {
+            // The two waves of row half wm (gate: wn = 0, up: wn = 1) finish its 128 x 32 slice.
+            const char *gl = (wm == 0 ? st0 : st1), *ul = gl + WT * EP;
+            const int pt = wn * 64 + lane;
+            for (int it = 0; it < WT * EC / 512; ++it) {
+                const int e = (it * 128 + pt) * 4;
+                const int rl = e / EC, cl = e % EC;
+                finish_swiglu4<false>(p, *(const f32x4 *)(gl + rl * EP + cl * 4),
+                                      *(const f32x4 *)(ul + rl * EP + cl * 4), m0 + wm * WT + rl, n0 + h * EC + cl,
+                                      coff);
+            }
+        } else {
+            for (int it = 0; it < WT * EC / 256; ++it) {
+                const int e = (it * 64 + lane) * 4;
+                const int rl = e / EC, cl = e % EC;
+                const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
+                finish4<false>(p, v, m0 + wm * WT + rl, n0 + wn * WT + h * EC + cl, coff, z);
+            }
         }
         __syncthreads();
     }
@@ -1227,14 +1248,15 @@ bool dtl_applicable(bool ta, bool tb, const GemmArgs &a) {
     auto fits = [&](bool kcontig, int64_t ld) {
         return kcontig ? ld * 2 * 256 < (1ll << 31) : a.k_per_split * ld * 2 < (1ll << 31);
     };
-    return !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.swiglu_bwd && !a.xent_stats &&
-           !a.a_kscale && tiles_exact(a, 256, 256, ET<uint16_t>::BK) && fits(!ta, a.lda) && fits(tb, a.ldb) &&
-           a.K * 2 < (1ll << 31);
+    return a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.swiglu_bwd && !a.xent_stats && !a.a_kscale &&
+           (!a.dual || (!ta && tb)) && tiles_exact(a, 256, a.dual ? 128 : 256, ET<uint16_t>::BK) &&
+           fits(!ta, a.lda) && fits(tb, a.ldb) && a.K * 2 < (1ll << 31);
 }
 
 hipError_t launch_bf16_256(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipStream_t s) {
     if (dtl_applicable(ta, tb, a)) {
-        if (!ta && tb) hipLaunchKernelGGL((gemm_bf16_dtl<false, true>), grid, dim3(NTHREADS), 0, s, a);
+        if (a.dual) hipLaunchKernelGGL((gemm_bf16_dtl<false, true, true>), grid, dim3(NTHREADS), 0, s, a);
+        else if (!ta && tb) hipLaunchKernelGGL((gemm_bf16_dtl<false, true>), grid, dim3(NTHREADS), 0, s, a);
         else if (!ta && !tb) hipLaunchKernelGGL((gemm_bf16_dtl<false, false>), grid, dim3(NTHREADS), 0, s, a);
         else if (ta && !tb) hipLaunchKernelGGL((gemm_bf16_dtl<true, false>), grid, dim3(NTHREADS), 0, s, a);
         else hipLaunchKernelGGL((gemm_bf16_dtl<true, true>), grid, dim3(NTHREADS), 0, s, a);
