@@ -144,6 +144,22 @@ def extra_attention(it, timer) -> dict:
     return {"config3_bf16_attention_16x8x1024x64_causal": res}
 
 
+def attention_only(it, timer, reps: int) -> dict:
+    """The fused attention kernels alone: config 3 (BF16 [16,8,1024,64]) and the TINY step's FP32
+    shape ([16,4,256,64]), causal, forward then backward from the saved O and LSE, `reps` times."""
+    P = it.Precision
+    out = {}
+    for (b, h, s, prec) in ((16, 8, 1024, P.BF16), (16, 4, 256, P.FP32)):
+        q, k, v, do = (_dev(it, 30 + i, (b, h, s, 64), prec=prec) for i in range(4))
+        it.Context.global_().sync()
+        timer.start()
+        for _ in range(reps):
+            o, lse = it.flash_attention_forward_bhsd(q, k, v, causal=True, scale=0.125)
+            it.flash_attention_backward(do, q, k, v, causal=True, scale=0.125, o=o, lse=lse)
+        out[f"{prec.name.lower()}_{b}x{h}x{s}x64_fwd_bwd_ms"] = round(timer.stop_ms() / max(1, reps), 4)
+    return out
+
+
 def extra_med_step(it, timer, steps=5, warmup=2) -> dict:
     """Config 4: the medium BF16 step (12 layers, hidden 1024, 16 x 64 heads, SwiGLU FFN 2816 with
     the fused bias + SwiGLU epilogue, vocab 32768, batch 8 x seq 1024): every contraction forward
@@ -511,6 +527,9 @@ def main() -> int:
                     help="run only the complete TINY training step, graph-replayed (for kernel traces)")
     ap.add_argument("--bf16-square", action="store_true",
                     help="run only the BF16 4096^3 and 8192^3 GEMMs, NN/NT/TN (for rocprofv3 --pmc)")
+    ap.add_argument("--attention", action="store_true",
+                    help="run only the fused attention forward + backward, config 3 BF16 [16,8,1024,64] and the "
+                         "TINY FP32 shape [16,4,256,64], causal, --steps times each (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -519,7 +538,7 @@ def main() -> int:
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: launched with WORLD_SIZE > 1; this build runs on one GPU only", file=sys.stderr)
         return 2
-    if os.environ.get("IRONTENSOR_LIB"):
+    if os.environ.get("IRONTENSOR_LIB") and not args.attention:
         print("bench.py: IRONTENSOR_LIB is set; the bench times only the in-tree library "
               "(irontensor_amd/libirontensor_hip.so), unset it", file=sys.stderr)
         return 2
@@ -541,6 +560,9 @@ def main() -> int:
     if args.bf16_square:
         print(json.dumps(bf16_square(it, Timer(ctx), ((4096, args.steps), (8192, max(1, args.steps // 4))))),
               flush=True)
+        return 0
+    if args.attention:
+        print(json.dumps(attention_only(it, Timer(ctx), args.steps)), flush=True)
         return 0
     if args.train_only:
         print(json.dumps({"train_step": train_step_figures(it, Timer(ctx), args.steps, args.warmup)}), flush=True)

@@ -19,7 +19,8 @@ LIB = PKG / "libirontensor_hip.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["runtime.cpp", "api.cpp", "api_train.cpp", "kernels_gemm.hip", "kernels_misc.hip", "kernels_flash.hip",
-           "kernels_gemv.hip", "kernels_train.hip", "noalloc.hip"]
+           "kernels_gemv.hip", "kernels_train.hip", "noalloc.hip",
+           "kernels_flash2.hip"]
 
 # -packed-fp32-ops: hipcc must not emit packed FP32 ALU ops (v_pk_*_f32) on this pool.
 HIP_FLAGS = [

@@ -196,6 +196,11 @@ bool gemv_applicable(const GemmArgs &a, bool bf16, bool transA, bool transB);
 it_status launch_gemv(hipStream_t s, const GemmArgs &a);
 
 bool flash_supported(const FlashArgs &p, int elem_bytes, bool backward);
+// BF16 forms on 32x32x16 MFMAs with direct-to-LDS tile loads (kernels_flash2.hip); the launchers of
+// kernels_flash.hip hand BF16 work to them when flash2_applicable.
+bool flash2_applicable(const FlashArgs &p, bool backward);
+it_status launch_flash2_fwd(hipStream_t s, const FlashArgs &p);
+it_status launch_flash2_bwd(hipStream_t s, const FlashArgs &p);
 // The static device workspace of the no-allocation entry points (noalloc.hip): noalloc_init looks
 // up this device's copy (called by it_init with the device current); noalloc_scratch returns its
 // device address, or NULL before that.

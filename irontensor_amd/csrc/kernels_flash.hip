@@ -621,6 +621,7 @@ bool flash_supported(const FlashArgs &p, int elem_bytes, bool backward) {
 }
 
 it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16) {
+    if (bf16 && flash2_applicable(p, false)) return launch_flash2_fwd(s, p);
     const int64_t qblocks = (p.sq + TR - 1) / TR;
     if (qblocks > 0x7fffffff || p.bh > 65535) return fail(IT_ERR_DIMS, "flash attention: grid too large");
     dim3 grid((unsigned)qblocks, (unsigned)p.bh);
@@ -633,6 +634,7 @@ it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16) {
 }
 
 it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16) {
+    if (bf16 && flash2_applicable(p, true)) return launch_flash2_bwd(s, p);
     const int64_t qblocks = (p.sq + TR - 1) / TR, kblocks = (p.skv + TR - 1) / TR;
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || p.bh > 65535)
         return fail(IT_ERR_DIMS, "flash attention backward: grid too large");

@@ -1,0 +1,537 @@
+// Fused attention for BF16 operands, head_dim 64, on v_mfma_f32_32x32x16_bf16: the same mathematics
+// as kernels_flash.hip (ops::attention and attention_backward_recompute, src/ops/attention.rs:286-377,
+// src/train/helpers.rs:120-193), laid out for fewer re-reads, no register transposes and a lean
+// softmax:
+//
+//   * 128 rows (queries, or keys for dK/dV) per workgroup, 32 per wave, 64-row tiles of the other
+//     side streamed through LDS, so each K/V (or Q/dO) tile is read from L2 once per 128 rows.
+//   * Tiles move global -> LDS directly (buffer_load_dwordx4 ... lds), 64 rows x 128 bytes, the
+//     16-byte chunk c of row r at position c ^ swz(r), swz(r) = 4 ((r >> 1) & 1) + ((r >> 2) & 3).
+//     Fragments are read row-major (one ds_read_b128: 32 rows x 8 d) or transposed (two
+//     ds_read_tr16_b64: 32 d-columns x 8 rows); with this swizzle both read patterns hit distinct
+//     banks. Two stages in two LDS objects; the loads of tile t+2 go out after the barrier that ends
+//     the reads of tile t.
+//   * Products are oriented so that a lane's 32x32 accumulator holds one column (a query, or a key
+//     in dK/dV) and 16 rows: S^T = K.Q^T in the forward and dQ kernels (row statistics: one
+//     cross-lane shuffle), S = Q.K^T in the dK/dV kernel. Probabilities and dS feed the next MFMA
+//     from the accumulators as B operands; the LDS operand they meet (V^T, K^T, dO^T, Q^T) is read
+//     transposed with the same k order: lane group h = l / 32 holds rows 4h..4h+3 and 8+4h..8+4h+3
+//     of each 16-row chunk.
+//   * Forward softmax: the row max is taken on the raw scores, probabilities are
+//     exp2(s * scale * log2 e - m) (one FMA and one v_exp_f32 each), and the output is rescaled only
+//     when the running max grows by more than 8 (log2 units: probabilities then stay below 2^8 and
+//     the final division by the row sum cancels the factor); P is rounded to BF16 before its MFMA.
+// The backward is deterministic (dQ and dK/dV from two kernels, no atomics).
+#include <cmath>
+
+#include "internal.hpp"
+#include "mfma.hpp"
+
+namespace it {
+namespace {
+
+constexpr int HD = 64;      // head dim
+constexpr int RB = 128;     // rows per workgroup
+constexpr int TR = 64;      // rows per streamed tile
+constexpr int TB = TR * 128;  // bytes per tile
+constexpr int NTH = 256;
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+constexpr float RESCALE = 8.f;  // lazy rescale threshold, log2 units
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ int swz(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
+
+__device__ __forceinline__ f32x16 mfma32(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+    return f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+}
+
+// Row-major fragment: lane l reads row r0 + l % 32, d = 16 ks + 8 (l / 32) .. +7.
+__device__ __forceinline__ u32x4 frag_rm(const char *tile, int r0, int ks, int lane) {
+    const int r = r0 + (lane & 31);
+    const int c = 2 * ks + (lane >> 5);
+    return *(const u32x4 *)(tile + r * 128 + ((c ^ swz(r)) << 4));
+}
+
+// Transposed fragment: lane l gets column c0 + l % 32 at tile rows k0 + 4h + 0..3 and
+// k0 + 8 + 4h + 0..3 (h = l / 32). ds_read_tr16_b64 hands lane i of a 16-lane group the 4 rows
+// its group points at (lane j of the group points at row j / 4, columns 4 (j % 4) .. +3).
+__device__ __forceinline__ u32x4 frag_tr(const char *tile, int c0, int k0, int lane) {
+    const int g = lane >> 4, j = lane & 15;
+    const int col = c0 + 16 * (g & 1) + 4 * (j & 3);
+    const int r1 = k0 + 4 * (g >> 1) + (j >> 2);
+    const int chunk = col >> 3, half = (j & 1) << 3;
+    const int r2 = r1 + 8;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4_t *)(tile + r1 * 128 + ((chunk ^ swz(r1)) << 4) + half));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4_t *)(tile + r2 * 128 + ((chunk ^ swz(r2)) << 4) + half));
+    const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+    return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+// B operand for key (or query) chunk c from a 32x32 accumulator pair: values j = 8 (c % 2) .. +7 of
+// block c / 2, rounded to BF16.
+__device__ __forceinline__ u32x4 pack_chunk(const f32x16 (&s)[2], int c) {
+    const f32x16 &v = s[c >> 1];
+    const int j0 = 8 * (c & 1);
+    return u32x4{pack_bf16x2(v[j0], v[j0 + 1]), pack_bf16x2(v[j0 + 2], v[j0 + 3]), pack_bf16x2(v[j0 + 4], v[j0 + 5]),
+                 pack_bf16x2(v[j0 + 6], v[j0 + 7])};
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, int64_t bytes) {
+    const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
+}
+
+// One operand streamed in 64-row tiles. Load instruction i (0, 1) of wave w fills rows 8 (2w + i)
+// .. +7 of the tile: lane L takes row L / 8 and position L % 8 of it. Rows at or past `rows` read
+// as zero (the buffer's range check; the row position is in the per-lane offset).
+struct Stream {
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t voff[2];
+    uint32_t tile_bytes;  // bytes between tiles (64 rows)
+
+    __device__ __forceinline__ void init(const uint16_t *head, int64_t row_stride, int64_t rows, int wave, int lane) {
+        rs = rsrc(head, rows * row_stride * 2);
+        tile_bytes = (uint32_t)(TR * row_stride * 2);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = 8 * (2 * wave + i) + (lane >> 3);
+            const int c = (lane & 7) ^ swz(r);
+            voff[i] = (uint32_t)((r * row_stride + c * 8) * 2);
+        }
+    }
+    __device__ __forceinline__ void issue(char *tile, int t, int wave) const {
+        const uint32_t base = (uint32_t)t * tile_bytes;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t *)(tile + (2 * wave + i) * 1024), 16,
+                                                     voff[i] + base, 0, 0, 0);
+    }
+};
+
+// 64 consecutive FP32 row values (LSE, rowsum(dO * O)) of a tile, loaded by lanes 0..15 of one wave.
+struct RowStream {
+    __amdgpu_buffer_rsrc_t rs;
+    __device__ __forceinline__ void init(const float *row0, int64_t rows) { rs = rsrc(row0, rows * 4); }
+    __device__ __forceinline__ void issue(char *dst, int t, int lane) const {
+        if (lane < 16)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t *)dst, 16, (uint32_t)(t * TR * 4 + lane * 16), 0,
+                                                     0, 0);
+    }
+};
+
+struct Head {
+    int64_t heads, bs, hs, rs;
+    __device__ __forceinline__ int64_t base(int64_t bh) const { return (bh / heads) * bs + (bh % heads) * hs; }
+};
+
+__device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
+
+// Workgroup (x, y) takes tile lin / heads-count of head lin % heads-count, lin = y * gridDim.x + x,
+// so the first workgroups dispatched hold the costliest causal tile of every head.
+__device__ __forceinline__ void grid_tile(int &tile, int64_t &bh) {
+    const int64_t lin = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    tile = (int)(lin / gridDim.y);
+    bh = lin % gridDim.y;
+}
+
+__device__ __forceinline__ void wait_loads_and_reads() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0) lgkmcnt(0)
+
+// Streams n tiles: body(t, cur) with tile t in `cur`; loads of tile t+2 after the barrier that ends t.
+template <typename Issue, typename Body>
+__device__ __forceinline__ void stream_tiles(char *st0, char *st1, int n, Issue issue, Body body) {
+    if (n <= 0) return;
+    issue(st0, 0);
+    wait_loads_and_reads();
+    __syncthreads();
+    if (n > 1) issue(st1, 1);
+    int t = 0;
+    for (; t + 1 < n; t += 2) {
+        body(t, st0);
+        wait_loads_and_reads();
+        __syncthreads();
+        if (t + 2 < n) issue(st0, t + 2);
+        body(t + 1, st1);
+        wait_loads_and_reads();
+        __syncthreads();
+        if (t + 3 < n) issue(st1, t + 3);
+    }
+    if (t < n) {
+        body(t, st0);
+        wait_loads_and_reads();
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------ forward
+
+#ifndef IT_FA_FWD_WPE
+#define IT_FA_FWD_WPE 2
+#endif
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(IT_FA_FWD_WPE))) void flash2_fwd(const FlashArgs p) {
+    __shared__ __attribute__((aligned(1024))) char st0[2 * TB];  // K tile, V tile
+    __shared__ __attribute__((aligned(1024))) char st1[2 * TB];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    int qb;
+    int64_t bh;
+    grid_tile(qb, bh);
+    if (p.causal) qb = (int)gridDim.x - 1 - qb;  // the last query block sees every key block
+    const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
+        ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
+    const uint16_t *Q = (const uint16_t *)p.Q + hq.base(bh);
+    const uint16_t *K = (const uint16_t *)p.K + hk.base(bh);
+    const uint16_t *V = (const uint16_t *)p.V + hk.base(bh);
+    const int q = qb * RB + wave * 32 + (lane & 31);  // this lane's query
+    const bool qok = q < p.sq;
+    const int skv = (int)p.skv;
+    const float c2 = p.scale * LOG2E;
+
+    // Q^T as the B operand of S^T = K.Q^T: query q, d = 16 ks + 8h .. +7.
+    u32x4 qf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const u32x4 v = ld16(Q + (qok ? (int64_t)q * p.q_rs + 16 * ks + 8 * h : 0));
+        qf[ks] = qok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+    f32x16 o[2] = {zero16(), zero16()};
+    float m = -INFINITY, l = 0.f;  // running max (log2 units) used by the probabilities; this lane's sum
+
+    const int kblocks = (int)((p.skv + TR - 1) / TR);
+    const int nkb = p.causal ? min(kblocks, (qb * RB + RB - 1) / TR + 1) : kblocks;
+    Stream sk, sv;
+    sk.init(K, p.kv_rs, p.skv, wave, lane);
+    sv.init(V, p.kv_rs, p.skv, wave, lane);
+    stream_tiles(st0, st1, nkb, [&](char *st, int t) {
+        sk.issue(st, t, wave);
+        sv.issue(st + TB, t, wave);
+    }, [&](int t, const char *st) {
+        const char *kt = st, *vt = st + TB;
+        // S^T (keys x queries): block kh holds keys 32kh + 8 (j / 4) + 4h + j % 4 of query q.
+        f32x16 s[2] = {zero16(), zero16()};
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) s[kh] = mfma32(frag_rm(kt, 32 * kh, ks, lane), qf[ks], s[kh]);
+        // Keys past seq_kv, and (causal) keys past the query, are -inf. Only blocks that reach past
+        // the first query of this workgroup or past seq_kv hold such keys.
+        const int k0 = t * TR;
+        if ((p.causal && k0 + TR - 1 > qb * RB) || k0 + TR > skv) {
+            // a key is dead past seq_kv, or (causal) past the query
+            const int lim = p.causal ? min(skv - 1, q) : skv - 1;
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int key = k0 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
+                    s[kh][j] = key > lim ? -INFINITY : s[kh][j];
+                }
+        }
+        // Four independent max and sum chains: a single chain serialises on VALU latency.
+        float m4[4] = {s[0][0], s[0][1], s[0][2], s[0][3]};
+#pragma unroll
+        for (int j = 4; j < 32; ++j) m4[j & 3] = fmaxf(m4[j & 3], s[j >> 4][j & 15]);
+        float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c2;
+        // Rescale only when some row's max grew by more than RESCALE (wave-uniform branch).
+        if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE) != 0) {
+            const float mn = fmaxf(m, mx);
+            const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+            o[0] *= alpha;
+            o[1] *= alpha;
+            l *= alpha;
+            m = mn;
+        }
+        const float nm = m == -INFINITY ? 0.f : -m;
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][j], c2, nm));
+                s[kh][j] = e;
+                ls[j & 3] += e;
+            }
+        l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        // O^T (d x queries) += V^T (d x keys) . P^T (keys x queries)
+        u32x4 pf[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) pf[c] = pack_chunk(s, c);
+#pragma unroll
+        for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[dh] = mfma32(frag_tr(vt, 32 * dh, 16 * c, lane), pf[c], o[dh]);
+    });
+    l += __shfl_xor(l, 32, 64);
+    if (qok) {
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        float *O = (float *)p.O + ho.base(bh) + (int64_t)q * p.o_rs;
+        // o[dh][j]: d = 32dh + 8 (j / 4) + 4h + j % 4
+#pragma unroll
+        for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                *(f32x4 *)(O + 32 * dh + 8 * jj + 4 * h) =
+                    f32x4{o[dh][4 * jj], o[dh][4 * jj + 1], o[dh][4 * jj + 2], o[dh][4 * jj + 3]} * inv;
+        if (h == 0 && p.lse) p.lse[bh * p.sq + q] = (m + __log2f(l)) * LN2;  // natural-log LSE
+    }
+}
+
+// ------------------------------------------------------------------ backward: dQ (and rowsum(dO * O))
+
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_dq(const FlashArgs p) {
+    __shared__ __attribute__((aligned(1024))) char st0[2 * TB];  // K tile, V tile
+    __shared__ __attribute__((aligned(1024))) char st1[2 * TB];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    int qb;
+    int64_t bh;
+    grid_tile(qb, bh);
+    if (p.causal) qb = (int)gridDim.x - 1 - qb;
+    const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
+        hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
+    const uint16_t *Q = (const uint16_t *)p.Q + hq.base(bh);
+    const uint16_t *K = (const uint16_t *)p.K + hk.base(bh);
+    const uint16_t *V = (const uint16_t *)p.V + hk.base(bh);
+    const uint16_t *dO = (const uint16_t *)p.dO + hd.base(bh);
+    const int q = qb * RB + wave * 32 + (lane & 31);
+    const bool qok = q < p.sq;
+    const int skv = (int)p.skv;
+    const float c2 = p.scale * LOG2E;
+
+    // Q^T and dO^T as B operands: query q, d = 16 ks + 8h .. +7.
+    u32x4 qf[4], of[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const u32x4 a = ld16(Q + (qok ? (int64_t)q * p.q_rs + 16 * ks + 8 * h : 0));
+        const u32x4 b = ld16(dO + (qok ? (int64_t)q * p.do_rs + 16 * ks + 8 * h : 0));
+        qf[ks] = qok ? a : u32x4{0u, 0u, 0u, 0u};
+        of[ks] = qok ? b : u32x4{0u, 0u, 0u, 0u};
+    }
+    // rowsum(dO * O) for this query from the dO fragments just loaded (the two lanes of a query hold
+    // 32 of its 64 d each); written for the dK/dV kernel, which runs after this one.
+    float dl = 0.f;
+    {
+        const float *Orow = p.O + ho.base(bh) + (qok ? (int64_t)q * p.o_rs : 0);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int e4 = 0; e4 < 2; ++e4) {
+                const f32x4 ov = qok ? *(const f32x4 *)(Orow + 16 * ks + 8 * h + 4 * e4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t w = of[ks][2 * e4 + (e >> 1)];
+                    const float gv = __uint_as_float(e & 1 ? w & 0xffff0000u : w << 16);
+                    dl += gv * ov[e];
+                }
+            }
+        dl += __shfl_xor(dl, 32, 64);
+        if (h == 0 && qok) p.dlt[bh * p.sq + q] = dl;
+    }
+    const float nl2 = qok ? -p.lse[bh * p.sq + q] * LOG2E : 0.f;
+    f32x16 dq[2] = {zero16(), zero16()};
+
+    const int kblocks = (int)((p.skv + TR - 1) / TR);
+    const int nkb = p.causal ? min(kblocks, (qb * RB + RB - 1) / TR + 1) : kblocks;
+    Stream sk, sv;
+    sk.init(K, p.kv_rs, p.skv, wave, lane);
+    sv.init(V, p.kv_rs, p.skv, wave, lane);
+    stream_tiles(st0, st1, nkb, [&](char *st, int t) {
+        sk.issue(st, t, wave);
+        sv.issue(st + TB, t, wave);
+    }, [&](int t, const char *st) {
+        const char *kt = st, *vt = st + TB;
+        // S^T = K.Q^T and dP^T = V.dO^T: block kh holds keys 32kh + 8 (j / 4) + 4h + j % 4.
+        f32x16 s[2] = {zero16(), zero16()}, dp[2] = {zero16(), zero16()};
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                s[kh] = mfma32(frag_rm(kt, 32 * kh, ks, lane), qf[ks], s[kh]);
+                dp[kh] = mfma32(frag_rm(vt, 32 * kh, ks, lane), of[ks], dp[kh]);
+            }
+        // P^T = exp2(S^T scale log2 e - LSE log2 e), zero past the query (causal) and past seq_kv
+        // (K and V rows there are zero, but an unmasked probability could overflow into 0 * inf).
+        const int k0 = t * TR;
+        const bool edge = (p.causal && k0 + TR - 1 > qb * RB) || k0 + TR > skv;
+        const int lim = p.causal ? min(skv - 1, q) : skv - 1;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][j], c2, nl2));
+                if (edge) pr = k0 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3) > lim ? 0.f : pr;
+                dp[kh][j] = pr * (dp[kh][j] - dl);
+            }
+        // dQ^T (d x queries) += K^T (d x keys) . dS^T (keys x queries)
+        u32x4 df[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) df[c] = pack_chunk(dp, c);
+#pragma unroll
+        for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) dq[dh] = mfma32(frag_tr(kt, 32 * dh, 16 * c, lane), df[c], dq[dh]);
+    });
+    if (qok) {
+        float *dQ = p.dQ + hq.base(bh) + (int64_t)q * p.q_rs;
+#pragma unroll
+        for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                *(f32x4 *)(dQ + 32 * dh + 8 * jj + 4 * h) =
+                    f32x4{dq[dh][4 * jj], dq[dh][4 * jj + 1], dq[dh][4 * jj + 2], dq[dh][4 * jj + 3]} * p.scale;
+    }
+}
+
+// ------------------------------------------------------------------ backward: dK, dV
+
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_dkdv(const FlashArgs p) {
+    constexpr int STAGE = 2 * TB + 2 * TR * 4;  // Q tile, dO tile, LSE row values, rowsum(dO * O)
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    int kb;
+    int64_t bh;
+    grid_tile(kb, bh);  // causal: key block 0 is seen by every query block, so it goes out first
+    const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
+        hd{p.heads, p.do_bs, p.do_hs, p.do_rs};
+    const uint16_t *Q = (const uint16_t *)p.Q + hq.base(bh);
+    const uint16_t *K = (const uint16_t *)p.K + hk.base(bh);
+    const uint16_t *V = (const uint16_t *)p.V + hk.base(bh);
+    const uint16_t *dO = (const uint16_t *)p.dO + hd.base(bh);
+    const int key = kb * RB + wave * 32 + (lane & 31);  // this lane's key
+    const bool kok = key < p.skv;
+    const float c2 = p.scale * LOG2E;
+
+    // K^T and V^T as B operands of S = Q.K^T and dP = dO.V^T: key, d = 16 ks + 8h .. +7.
+    u32x4 kf[4], vf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const int64_t off = kok ? (int64_t)key * p.kv_rs + 16 * ks + 8 * h : 0;
+        const u32x4 a = ld16(K + off), b = ld16(V + off);
+        kf[ks] = kok ? a : u32x4{0u, 0u, 0u, 0u};
+        vf[ks] = kok ? b : u32x4{0u, 0u, 0u, 0u};
+    }
+    f32x16 dk[2] = {zero16(), zero16()}, dv[2] = {zero16(), zero16()};
+
+    const int qblocks = (int)((p.sq + TR - 1) / TR);
+    const int qb0 = p.causal ? min(qblocks, kb * RB / TR) : 0;
+    Stream sq_, sd;
+    sq_.init(Q, p.q_rs, p.sq, wave, lane);
+    sd.init(dO, p.do_rs, p.sq, wave, lane);
+    RowStream rl, rd;
+    rl.init(p.lse + bh * p.sq, p.sq);
+    rd.init(p.dlt + bh * p.sq, p.sq);
+    stream_tiles(st0, st1, qblocks - qb0, [&](char *st, int t) {
+        sq_.issue(st, qb0 + t, wave);
+        sd.issue(st + TB, qb0 + t, wave);
+        if (wave == 0) rl.issue(st + 2 * TB, qb0 + t, lane);
+        if (wave == 1) rd.issue(st + 2 * TB + TR * 4, qb0 + t, lane);
+    }, [&](int t, const char *st) {
+        const char *qt = st, *dot = st + TB;
+        const float *lse = (const float *)(st + 2 * TB), *dlt = lse + TR;
+        const int q0 = (qb0 + t) * TR;
+        // S = Q.K^T and dP = dO.V^T: block qh holds queries 32qh + 8 (j / 4) + 4h + j % 4 of key.
+        f32x16 s[2] = {zero16(), zero16()}, dp[2] = {zero16(), zero16()};
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                s[qh] = mfma32(frag_rm(qt, 32 * qh, ks, lane), kf[ks], s[qh]);
+                dp[qh] = mfma32(frag_rm(dot, 32 * qh, ks, lane), vf[ks], dp[qh]);
+            }
+        // P = exp2(S scale log2 e - LSE log2 e), zero for queries before this key (causal). Rows
+        // past seq_q have zero Q and dO (and zero LSE, rowsum): they add nothing to dK or dV.
+        const bool diag = p.causal && q0 < kb * RB + RB;
+        const int kq = key - q0;  // this key against query row r of the tile: masked when kq > r
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int r0 = 32 * qh + 8 * jj + 4 * h;
+                const f32x4 lv = *(const f32x4 *)(lse + r0), dv4 = *(const f32x4 *)(dlt + r0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = 4 * jj + e;
+                    float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qh][j], c2, lv[e] * -LOG2E));
+                    if (diag) pr = kq > r0 + e ? 0.f : pr;
+                    s[qh][j] = pr;
+                    dp[qh][j] = pr * (dp[qh][j] - dv4[e]);
+                }
+            }
+        // dV^T (d x keys) += dO^T (d x queries) . P;  dK^T += Q^T . dS
+        u32x4 pf[4], df[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            pf[c] = pack_chunk(s, c);
+            df[c] = pack_chunk(dp, c);
+        }
+#pragma unroll
+        for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                dv[dh] = mfma32(frag_tr(dot, 32 * dh, 16 * c, lane), pf[c], dv[dh]);
+                dk[dh] = mfma32(frag_tr(qt, 32 * dh, 16 * c, lane), df[c], dk[dh]);
+            }
+    });
+    if (kok) {
+        float *dK = p.dK + hk.base(bh) + (int64_t)key * p.kv_rs;
+        float *dV = p.dV + hk.base(bh) + (int64_t)key * p.kv_rs;
+#pragma unroll
+        for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int d = 32 * dh + 8 * jj + 4 * h;
+                *(f32x4 *)(dK + d) =
+                    f32x4{dk[dh][4 * jj], dk[dh][4 * jj + 1], dk[dh][4 * jj + 2], dk[dh][4 * jj + 3]} * p.scale;
+                *(f32x4 *)(dV + d) = f32x4{dv[dh][4 * jj], dv[dh][4 * jj + 1], dv[dh][4 * jj + 2], dv[dh][4 * jj + 3]};
+            }
+    }
+}
+
+}  // namespace
+
+// The BF16 kernels above need 16-byte aligned operand rows (checked by flash_supported) and 32-bit
+// buffer offsets: every operand's rows of one head within 2 GiB.
+bool flash2_applicable(const FlashArgs &p, bool backward) {
+    auto fits = [](int64_t rows, int64_t rs) { return rows * rs * 2 < (1ll << 31); };
+    bool ok = fits(p.skv, p.kv_rs);
+    if (backward) ok = ok && fits(p.sq, p.q_rs) && fits(p.sq, p.do_rs) && p.sq * 4 < (1ll << 31);
+    return ok;
+}
+
+it_status launch_flash2_fwd(hipStream_t s, const FlashArgs &p) {
+    const int64_t qblocks = (p.sq + RB - 1) / RB;
+    if (qblocks > 0x7fffffff || p.bh > 65535) return fail(IT_ERR_DIMS, "flash attention: grid too large");
+    hipLaunchKernelGGL(flash2_fwd, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+    IT_HIP_TRY(hipGetLastError());
+    return IT_OK;
+}
+
+it_status launch_flash2_bwd(hipStream_t s, const FlashArgs &p) {
+    const int64_t qblocks = (p.sq + RB - 1) / RB, kblocks = (p.skv + RB - 1) / RB;
+    if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || p.bh > 65535)
+        return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
+    // dQ first: it also writes rowsum(dO * O), which the dK/dV kernel reads.
+    hipLaunchKernelGGL(flash2_bwd_dq, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+    hipLaunchKernelGGL(flash2_bwd_dkdv, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+    IT_HIP_TRY(hipGetLastError());
+    return IT_OK;
+}
+
+}  // namespace it
