@@ -174,12 +174,21 @@ __device__ __forceinline__ void stream_tiles(char *st0, char *st1, int n, Issue 
     }
 }
 
+// NaN-propagating max (v_maximum3_f32 on gfx950: no operand canonicalisation, unlike fmaxf).
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// Max over the lane pair l, l ^ 32 (the two halves of one query's keys): one v_permlane32_swap.
+__device__ __forceinline__ float pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // ------------------------------------------------------------------ forward
 
-#ifndef IT_FA_FWD_WPE
-#define IT_FA_FWD_WPE 2
-#endif
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(IT_FA_FWD_WPE))) void flash2_fwd(const FlashArgs p) {
+// Three waves per SIMD (168 registers): the forward's max -> exp -> P.V chain is serial within a wave,
+// and a third wave hides more of it than software pipelining within the wave (which needs registers
+// for two score tiles and so allows only two).
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void flash2_fwd(const FlashArgs p) {
     __shared__ __attribute__((aligned(1024))) char st0[2 * TB];  // K tile, V tile
     __shared__ __attribute__((aligned(1024))) char st1[2 * TB];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -239,12 +248,12 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(IT_FA_FWD_W
                     s[kh][j] = key > lim ? -INFINITY : s[kh][j];
                 }
         }
-        // Four independent max and sum chains: a single chain serialises on VALU latency.
+        // Four independent max and sum chains: a single chain serialises on VALU latency; the lane
+        // pair's max with a permlane swap.
         float m4[4] = {s[0][0], s[0][1], s[0][2], s[0][3]};
 #pragma unroll
-        for (int j = 4; j < 32; ++j) m4[j & 3] = fmaxf(m4[j & 3], s[j >> 4][j & 15]);
-        float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c2;
+        for (int j = 4; j < 32; ++j) m4[j & 3] = vmax(m4[j & 3], s[j >> 4][j & 15]);
+        const float mx = pair_max(vmax(vmax(m4[0], m4[1]), vmax(m4[2], m4[3]))) * c2;
         // Rescale only when some row's max grew by more than RESCALE (wave-uniform branch).
         if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE) != 0) {
             const float mn = fmaxf(m, mx);
