@@ -297,16 +297,16 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
  * that forbid hipMalloc). Same arguments, kernels and results as it_flash_attention_backward, except:
  *   - O and lse (the forward's outputs) are required, since the forward is not recomputed
  *     (IT_ERR_NULL otherwise);
- *   - its one workspace, rowsum(dO * O) per query row (4 bytes per row), lives in a static device
- *     array of IT_NOALLOC_SCRATCH_BYTES (4 MiB) that each GPU the library runs on holds until the
- *     process ends, so bh * seq may be at most 1048576 rows (IT_ERR_DIMS otherwise, before any
- *     device work);
+ *   - its one workspace, two floats per query row (rowsum(dO * O) and the row's LSE in the form the
+ *     dK/dV kernel reads; 8 bytes per row), lives in a static device array of
+ *     IT_NOALLOC_SCRATCH_BYTES (8 MiB) that each GPU the library runs on holds until the process
+ *     ends, so bh * seq may be at most 1048576 rows (IT_ERR_DIMS otherwise, before any device work);
  *   - every call on a GPU shares that GPU's array: calls that overlap on one GPU (other streams or
  *     contexts) race. The array keeps the last call's values and needs no clearing: each call
  *     writes every row before it reads it.
  * Calls no hipMalloc, hipFree or other allocating routine, and no profiler hooks.
  */
-#define IT_NOALLOC_SCRATCH_BYTES (4u << 20)
+#define IT_NOALLOC_SCRATCH_BYTES (8u << 20)
 it_status it_flash_attention_backward_noalloc(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
                                               int64_t head_dim, float scale, int causal,
                                               const it_attn_layout *q_layout, const it_attn_layout *kv_layout,

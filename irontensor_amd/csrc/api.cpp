@@ -620,8 +620,9 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
                                   q_layout, kv_layout, o_layout, dO, Q, K, V, O, lse, dQ, dK, dV, &g, &f, &empty);
     if (st != IT_OK || empty) return st;
     const size_t rows = (size_t)bh * (size_t)seq;
-    // Workspace: when the forward is recomputed, O [rows, 64] and lse [rows]; then dlt [rows].
-    const size_t bytes = rows * 4 * (O ? 1 : 64 + 2);
+    // Workspace: when the forward is recomputed, O [rows, 64] and lse [rows]; then the two row arrays
+    // the dQ kernel leaves for the dK/dV kernel, dlt [2 rows].
+    const size_t bytes = rows * 4 * (O ? 2 : 64 + 1 + 2);
     void *ws = nullptr;
     if ((st = it::ensure_attn_scratch(ctx, bytes, &ws)) != IT_OK) return st;
     f.dlt = (float *)ws + (O ? 0 : rows * 65);
@@ -656,9 +657,10 @@ it_status it_flash_attention_backward_noalloc(it_context *ctx, it_dtype dtype, i
                                               const void *K, const void *V, const float *O, const float *lse,
                                               float *dQ, float *dK, float *dV) {
     const char *op = "flash_attention_backward_noalloc";
-    // The static workspace holds rowsum(dO * O) for at most max_rows query rows; checked first, so a
-    // call it cannot hold is refused before anything else is looked at.
-    const int64_t max_rows = (int64_t)(IT_NOALLOC_SCRATCH_BYTES / sizeof(float));
+    // The static workspace holds two floats per query row (rowsum(dO * O), and the LSE in the form
+    // the dK/dV kernel reads) for at most max_rows rows; checked first, so a call it cannot hold is
+    // refused before anything else is looked at.
+    const int64_t max_rows = (int64_t)(IT_NOALLOC_SCRATCH_BYTES / (2 * sizeof(float)));
     if (bh > 0 && seq > 0 && bh > max_rows / seq)
         return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, bh * seq = " + i64(bh) + " * " +
                                      i64(seq) + " query rows exceed the " + i64(max_rows) +

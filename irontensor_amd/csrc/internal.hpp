@@ -181,7 +181,9 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
 struct FlashArgs {
     const void *Q, *K, *V, *dO;  // operand dtype
     float *O;                    // forward output / backward input (f32)
-    float *lse, *dlt;            // [bh][sq] row log-sum-exp, rowsum(dO * O)
+    float *lse, *dlt;            // [bh][sq] row log-sum-exp; dlt: workspace of 2 [bh][sq] row arrays
+                                 // (FP32 kernels: rowsum(dO * O) in the first; BF16 kernels:
+                                 // -rowsum(dO * O), then -LSE log2 e)
     float *dQ, *dK, *dV;         // f32 gradients
     int64_t bh, sq, skv, head_dim, heads;
     int64_t q_bs, q_hs, q_rs;     // Q and dQ

@@ -331,7 +331,8 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
         of[ks] = qok ? b : u32x4{0u, 0u, 0u, 0u};
     }
     // rowsum(dO * O) for this query from the dO fragments just loaded (the two lanes of a query hold
-    // 32 of its 64 d each); written for the dK/dV kernel, which runs after this one.
+    // 32 of its 64 d each). For the dK/dV kernel, which runs after this one, the workspace gets
+    // -rowsum at dlt[row] and -LSE log2 e at dlt[bh seq + row].
     float dl = 0.f;
     {
         const float *Orow = p.O + ho.base(bh) + (qok ? (int64_t)q * p.o_rs : 0);
@@ -348,9 +349,16 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
                 }
             }
         dl += __shfl_xor(dl, 32, 64);
-        if (h == 0 && qok) p.dlt[bh * p.sq + q] = dl;
     }
     const float nl2 = qok ? -p.lse[bh * p.sq + q] * LOG2E : 0.f;
+    if (h == 0 && qok) {
+        p.dlt[bh * p.sq + q] = -dl;
+        p.dlt[p.bh * p.sq + bh * p.sq + q] = nl2;
+    }
+    // dP^T accumulates from -rowsum (the same for all 16 rows of a lane's column), so the MFMA
+    // leaves dP - rowsum(dO * O) and dS = P (dP - rowsum) is one multiply.
+    const float ndl = -dl;
+    const f32x16 ndl16 = {ndl, ndl, ndl, ndl, ndl, ndl, ndl, ndl, ndl, ndl, ndl, ndl, ndl, ndl, ndl, ndl};
     f32x16 dq[2] = {zero16(), zero16()};
 
     const int kblocks = (int)((p.skv + TR - 1) / TR);
@@ -364,7 +372,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
     }, [&](int t, const char *st) {
         const char *kt = st, *vt = st + TB;
         // S^T = K.Q^T and dP^T = V.dO^T: block kh holds keys 32kh + 8 (j / 4) + 4h + j % 4.
-        f32x16 s[2] = {zero16(), zero16()}, dp[2] = {zero16(), zero16()};
+        f32x16 s[2] = {zero16(), zero16()}, dp[2] = {ndl16, ndl16};
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
@@ -383,7 +391,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
             for (int j = 0; j < 16; ++j) {
                 float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][j], c2, nl2));
                 if (edge) pr = k0 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3) > lim ? 0.f : pr;
-                dp[kh][j] = pr * (dp[kh][j] - dl);
+                dp[kh][j] = pr * dp[kh][j];
             }
         // dQ^T (d x queries) += K^T (d x keys) . dS^T (keys x queries)
         u32x4 df[4];
@@ -408,7 +416,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
 // ------------------------------------------------------------------ backward: dK, dV
 
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_dkdv(const FlashArgs p) {
-    constexpr int STAGE = 2 * TB + 2 * TR * 4;  // Q tile, dO tile, LSE row values, rowsum(dO * O)
+    constexpr int STAGE = 2 * TB + 2 * TR * 4;  // Q tile, dO tile, -LSE log2 e and -rowsum(dO * O) rows
     __shared__ __attribute__((aligned(1024))) char st0[STAGE];
     __shared__ __attribute__((aligned(1024))) char st1[STAGE];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -443,8 +451,8 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
     Stream sq_, sd;
     sq_.init(Q, p.q_rs, p.sq, wave, lane);
     sd.init(dO, p.do_rs, p.sq, wave, lane);
-    RowStream rl, rd;
-    rl.init(p.lse + bh * p.sq, p.sq);
+    RowStream rl, rd;  // rows the dQ kernel left in the workspace
+    rl.init(p.dlt + p.bh * p.sq + bh * p.sq, p.sq);
     rd.init(p.dlt + bh * p.sq, p.sq);
     stream_tiles(st0, st1, qblocks - qb0, [&](char *st, int t) {
         sq_.issue(st, qb0 + t, wave);
@@ -453,10 +461,19 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
         if (wave == 1) rd.issue(st + 2 * TB + TR * 4, qb0 + t, lane);
     }, [&](int t, const char *st) {
         const char *qt = st, *dot = st + TB;
-        const float *lse = (const float *)(st + 2 * TB), *dlt = lse + TR;
+        const float *nl2 = (const float *)(st + 2 * TB), *ndl = nl2 + TR;
         const int q0 = (qb0 + t) * TR;
         // S = Q.K^T and dP = dO.V^T: block qh holds queries 32qh + 8 (j / 4) + 4h + j % 4 of key.
-        f32x16 s[2] = {zero16(), zero16()}, dp[2] = {zero16(), zero16()};
+        // dP accumulates from -rowsum(dO * O) of those queries, so the MFMA leaves dP - rowsum.
+        f32x16 s[2] = {zero16(), zero16()}, dp[2];
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const f32x4 v = *(const f32x4 *)(ndl + 32 * qh + 8 * jj + 4 * h);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dp[qh][4 * jj + e] = v[e];
+            }
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
@@ -465,7 +482,8 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
                 dp[qh] = mfma32(frag_rm(dot, 32 * qh, ks, lane), vf[ks], dp[qh]);
             }
         // P = exp2(S scale log2 e - LSE log2 e), zero for queries before this key (causal). Rows
-        // past seq_q have zero Q and dO (and zero LSE, rowsum): they add nothing to dK or dV.
+        // past seq_q have zero Q and dO (and read as zero from the workspace rows): they add nothing
+        // to dK or dV.
         const bool diag = p.causal && q0 < kb * RB + RB;
         const int kq = key - q0;  // this key against query row r of the tile: masked when kq > r
 #pragma unroll
@@ -473,14 +491,14 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
                 const int r0 = 32 * qh + 8 * jj + 4 * h;
-                const f32x4 lv = *(const f32x4 *)(lse + r0), dv4 = *(const f32x4 *)(dlt + r0);
+                const f32x4 lv = *(const f32x4 *)(nl2 + r0);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = 4 * jj + e;
-                    float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qh][j], c2, lv[e] * -LOG2E));
+                    float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qh][j], c2, lv[e]));
                     if (diag) pr = kq > r0 + e ? 0.f : pr;
                     s[qh][j] = pr;
-                    dp[qh][j] = pr * (dp[qh][j] - dv4[e]);
+                    dp[qh][j] = pr * dp[qh][j];
                 }
             }
         // dV^T (d x keys) += dO^T (d x queries) . P;  dK^T += Q^T . dS

@@ -179,7 +179,7 @@ def test_error_display_formats():
 
 
 def test_noalloc_backward_refuses_sizes_beyond_its_static_workspace():
-    """it_flash_attention_backward_noalloc keeps rowsum(dO * O) in a 4 MiB static device array:
+    """it_flash_attention_backward_noalloc keeps two floats per query row in an 8 MiB static device array:
     more than 1048576 query rows (bh * seq) are refused on the host, before the context or any
     buffer is looked at (so no device is needed here)."""
     lib = _lib.load()
