@@ -1144,17 +1144,54 @@ void gemm_bf16_dtl(const GemmArgs p) {
         __syncthreads();
         issue(1, st1);
         frags(fa0, fb0, st0, 0);
-        int t = 0;
-        for (; t + 1 < ntiles; t += 2) {
+        // An even number of k-tiles (dtl_applicable): no odd tail body, whose prefetched fragments
+        // would stay live past the loop and spill.
+        for (int t = 0; t < ntiles; t += 2) {
             body(st0, st1, t);
             body(st1, st0, t + 1);
         }
-        if (t < ntiles) body(st0, st1, t);
         __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads into dead stages have landed
     }
     __syncthreads();
 
-    // Epilogue through LDS, as gemm_bf16_256's (waves 0-1 stage in st0, waves 2-3 in st1).
+    if constexpr (!DUAL) {
+        // Epilogue through LDS in two passes of 128 x 64 columns per wave (waves 0-1 stage in st0,
+        // waves 2-3 in st1, 32 KB each): 16 lanes then read a whole 256-byte staged row, so every
+        // store covers whole 128-byte lines of a BF16 (or FP32) output row. Row r's columns sit
+        // at c ^ 32 ((r >> 2) & 1): the two rows one accumulator write instruction touches
+        // (4 apart) then fall in different banks.
+        constexpr int EC2 = 64, EP2 = EC2 * 4;
+        static_assert(2 * WT * EP2 <= STAGE, "epilogue staging fits in the operand stages");
+        char *wl2 = (wave < 2 ? st0 : st1) + (wave & 1) * (WT * EP2);
+        // A lane's accumulator rows all have bit 2 equal to lane / 32, so its swizzle is per lane.
+        float *wlane = (float *)(wl2 + (lane >> 5) * 4 * EP2 + (lane & 31) * 4) + ((lane >> 5) << 5);
+#pragma unroll
+        for (int hp = 0; hp < F / 2; ++hp) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int i = 0; i < F; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int rr = i * 32 + (r >> 2) * 8 + (r & 3);  // row less the lane's 4 (lane / 32)
+                        // column hh * 32 + lane % 32, bit 5 flipped for odd lane / 32: one XOR per lane,
+                        // folded into wlane for hh = 0 and undone (^ 32 = +-32) for hh = 1.
+                        float *dst = wlane + rr * (EP2 / 4) + (hh ? (((lane >> 5) & 1) ? -32 : 32) : 0);
+                        *dst = acc[i][2 * hp + hh][r];
+                    }
+            __syncthreads();
+#pragma unroll 4
+            for (int it = 0; it < WT * EC2 / 256; ++it) {
+                const int e = (it * 64 + lane) * 4;
+                const int rl = e / EC2, cl = e % EC2;  // rl = 4 it + lane / 16: bit 2 of rl is it & 1
+                const f32x4 v = *(const f32x4 *)(wl2 + rl * EP2 + ((cl ^ ((it & 1) << 5)) * 4));
+                finish4<false>(p, v, m0 + wm * WT + rl, n0 + wn * WT + hp * EC2 + cl, coff, z);
+            }
+            __syncthreads();
+        }
+        return;
+    }
+    // SwiGLU epilogue through LDS, as gemm_bf16_256's (waves 0-1 stage in st0, waves 2-3 in st1).
     constexpr int EC = 32, EP = EC * 4 + 16;
     static_assert(2 * WT * EP <= STAGE, "epilogue staging fits in the operand stages");
     char *wl = (wave < 2 ? st0 : st1) + (wave & 1) * (WT * EP);
@@ -1242,14 +1279,16 @@ bool tiles_exact(const GemmArgs &a, int bm, int bn, int bk) {
 }
 
 
-// The direct-to-LDS kernel takes whole tiles without epilogue masks or k limits, and 32-bit buffer
-// offsets: a k-contiguous operand's 256 rows, or an mn-contiguous operand's k range, within 2 GiB.
+// The direct-to-LDS kernel takes whole tiles without epilogue masks or k limits, an even number of
+// k-tiles per split, and 32-bit buffer offsets: a k-contiguous operand's 256 rows, or an
+// mn-contiguous operand's k range, within 2 GiB.
 bool dtl_applicable(bool ta, bool tb, const GemmArgs &a) {
     auto fits = [&](bool kcontig, int64_t ld) {
         return kcontig ? ld * 2 * 256 < (1ll << 31) : a.k_per_split * ld * 2 < (1ll << 31);
     };
     return a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.swiglu_bwd && !a.xent_stats && !a.a_kscale &&
            (!a.dual || (!ta && tb)) && tiles_exact(a, 256, a.dual ? 128 : 256, ET<uint16_t>::BK) &&
+           a.k_per_split % (2 * ET<uint16_t>::BK) == 0 && a.K % (2 * ET<uint16_t>::BK) == 0 &&
            fits(!ta, a.lda) && fits(tb, a.ldb) && a.K * 2 < (1ll << 31);
 }
 
