@@ -527,6 +527,9 @@ def main() -> int:
                     help="run only the complete TINY training step, graph-replayed (for kernel traces)")
     ap.add_argument("--bf16-square", action="store_true",
                     help="run only the BF16 4096^3 and 8192^3 GEMMs, NN/NT/TN (for rocprofv3 --pmc)")
+    ap.add_argument("--medium-step", action="store_true",
+                    help="run only config 4, the medium BF16 step (graph replay, single stream, and one "
+                         "profiled eager step; for rocprofv3)")
     ap.add_argument("--attention", action="store_true",
                     help="run only the fused attention forward + backward, config 3 BF16 [16,8,1024,64] and the "
                          "TINY FP32 shape [16,4,256,64], causal, --steps times each (for rocprofv3)")
@@ -538,7 +541,7 @@ def main() -> int:
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: launched with WORLD_SIZE > 1; this build runs on one GPU only", file=sys.stderr)
         return 2
-    if os.environ.get("IRONTENSOR_LIB") and not args.attention:
+    if os.environ.get("IRONTENSOR_LIB") and not (args.attention or args.medium_step or args.bf16_square):
         print("bench.py: IRONTENSOR_LIB is set; the bench times only the in-tree library "
               "(irontensor_amd/libirontensor_hip.so), unset it", file=sys.stderr)
         return 2
@@ -563,6 +566,9 @@ def main() -> int:
         return 0
     if args.attention:
         print(json.dumps(attention_only(it, Timer(ctx), args.steps)), flush=True)
+        return 0
+    if args.medium_step:
+        print(json.dumps(extra_med_step(it, Timer(ctx), steps=args.steps, warmup=args.warmup)), flush=True)
         return 0
     if args.train_only:
         print(json.dumps({"train_step": train_step_figures(it, Timer(ctx), args.steps, args.warmup)}), flush=True)

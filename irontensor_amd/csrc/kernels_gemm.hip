@@ -1180,12 +1180,42 @@ void gemm_bf16_dtl(const GemmArgs p) {
                         *dst = acc[i][2 * hp + hh][r];
                     }
             __syncthreads();
+            // Lane reads row 4 it + lane / 16 of the pass, columns cl .. cl + 3; bit 2 of the row is it & 1.
+            const int cl = (lane & 15) * 4;
+            const int64_t row0 = m0 + wm * WT + (lane >> 4), col = n0 + wn * WT + hp * EC2 + cl;
+            if (p.splits > 1) {
+                // split-K partial sums: plain f32 rows of N
+                float *dst = p.partial + (z * p.M + row0) * p.N + col;
 #pragma unroll 4
-            for (int it = 0; it < WT * EC2 / 256; ++it) {
-                const int e = (it * 64 + lane) * 4;
-                const int rl = e / EC2, cl = e % EC2;  // rl = 4 it + lane / 16: bit 2 of rl is it & 1
-                const f32x4 v = *(const f32x4 *)(wl2 + rl * EP2 + ((cl ^ ((it & 1) << 5)) * 4));
-                finish4<false>(p, v, m0 + wm * WT + rl, n0 + wn * WT + hp * EC2 + cl, coff, z);
+                for (int it = 0; it < WT * EC2 / 256; ++it, dst += 4 * p.N)
+                    *(f32x4 *)dst = *(const f32x4 *)(wl2 + (4 * it + (lane >> 4)) * EP2 + ((cl ^ ((it & 1) << 5)) * 4));
+            } else if (p.c_vec_ok && !p.row_scale && p.beta == 0.f && !p.rope_table) {
+                // the common epilogue: alpha (and a column bias) only, with one base pointer per pass
+                f32x4 bias = {0.f, 0.f, 0.f, 0.f};
+                if (p.has_bias) bias = f32x4{p.bias[col], p.bias[col + 1], p.bias[col + 2], p.bias[col + 3]};
+                const int64_t idx = coff + row0 * p.ldc + col;
+                if (p.out_bf16) {
+                    uint16_t *dst = (uint16_t *)p.C + idx;
+#pragma unroll 4
+                    for (int it = 0; it < WT * EC2 / 256; ++it, dst += 4 * p.ldc) {
+                        const f32x4 v = *(const f32x4 *)(wl2 + (4 * it + (lane >> 4)) * EP2 + ((cl ^ ((it & 1) << 5)) * 4)) *
+                                            p.alpha + bias;
+                        *(u32x2 *)dst = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    }
+                } else {
+                    float *dst = (float *)p.C + idx;
+#pragma unroll 4
+                    for (int it = 0; it < WT * EC2 / 256; ++it, dst += 4 * p.ldc)
+                        *(f32x4 *)dst = *(const f32x4 *)(wl2 + (4 * it + (lane >> 4)) * EP2 + ((cl ^ ((it & 1) << 5)) * 4)) *
+                                            p.alpha + bias;
+                }
+            } else {
+#pragma unroll 4
+                for (int it = 0; it < WT * EC2 / 256; ++it) {
+                    const int rl = 4 * it + (lane >> 4);
+                    const f32x4 v = *(const f32x4 *)(wl2 + rl * EP2 + ((cl ^ ((it & 1) << 5)) * 4));
+                    finish4<false>(p, v, m0 + wm * WT + rl, col, coff, z);
+                }
             }
             __syncthreads();
         }
