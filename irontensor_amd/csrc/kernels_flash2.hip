@@ -463,31 +463,29 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
         const char *qt = st, *dot = st + TB;
         const float *nl2 = (const float *)(st + 2 * TB), *ndl = nl2 + TR;
         const int q0 = (qb0 + t) * TR;
-        // S = Q.K^T and dP = dO.V^T: block qh holds queries 32qh + 8 (j / 4) + 4h + j % 4 of key.
-        // dP accumulates from -rowsum(dO * O) of those queries, so the MFMA leaves dP - rowsum.
-        f32x16 s[2] = {zero16(), zero16()}, dp[2];
+        const bool diag = p.causal && q0 < kb * RB + RB;
+        const int kq = key - q0;  // this key against query row r of the tile: masked when kq > r
+        // One 32-query half of the tile at a time (S, dP, P, dS of half qh live together, not both
+        // halves), which keeps the kernel within three waves' registers per SIMD.
 #pragma unroll
-        for (int qh = 0; qh < 2; ++qh)
+        for (int qh = 0; qh < 2; ++qh) {
+            // S = Q.K^T and dP = dO.V^T: queries 32qh + 8 (j / 4) + 4h + j % 4 of this lane's key;
+            // dP accumulates from -rowsum(dO * O) of those queries.
+            f32x16 sv = zero16(), dpv;
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
                 const f32x4 v = *(const f32x4 *)(ndl + 32 * qh + 8 * jj + 4 * h);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dp[qh][4 * jj + e] = v[e];
+                for (int e = 0; e < 4; ++e) dpv[4 * jj + e] = v[e];
             }
-#pragma unroll
-        for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                s[qh] = mfma32(frag_rm(qt, 32 * qh, ks, lane), kf[ks], s[qh]);
-                dp[qh] = mfma32(frag_rm(dot, 32 * qh, ks, lane), vf[ks], dp[qh]);
+                sv = mfma32(frag_rm(qt, 32 * qh, ks, lane), kf[ks], sv);
+                dpv = mfma32(frag_rm(dot, 32 * qh, ks, lane), vf[ks], dpv);
             }
-        // P = exp2(S scale log2 e - LSE log2 e), zero for queries before this key (causal). Rows
-        // past seq_q have zero Q and dO (and read as zero from the workspace rows): they add nothing
-        // to dK or dV.
-        const bool diag = p.causal && q0 < kb * RB + RB;
-        const int kq = key - q0;  // this key against query row r of the tile: masked when kq > r
-#pragma unroll
-        for (int qh = 0; qh < 2; ++qh)
+            // P = exp2(S scale log2 e - LSE log2 e), zero for queries before this key (causal); rows
+            // past seq_q have zero Q and dO (and read as zero from the workspace rows): they add
+            // nothing to dK or dV. dS = P (dP - rowsum).
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
                 const int r0 = 32 * qh + 8 * jj + 4 * h;
@@ -495,26 +493,27 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = 4 * jj + e;
-                    float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qh][j], c2, lv[e]));
+                    float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], c2, lv[e]));
                     if (diag) pr = kq > r0 + e ? 0.f : pr;
-                    s[qh][j] = pr;
-                    dp[qh][j] = pr * dp[qh][j];
+                    sv[j] = pr;
+                    dpv[j] = pr * dpv[j];
                 }
             }
-        // dV^T (d x keys) += dO^T (d x queries) . P;  dK^T += Q^T . dS
-        u32x4 pf[4], df[4];
+            // dV^T (d x keys) += dO^T (d x queries) . P;  dK^T += Q^T . dS  (query chunks 2qh, 2qh + 1)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            pf[c] = pack_chunk(s, c);
-            df[c] = pack_chunk(dp, c);
-        }
+            for (int cc = 0; cc < 2; ++cc) {
+                const u32x4 pf = u32x4{pack_bf16x2(sv[8 * cc], sv[8 * cc + 1]), pack_bf16x2(sv[8 * cc + 2], sv[8 * cc + 3]),
+                                       pack_bf16x2(sv[8 * cc + 4], sv[8 * cc + 5]), pack_bf16x2(sv[8 * cc + 6], sv[8 * cc + 7])};
+                const u32x4 df = u32x4{pack_bf16x2(dpv[8 * cc], dpv[8 * cc + 1]), pack_bf16x2(dpv[8 * cc + 2], dpv[8 * cc + 3]),
+                                       pack_bf16x2(dpv[8 * cc + 4], dpv[8 * cc + 5]),
+                                       pack_bf16x2(dpv[8 * cc + 6], dpv[8 * cc + 7])};
 #pragma unroll
-        for (int dh = 0; dh < 2; ++dh)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                dv[dh] = mfma32(frag_tr(dot, 32 * dh, 16 * c, lane), pf[c], dv[dh]);
-                dk[dh] = mfma32(frag_tr(qt, 32 * dh, 16 * c, lane), df[c], dk[dh]);
+                for (int dh = 0; dh < 2; ++dh) {
+                    dv[dh] = mfma32(frag_tr(dot, 32 * dh, 16 * (2 * qh + cc), lane), pf, dv[dh]);
+                    dk[dh] = mfma32(frag_tr(qt, 32 * dh, 16 * (2 * qh + cc), lane), df, dk[dh]);
+                }
             }
+        }
     });
     if (kok) {
         float *dK = p.dK + hk.base(bh) + (int64_t)key * p.kv_rs;
