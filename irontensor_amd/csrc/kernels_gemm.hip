@@ -25,6 +25,7 @@
 //   * Tiles are enumerated XCD-aware: the 8 XCDs each receive a contiguous range of the grouped
 //     tile order, so blocks sharing A rows or B columns hit the same L2.
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <string>
 #include <type_traits>
@@ -320,17 +321,24 @@ __device__ __forceinline__ void mma(f32x4 &acc, const u32x4 &a, const u32x4 &b) 
     }
 }
 
-// Tile order: XCD-aware remap then GROUP_M-grouped raster.
-__device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int &tm, int &tn) {
-    constexpr int NXCD = 8, GROUP = 8;
-    const int total = tiles_m * tiles_n;
-    if (total % NXCD == 0) pid = (pid % NXCD) * (total / NXCD) + pid / NXCD;
+// Grouped raster order: tile `idx` of groups of 8 tile rows, column-major within a group.
+__device__ __forceinline__ void raster_tile(int idx, int tiles_m, int tiles_n, int &tm, int &tn) {
+    constexpr int GROUP = 8;
     const int span = GROUP * tiles_n;
-    const int first_m = (pid / span) * GROUP;
+    const int first_m = (idx / span) * GROUP;
     const int gsize = min(tiles_m - first_m, GROUP);
-    const int in = pid % span;
+    const int in = idx % span;
     tm = first_m + in % gsize;
     tn = in / gsize;
+}
+
+// Tile order: XCD-aware remap (workgroup w runs on XCD w % 8, which then takes a contiguous range
+// of the grouped order) then the grouped raster.
+__device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int &tm, int &tn) {
+    constexpr int NXCD = 8;
+    const int total = tiles_m * tiles_n;
+    if (total % NXCD == 0) pid = (pid % NXCD) * (total / NXCD) + pid / NXCD;
+    raster_tile(pid, tiles_m, tiles_n, tm, tn);
 }
 
 // Final value of one output element (alpha, beta, bias, causal), shared by the GEMM epilogue and
@@ -1043,145 +1051,140 @@ struct DtlOperand {
     }
 };
 
-template <bool TA, bool TB, bool DUAL = false>
-__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void gemm_bf16_dtl(const GemmArgs p) {
-    // DUAL (SwiGLU, Y = X.W^T only): the B stage's rows 0..127 are 128 gate-weight rows (loaded
-    // by waves 0-1) and rows 128..255 the same rows of the up weight (waves 2-3), so waves wn = 0
-    // accumulate gate and wn = 1 up for one 256 x 128 output tile; the epilogue pairs them.
-    static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
-    using T = uint16_t;
-    constexpr int BM = 256, BN = 256, BK = 64, WT = 128, F = 4;
-    constexpr int TILE = BM * BK * 2;  // bytes of one operand in one stage (32 KB)
-    constexpr int STAGE = 2 * TILE;
+// The k loop of one tile: acc = op(A)[m0.., kb..] . op(B)[.., n0..] over `ntiles` k-tiles (even).
+// A and B point at element (row 0, k kb) of the tile's operands; `krange` bounds an mn-contiguous
+// operand's buffer. The caller synchronises the block before (the stages may still be read) and
+// after (the epilogue reuses them).
+template <bool TA, bool TB, bool DUAL>
+__device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *st0, char *st1, const uint16_t *A,
+                                         const uint16_t *B, int64_t krange, int ntiles, f32x16 (&acc)[4][4],
+                                         int wave, int lane) {
+    constexpr int BN = 256, BK = 64, WT = 128, F = 4;
+    constexpr int TILE = 256 * BK * 2;
     using OA = DtlOperand<!TA>;
     using OB = DtlOperand<TB>;
-    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
-    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    int tm, tn;
-    map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int64_t z = blockIdx.y;
-    const int64_t b = z % p.batch, split = z / p.batch;
-    const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (DUAL ? BN / 2 : BN);
-    const int64_t coff = bo * p.sC_out + bi * p.sC_in;
-    const int64_t kb = split * p.k_per_split;
-    const int64_t ke = min(p.K, kb + p.k_per_split);
-    const int ntiles = ke > kb ? (int)((ke - kb) / BK) : 0;
-
     const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    f32x16 acc[F][F];
 #pragma unroll
     for (int i = 0; i < F; ++i)
 #pragma unroll
         for (int j = 0; j < F; ++j) acc[i][j] = zero;
+    if (ntiles <= 0) return;
+    OA oa;
+    OB ob;
+    oa.init(A, p.lda, krange, wave, lane);
+    ob.init(B, p.ldb, krange, wave, lane, DUAL && wave >= 2 ? BN / 2 : 0);
+    const int last = ntiles - 1;
+    auto issue = [&](int t, char *stage) {
+        const int64_t kk = (int64_t)min(t, last) * BK;
+        oa.issue(stage, kk, wave);
+        ob.issue(stage + TILE, kk, wave);
+    };
+    u32x4 fa0[F], fb0[F], fa1[F], fb1[F];
+    auto frags = [&](u32x4 (&fa)[F], u32x4 (&fb)[F], const char *st, int ks) {
+#pragma unroll
+        for (int i = 0; i < F; ++i) fa[i] = OA::frag(st, wm * WT + i * 32, ks, lane);
+#pragma unroll
+        for (int j = 0; j < F; ++j) fb[j] = OB::frag(st + TILE, wn * WT + j * 32, ks, lane);
+    };
+    auto mfma16 = [&](const u32x4 (&fa)[F], const u32x4 (&fb)[F]) {
+#pragma unroll
+        for (int i = 0; i < F; ++i)
+#pragma unroll
+            for (int j = 0; j < F; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8, fa[i]), __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
+    };
+    // DS reads per MFMA pair (a fragment set is 8 fragments, an mn-contiguous one two reads).
+    constexpr int DSR = (4 * (TA ? 2 : 1) + 4 * (TB ? 1 : 2) + 7) / 8;
+    // Tile t from `cur` (its k-step 0 fragments already in fa0/fb0); tile t+1 is streaming into
+    // `nxt`; the loads of tile t+2 go into `cur` once every wave has passed the barrier.
+    auto body = [&](char *cur, char *nxt, int t) {
+        frags(fa1, fb1, cur, 1);
+        mfma16(fa0, fb0);
+        frags(fa0, fb0, cur, 2);
+        mfma16(fa1, fb1);
+        frags(fa1, fb1, cur, 3);
+        mfma16(fa0, fb0);
+        // k-steps 0..2, each step's MFMAs interleaved with the next step's fragment reads.
+#pragma unroll
+        for (int g = 0; g < 24; ++g) {
+            __builtin_amdgcn_sched_group_barrier(sg::DS_READ, DSR, 0);
+            __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile t+1 landed, `cur` read
+        __syncthreads();
+        issue(t + 2, cur);
+        // k-step 3 with the next tile's first fragment reads and the loads of tile t+2.
+        frags(fa0, fb0, nxt, 0);
+        mfma16(fa1, fb1);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            __builtin_amdgcn_sched_group_barrier(sg::DS_READ, DSR, 0);
+            __builtin_amdgcn_sched_group_barrier(sg::VMEM_READ, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
+        }
+    };
+    issue(0, st0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();
+    issue(1, st1);
+    frags(fa0, fb0, st0, 0);
+    // An even number of k-tiles (dtl_applicable): no odd tail body, whose prefetched fragments
+    // would stay live past the loop and spill.
+    for (int t = 0; t < ntiles; t += 2) {
+        body(st0, st1, t);
+        body(st1, st0, t + 1);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads into dead stages have landed
+}
 
-    if (ntiles > 0) {
-        const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in + (TA ? kb * p.lda + m0 : m0 * p.lda + kb);
-        const T *Bm = (const T *)(DUAL && wave >= 2 ? p.B2 : p.B);
-        const T *B = Bm + bo * p.sB_out + bi * p.sB_in + (TB ? n0 * p.ldb + kb : kb * p.ldb + n0);
-        OA oa;
-        OB ob;
-        oa.init(A, p.lda, ke - kb, wave, lane);
-        ob.init(B, p.ldb, ke - kb, wave, lane, DUAL && wave >= 2 ? BN / 2 : 0);
-        const int last = ntiles - 1;
-        auto issue = [&](int t, char *stage) {
-            const int64_t kk = (int64_t)min(t, last) * BK;
-            oa.issue(stage, kk, wave);
-            ob.issue(stage + TILE, kk, wave);
-        };
-        u32x4 fa0[F], fb0[F], fa1[F], fb1[F];
-        auto frags = [&](u32x4 (&fa)[F], u32x4 (&fb)[F], const char *st, int ks) {
+// Epilogue of one tile of gemm_bf16_dtl (begins with a block barrier: the stages are reused).
+// Two passes of 128 x 64 columns per wave (waves 0-1 stage in st0, waves 2-3 in st1, 32 KB each):
+// 16 lanes then read a whole 256-byte staged row, so every store covers whole 128-byte lines of a
+// BF16 (or FP32) output row. Row r's columns sit at c ^ 32 ((r >> 2) & 1): the two rows one
+// accumulator write instruction touches (4 apart) then fall in different banks. In the SwiGLU form
+// the gate wave (wn = 0) and the up wave (wn = 1) of a row half stage the same output columns and
+// then finish 64 rows each of the pair.
+template <bool DUAL>
+__device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char *st1, const f32x16 (&acc)[4][4],
+                                             int64_t m0, int64_t n0, int64_t coff, int64_t z, int wave, int lane) {
+    constexpr int WT = 128, F = 4, STAGE = 2 * 256 * 64 * 2;
+    constexpr int EC2 = 64, EP2 = EC2 * 4;
+    static_assert(2 * WT * EP2 <= STAGE, "epilogue staging fits in the operand stages");
+    const int wm = wave >> 1, wn = wave & 1;
+    __syncthreads();
+    char *wl2 = (wave < 2 ? st0 : st1) + (wave & 1) * (WT * EP2);
+    // A lane's accumulator rows all have bit 2 equal to lane / 32, so its swizzle is per lane.
+    float *wlane = (float *)(wl2 + (lane >> 5) * 4 * EP2 + (lane & 31) * 4) + ((lane >> 5) << 5);
 #pragma unroll
-            for (int i = 0; i < F; ++i) fa[i] = OA::frag(st, wm * WT + i * 32, ks, lane);
+    for (int hp = 0; hp < F / 2; ++hp) {
 #pragma unroll
-            for (int j = 0; j < F; ++j) fb[j] = OB::frag(st + TILE, wn * WT + j * 32, ks, lane);
-        };
-        auto mfma16 = [&](const u32x4 (&fa)[F], const u32x4 (&fb)[F]) {
+        for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int i = 0; i < F; ++i)
 #pragma unroll
-                for (int j = 0; j < F; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        __builtin_bit_cast(bf16x8, fa[i]), __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
-        };
-        // DS reads per MFMA pair (a fragment set is 8 fragments, an mn-contiguous one two reads).
-        constexpr int DSR = (4 * (TA ? 2 : 1) + 4 * (TB ? 1 : 2) + 7) / 8;
-        // Tile t from `cur` (its k-step 0 fragments already in fa0/fb0); tile t+1 is streaming into
-        // `nxt`; the loads of tile t+2 go into `cur` once every wave has passed the barrier.
-        auto body = [&](char *cur, char *nxt, int t) {
-            frags(fa1, fb1, cur, 1);
-            mfma16(fa0, fb0);
-            frags(fa0, fb0, cur, 2);
-            mfma16(fa1, fb1);
-            frags(fa1, fb1, cur, 3);
-            mfma16(fa0, fb0);
-            // k-steps 0..2, each step's MFMAs interleaved with the next step's fragment reads.
-#pragma unroll
-            for (int g = 0; g < 24; ++g) {
-                __builtin_amdgcn_sched_group_barrier(sg::DS_READ, DSR, 0);
-                __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
-            }
-            __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile t+1 landed, `cur` read
-            __syncthreads();
-            issue(t + 2, cur);
-            // k-step 3 with the next tile's first fragment reads and the loads of tile t+2.
-            frags(fa0, fb0, nxt, 0);
-            mfma16(fa1, fb1);
-#pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                __builtin_amdgcn_sched_group_barrier(sg::DS_READ, DSR, 0);
-                __builtin_amdgcn_sched_group_barrier(sg::VMEM_READ, 2, 0);
-                __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
-            }
-        };
-        issue(0, st0);
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+                for (int r = 0; r < 16; ++r) {
+                    const int rr = i * 32 + (r >> 2) * 8 + (r & 3);  // row less the lane's 4 (lane / 32)
+                    // column hh * 32 + lane % 32, bit 5 flipped for odd lane / 32: one XOR per lane,
+                    // folded into wlane for hh = 0 and undone (^ 32 = +-32) for hh = 1.
+                    float *dst = wlane + rr * (EP2 / 4) + (hh ? (((lane >> 5) & 1) ? -32 : 32) : 0);
+                    *dst = acc[i][2 * hp + hh][r];
+                }
         __syncthreads();
-        issue(1, st1);
-        frags(fa0, fb0, st0, 0);
-        // An even number of k-tiles (dtl_applicable): no odd tail body, whose prefetched fragments
-        // would stay live past the loop and spill.
-        for (int t = 0; t < ntiles; t += 2) {
-            body(st0, st1, t);
-            body(st1, st0, t + 1);
-        }
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads into dead stages have landed
-    }
-    __syncthreads();
-
-    if constexpr (!DUAL) {
-        // Epilogue through LDS in two passes of 128 x 64 columns per wave (waves 0-1 stage in st0,
-        // waves 2-3 in st1, 32 KB each): 16 lanes then read a whole 256-byte staged row, so every
-        // store covers whole 128-byte lines of a BF16 (or FP32) output row. Row r's columns sit
-        // at c ^ 32 ((r >> 2) & 1): the two rows one accumulator write instruction touches
-        // (4 apart) then fall in different banks.
-        constexpr int EC2 = 64, EP2 = EC2 * 4;
-        static_assert(2 * WT * EP2 <= STAGE, "epilogue staging fits in the operand stages");
-        char *wl2 = (wave < 2 ? st0 : st1) + (wave & 1) * (WT * EP2);
-        // A lane's accumulator rows all have bit 2 equal to lane / 32, so its swizzle is per lane.
-        float *wlane = (float *)(wl2 + (lane >> 5) * 4 * EP2 + (lane & 31) * 4) + ((lane >> 5) << 5);
-#pragma unroll
-        for (int hp = 0; hp < F / 2; ++hp) {
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                for (int i = 0; i < F; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int rr = i * 32 + (r >> 2) * 8 + (r & 3);  // row less the lane's 4 (lane / 32)
-                        // column hh * 32 + lane % 32, bit 5 flipped for odd lane / 32: one XOR per lane,
-                        // folded into wlane for hh = 0 and undone (^ 32 = +-32) for hh = 1.
-                        float *dst = wlane + rr * (EP2 / 4) + (hh ? (((lane >> 5) & 1) ? -32 : 32) : 0);
-                        *dst = acc[i][2 * hp + hh][r];
-                    }
-            __syncthreads();
-            // Lane reads row 4 it + lane / 16 of the pass, columns cl .. cl + 3; bit 2 of the row is it & 1.
-            const int cl = (lane & 15) * 4;
+        // Lane reads row 4 it + lane / 16 of the pass, columns cl .. cl + 3; bit 2 of the row is it & 1.
+        const int cl = (lane & 15) * 4;
+        if constexpr (DUAL) {
+            const char *gl = wm == 0 ? st0 : st1, *ul = gl + WT * EP2;
+            const int64_t col = n0 + hp * EC2 + cl;
+#pragma unroll 4
+            for (int it = wn * 16; it < wn * 16 + 16; ++it) {
+                const int rl = 4 * it + (lane >> 4);
+                const int off = rl * EP2 + ((cl ^ ((it & 1) << 5)) * 4);
+                finish_swiglu4<false>(p, *(const f32x4 *)(gl + off), *(const f32x4 *)(ul + off), m0 + wm * WT + rl,
+                                      col, coff);
+            }
+        } else {
             const int64_t row0 = m0 + wm * WT + (lane >> 4), col = n0 + wn * WT + hp * EC2 + cl;
             if (p.splits > 1) {
                 // split-K partial sums: plain f32 rows of N
@@ -1217,46 +1220,40 @@ void gemm_bf16_dtl(const GemmArgs p) {
                     finish4<false>(p, v, m0 + wm * WT + rl, col, coff, z);
                 }
             }
-            __syncthreads();
-        }
-        return;
-    }
-    // SwiGLU epilogue through LDS, as gemm_bf16_256's (waves 0-1 stage in st0, waves 2-3 in st1).
-    constexpr int EC = 32, EP = EC * 4 + 16;
-    static_assert(2 * WT * EP <= STAGE, "epilogue staging fits in the operand stages");
-    char *wl = (wave < 2 ? st0 : st1) + (wave & 1) * (WT * EP);
-#pragma unroll
-    for (int h = 0; h < F; ++h) {
-#pragma unroll
-        for (int i = 0; i < F; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int rl = i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                const int cl = lane & 31;
-                *(float *)(wl + rl * EP + cl * 4) = acc[i][h][r];
-            }
-        __syncthreads();
-        if constexpr (DUAL) {
-            // The two waves of row half wm (gate: wn = 0, up: wn = 1) finish its 128 x 32 slice.
-            const char *gl = (wm == 0 ? st0 : st1), *ul = gl + WT * EP;
-            const int pt = wn * 64 + lane;
-            for (int it = 0; it < WT * EC / 512; ++it) {
-                const int e = (it * 128 + pt) * 4;
-                const int rl = e / EC, cl = e % EC;
-                finish_swiglu4<false>(p, *(const f32x4 *)(gl + rl * EP + cl * 4),
-                                      *(const f32x4 *)(ul + rl * EP + cl * 4), m0 + wm * WT + rl, n0 + h * EC + cl,
-                                      coff);
-            }
-        } else {
-            for (int it = 0; it < WT * EC / 256; ++it) {
-                const int e = (it * 64 + lane) * 4;
-                const int rl = e / EC, cl = e % EC;
-                const f32x4 v = *(const f32x4 *)(wl + rl * EP + cl * 4);
-                finish4<false>(p, v, m0 + wm * WT + rl, n0 + wn * WT + h * EC + cl, coff, z);
-            }
         }
         __syncthreads();
     }
+}
+
+template <bool TA, bool TB, bool DUAL = false>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_dtl(const GemmArgs p) {
+    // DUAL (SwiGLU, Y = X.W^T only): the B stage's rows 0..127 are 128 gate-weight rows (loaded
+    // by waves 0-1) and rows 128..255 the same rows of the up weight (waves 2-3), so waves wn = 0
+    // accumulate gate and wn = 1 up for one 256 x 128 output tile; the epilogue pairs them.
+    static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
+    using T = uint16_t;
+    constexpr int BM = 256, BN = 256, BK = 64, F = 4;
+    constexpr int STAGE = 2 * BM * BK * 2;
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tm, tn;
+    map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int64_t z = blockIdx.y;
+    const int64_t b = z % p.batch, split = z / p.batch;
+    const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (DUAL ? BN / 2 : BN);
+    const int64_t kb = split * p.k_per_split;
+    const int64_t ke = min(p.K, kb + p.k_per_split);
+    const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in + (TA ? kb * p.lda + m0 : m0 * p.lda + kb);
+    const T *Bm = (const T *)(DUAL && wave >= 2 ? p.B2 : p.B);
+    const T *B = Bm + bo * p.sB_out + bi * p.sB_in + (TB ? n0 * p.ldb + kb : kb * p.ldb + n0);
+    f32x16 acc[F][F];
+    dtl_tile<TA, TB, DUAL>(p, st0, st1, A, B, ke - kb, ke > kb ? (int)((ke - kb) / BK) : 0, acc, wave, lane);
+    dtl_epilogue<DUAL>(p, st0, st1, acc, m0, n0, bo * p.sC_out + bi * p.sC_in, z, wave, lane);
 }
 
 // Deterministic split-K reduction: partial sums are added in split order.
@@ -1435,18 +1432,22 @@ struct Plan {
 //     weight gradients), which is what split-K fixes by running more blocks at once;
 //   * split-K adds its partial-sum traffic and a reduction launch.
 // Estimated seconds, lowest wins.
-Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
+Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
     struct Cand {
         int b, occ;
         double eff;
     };
     const Cand f32c[] = {{128, 2, 0.50}, {64, 4, 0.60}};
     const Cand b16c[] = {{256, 1, 0.40}, {128, 2, 0.20}, {64, 4, 0.20}};
+    // The direct-to-LDS kernel (whole 256 x 256 tiles, an even number of k-tiles per split).
+    constexpr double DTL_EFF = 0.53;
     const Cand *cands = bf16 ? b16c : f32c;
     const int ncand = bf16 ? 3 : 2;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
     const double cu_peak = (bf16 ? 2.5e15 : 157.3e12) / 256.0;  // FLOP/s per CU
-    const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = 4e12;
+    // BF16 split-K partials mostly stay in the 256 MB Infinity Cache between the GEMM and its
+    // reduction (measured: [1024,2816,8192] with 4 splits pays 10 us for 92 MB of partials).
+    const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = bf16 ? 8e12 : 4e12;
     const double step_floor = bf16 ? 1.0e-6 : 0.5e-6;
     const bool can_split = !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.no_split;
     Plan best{64, 64, 1};
@@ -1472,7 +1473,12 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus) {
             const int64_t rounds = cdiv(per_cu, cd.occ);
             const int64_t ksteps = std::max<int64_t>(1, cdiv(kps, bk));
             // A lone block on a CU whose tile could run two at once hides less latency.
-            const double eff = conc == 1 && cd.occ > 1 ? 0.9 * cd.eff : cd.eff;
+            double eff = conc == 1 && cd.occ > 1 ? 0.9 * cd.eff : cd.eff;
+            if (bf16 && cd.b == 256) {
+                GemmArgs d = a;
+                d.k_per_split = kps;
+                if (dtl_applicable(ta, tb, d)) eff = DTL_EFF;
+            }
             const double step = (a.dual ? 4.0 : 2.0) * cd.b * bn * bk / (cu_peak * eff);
             double t = rounds * (round_overhead + ksteps * std::max(conc * step, step_floor));
             if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
@@ -1526,7 +1532,14 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     }
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    const Plan plan = choose_plan(a, bf16, cus);
+    Plan plan = choose_plan(a, bf16, cus, transA, transB);
+#ifdef IT_TUNING
+    // Planner sweeps only (a tuning build): IT_PLAN="tile,splits" forces the plan.
+    if (const char *env = std::getenv("IT_PLAN")) {
+        int b = 0, sp = 0;
+        if (std::sscanf(env, "%d,%d", &b, &sp) == 2) plan = Plan{b, a.dual ? b / 2 : b, sp};
+    }
+#endif
     TileCfg cfg{plan.bm, plan.bn};
     int splits = plan.splits;
     a.tiles_m = (int)cdiv(a.M, cfg.bm);

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from irontensor_amd import synth
-from tests.numerics import BF16_FROB_TOL, FP32_TOL, frob_rel, normwise_rel, op
+from tests.numerics import BF16_FROB_TOL, FP32_TOL, bf16_out_excess, frob_rel, normwise_rel, op
 
 pytestmark = pytest.mark.gpu
 
@@ -418,6 +418,79 @@ def test_bf16_large_tile_split_k(it, m, n, k):
     assert np.array_equal(c.numpy(), exact.astype(np.float32))
     again = it.gemm(ta, tb, trans_a=True)
     assert np.array_equal(c.numpy(), again.numpy())  # ordered reduction: deterministic
+
+
+def _plan_keys(it, fn):
+    from irontensor_amd import profiler
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    out = fn()
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    return out, keys
+
+
+@pytest.mark.parametrize("ta,tb,m,n,k", [(1, 0, 1024, 2816, 8192), (0, 0, 8192, 2816, 1024), (0, 1, 8192, 1024, 1024),
+                                         (1, 1, 3072, 1024, 8192), (1, 0, 5632, 1024, 8192)])
+def test_bf16_uneven_tile_counts_exact(it, ta, tb, m, n, k):
+    """The medium step's shapes whose 256x256 tiles do not fill the CUs evenly (44, 352, 128, 48
+    and 88 tiles) in every layout, on the direct-to-LDS kernel (whole tiles, split-K or a partial
+    round): small integers are exact in every FP32 summation order, so the result must equal a
+    float64 product bit for bit, and a second run must repeat it."""
+    a = synth.small_ints(230 + m, (k, m) if ta else (m, k), -2, 2)
+    b = synth.small_ints(231 + n, (n, k) if tb else (k, n), -2, 2)
+    at, bt = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    c, keys = _plan_keys(it, lambda: it.gemm(at, bt, trans_a=bool(ta), trans_b=bool(tb)))
+    _log(f"[uneven tiles exact] ta={ta} tb={tb} {m}x{n}x{k}: {keys}")
+    assert any("_dtl" in key for key in keys), keys
+    exact = np.matmul(op(a, ta).astype(np.float64), op(b, tb).astype(np.float64))
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    again = it.gemm(at, bt, trans_a=bool(ta), trans_b=bool(tb))
+    assert np.array_equal(c.numpy(), again.numpy())
+
+
+def test_bf16_long_k_gaussian(it, oracle):
+    """The medium step's down.dW shape (K = 8192 tokens, 44 tiles, split-K) on Gaussian data: 64
+    sampled output rows within the FP32 contract of the oracle on the same BF16 operands and
+    within the BF16 contract of the unrounded product; the BF16 output equals the rounding of the
+    FP32 result to the FP32 contract."""
+    m, n, k = 1024, 2816, 8192
+    a = synth.normal(240, (k, m))
+    b = synth.normal(241, (k, n))
+    at, bt = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    c, keys = _plan_keys(it, lambda: it.gemm(at, bt, trans_a=True))
+    _log(f"[long-K gaussian] {keys}")
+    rows = np.random.default_rng(7).choice(m, 64, replace=False)
+    a_rows = np.ascontiguousarray(a[:, rows].T)
+    ref16 = oracle.gemm_bf16(oracle.f32_to_bf16(a_rows), oracle.f32_to_bf16(b), False, False)
+    got = c.numpy()[rows]
+    assert normwise_rel(got, ref16) <= FP32_TOL
+    assert frob_rel(got, oracle.gemm_f32(a_rows, b)) <= BF16_FROB_TOL
+    c16 = it.gemm(at, bt, trans_a=True, out_precision=it.Precision.BF16)
+    assert bf16_out_excess(c16.numpy()[rows], ref16) <= FP32_TOL
+
+
+def test_bf16_swiglu_medium_shape(it, oracle):
+    """The SwiGLU dual form at the medium step's gate|up projection shape (704 tiles of 256 x 128,
+    the direct-to-LDS kernel's paired epilogue): gate and up exact on small integers, h =
+    silu(gate) * up to FP32 rounding."""
+    rows, h, f = 8192, 1024, 2816
+    x = synth.small_ints(250, (rows, h), -2, 2)
+    wg = synth.small_ints(251, (f, h), -2, 2)
+    wu = synth.small_ints(252, (f, h), -2, 2)
+    (hh, g, u), keys = _plan_keys(it, lambda: it.swiglu_up(
+        it.Tensor.from_f32_as_bf16(x, x.shape), it.Tensor.from_f32_as_bf16(wg, wg.shape),
+        it.Tensor.from_f32_as_bf16(wu, wu.shape), out_precision=it.Precision.FP32))
+    _log(f"[swiglu medium] {keys}")
+    assert any("_dtl_swiglu" in key for key in keys), keys
+    xd = x.astype(np.float64)
+    g_ref = (xd @ wg.astype(np.float64).T).astype(np.float32)
+    u_ref = (xd @ wu.astype(np.float64).T).astype(np.float32)
+    assert np.array_equal(g.numpy(), g_ref)
+    assert np.array_equal(u.numpy(), u_ref)
+    rows_chk = np.arange(0, rows, 61)
+    assert normwise_rel(hh.numpy()[rows_chk], oracle.swiglu(g_ref[rows_chk], u_ref[rows_chk])) <= FP32_TOL
 
 
 def test_bf16_large_tile_epilogues(it, oracle):
