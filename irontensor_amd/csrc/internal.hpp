@@ -65,6 +65,9 @@ struct it_context {
     size_t scratch_bytes[2] = {0, 0};
     void *attn_scratch[2] = {nullptr, nullptr};
     size_t attn_scratch_bytes[2] = {0, 0};
+    // Arrival counters of kernels whose last block finishes a shared output (the decode kernel's
+    // k splits), zeroed once at allocation; every launch leaves them zero.
+    int *counters[2] = {nullptr, nullptr};
 
     // RoPE (cos, sin) tables per (seq, head_dim, base bits, position offset), built on first use
     // and kept until shutdown (every layer's forward and backward share one).
@@ -99,6 +102,9 @@ it_status join_side(it_context *ctx);
 // Grows the current stream's scratch to at least `bytes` (synchronises before freeing the old block).
 it_status ensure_scratch(it_context *ctx, size_t bytes, void **out);
 it_status ensure_attn_scratch(it_context *ctx, size_t bytes, void **out);
+// The current stream's arrival counters (COUNTERS ints, zero), allocated on first use.
+constexpr int64_t COUNTERS = 1 << 16;
+it_status ensure_counters(it_context *ctx, int **out);
 
 // Profiler hooks around one kernel launch.
 void profile_begin(it_context *ctx, const std::string &key, hipEvent_t *start_out);
@@ -196,6 +202,14 @@ struct FlashArgs {
 // Decode-shaped BF16 NT GEMM (M <= 16), HBM-bound: kernels_gemv.hip.
 bool gemv_applicable(const GemmArgs &a, bool bf16, bool transA, bool transB);
 it_status launch_gemv(hipStream_t s, const GemmArgs &a);
+// Decode-shaped BF16 GEMM with the weight stored [K, N] (NN, and TN with X stored [K, M]), M <= 16:
+// gemv_kn_splits picks the k splits; with more than one, a.partial must hold
+// splits * batch * M * N floats and `counters` one zero int per (column strip, batch item).
+bool gemv_kn_applicable(const GemmArgs &a, bool bf16, bool transA, bool transB);
+int gemv_kn_splits(const GemmArgs &a, bool transA);
+int gemv_kn_min_splits(const GemmArgs &a, bool transA);
+int64_t gemv_kn_strips(const GemmArgs &a);
+it_status launch_gemv_kn(hipStream_t s, bool transA, const GemmArgs &a, int *counters);
 
 bool flash_supported(const FlashArgs &p, int elem_bytes, bool backward);
 // BF16 forms on 32x32x16 MFMAs with direct-to-LDS tile loads (kernels_flash2.hip); the launchers of

@@ -71,6 +71,25 @@ it_status ensure_attn_scratch(it_context *ctx, size_t bytes, void **out) {
     return grow(ctx, ctx->attn_scratch[ctx->cur], ctx->attn_scratch_bytes[ctx->cur], bytes, out);
 }
 
+it_status ensure_counters(it_context *ctx, int **out) {
+    int *&f = ctx->counters[ctx->cur];
+    if (!f) {
+        if (ctx->capturing)
+            return fail(IT_ERR_INVALID, "arrival counters needed during graph capture: run the work once before capturing");
+        IT_HIP_TRY(hipMalloc(&f, COUNTERS * sizeof(int)));
+        // Synchronous zero fill at allocation (never inside a captured graph).
+        hipError_t e = hipMemset(f, 0, COUNTERS * sizeof(int));
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            (void)hipFree(f);
+            f = nullptr;
+            return fail_hip(e, "zeroing the arrival counters");
+        }
+    }
+    *out = f;
+    return IT_OK;
+}
+
 static hipEvent_t pool_event(it_context *ctx) {
     if (!ctx->event_pool.empty()) {
         hipEvent_t e = ctx->event_pool.back();
@@ -196,6 +215,7 @@ it_status it_shutdown(it_context *ctx) {
     for (int i = 0; i < 2; ++i) {
         if (ctx->scratch[i]) (void)hipFree(ctx->scratch[i]);
         if (ctx->attn_scratch[i]) (void)hipFree(ctx->attn_scratch[i]);
+        if (ctx->counters[i]) (void)hipFree(ctx->counters[i]);
     }
     (void)hipEventDestroy(ctx->fork_ev);
     (void)hipEventDestroy(ctx->join_ev);

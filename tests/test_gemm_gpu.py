@@ -326,6 +326,38 @@ def test_bf16_decode_kn_ragged(it, m, k, n, ta):
     assert np.array_equal(out.numpy(), (2.0 * exact + c0 + bias).astype(np.float32))
 
 
+@pytest.mark.parametrize("m,k,n,ta", [(1, 4096, 11008, 0), (4, 4096, 11008, 1), (16, 4096, 11008, 0),
+                                      (16, 4096, 11008, 1), (5, 1024, 1032, 1), (16, 256, 136, 0), (3, 32, 8, 0)])
+def test_bf16_decode_kn_kernel(it, m, k, n, ta):
+    """The decode kernel for a weight stored [K, N] (in-register 8 x 8 transposes feeding the MFMA,
+    k split over waves and blocks): the BASELINE decode shapes in both layouts, a last column strip
+    of 8 columns, one split and a single k chunk. Exact small integers against a float64 product,
+    BF16 output against the RNE rounding of the exact result, and the plan key names the kernel."""
+    from irontensor_amd import profiler
+    _log(f"[decode kn kernel] m={m} k={k} n={n} ta={ta}")
+    a = synth.small_ints(260 + m, (k, m) if ta else (m, k), -3, 3)
+    b = synth.small_ints(261, (k, n), -3, 3)
+    A, B = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    c = it.gemm(A, B, trans_a=bool(ta), out_precision=it.Precision.FP32)
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    _log(f"[decode kn kernel] {keys}")
+    assert any(key.startswith("gemv_bf16_TN" if ta else "gemv_bf16_NN") for key in keys), keys
+    exact = op(a, ta).astype(np.float64) @ b.astype(np.float64)
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    c16 = it.gemm(A, B, trans_a=bool(ta), out_precision=it.Precision.BF16)
+    assert np.array_equal(c16.as_bf16_slice().reshape(m, n), synth_bf16(exact))
+
+
+def synth_bf16(x):
+    """RNE rounding of float64 values (exactly representable in FP32 here) to BF16 bits."""
+    from oracle import f32_to_bf16
+    return f32_to_bf16(np.asarray(x, dtype=np.float32))
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
 def test_bf16_square_1024_against_oracle(it, oracle, ta, tb):
     """BASELINE config 5a at n = 1024 in the NN, NT and TN layouts, whole output against the oracle:
