@@ -99,23 +99,3 @@ def small_ints(seed: int, shape, lo: int, hi: int) -> np.ndarray:
     span = np.uint64(hi - lo + 1)
     vals = ((bits * span) >> np.uint64(32)).astype(np.int64) + lo
     return vals.astype(np.float32).reshape(shape)
-
-
-_POOL_SIZE = 1 << 24
-_pool_cache: dict = {}
-
-
-def pooled_normal(seed: int, shape, std: float = 1.0) -> np.ndarray:
-    """float32 N(0, std^2) values of the given shape for timing runs at large sizes: a fixed pool of
-    2^24 seeded normals, read cyclically from a seed-dependent start. Cheap to make at any size
-    (a copy, not a transform per element); neighbouring tensors share values, so use it only
-    where the values do not enter a parity check."""
-    if "pool" not in _pool_cache:
-        _pool_cache["pool"] = normal(0x5EED, (_POOL_SIZE,))
-    pool = _pool_cache["pool"]
-    n = int(np.prod(shape)) if np.ndim(shape) else int(shape)
-    start = int(splitmix64(seed, 1)[0] % np.uint64(_POOL_SIZE))
-    vals = np.resize(np.roll(pool, -start), n)
-    if std != 1.0:
-        vals = vals * np.float32(std)
-    return vals.astype(np.float32, copy=False).reshape(shape)
