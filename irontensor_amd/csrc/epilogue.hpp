@@ -25,7 +25,7 @@ __device__ __forceinline__ void store_out(void *C, int64_t idx, float v, int bf1
 // Final value of one output element (alpha, beta, bias, causal), shared by the GEMM epilogue and
 // the split-K reduction.
 __device__ __forceinline__ float silu_grad(float go, float g, float u, float &du) {
-    const float sig = 1.0f / (1.0f + expf(-g));
+    const float sig = sigmoid_fast(g);
     du = go * (g * sig);
     return go * u * (sig * (1.0f + g * (1.0f - sig)));
 }
@@ -48,7 +48,7 @@ __device__ __forceinline__ void finish_store(const GemmArgs &p, void *C, int64_t
     store_out(C, idx, v, p.out_bf16);
 }
 
-__device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
+__device__ __forceinline__ float silu(float g) { return g * sigmoid_fast(g); }
 
 // Final values of 4 consecutive output columns (the vector form of finish_store), or raw partial
 // sums for split-K. Falls back to element stores at the right edge or for unaligned outputs.

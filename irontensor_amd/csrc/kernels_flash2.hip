@@ -79,6 +79,49 @@ __device__ __forceinline__ u32x4 frag_tr(const char *tile, int c0, int k0, int l
     return u32x4{a[0], a[1], b[0], b[1]};
 }
 
+// Per-lane LDS byte offsets of the fragment reads, computed once per kernel: the swizzle depends
+// only on row bits 1..3, so the row block (a multiple of 16 rows), the k chunk of a transposed
+// read and the stage are compile-time offsets added to these (ds_read immediates). Kept opaque
+// so the compiler holds them in 8 registers instead of recomputing the swizzle for every read.
+struct FragOff {
+    uint32_t rm[4];     // frag_rm at r0 = 0, ks = 0..3
+    uint32_t tr[2][2];  // frag_tr at c0 = 32 dh, k0 = 0: rows r1 (lo) and r1 + 8 (hi)
+};
+
+__device__ __forceinline__ FragOff frag_offsets(int lane) {
+    FragOff f;
+    const int r = lane & 31;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) f.rm[ks] = (uint32_t)(r * 128 + (((2 * ks + (lane >> 5)) ^ swz(r)) << 4));
+    const int g = lane >> 4, j = lane & 15;
+    const int r1 = 4 * (g >> 1) + (j >> 2), r2 = r1 + 8, half = (j & 1) << 3;
+#pragma unroll
+    for (int dh = 0; dh < 2; ++dh) {
+        const int chunk = (32 * dh + 16 * (g & 1) + 4 * (j & 3)) >> 3;
+        f.tr[dh][0] = (uint32_t)(r1 * 128 + ((chunk ^ swz(r1)) << 4) + half);
+        f.tr[dh][1] = (uint32_t)(r2 * 128 + ((chunk ^ swz(r2)) << 4) + half);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) asm volatile("" : "+v"(f.rm[ks]));
+#pragma unroll
+    for (int dh = 0; dh < 2; ++dh) asm volatile("" : "+v"(f.tr[dh][0]), "+v"(f.tr[dh][1]));
+    return f;
+}
+
+// frag_rm(tile, r0, ks, lane) with r0 a multiple of 16.
+__device__ __forceinline__ u32x4 frag_rm_o(const char *tile, const FragOff &f, int r0, int ks) {
+    return *(const u32x4 *)(tile + r0 * 128 + f.rm[ks]);
+}
+
+// frag_tr(tile, c0, k0, lane) with c0 = 0 or 32 and k0 a multiple of 16.
+__device__ __forceinline__ u32x4 frag_tr_o(const char *tile, const FragOff &f, int c0, int k0) {
+    const int dh = c0 >> 5;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(tile + k0 * 128 + f.tr[dh][0]));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(tile + k0 * 128 + f.tr[dh][1]));
+    const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+    return u32x4{a[0], a[1], b[0], b[1]};
+}
+
 // B operand for key (or query) chunk c from a 32x32 accumulator pair: values j = 8 (c % 2) .. +7 of
 // block c / 2, rounded to BF16.
 __device__ __forceinline__ u32x4 pack_chunk(const f32x16 (&s)[2], int c) {
@@ -215,14 +258,20 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void f
         const u32x4 v = ld16(Q + (qok ? (int64_t)q * p.q_rs + 16 * ks + 8 * h : 0));
         qf[ks] = qok ? v : u32x4{0u, 0u, 0u, 0u};
     }
-    f32x16 o[2] = {zero16(), zero16()};
-    float m = -INFINITY, l = 0.f;  // running max (log2 units) used by the probabilities; this lane's sum
+    // o[0], o[1]: O^T rows d 0..31, 32..63; o[2]: row 0 accumulates the row sum of P through the
+    // same MFMAs (A = a ones row), so the softmax denominator costs no VALU adds and uses the same
+    // BF16-rounded probabilities as the numerator.
+    f32x16 o[3] = {zero16(), zero16(), zero16()};
+    float m = -INFINITY;  // running max (log2 units) used by the probabilities
+    const uint32_t one2 = (lane & 31) == 0 ? 0x3f803f80u : 0u;  // BF16 1.0 pair in row 0 only
+    const u32x4 ones = {one2, one2, one2, one2};
 
     const int kblocks = (int)((p.skv + TR - 1) / TR);
     const int nkb = p.causal ? min(kblocks, (qb * RB + RB - 1) / TR + 1) : kblocks;
     Stream sk, sv;
     sk.init(K, p.kv_rs, p.skv, wave, lane);
     sv.init(V, p.kv_rs, p.skv, wave, lane);
+    const FragOff fo = frag_offsets(lane);
     stream_tiles(st0, st1, nkb, [&](char *st, int t) {
         sk.issue(st, t, wave);
         sv.issue(st + TB, t, wave);
@@ -233,7 +282,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void f
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) s[kh] = mfma32(frag_rm(kt, 32 * kh, ks, lane), qf[ks], s[kh]);
+            for (int ks = 0; ks < 4; ++ks) s[kh] = mfma32(frag_rm_o(kt, fo, 32 * kh, ks), qf[ks], s[kh]);
         // Keys past seq_kv, and (causal) keys past the query, are -inf. Only blocks that reach past
         // the first query of this workgroup or past seq_kv hold such keys.
         const int k0 = t * TR;
@@ -260,30 +309,27 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void f
             const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
             o[0] *= alpha;
             o[1] *= alpha;
-            l *= alpha;
+            o[2][0] *= alpha;  // the row sum (the block's other entries stay zero)
             m = mn;
         }
         const float nm = m == -INFINITY ? 0.f : -m;
-        float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][j], c2, nm));
-                s[kh][j] = e;
-                ls[j & 3] += e;
-            }
-        l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-        // O^T (d x queries) += V^T (d x keys) . P^T (keys x queries)
+            for (int j = 0; j < 16; ++j) s[kh][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][j], c2, nm));
+        // O^T (d x queries) += V^T (d x keys) . P^T (keys x queries), and the row sums
         u32x4 pf[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) pf[c] = pack_chunk(s, c);
 #pragma unroll
         for (int dh = 0; dh < 2; ++dh)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) o[dh] = mfma32(frag_tr(vt, 32 * dh, 16 * c, lane), pf[c], o[dh]);
+            for (int c = 0; c < 4; ++c) o[dh] = mfma32(frag_tr_o(vt, fo, 32 * dh, 16 * c), pf[c], o[dh]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[2] = mfma32(ones, pf[c], o[2]);
     });
-    l += __shfl_xor(l, 32, 64);
+    // Row 0 of the sum block sits in lanes l < 32 (element 0); lanes l >= 32 hold row 4, zero.
+    const float l = o[2][0] + __shfl_xor(o[2][0], 32, 64);
     if (qok) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
         float *O = (float *)p.O + ho.base(bh) + (int64_t)q * p.o_rs;

@@ -573,7 +573,7 @@ __global__ __launch_bounds__(256) void scale_by_device_kernel(float *x, int64_t 
 // One block per row; VEC consecutive columns per thread (VEC = 4 when every row start is aligned
 // for 16-byte f32 / 8-byte bf16 accesses and cols % 4 == 0).
 __device__ __forceinline__ void swiglu_grad(float go, float g, float u, float &dg, float &du) {
-    const float sig = 1.0f / (1.0f + expf(-g));
+    const float sig = sigmoid_fast(g);
     const float silu = g * sig;
     du = go * silu;
     const float d_silu = sig * (1.0f + g * (1.0f - sig));

@@ -32,6 +32,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) { return __builtin_
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
+// Logistic sigmoid 1 / (1 + e^-x) from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32; a
+// few ulps): e^-x = 2^(-x log2 e). Large negative x gives 2^+inf = inf and a sigmoid of 0; NaN
+// stays NaN.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
 // acc += a . b over one fragment chunk.
 template <typename T>
 __device__ __forceinline__ void mma16(f32x4 &acc, const u32x4 &a, const u32x4 &b) {
