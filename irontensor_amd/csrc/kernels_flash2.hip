@@ -428,17 +428,21 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
             }
         // P^T = exp2(S^T scale log2 e - LSE log2 e), zero past the query (causal) and past seq_kv
         // (K and V rows there are zero, but an unmasked probability could overflow into 0 * inf).
+        // Masked scores become -inf before the exponential (exp2(-inf) = 0), in a wave-uniform
+        // branch taken only by the tiles that hold such keys.
         const int k0 = t * TR;
-        const bool edge = (p.causal && k0 + TR - 1 > qb * RB) || k0 + TR > skv;
-        const int lim = p.causal ? min(skv - 1, q) : skv - 1;
+        if ((p.causal && k0 + TR - 1 > qb * RB) || k0 + TR > skv) {
+            const int lim = p.causal ? min(skv - 1, q) : skv - 1;
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    s[kh][j] = k0 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3) > lim ? -INFINITY : s[kh][j];
+        }
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][j], c2, nl2));
-                if (edge) pr = k0 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3) > lim ? 0.f : pr;
-                dp[kh][j] = pr * dp[kh][j];
-            }
+            for (int j = 0; j < 16; ++j) dp[kh][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][j], c2, nl2)) * dp[kh][j];
         // dQ^T (d x queries) += K^T (d x keys) . dS^T (keys x queries)
         u32x4 df[4];
 #pragma unroll
@@ -529,18 +533,22 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
                 sv = mfma32(frag_rm(qt, 32 * qh, ks, lane), kf[ks], sv);
                 dpv = mfma32(frag_rm(dot, 32 * qh, ks, lane), vf[ks], dpv);
             }
-            // P = exp2(S scale log2 e - LSE log2 e), zero for queries before this key (causal); rows
-            // past seq_q have zero Q and dO (and read as zero from the workspace rows): they add
-            // nothing to dK or dV. dS = P (dP - rowsum).
+            // P = exp2(S scale log2 e - LSE log2 e), zero for queries before this key (causal: the
+            // score becomes -inf in a wave-uniform branch that only diagonal tiles take); rows past
+            // seq_q have zero Q and dO (and read as zero from the workspace rows): they add nothing
+            // to dK or dV. dS = P (dP - rowsum).
+            if (diag) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    sv[j] = kq > 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3) ? -INFINITY : sv[j];
+            }
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
-                const int r0 = 32 * qh + 8 * jj + 4 * h;
-                const f32x4 lv = *(const f32x4 *)(nl2 + r0);
+                const f32x4 lv = *(const f32x4 *)(nl2 + 32 * qh + 8 * jj + 4 * h);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = 4 * jj + e;
-                    float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], c2, lv[e]));
-                    if (diag) pr = kq > r0 + e ? 0.f : pr;
+                    const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], c2, lv[e]));
                     sv[j] = pr;
                     dpv[j] = pr * dpv[j];
                 }
