@@ -449,14 +449,21 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
         // load as zeros (and their LSE as 0), so they add nothing. A key past seq_kv only reaches
         // its own dK, dV row, which is not stored. Only the causal diagonal block masks keys above
         // the query.
-        const bool diag = p.causal && qb == kb;
+        // The mask sets the score to -inf (exp2(-inf) = 0) in a wave-uniform branch, so the other
+        // blocks run the exponentials without a compare and select per probability.
+        if (p.causal && qb == kb) {
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (key > qb * TR + mb * 16 + g * 4 + r) sp[mb][r] = -INFINITY;
+        }
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int ql_ = mb * 16 + g * 4 + r;
-                float pr = exp2_fast(sp[mb][r] * c2 - ls[ql_]);
-                if (diag && key > qb * TR + ql_) pr = 0.f;
+                const float pr = exp2_fast(sp[mb][r] * c2 - ls[ql_]);
                 sp[mb][r] = pr;
                 dp[mb][r] = pr * (dp[mb][r] - dl[ql_]);
             }
@@ -580,16 +587,21 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
         // Queries past seq_q are not stored. The causal diagonal block masks keys above the query,
         // and the last block keys past seq_kv (their K rows are zero, but an unmasked probability
         // exp2(-LSE2) could overflow and turn 0 * inf into NaN).
-        const bool edge = (p.causal && kb == qb) || (kb == nkb - 1 && p.skv % TR != 0);
+        // The masks set the score to -inf (exp2(-inf) = 0) in a wave-uniform branch that only these
+        // blocks take.
+        if ((p.causal && kb == qb) || (kb == nkb - 1 && p.skv % TR != 0)) {
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = kb * TR + mb * 16 + g * 4 + r;
+                    if (key >= p.skv || (p.causal && key > q)) sp[mb][r] = -INFINITY;
+                }
+        }
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float pr = exp2_fast(sp[mb][r] * c2 - lse2);
-                const int key = kb * TR + mb * 16 + g * 4 + r;
-                if (edge && (key >= p.skv || (p.causal && key > q))) pr = 0.f;
-                dp[mb][r] = pr * (dp[mb][r] - dl);
-            }
+            for (int r = 0; r < 4; ++r) dp[mb][r] = exp2_fast(sp[mb][r] * c2 - lse2) * (dp[mb][r] - dl);
         // dQ^T (d x q) += K^T (d x keys) . dS^T (keys x q)
 #pragma unroll
         for (int d = 0; d < 4; ++d)
