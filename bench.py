@@ -230,11 +230,20 @@ def bf16_square(it, timer, sizes) -> dict:
 
 def extra_sweep(it, timer) -> dict:
     """Config 5: BF16 square GEMMs n^3, n in {1024 .. 16384}, NN/NT/TN, BF16 out; and the decode
-    shapes M in {1, 4, 16}, K 4096, N 11008 (HBM-bound: bytes / time against 8 TB/s). The decode
-    timing rotates over DECODE_COPIES distinct weight copies (8 x 90 MB, more than the 256 MB
-    Infinity Cache), so every call streams its weight from HBM. Operands are seeded N(0,1)."""
-    P = it.Precision
+    shapes (decode_shapes)."""
     out = bf16_square(it, timer, ((1024, 50), (2048, 30), (4096, 20), (8192, 8), (16384, 3)))
+    out.update(decode_shapes(it, timer))
+    return out
+
+
+def decode_shapes(it, timer, rounds: int = 4) -> dict:
+    """Config 5b: the decode shapes M in {1, 4, 16}, K 4096, N 11008 in the NT (W [N, K]), NN and TN
+    (W [K, N]) layouts, BF16 in and out (HBM-bound: bytes / time against 8 TB/s). The timing rotates
+    over DECODE_COPIES distinct weight copies (8 x 90 MB, more than the 256 MB Infinity Cache), so
+    every call streams its weight from HBM; `rounds` passes over the copies are timed. Operands
+    are seeded N(0,1)."""
+    P = it.Precision
+    out = {}
     k, n = 4096, 11008
     copies = DECODE_COPIES
     w_nk = [_dev(it, 500 + c, (n, k), prec=P.BF16) for c in range(copies)]
@@ -249,7 +258,7 @@ def extra_sweep(it, timer) -> dict:
             for c in range(copies):
                 it.gemm(A, Bs[c], trans_a=ta, trans_b=tb, out=yo)
             ctx.sync()
-            iters = 4 * copies
+            iters = rounds * copies
             timer.start()
             for i in range(iters):
                 it.gemm(A, Bs[i % copies], trans_a=ta, trans_b=tb, out=yo)
@@ -530,6 +539,9 @@ def main() -> int:
     ap.add_argument("--medium-step", action="store_true",
                     help="run only config 4, the medium BF16 step (graph replay, single stream, and one "
                          "profiled eager step; for rocprofv3)")
+    ap.add_argument("--decode", action="store_true",
+                    help="run only the BF16 decode shapes (M 1/4/16, K 4096, N 11008; NT, NN, TN) with cold "
+                         "weights, --steps passes over the rotated copies (for rocprofv3)")
     ap.add_argument("--attention", action="store_true",
                     help="run only the fused attention forward + backward, config 3 BF16 [16,8,1024,64] and the "
                          "TINY FP32 shape [16,4,256,64], causal, --steps times each (for rocprofv3)")
@@ -541,7 +553,7 @@ def main() -> int:
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: launched with WORLD_SIZE > 1; this build runs on one GPU only", file=sys.stderr)
         return 2
-    if os.environ.get("IRONTENSOR_LIB") and not (args.attention or args.medium_step or args.bf16_square):
+    if os.environ.get("IRONTENSOR_LIB") and not (args.attention or args.medium_step or args.bf16_square or args.decode):
         print("bench.py: IRONTENSOR_LIB is set; the bench times only the in-tree library "
               "(irontensor_amd/libirontensor_hip.so), unset it", file=sys.stderr)
         return 2
@@ -566,6 +578,9 @@ def main() -> int:
         return 0
     if args.attention:
         print(json.dumps(attention_only(it, Timer(ctx), args.steps)), flush=True)
+        return 0
+    if args.decode:
+        print(json.dumps(decode_shapes(it, Timer(ctx), rounds=max(1, args.steps))), flush=True)
         return 0
     if args.medium_step:
         print(json.dumps(extra_med_step(it, Timer(ctx), steps=args.steps, warmup=args.warmup)), flush=True)
