@@ -352,6 +352,78 @@ def test_bf16_decode_kn_kernel(it, m, k, n, ta):
     assert np.array_equal(c16.as_bf16_slice().reshape(m, n), synth_bf16(exact))
 
 
+@pytest.mark.parametrize("ta", [0, 1])
+def test_bf16_decode_kn_batched_and_broadcast(it, ta):
+    """The [K, N]-weight decode kernel on batched products (3 items, each its own weight, split K:
+    the arrival counters are per strip and item) and with one weight broadcast over the batch."""
+    from irontensor_amd import profiler
+    bt, m, k, n = 3, 5, 2048, 264
+    a = synth.small_ints(270 + ta, (bt, k, m) if ta else (bt, m, k), -3, 3)
+    b = synth.small_ints(272, (bt, k, n), -3, 3)
+    A, B = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    c = it.gemm(A, B, trans_a=bool(ta))
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    _log(f"[decode kn batched] ta={ta} {keys}")
+    assert any(key.startswith("gemv_bf16_TN" if ta else "gemv_bf16_NN") and not key.endswith(" s1") for key in keys), keys
+    exact = np.matmul(op(a, ta).astype(np.float64), b.astype(np.float64))
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    b0 = b[0]
+    c2 = it.gemm(A, it.Tensor.from_f32_as_bf16(b0, b0.shape), trans_a=bool(ta))
+    assert np.array_equal(c2.numpy(), np.matmul(op(a, ta).astype(np.float64), b0.astype(np.float64)).astype(np.float32))
+
+
+def test_bf16_decode_kn_epilogue_after_split_sum(it):
+    """alpha, beta and a bias applied by the strip's last block after it adds the split partial sums
+    (NN, M = 4: eight k splits)."""
+    m, k, n = 4, 4096, 1032
+    a = synth.small_ints(280, (m, k), -3, 3)
+    b = synth.small_ints(281, (k, n), -3, 3)
+    bias = synth.small_ints(282, (n,), -4, 4)
+    c0 = synth.small_ints(283, (m, n), -4, 4)
+    A, B = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    out = it.Tensor.from_f32_slice(c0, [m, n])
+    it.gemm(A, B, alpha=2.0, beta=1.0, out=out, bias=it.Tensor.from_f32_slice(bias, [n]))
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.array_equal(out.numpy(), (2.0 * exact + c0 + bias).astype(np.float32))
+
+
+def test_bf16_decode_kn_graph_replays(it):
+    """A captured [K, N]-weight decode GEMM (split K, so the captured kernel uses the arrival
+    counters) replayed three times with eager decode GEMMs on other shapes between the replays:
+    every replay equals the eager result, so each launch leaves the counters at zero."""
+    import ctypes as C
+    from irontensor_amd import _lib
+    m, k, n = 4, 4096, 2056
+    a = synth.small_ints(290, (m, k), -3, 3)
+    b = synth.small_ints(291, (k, n), -3, 3)
+    A, B = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    ref = it.gemm(A, B).numpy()  # eager first: sizes the scratch and allocates the counters
+    out = it.Tensor.empty([m, n])
+    xo = it.Tensor.from_f32_as_bf16(synth.small_ints(292, (16, k), -3, 3), [16, k])
+    ctx = it.Context.global_()
+    ctx.sync()
+    assert ctx.lib.it_capture_begin(ctx.handle) == 0
+    it.gemm(A, B, out=out)
+    graph = C.c_void_p()
+    assert ctx.lib.it_capture_end(ctx.handle, C.byref(graph)) == 0, _lib.last_error()
+    try:
+        for rep in range(3):
+            zero = np.zeros(m * n, np.float32)
+            ctx.lib.it_memcpy_h2d(ctx.handle, C.c_void_p(out.ptr), zero.ctypes.data_as(C.c_void_p), zero.nbytes)
+            other = it.gemm(xo, B)  # eager work on the same counters between the replays
+            assert ctx.lib.it_graph_launch(ctx.handle, graph) == 0
+            ctx.sync()
+            assert np.array_equal(out.numpy(), ref), rep
+            assert other.shape() == [16, n]
+    finally:
+        ctx.lib.it_graph_destroy(graph)
+    assert np.array_equal(ref, (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32))
+
+
 def synth_bf16(x):
     """RNE rounding of float64 values (exactly representable in FP32 here) to BF16 bits."""
     from oracle import f32_to_bf16
