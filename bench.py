@@ -228,6 +228,38 @@ def bf16_square(it, timer, sizes) -> dict:
     return out
 
 
+def vs_library(it, timer, n: int = 4096, iters: int = 20) -> dict:
+    """The BF16 n^3 GEMM against AMD's library in the same process: torch.mm on two contiguous BF16
+    [n, n] tensors (served by hipBLASLt), then this library's NN, NT and TN forms; three batches of
+    `iters` launches each, TFLOP/s per batch. For same-box A/B kernel traces and counter passes."""
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
+    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
+    for _ in range(5):
+        torch.mm(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    tf = lambda ms: round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)  # noqa: E731
+    out = {"hipblaslt_torch_mm_NN": []}
+    for _ in range(3):
+        e0.record()
+        for _ in range(iters):
+            torch.mm(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        out["hipblaslt_torch_mm_NN"].append(tf(e0.elapsed_time(e1) / iters))
+    del a, b
+    P = it.Precision
+    A, B = _dev(it, 3, (n, n), prec=P.BF16), _dev(it, 4, (n, n), prec=P.BF16)
+    Cm = it.Tensor.empty([n, n], P.BF16)
+    for lay, (ta, tb) in (("NN", (False, False)), ("NT", (False, True)), ("TN", (True, False))):
+        out[f"this_{lay}"] = [tf(time_gemm(it, timer, A, B, Cm, ta, tb, iters, warm=3)) for _ in range(3)]
+    return {f"bf16_{n}_vs_library_tflops": out}
+
+
 def extra_sweep(it, timer) -> dict:
     """Config 5: BF16 square GEMMs n^3, n in {1024 .. 16384}, NN/NT/TN, BF16 out; and the decode
     shapes (decode_shapes)."""
@@ -539,6 +571,9 @@ def main() -> int:
     ap.add_argument("--medium-step", action="store_true",
                     help="run only config 4, the medium BF16 step (graph replay, single stream, and one "
                          "profiled eager step; for rocprofv3)")
+    ap.add_argument("--vs-library", action="store_true",
+                    help="time the BF16 4096^3 GEMM through torch.mm (hipBLASLt) and through this library, "
+                         "in one process (for same-box A/B traces and counters)")
     ap.add_argument("--decode", action="store_true",
                     help="run only the BF16 decode shapes (M 1/4/16, K 4096, N 11008; NT, NN, TN) with cold "
                          "weights, --steps passes over the rotated copies (for rocprofv3)")
@@ -553,11 +588,17 @@ def main() -> int:
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: launched with WORLD_SIZE > 1; this build runs on one GPU only", file=sys.stderr)
         return 2
-    if os.environ.get("IRONTENSOR_LIB") and not (args.attention or args.medium_step or args.bf16_square or args.decode):
+    if os.environ.get("IRONTENSOR_LIB") and not (args.attention or args.medium_step or args.bf16_square or args.decode
+                                                 or args.vs_library):
         print("bench.py: IRONTENSOR_LIB is set; the bench times only the in-tree library "
               "(irontensor_amd/libirontensor_hip.so), unset it", file=sys.stderr)
         return 2
 
+    if args.vs_library:
+        # torch's HIP runtime must take the device before this library's context does (the other
+        # order leaves torch without a visible device in this process).
+        import torch
+        torch.empty(1, device="cuda:0")
     import irontensor_amd as it
     from irontensor_amd.step import TINY, GemmStep
 
@@ -578,6 +619,9 @@ def main() -> int:
         return 0
     if args.attention:
         print(json.dumps(attention_only(it, Timer(ctx), args.steps)), flush=True)
+        return 0
+    if args.vs_library:
+        print(json.dumps(vs_library(it, Timer(ctx), iters=args.steps)), flush=True)
         return 0
     if args.decode:
         print(json.dumps(decode_shapes(it, Timer(ctx), rounds=max(1, args.steps))), flush=True)
