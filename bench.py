@@ -419,11 +419,31 @@ def extra_fusions(it, timer, iters: int = 10) -> dict:
     return {"fusions": out}
 
 
+TORCH_STATE = {"ready": False, "error": None}
+
+
+def init_torch_first() -> None:
+    """Lets torch's HIP runtime take the device before this library's context does (the other order
+    leaves torch without a visible device), for the same-process library comparison; a failure is
+    recorded and the comparison skipped."""
+    try:
+        import torch
+        torch.empty(1, device="cuda:0")
+        TORCH_STATE["ready"] = True
+    except Exception as e:  # noqa: BLE001 - recorded in the line, the bench goes on without it
+        TORCH_STATE["error"] = f"{type(e).__name__}: {e}"[:200]
+
+
 def extras(it, timer) -> dict:
     out = {}
     for fn in (extra_config1, extra_attention, extra_fusions, extra_sweep, extra_med_step):
         log(f"[bench] extra: {fn.__name__}")
         out.update(fn(it, timer))
+    if TORCH_STATE["ready"]:
+        log("[bench] extra: vs_library")
+        out.update(vs_library(it, timer))
+    else:
+        out["bf16_4096_vs_library_tflops"] = {"skipped": TORCH_STATE["error"] or "torch not initialised first"}
     return out
 
 
@@ -594,11 +614,12 @@ def main() -> int:
               "(irontensor_amd/libirontensor_hip.so), unset it", file=sys.stderr)
         return 2
 
-    if args.vs_library:
-        # torch's HIP runtime must take the device before this library's context does (the other
-        # order leaves torch without a visible device in this process).
-        import torch
-        torch.empty(1, device="cuda:0")
+    if args.vs_library or not (args.no_extra or args.kernel_only or args.train_only or args.bf16_square
+                               or args.attention or args.medium_step or args.decode):
+        init_torch_first()
+        if args.vs_library and not TORCH_STATE["ready"]:
+            print(f"bench.py: torch could not take the device: {TORCH_STATE['error']}", file=sys.stderr)
+            return 1
     import irontensor_amd as it
     from irontensor_amd.step import TINY, GemmStep
 
