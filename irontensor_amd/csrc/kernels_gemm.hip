@@ -795,7 +795,10 @@ void gemm_bf16_256(const GemmArgs p) {
 //     (rows x k) block transposed: lane j of the group points at the 4 rows 4 (j % 4) .. +3 of
 //     k-row j / 4 and receives 4 consecutive k of row j. The 32 lanes served together hit 16
 //     distinct 16-byte bank groups.
-// Whole tiles only (M, N multiples of 256, K of 64); no k limits or masked epilogues.
+// The 256 x 128 form (FB = 2: each wave 128 x 64) stages 128 B rows: 4 load instructions per wave,
+// an mn-contiguous k-row of 256 bytes (16 chunks, the same XOR, 4 k-rows per load instruction).
+// Whole tiles only (M a multiple of 256, N of the tile width, K of 128); no k limits or masked
+// epilogues.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t dtl_rsrc(const void *base, int64_t bytes) {
     const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
@@ -805,11 +808,24 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 
-template <bool KCONTIG>
+// p through an empty asm: the compiler no longer knows which LDS object it points into.
+__device__ __forceinline__ lds_void_t *opaque_lds(lds_void_t *p) {
+    uint32_t x = (uint32_t)(uintptr_t)p;
+    asm("" : "+s"(x));
+    return (lds_void_t *)(uintptr_t)x;
+}
+
+template <bool KCONTIG, int ROWS = 256>
 struct DtlOperand {
-    static constexpr int ROWS = 256, BK = 64;
+    static constexpr int BK = 64;
+    // Load instructions per wave per k-tile (each fills 1 KB: 8 k-contiguous rows, or 1024 / (2
+    // ROWS) k-rows of an mn-contiguous operand).
+    static constexpr int NI = ROWS / 32;
+    static constexpr int RB = ROWS * 2;     // bytes per k-row (mn-contiguous)
+    static constexpr int CPR = ROWS / 8;    // 16-byte chunks per k-row
+    static_assert(ROWS == 256 || ROWS == 128, "256 or 128 rows");
     __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t voff[8];
+    uint32_t voff[NI];
     uint32_t kstride;  // bytes per k of the global operand (2 for k-contiguous, 2 ld otherwise)
 
     // base: element (row 0, k kb) of this block; krange: k extent of this block's split. A
@@ -821,8 +837,8 @@ struct DtlOperand {
             rsrc = dtl_rsrc(base, (int64_t)(ROWS - row_shift) * ld * 2);
             kstride = 2;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int r = 8 * (8 * wave + j) + (lane >> 3);
+            for (int j = 0; j < NI; ++j) {
+                const int r = 8 * (NI * wave + j) + (lane >> 3);
                 const int c = (lane & 7) ^ ((r >> 1) & 7);
                 voff[j] = (uint32_t)(((r - row_shift) * ld + c * 8) * 2);
             }
@@ -830,21 +846,27 @@ struct DtlOperand {
             rsrc = dtl_rsrc(base, krange * ld * 2);
             kstride = (uint32_t)(ld * 2);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int q = 2 * (8 * wave + j) + (lane >> 5);
-                const int c = (lane & 31) ^ (4 * (q & 3));
+            for (int j = 0; j < NI; ++j) {
+                const int q = (64 / CPR) * (NI * wave + j) + lane / CPR;
+                const int c = (lane % CPR) ^ (4 * (q & 3));
                 voff[j] = (uint32_t)((q * ld + c * 8) * 2);
             }
         }
     }
 
-    // The k-tile starting kk elements into the split, into `stage`.
-    __device__ __forceinline__ void issue(char *stage, int64_t kk, int wave) const {
+    // The k-tile starting kk elements into the split, into `stage`. opaque (a constant at each
+    // call): the LDS address reaches the load through an empty asm, so the compiler cannot tie
+    // the load to an LDS object and inserts no waits of its own before LDS reads (which, not
+    // knowing which stage a pending load writes, would wait for all of them); the caller's
+    // explicit waits then order them.
+    __device__ __forceinline__ void issue(char *stage, int64_t kk, int wave, bool opaque) const {
         const uint32_t soff = (uint32_t)(kk * kstride);
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(stage + (8 * wave + j) * 1024), 16, voff[j],
-                                                     soff, 0, 0);
+        for (int j = 0; j < NI; ++j) {
+            lds_void_t *dst = (lds_void_t *)(stage + (NI * wave + j) * 1024);
+            if (opaque) dst = opaque_lds(dst);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, voff[j], soff, 0, 0);
+        }
     }
 
     // Fragment (rows row .. row + 31, k 16 ks .. +15) of a 32x32x16 MFMA operand: lane l holds row
@@ -860,8 +882,8 @@ struct DtlOperand {
             const int q = 16 * ks + 8 * (g >> 1) + (j >> 2);  // k-row of this lane's chunk
             const int cbyte = n * 2 + 8 * (j & 3);       // byte of the chunk within the k-row
             const int off = (((cbyte >> 4) ^ (4 * (q & 3))) << 4) + (cbyte & 15);
-            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(st + q * 512 + off));
-            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(st + (q + 4) * 512 + off));
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(st + q * RB + off));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(st + (q + 4) * RB + off));
             u32x4 v;
             v[0] = (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
             v[1] = (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
@@ -876,20 +898,28 @@ struct DtlOperand {
 // A and B point at element (row 0, k kb) of the tile's operands; `krange` bounds an mn-contiguous
 // operand's buffer. The caller synchronises the block before (the stages may still be read) and
 // after (the epilogue reuses them).
-template <bool TA, bool TB, bool DUAL>
-__device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *st0, char *st1, const uint16_t *A,
-                                         const uint16_t *B, int64_t krange, int ntiles, f32x16 (&acc)[4][4],
+// s_waitcnt immediate: vmcnt(vm) lgkmcnt(lgkm), expcnt not waited on.
+constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8); }
+
+template <bool TA, bool TB, bool DUAL, int FB>
+__device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *__restrict__ st0, char *__restrict__ st1,
+                                         char *__restrict__ st2, const uint16_t *A,
+                                         const uint16_t *B, int64_t krange, int ntiles, f32x16 (&acc)[4][FB],
                                          int wave, int lane) {
-    constexpr int BN = 256, BK = 64, WT = 128, F = 4;
+    // FB: 32-column B fragments per wave (4: 256 x 256 tile, 128 x 128 per wave, two 64 KB
+    // stages; 2: 256 x 128 tile, 128 x 64 per wave, three 48 KB stages, so that loads run two
+    // k-tiles ahead of a k-tile that takes half as long).
+    constexpr int BN = FB * 64, BK = 64, WT = 128, F = 4;
+    constexpr int NS = FB == 2 ? 3 : 2;
     constexpr int TILE = 256 * BK * 2;
     using OA = DtlOperand<!TA>;
-    using OB = DtlOperand<TB>;
+    using OB = DtlOperand<TB, BN>;
     const int wm = wave >> 1, wn = wave & 1;
     const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < F; ++i)
 #pragma unroll
-        for (int j = 0; j < F; ++j) acc[i][j] = zero;
+        for (int j = 0; j < FB; ++j) acc[i][j] = zero;
     if (ntiles <= 0) return;
     OA oa;
     OB ob;
@@ -898,29 +928,38 @@ __device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *st0, char *st1
     const int last = ntiles - 1;
     auto issue = [&](int t, char *stage) {
         const int64_t kk = (int64_t)min(t, last) * BK;
-        oa.issue(stage, kk, wave);
-        ob.issue(stage + TILE, kk, wave);
+        oa.issue(stage, kk, wave, NS == 3);
+        ob.issue(stage + TILE, kk, wave, NS == 3);
     };
-    u32x4 fa0[F], fb0[F], fa1[F], fb1[F];
-    auto frags = [&](u32x4 (&fa)[F], u32x4 (&fb)[F], const char *st, int ks) {
+    u32x4 fa0[F], fb0[FB], fa1[F], fb1[FB];
+    auto frags = [&](u32x4 (&fa)[F], u32x4 (&fb)[FB], const char *st, int ks) {
 #pragma unroll
         for (int i = 0; i < F; ++i) fa[i] = OA::frag(st, wm * WT + i * 32, ks, lane);
 #pragma unroll
-        for (int j = 0; j < F; ++j) fb[j] = OB::frag(st + TILE, wn * WT + j * 32, ks, lane);
+        for (int j = 0; j < FB; ++j) fb[j] = OB::frag(st + TILE, wn * (FB * 32) + j * 32, ks, lane);
     };
-    auto mfma16 = [&](const u32x4 (&fa)[F], const u32x4 (&fb)[F]) {
+    auto mfma16 = [&](const u32x4 (&fa)[F], const u32x4 (&fb)[FB]) {
 #pragma unroll
         for (int i = 0; i < F; ++i)
 #pragma unroll
-            for (int j = 0; j < F; ++j)
+            for (int j = 0; j < FB; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                     __builtin_bit_cast(bf16x8, fa[i]), __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
     };
-    // DS reads per MFMA pair (a fragment set is 8 fragments, an mn-contiguous one two reads).
-    constexpr int DSR = (4 * (TA ? 2 : 1) + 4 * (TB ? 1 : 2) + 7) / 8;
-    // Tile t from `cur` (its k-step 0 fragments already in fa0/fb0); tile t+1 is streaming into
-    // `nxt`; the loads of tile t+2 go into `cur` once every wave has passed the barrier.
-    auto body = [&](char *cur, char *nxt, int t) {
+    // DS reads per MFMA pair (a k-step's fragment set is F + FB fragments, an mn-contiguous one
+    // two reads each; the k-step has 2 FB MFMA pairs), and load instructions per pair in the
+    // k-step that issues them.
+    constexpr int PAIRS = 2 * FB;
+    constexpr int DSR = (F * (TA ? 2 : 1) + FB * (TB ? 1 : 2) + PAIRS - 1) / PAIRS;
+    constexpr int VMR = (OA::NI + OB::NI + PAIRS - 1) / PAIRS;
+    // Load instructions a wave issues per k-tile: with three stages the wait before the barrier
+    // lets the newest k-tile's loads stay in flight.
+    constexpr int NLOAD = OA::NI + OB::NI;
+    constexpr int WAIT_NEXT = waitcnt_imm((NS - 2) * NLOAD, 0);
+    // Tile t from `cur` (its k-step 0 fragments already in fa0/fb0); tile t+1 has been streaming
+    // into `nxt` (and, with three stages, tile t+2 into the third); the loads of tile t+NS go into
+    // `cur` once every wave has passed the barrier.
+    auto body = [&](char *cur, const char *nxt, int t) {
         frags(fa1, fb1, cur, 1);
         mfma16(fa0, fb0);
         frags(fa0, fb0, cur, 2);
@@ -929,74 +968,117 @@ __device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *st0, char *st1
         mfma16(fa0, fb0);
         // k-steps 0..2, each step's MFMAs interleaved with the next step's fragment reads.
 #pragma unroll
-        for (int g = 0; g < 24; ++g) {
+        for (int g = 0; g < 3 * PAIRS; ++g) {
             __builtin_amdgcn_sched_group_barrier(sg::DS_READ, DSR, 0);
             __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
         }
-        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): tile t+1 landed, `cur` read
-        __syncthreads();
-        issue(t + 2, cur);
-        // k-step 3 with the next tile's first fragment reads and the loads of tile t+2.
+        __builtin_amdgcn_s_waitcnt(WAIT_NEXT);  // lgkmcnt(0): `cur` read; tile t+1 landed
+        if constexpr (NS == 2) {
+            __syncthreads();
+        } else {
+            // No release fence: at workgroup scope it would also wait for the newest tile's
+            // loads (vmcnt(0)). The explicit wait above has completed this wave's reads of `cur`,
+            // and the barrier keeps them ahead of the loads into it; the acquire fence keeps the
+            // reads of `nxt` behind the barrier.
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        }
+        issue(t + NS, cur);
+        // k-step 3 with the next tile's first fragment reads and the loads of tile t+NS.
         frags(fa0, fb0, nxt, 0);
         mfma16(fa1, fb1);
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
+        for (int g = 0; g < PAIRS; ++g) {
             __builtin_amdgcn_sched_group_barrier(sg::DS_READ, DSR, 0);
-            __builtin_amdgcn_sched_group_barrier(sg::VMEM_READ, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(sg::VMEM_READ, VMR, 0);
             __builtin_amdgcn_sched_group_barrier(sg::MFMA, 2, 0);
         }
     };
-    issue(0, st0);
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    __syncthreads();
-    issue(1, st1);
-    frags(fa0, fb0, st0, 0);
-    // An even number of k-tiles (dtl_applicable): no odd tail body, whose prefetched fragments
-    // would stay live past the loop and spill.
-    for (int t = 0; t < ntiles; t += 2) {
-        body(st0, st1, t);
-        body(st1, st0, t + 1);
+    if constexpr (NS == 2) {
+        issue(0, st0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+        __syncthreads();
+        issue(1, st1);
+        frags(fa0, fb0, st0, 0);
+        // An even number of k-tiles (dtl_applicable): no odd tail body, whose prefetched fragments
+        // would stay live past the loop and spill.
+        for (int t = 0; t < ntiles; t += 2) {
+            body(st0, st1, t);
+            body(st1, st0, t + 1);
+        }
+    } else {
+        issue(0, st0);
+        issue(1, st1);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(NLOAD, 15));  // tile 0 landed
+        __syncthreads();
+        issue(2, st2);
+        frags(fa0, fb0, st0, 0);
+        // Any number of k-tiles (the 256 x 128 tile has registers to spare for the tail).
+        for (int t = 0;; t += 3) {
+            body(st0, st1, t);
+            if (t + 1 >= ntiles) break;
+            body(st1, st2, t + 1);
+            if (t + 2 >= ntiles) break;
+            body(st2, st0, t + 2);
+            if (t + 3 >= ntiles) break;
+        }
     }
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // the loads into dead stages have landed
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the loads into dead stages have landed
 }
 
 // Epilogue of one tile of gemm_bf16_dtl (begins with a block barrier: the stages are reused).
-// Two passes of 128 x 64 columns per wave (waves 0-1 stage in st0, waves 2-3 in st1, 32 KB each):
-// 16 lanes then read a whole 256-byte staged row, so every store covers whole 128-byte lines of a
-// BF16 (or FP32) output row. Row r's columns sit at c ^ 32 ((r >> 2) & 1): the two rows one
-// accumulator write instruction touches (4 apart) then fall in different banks. In the SwiGLU form
-// the gate wave (wn = 0) and the up wave (wn = 1) of a row half stage the same output columns and
-// then finish 64 rows each of the pair.
-template <bool DUAL>
-__device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char *st1, const f32x16 (&acc)[4][4],
-                                             int64_t m0, int64_t n0, int64_t coff, int64_t z, int wave, int lane) {
-    constexpr int WT = 128, F = 4, STAGE = 2 * 256 * 64 * 2;
-    constexpr int EC2 = 64, EP2 = EC2 * 4;
-    static_assert(2 * WT * EP2 <= STAGE, "epilogue staging fits in the operand stages");
+// Passes of 128 x 64 columns per wave (two with FB = 4, one with FB = 2), each wave staging 32 KB
+// as two 16 KB halves of 64 rows: FB = 4, waves 0-1 in st0 and 2-3 in st1 (64 KB stages); FB = 2,
+// waves 0-2 in st0, st1, st2 and wave 3 in the 16 KB tails of st0 and st1 (48 KB stages). 16 lanes
+// then read a whole 256-byte staged row, so every store covers whole 128-byte lines of a BF16 (or
+// FP32) output row. Row r's columns sit at c ^ 32 ((r >> 2) & 1): the two rows one accumulator
+// write instruction touches (4 apart) then fall in different banks. In the SwiGLU form the gate
+// wave (wn = 0) and the up wave (wn = 1) of a row half stage the same output columns and then
+// finish 64 rows each of the pair.
+template <bool DUAL, int FB>
+__device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char *st1, char *st2,
+                                             const f32x16 (&acc)[4][FB], int64_t m0, int64_t n0, int64_t coff,
+                                             int64_t z, int wave, int lane) {
+    static_assert(!DUAL || FB == 4, "the SwiGLU form pairs 128-column gate and up waves");
+    constexpr int WT = 128, F = 4, STAGE = FB == 4 ? 2 * 256 * 64 * 2 : (256 + 128) * 64 * 2;
+    constexpr int EC2 = 64, EP2 = EC2 * 4, HALF = 64 * EP2;
+    static_assert(FB == 4 ? 4 * HALF <= STAGE : 3 * HALF <= STAGE, "epilogue staging fits in the stages");
     const int wm = wave >> 1, wn = wave & 1;
     __syncthreads();
-    char *wl2 = (wave < 2 ? st0 : st1) + (wave & 1) * (WT * EP2);
+    char *lo, *hi;  // this wave's staging for rows 0-63 and 64-127 of its 128
+    if constexpr (FB == 4) {
+        lo = (wave < 2 ? st0 : st1) + (wave & 1) * (2 * HALF);
+        hi = lo + HALF;
+    } else {
+        (void)st2;
+        lo = wave == 0 ? st0 : wave == 1 ? st1 : wave == 2 ? st2 : st0 + 2 * HALF;
+        hi = wave == 3 ? st1 + 2 * HALF : lo + HALF;
+    }
     // A lane's accumulator rows all have bit 2 equal to lane / 32, so its swizzle is per lane.
-    float *wlane = (float *)(wl2 + (lane >> 5) * 4 * EP2 + (lane & 31) * 4) + ((lane >> 5) << 5);
+    const int lane_off = (lane >> 5) * 4 * EP2 + (lane & 31) * 4 + ((lane >> 5) << 7);
 #pragma unroll
-    for (int hp = 0; hp < F / 2; ++hp) {
+    for (int hp = 0; hp < FB / 2; ++hp) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int i = 0; i < F; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int rr = i * 32 + (r >> 2) * 8 + (r & 3);  // row less the lane's 4 (lane / 32)
+                    // row less the lane's 4 (lane / 32), within the half (i < 2: rows 0-63)
+                    const int rr = (i & 1) * 32 + (r >> 2) * 8 + (r & 3);
                     // column hh * 32 + lane % 32, bit 5 flipped for odd lane / 32: one XOR per lane,
-                    // folded into wlane for hh = 0 and undone (^ 32 = +-32) for hh = 1.
-                    float *dst = wlane + rr * (EP2 / 4) + (hh ? (((lane >> 5) & 1) ? -32 : 32) : 0);
+                    // folded into lane_off for hh = 0 and undone (^ 32 = +-32) for hh = 1.
+                    float *dst = (float *)((i < 2 ? lo : hi) + lane_off) + rr * (EP2 / 4) +
+                                 (hh ? (((lane >> 5) & 1) ? -32 : 32) : 0);
                     *dst = acc[i][2 * hp + hh][r];
                 }
         __syncthreads();
-        // Lane reads row 4 it + lane / 16 of the pass, columns cl .. cl + 3; bit 2 of the row is it & 1.
+        // Lane reads row 4 it + lane / 16 of a half, columns cl .. cl + 3; bit 2 of the row is it & 1.
         const int cl = (lane & 15) * 4;
         if constexpr (DUAL) {
-            const char *gl = wm == 0 ? st0 : st1, *ul = gl + WT * EP2;
+            // The gate wave's staging (wn = 0) and the up wave's (wn = 1) of this row half are
+            // consecutive 32 KB in one stage.
+            const char *gl = wm == 0 ? st0 : st1, *ul = gl + 2 * HALF;
             const int64_t col = n0 + hp * EC2 + cl;
 #pragma unroll 4
             for (int it = wn * 16; it < wn * 16 + 16; ++it) {
@@ -1006,39 +1088,39 @@ __device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char 
                                       col, coff);
             }
         } else {
-            const int64_t row0 = m0 + wm * WT + (lane >> 4), col = n0 + wn * WT + hp * EC2 + cl;
-            if (p.splits > 1) {
-                // split-K partial sums: plain f32 rows of N
-                float *dst = p.partial + (z * p.M + row0) * p.N + col;
+            const int64_t col = n0 + wn * (FB * 32) + hp * EC2 + cl;
+            auto staged = [&](int h, int it) {
+                return *(const f32x4 *)((h ? hi : lo) + (4 * it + (lane >> 4)) * EP2 + ((cl ^ ((it & 1) << 5)) * 4));
+            };
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int64_t row0 = m0 + wm * WT + h * 64 + (lane >> 4);
+                if (p.splits > 1) {
+                    // split-K partial sums: plain f32 rows of N
+                    float *dst = p.partial + (z * p.M + row0) * p.N + col;
 #pragma unroll 4
-                for (int it = 0; it < WT * EC2 / 256; ++it, dst += 4 * p.N)
-                    *(f32x4 *)dst = *(const f32x4 *)(wl2 + (4 * it + (lane >> 4)) * EP2 + ((cl ^ ((it & 1) << 5)) * 4));
-            } else if (p.c_vec_ok && !p.row_scale && p.beta == 0.f && !p.rope_table) {
-                // the common epilogue: alpha (and a column bias) only, with one base pointer per pass
-                f32x4 bias = {0.f, 0.f, 0.f, 0.f};
-                if (p.has_bias) bias = f32x4{p.bias[col], p.bias[col + 1], p.bias[col + 2], p.bias[col + 3]};
-                const int64_t idx = coff + row0 * p.ldc + col;
-                if (p.out_bf16) {
-                    uint16_t *dst = (uint16_t *)p.C + idx;
+                    for (int it = 0; it < 16; ++it, dst += 4 * p.N) *(f32x4 *)dst = staged(h, it);
+                } else if (p.c_vec_ok && !p.row_scale && p.beta == 0.f && !p.rope_table) {
+                    // the common epilogue: alpha (and a column bias) only, with one base pointer per half
+                    f32x4 bias = {0.f, 0.f, 0.f, 0.f};
+                    if (p.has_bias) bias = f32x4{p.bias[col], p.bias[col + 1], p.bias[col + 2], p.bias[col + 3]};
+                    const int64_t idx = coff + row0 * p.ldc + col;
+                    if (p.out_bf16) {
+                        uint16_t *dst = (uint16_t *)p.C + idx;
 #pragma unroll 4
-                    for (int it = 0; it < WT * EC2 / 256; ++it, dst += 4 * p.ldc) {
-                        const f32x4 v = *(const f32x4 *)(wl2 + (4 * it + (lane >> 4)) * EP2 + ((cl ^ ((it & 1) << 5)) * 4)) *
-                                            p.alpha + bias;
-                        *(u32x2 *)dst = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                        for (int it = 0; it < 16; ++it, dst += 4 * p.ldc) {
+                            const f32x4 v = staged(h, it) * p.alpha + bias;
+                            *(u32x2 *)dst = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                        }
+                    } else {
+                        float *dst = (float *)p.C + idx;
+#pragma unroll 4
+                        for (int it = 0; it < 16; ++it, dst += 4 * p.ldc) *(f32x4 *)dst = staged(h, it) * p.alpha + bias;
                     }
                 } else {
-                    float *dst = (float *)p.C + idx;
 #pragma unroll 4
-                    for (int it = 0; it < WT * EC2 / 256; ++it, dst += 4 * p.ldc)
-                        *(f32x4 *)dst = *(const f32x4 *)(wl2 + (4 * it + (lane >> 4)) * EP2 + ((cl ^ ((it & 1) << 5)) * 4)) *
-                                            p.alpha + bias;
-                }
-            } else {
-#pragma unroll 4
-                for (int it = 0; it < WT * EC2 / 256; ++it) {
-                    const int rl = 4 * it + (lane >> 4);
-                    const f32x4 v = *(const f32x4 *)(wl2 + rl * EP2 + ((cl ^ ((it & 1) << 5)) * 4));
-                    finish4<false>(p, v, m0 + wm * WT + rl, col, coff, z);
+                    for (int it = 0; it < 16; ++it)
+                        finish4<false>(p, staged(h, it), row0 + 4 * it, col, coff, z);
                 }
             }
         }
@@ -1046,18 +1128,21 @@ __device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char 
     }
 }
 
-template <bool TA, bool TB, bool DUAL = false>
+template <bool TA, bool TB, bool DUAL = false, int FB = 4>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_dtl(const GemmArgs p) {
     // DUAL (SwiGLU, Y = X.W^T only): the B stage's rows 0..127 are 128 gate-weight rows (loaded
     // by waves 0-1) and rows 128..255 the same rows of the up weight (waves 2-3), so waves wn = 0
     // accumulate gate and wn = 1 up for one 256 x 128 output tile; the epilogue pairs them.
+    // FB = 2: a 256 x 128 output tile (twice the tiles where 256 x 256 would leave CUs idle), with
+    // three stages of 48 KB.
     static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
     using T = uint16_t;
-    constexpr int BM = 256, BN = 256, BK = 64, F = 4;
-    constexpr int STAGE = 2 * BM * BK * 2;
+    constexpr int BM = 256, BN = FB * 64, BK = 64, F = 4;
+    constexpr int STAGE = (BM + (FB == 4 ? 256 : 128)) * BK * 2;
     __shared__ __attribute__((aligned(1024))) char st0[STAGE];
     __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st2[FB == 2 ? STAGE : 16];  // FB = 2 only
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1072,9 +1157,10 @@ void gemm_bf16_dtl(const GemmArgs p) {
     const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in + (TA ? kb * p.lda + m0 : m0 * p.lda + kb);
     const T *Bm = (const T *)(DUAL && wave >= 2 ? p.B2 : p.B);
     const T *B = Bm + bo * p.sB_out + bi * p.sB_in + (TB ? n0 * p.ldb + kb : kb * p.ldb + n0);
-    f32x16 acc[F][F];
-    dtl_tile<TA, TB, DUAL>(p, st0, st1, A, B, ke - kb, ke > kb ? (int)((ke - kb) / BK) : 0, acc, wave, lane);
-    dtl_epilogue<DUAL>(p, st0, st1, acc, m0, n0, bo * p.sC_out + bi * p.sC_in, z, wave, lane);
+    f32x16 acc[F][FB];
+    dtl_tile<TA, TB, DUAL, FB>(p, st0, st1, st2, A, B, ke - kb, ke > kb ? (int)((ke - kb) / BK) : 0, acc, wave,
+                               lane);
+    dtl_epilogue<DUAL, FB>(p, st0, st1, st2, acc, m0, n0, bo * p.sC_out + bi * p.sC_in, z, wave, lane);
 }
 
 // Deterministic split-K reduction: partial sums are added in split order.
@@ -1130,17 +1216,27 @@ bool tiles_exact(const GemmArgs &a, int bm, int bn, int bk) {
 // The direct-to-LDS kernel takes whole tiles without epilogue masks or k limits, an even number of
 // k-tiles per split, and 32-bit buffer offsets: a k-contiguous operand's 256 rows, or an
 // mn-contiguous operand's k range, within 2 GiB.
-bool dtl_applicable(bool ta, bool tb, const GemmArgs &a) {
+// bn: the output tile width, 256 or 128 (the SwiGLU form's 256 x 128 output tile is given as 256).
+bool dtl_applicable(bool ta, bool tb, const GemmArgs &a, int bn = 256) {
     auto fits = [&](bool kcontig, int64_t ld) {
         return kcontig ? ld * 2 * 256 < (1ll << 31) : a.k_per_split * ld * 2 < (1ll << 31);
     };
+    if (bn != 256 && (bn != 128 || a.dual)) return false;
     return a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.swiglu_bwd && !a.xent_stats && !a.a_kscale &&
-           (!a.dual || (!ta && tb)) && tiles_exact(a, 256, a.dual ? 128 : 256, ET<uint16_t>::BK) &&
+           (!a.dual || (!ta && tb)) && tiles_exact(a, 256, a.dual ? 128 : bn, ET<uint16_t>::BK) &&
            a.k_per_split % (2 * ET<uint16_t>::BK) == 0 && a.K % (2 * ET<uint16_t>::BK) == 0 &&
            fits(!ta, a.lda) && fits(tb, a.ldb) && a.K * 2 < (1ll << 31);
 }
 
-hipError_t launch_bf16_256(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipStream_t s) {
+hipError_t launch_bf16_256(bool ta, bool tb, int bn, const GemmArgs &a, dim3 grid, hipStream_t s) {
+    if (bn == 128) {  // the planner offers 256 x 128 only where the direct-to-LDS kernel applies
+        if (!dtl_applicable(ta, tb, a, 128)) return hipErrorInvalidConfiguration;
+        if (!ta && tb) hipLaunchKernelGGL((gemm_bf16_dtl<false, true, false, 2>), grid, dim3(NTHREADS), 0, s, a);
+        else if (!ta && !tb) hipLaunchKernelGGL((gemm_bf16_dtl<false, false, false, 2>), grid, dim3(NTHREADS), 0, s, a);
+        else if (ta && !tb) hipLaunchKernelGGL((gemm_bf16_dtl<true, false, false, 2>), grid, dim3(NTHREADS), 0, s, a);
+        else hipLaunchKernelGGL((gemm_bf16_dtl<true, true, false, 2>), grid, dim3(NTHREADS), 0, s, a);
+        return hipGetLastError();
+    }
     if (dtl_applicable(ta, tb, a)) {
         if (a.dual) hipLaunchKernelGGL((gemm_bf16_dtl<false, true, true>), grid, dim3(NTHREADS), 0, s, a);
         else if (!ta && tb) hipLaunchKernelGGL((gemm_bf16_dtl<false, true>), grid, dim3(NTHREADS), 0, s, a);
@@ -1255,15 +1351,17 @@ struct Plan {
 // Estimated seconds, lowest wins.
 Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
     struct Cand {
-        int b, occ;
+        int b, bn, occ;  // b x bn tiles (bn 0: square)
         double eff;
     };
-    const Cand f32c[] = {{128, 2, 0.50}, {64, 4, 0.60}};
-    const Cand b16c[] = {{256, 1, 0.40}, {128, 2, 0.20}, {64, 4, 0.20}};
-    // The direct-to-LDS kernel (whole 256 x 256 tiles, an even number of k-tiles per split).
-    constexpr double DTL_EFF = 0.53;
+    const Cand f32c[] = {{128, 0, 2, 0.50}, {64, 0, 4, 0.60}};
+    // 256 x 128 exists only as the direct-to-LDS kernel (eff 0: skipped where that does not apply).
+    const Cand b16c[] = {{256, 0, 1, 0.40}, {256, 128, 1, 0.0}, {128, 0, 2, 0.20}, {64, 0, 4, 0.20}};
+    // The direct-to-LDS kernel (whole tiles, an even number of k-tiles per split): 256 x 256, and
+    // 256 x 128, whose waves read 50% more LDS per MFMA.
+    constexpr double DTL_EFF = 0.53, DTL_HALF_EFF = 0.48;
     const Cand *cands = bf16 ? b16c : f32c;
-    const int ncand = bf16 ? 3 : 2;
+    const int ncand = bf16 ? 4 : 2;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
     const double cu_peak = (bf16 ? 2.5e15 : 157.3e12) / 256.0;  // FLOP/s per CU
     const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = 4e12;
@@ -1274,8 +1372,9 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
     int64_t best_blocks = 0;
     for (int c = 0; c < ncand; ++c) {
         const Cand &cd = cands[c];
+        if (cd.bn && a.dual) continue;
         // A dual (SwiGLU) tile covers b x b/2 outputs: its b B-tile rows are gate and up halves.
-        const int bn = a.dual ? cd.b / 2 : cd.b;
+        const int bn = a.dual ? cd.b / 2 : cd.bn ? cd.bn : cd.b;
         const int64_t tiles = cdiv(a.M, cd.b) * cdiv(a.N, bn) * a.batch;
         if (cd.b == 256) {
             const double fill = (double)a.M * a.N * a.batch / ((double)tiles * 256.0 * bn);
@@ -1296,8 +1395,9 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
             if (bf16 && cd.b == 256) {
                 GemmArgs d = a;
                 d.k_per_split = kps;
-                if (dtl_applicable(ta, tb, d)) eff = DTL_EFF;
+                if (dtl_applicable(ta, tb, d, a.dual ? 256 : bn)) eff = bn == 128 && !a.dual ? DTL_HALF_EFF : DTL_EFF;
             }
+            if (eff <= 0.0) continue;
             const double step = (a.dual ? 4.0 : 2.0) * cd.b * bn * bk / (cu_peak * eff);
             double t = rounds * (round_overhead + ksteps * std::max(conc * step, step_floor));
             if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
@@ -1384,10 +1484,11 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     Plan plan = choose_plan(a, bf16, cus, transA, transB);
 #ifdef IT_TUNING
-    // Planner sweeps only (a tuning build): IT_PLAN="tile,splits" forces the plan.
+    // Planner sweeps only (a tuning build): IT_PLAN="tile,splits[,width]" forces the plan.
     if (const char *env = std::getenv("IT_PLAN")) {
-        int b = 0, sp = 0;
-        if (std::sscanf(env, "%d,%d", &b, &sp) == 2) plan = Plan{b, a.dual ? b / 2 : b, sp};
+        int b = 0, sp = 0, w = 0;
+        const int n = std::sscanf(env, "%d,%d,%d", &b, &sp, &w);
+        if (n >= 2) plan = Plan{b, a.dual ? b / 2 : n == 3 ? w : b, sp};
     }
 #endif
     TileCfg cfg{plan.bm, plan.bn};
@@ -1406,6 +1507,7 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
         if (st != IT_OK) return st;
         a.partial = (float *)ws;
     }
+    const bool dtl = cfg.bm == 256 && dtl_applicable(transA, transB, a, a.dual ? 256 : cfg.bn);
 
     const int64_t gx = (int64_t)a.tiles_m * a.tiles_n;
     const int64_t gy = a.batch * splits;
@@ -1420,14 +1522,14 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
         char buf[192];
         std::snprintf(buf, sizeof(buf), "gemm_%s_%c%c_%dx%d%s%s%s%s|%s[%lld,%lld,%lld]x%lld s%d",
                       bf16 ? "bf16" : "f32", transA ? 'T' : 'N', transB ? 'T' : 'N', cfg.bm, cfg.bn,
-                      cfg.bm == 256 && dtl_applicable(transA, transB, a) ? "_dtl" : "",
+                      dtl ? "_dtl" : "",
                       a.dual ? "_swiglu" : "", a.causal || a.kmode ? "_causal" : "", a.a_kscale ? "_rmsnorm" : a.xent_stats ? "_xent" : "",
                       profile_tag ? profile_tag : "", (long long)a.M, (long long)a.N,
                       (long long)a.K, (long long)a.batch, splits);
         key = buf;
         profile_begin(ctx, key, &ev);
     }
-    hipError_t e = cfg.bm == 256 ? launch_bf16_256(transA, transB, a, grid, ctx->stream)
+    hipError_t e = cfg.bm == 256 ? launch_bf16_256(transA, transB, a.dual ? 256 : cfg.bn, a, grid, ctx->stream)
                    : bf16        ? launch_typed<uint16_t>(transA, transB, a.dual, cfg, a, grid, ctx->stream)
                                  : launch_typed<float>(transA, transB, a.dual, cfg, a, grid, ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "gemm_mfma launch");

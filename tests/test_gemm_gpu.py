@@ -554,6 +554,57 @@ def test_bf16_uneven_tile_counts_exact(it, ta, tb, m, n, k):
     assert np.array_equal(c.numpy(), again.numpy())
 
 
+@pytest.mark.parametrize("ta,tb,m,n,k", [(0, 0, 4096, 1152, 1024), (0, 1, 2048, 1152, 2048), (1, 0, 1024, 896, 4096),
+                                         (1, 1, 4096, 1152, 256), (0, 0, 8192, 1024, 1024), (1, 0, 1024, 1024, 8192)])
+def test_bf16_dtl_256x128_exact(it, ta, tb, m, n, k):
+    """The 256 x 128 direct-to-LDS tile (each wave 128 x 64; B staged as 128 rows) in every
+    layout: N an odd multiple of 128 rules the 256 x 256 tile out, and the medium step's
+    N = 1024 data gradient and 1024 x 1024 weight gradient (split-K) take it to fill the CUs.
+    Small integers are exact in any FP32 summation order: the result equals a float64 product
+    bit for bit, and a second run repeats it."""
+    a = synth.small_ints(250 + m, (k, m) if ta else (m, k), -2, 2)
+    b = synth.small_ints(251 + n, (n, k) if tb else (k, n), -2, 2)
+    at, bt = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    c, keys = _plan_keys(it, lambda: it.gemm(at, bt, trans_a=bool(ta), trans_b=bool(tb)))
+    _log(f"[256x128 exact] ta={ta} tb={tb} {m}x{n}x{k}: {keys}")
+    assert any("256x128_dtl" in key for key in keys), keys
+    exact = np.matmul(op(a, ta).astype(np.float64), op(b, tb).astype(np.float64))
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    again = it.gemm(at, bt, trans_a=bool(ta), trans_b=bool(tb))
+    assert np.array_equal(c.numpy(), again.numpy())
+
+
+def test_bf16_dtl_256x128_epilogues(it, oracle):
+    """The 256 x 128 tile's epilogues: alpha/beta into a BF16 output (exact on small integers),
+    a bias with FP32 output, a bias with BF16 output (the rounding of the FP32 result), and
+    Gaussian operands within the FP32 contract of the oracle on the same BF16 values."""
+    m, n, k = 4096, 1152, 256
+    a = synth.small_ints(260, (m, k), -4, 4)
+    b = synth.small_ints(261, (n, k), -4, 4)
+    c0 = synth.small_ints(262, (m, n), -4, 4)
+    at, bt = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    out = it.Tensor.from_f32_as_bf16(c0, c0.shape)
+    _, keys = _plan_keys(it, lambda: it.gemm(at, bt, trans_b=True, alpha=0.5, beta=2.0, out=out))
+    _log(f"[256x128 epilogues] {keys}")
+    assert any("256x128_dtl" in key for key in keys), keys
+    exact = 0.5 * (a.astype(np.float64) @ b.astype(np.float64).T) + 2.0 * c0
+    assert np.array_equal(out.as_bf16_slice().reshape(m, n), oracle.f32_to_bf16(exact.astype(np.float32)))
+    bias = synth.normal(263, (n,))
+    tbias = it.Tensor.from_f32_slice(bias, bias.shape)
+    y = it.gemm(at, bt, trans_b=True, bias=tbias)
+    ref = (a.astype(np.float64) @ b.astype(np.float64).T) + bias
+    assert normwise_rel(y.numpy(), ref) <= FP32_TOL
+    y16 = it.gemm(at, bt, trans_b=True, bias=tbias, out_precision=it.Precision.BF16)
+    assert bf16_out_excess(y16.numpy(), ref) <= FP32_TOL
+    ga, gb = synth.normal(264, (m, 2 * k)), synth.normal(265, (2 * k, n))
+    g, keys = _plan_keys(it, lambda: it.gemm(it.Tensor.from_f32_as_bf16(ga, ga.shape),
+                                             it.Tensor.from_f32_as_bf16(gb, gb.shape)))
+    assert any("256x128_dtl" in key for key in keys), keys
+    rows = np.random.default_rng(8).choice(m, 256, replace=False)
+    ref16 = oracle.gemm_bf16(oracle.f32_to_bf16(np.ascontiguousarray(ga[rows])), oracle.f32_to_bf16(gb), False, False)
+    assert normwise_rel(g.numpy()[rows], ref16) <= FP32_TOL
+
+
 def test_bf16_long_k_gaussian(it, oracle):
     """The medium step's down.dW shape (K = 8192 tokens, 44 tiles, split-K) on Gaussian data: 64
     sampled output rows within the FP32 contract of the oracle on the same BF16 operands and
