@@ -1358,8 +1358,10 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
     // 256 x 128 exists only as the direct-to-LDS kernel (eff 0: skipped where that does not apply).
     const Cand b16c[] = {{256, 0, 1, 0.40}, {256, 128, 1, 0.0}, {128, 0, 2, 0.20}, {64, 0, 4, 0.20}};
     // The direct-to-LDS kernel (whole tiles, an even number of k-tiles per split): 256 x 256, and
-    // 256 x 128, whose waves read 50% more LDS per MFMA.
-    constexpr double DTL_EFF = 0.53, DTL_HALF_EFF = 0.48;
+    // 256 x 128, whose waves read 50% more LDS per MFMA (two transposed reads per fragment of a
+    // transposed A: lower still), and whose third stage lowers the memory-latency floor.
+    constexpr double DTL_EFF = 0.53, DTL_HALF_FLOOR = 0.85e-6;
+    const double DTL_HALF_EFF = ta ? 0.42 : 0.52;
     const Cand *cands = bf16 ? b16c : f32c;
     const int ncand = bf16 ? 4 : 2;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
@@ -1399,7 +1401,8 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
             }
             if (eff <= 0.0) continue;
             const double step = (a.dual ? 4.0 : 2.0) * cd.b * bn * bk / (cu_peak * eff);
-            double t = rounds * (round_overhead + ksteps * std::max(conc * step, step_floor));
+            const double floor = cd.bn == 128 ? DTL_HALF_FLOOR : step_floor;
+            double t = rounds * (round_overhead + ksteps * std::max(conc * step, floor));
             if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
             // Near ties (3%) keep the earlier, larger and less split plan, except that between two
             // unsplit plans the one with more blocks wins (more loads in flight per k-step).
