@@ -1328,6 +1328,7 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 struct Plan {
     int bm, bn, splits;
+    int64_t k_per_split;  // 0: K / splits rounded up to the k-tile
 };
 
 // Picks the tile shape and split-K factor with a cost model fitted to MI355X timings of these
@@ -1369,7 +1370,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
     const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = 4e12;
     const double step_floor = bf16 ? 1.0e-6 : 0.5e-6;
     const bool can_split = !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.no_split;
-    Plan best{64, 64, 1};
+    Plan best{64, 64, 1, 0};
     double best_t = 1e30;
     int64_t best_blocks = 0;
     for (int c = 0; c < ncand; ++c) {
@@ -1382,9 +1383,13 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
             const double fill = (double)a.M * a.N * a.batch / ((double)tiles * 256.0 * bn);
             if (fill < 0.7) continue;
         }
-        for (int s = 1; s <= 32; s *= 2) {
+        // BF16 tries every split count (a multiple of 128 per split, as the direct-to-LDS kernel
+        // needs: 5 splits fill 240 CUs with a 48-tile weight gradient where 4 fill 192); FP32
+        // powers of two.
+        for (int s = 1; s <= 32; s = bf16 ? s + 1 : 2 * s) {
             if (s > 1 && !can_split) break;
-            const int64_t kps = cdiv(cdiv(a.K, s), bk) * bk;
+            const int64_t kunit = bf16 ? 2 * bk : bk;
+            const int64_t kps = cdiv(cdiv(a.K, s), kunit) * kunit;
             if (s > 1 && kps < 4 * bk) break;
             const int64_t splits = s > 1 ? cdiv(a.K, kps) : 1;
             const int64_t blocks = tiles * splits;
@@ -1411,7 +1416,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
                                          blocks > best_blocks;
             if (better || tie_more_blocks) {
                 best_t = better ? t : std::min(t, best_t);
-                best = Plan{cd.b, bn, (int)splits};
+                best = Plan{cd.b, bn, (int)splits, splits > 1 ? kps : 0};
                 best_blocks = blocks;
             }
         }
@@ -1491,15 +1496,15 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     if (const char *env = std::getenv("IT_PLAN")) {
         int b = 0, sp = 0, w = 0;
         const int n = std::sscanf(env, "%d,%d,%d", &b, &sp, &w);
-        if (n >= 2) plan = Plan{b, a.dual ? b / 2 : n == 3 ? w : b, sp};
+        if (n >= 2) plan = Plan{b, a.dual ? b / 2 : n == 3 ? w : b, sp, bf16 && sp > 1 ? cdiv(cdiv(a.K, sp), 128) * 128 : 0};
     }
 #endif
     TileCfg cfg{plan.bm, plan.bn};
     int splits = plan.splits;
     a.tiles_m = (int)cdiv(a.M, cfg.bm);
     a.tiles_n = (int)cdiv(a.N, cfg.bn);
-    int64_t kps = cdiv(a.K, splits);
-    kps = cdiv(kps, bk) * bk;
+    int64_t kps = plan.k_per_split;
+    if (kps <= 0) kps = cdiv(cdiv(a.K, splits), bk) * bk;
     if (kps == 0) kps = bk;
     splits = (int)std::max<int64_t>(1, cdiv(a.K, kps));
     a.k_per_split = kps;
