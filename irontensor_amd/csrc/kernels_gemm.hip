@@ -1080,12 +1080,42 @@ __device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char 
             // consecutive 32 KB in one stage.
             const char *gl = wm == 0 ? st0 : st1, *ul = gl + 2 * HALF;
             const int64_t col = n0 + hp * EC2 + cl;
+            if (p.c_vec_ok && p.out_bf16) {
+                // BF16 outputs (as finish_swiglu4's vector path): the bias and the row pointers
+                // once per pass, then per row h = silu(g) u with g, u = alpha acc + bias.
+                f32x4 bg = {0.f, 0.f, 0.f, 0.f}, bu = {0.f, 0.f, 0.f, 0.f};
+                if (p.has_bias) {
+                    bg = f32x4{p.bias[col], p.bias[col + 1], p.bias[col + 2], p.bias[col + 3]};
+                    bu = f32x4{p.bias[p.N + col], p.bias[p.N + col + 1], p.bias[p.N + col + 2], p.bias[p.N + col + 3]};
+                }
+                const int64_t idx = coff + (m0 + wm * WT + 4 * (wn * 16) + (lane >> 4)) * p.ldc + col;
+                uint16_t *hd = (uint16_t *)p.C + idx;
+                uint16_t *gd = p.G ? (uint16_t *)p.G + idx : nullptr;
+                uint16_t *ud = p.U ? (uint16_t *)p.U + idx : nullptr;
+                const int64_t step = 4 * p.ldc;
 #pragma unroll 4
-            for (int it = wn * 16; it < wn * 16 + 16; ++it) {
-                const int rl = 4 * it + (lane >> 4);
-                const int off = rl * EP2 + ((cl ^ ((it & 1) << 5)) * 4);
-                finish_swiglu4<false>(p, *(const f32x4 *)(gl + off), *(const f32x4 *)(ul + off), m0 + wm * WT + rl,
-                                      col, coff);
+                for (int it = wn * 16; it < wn * 16 + 16; ++it) {
+                    const int off = (4 * it + (lane >> 4)) * EP2 + ((cl ^ ((it & 1) << 5)) * 4);
+                    const f32x4 g = *(const f32x4 *)(gl + off) * p.alpha + bg;
+                    const f32x4 u = *(const f32x4 *)(ul + off) * p.alpha + bu;
+                    f32x4 h;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) h[e] = silu(g[e]) * u[e];
+                    *(u32x2 *)hd = u32x2{pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3])};
+                    if (gd) *(u32x2 *)gd = u32x2{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3])};
+                    if (ud) *(u32x2 *)ud = u32x2{pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3])};
+                    hd += step;
+                    if (gd) gd += step;
+                    if (ud) ud += step;
+                }
+            } else {
+#pragma unroll 4
+                for (int it = wn * 16; it < wn * 16 + 16; ++it) {
+                    const int rl = 4 * it + (lane >> 4);
+                    const int off = rl * EP2 + ((cl ^ ((it & 1) << 5)) * 4);
+                    finish_swiglu4<false>(p, *(const f32x4 *)(gl + off), *(const f32x4 *)(ul + off),
+                                          m0 + wm * WT + rl, col, coff);
+                }
             }
         } else {
             const int64_t col = n0 + wn * (FB * 32) + hp * EC2 + cl;
