@@ -163,6 +163,34 @@ it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op 
                   float beta, void *C, int64_t ldc, int64_t strideC,
                   int64_t batch, const it_epilogue *epi);
 
+/* One GEMM of an it_gemm_group call: it_gemm's arguments after dtype_in and dtype_out. */
+typedef struct it_gemm_call {
+    it_op transA, transB;
+    int64_t M, N, K;
+    float alpha;
+    const void *A;
+    int64_t lda, strideA;
+    const void *B;
+    int64_t ldb, strideB;
+    float beta;
+    void *C;
+    int64_t ldc, strideC;
+    int64_t batch;
+    const it_epilogue *epi;
+} it_gemm_call;
+
+/* `count` (<= 8) independent GEMMs with the same dtypes, stream-ordered on the context's stream as
+ * `count` it_gemm calls would be, each validated as it_gemm validates (the first failure is
+ * returned before anything is launched). No counterpart in the reference, whose CommandBatch
+ * (src/command_batch.rs:166-181) gathers a step's dispatches into one command buffer but issues
+ * each GEMM as its own dispatch; for callers holding several GEMMs at once (a layer's weight
+ * gradients). When every call is a BF16 GEMM of batch 1 in one layout on whole 256 x 256 tiles
+ * with a plain epilogue and their tiles fit one round of the GPU, they run as one launch with K
+ * unsplit (results can differ in the last bits from separate calls that split K); otherwise each
+ * runs exactly as it_gemm would. The outputs must not overlap each other's inputs. */
+it_status it_gemm_group(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, int count,
+                        const it_gemm_call *calls);
+
 /* Validates it_gemm's arguments without touching the device (same status and message as it_gemm). */
 it_status it_gemm_check(it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_op transB,
                         int64_t M, int64_t N, int64_t K, const void *A, int64_t lda, int64_t strideA,

@@ -58,6 +58,30 @@ class Epilogue(C.Structure):
     ]
 
 
+class GemmCall(C.Structure):
+    """One GEMM of it_gemm_group (it_gemm's arguments after the dtypes)."""
+    _fields_ = [
+        ("transA", C.c_int),
+        ("transB", C.c_int),
+        ("M", c_i64),
+        ("N", c_i64),
+        ("K", c_i64),
+        ("alpha", c_float),
+        ("A", c_void_p),
+        ("lda", c_i64),
+        ("strideA", c_i64),
+        ("B", c_void_p),
+        ("ldb", c_i64),
+        ("strideB", c_i64),
+        ("beta", c_float),
+        ("C", c_void_p),
+        ("ldc", c_i64),
+        ("strideC", c_i64),
+        ("batch", c_i64),
+        ("epi", C.POINTER(Epilogue)),
+    ]
+
+
 class AttnLayout(C.Structure):
     _fields_ = [
         ("heads", c_i64),
@@ -94,6 +118,7 @@ _SIGNATURES = {
     "it_gemm": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_float,
                         c_void_p, c_i64, c_i64, c_void_p, c_i64, c_i64, c_float,
                         c_void_p, c_i64, c_i64, c_i64, C.POINTER(Epilogue)]),
+    "it_gemm_group": (c_int, [c_void_p, c_int, c_int, c_int, C.POINTER(GemmCall)]),
     "it_gemm_check": (c_int, [c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64,
                               c_void_p, c_i64, c_i64, c_void_p, c_i64, c_i64, c_float,
                               c_void_p, c_i64, c_i64, c_i64, C.POINTER(Epilogue)]),

@@ -116,20 +116,13 @@ it_status it_gemm_check(it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_
     return IT_OK;
 }
 
-it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_op transB,
-                  int64_t M, int64_t N, int64_t K, float alpha,
-                  const void *A, int64_t lda, int64_t strideA,
-                  const void *B, int64_t ldb, int64_t strideB,
-                  float beta, void *C, int64_t ldc, int64_t strideC,
-                  int64_t batch, const it_epilogue *epi) {
-    it_status st = it_gemm_check(dtype_in, dtype_out, transA, transB, M, N, K, A, lda, strideA, B,
-                                 ldb, strideB, beta, C, ldc, strideC, batch, epi);
-    if (st != IT_OK) return st;
-    if (!ctx) return fail(IT_ERR_NULL, "matmul: ctx is NULL");
-    if (M == 0 || N == 0 || batch == 0) return IT_OK;
-
+// The kernel arguments of one it_gemm call (already validated).
+static it_status gemm_args(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, int64_t M, int64_t N, int64_t K,
+                           float alpha, const void *A, int64_t lda, int64_t strideA, const void *B, int64_t ldb,
+                           int64_t strideB, float beta, void *C, int64_t ldc, int64_t strideC, int64_t batch,
+                           const it_epilogue *epi, it::GemmArgs &a) {
     const int eb = dtype_in == IT_BF16 ? 2 : 4;
-    it::GemmArgs a{};
+    a = it::GemmArgs{};
     a.A = A;
     a.B = B;
     a.C = C;
@@ -191,7 +184,64 @@ it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op 
             a.rope_cols = epi->rope_cols;
         }
     }
+    return IT_OK;
+}
+
+it_status it_gemm(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, it_op transA, it_op transB,
+                  int64_t M, int64_t N, int64_t K, float alpha,
+                  const void *A, int64_t lda, int64_t strideA,
+                  const void *B, int64_t ldb, int64_t strideB,
+                  float beta, void *C, int64_t ldc, int64_t strideC,
+                  int64_t batch, const it_epilogue *epi) {
+    it_status st = it_gemm_check(dtype_in, dtype_out, transA, transB, M, N, K, A, lda, strideA, B,
+                                 ldb, strideB, beta, C, ldc, strideC, batch, epi);
+    if (st != IT_OK) return st;
+    if (!ctx) return fail(IT_ERR_NULL, "matmul: ctx is NULL");
+    if (M == 0 || N == 0 || batch == 0) return IT_OK;
+    it::GemmArgs a;
+    st = gemm_args(ctx, dtype_in, dtype_out, M, N, K, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc, strideC,
+                   batch, epi, a);
+    if (st != IT_OK) return st;
     return it::launch_gemm(ctx, dtype_in, transA == IT_OP_T, transB == IT_OP_T, a, "");
+}
+
+it_status it_gemm_group(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, int count,
+                        const it_gemm_call *calls) {
+    if (count < 0 || count > 8) return fail(IT_ERR_INVALID, "matmul group: count must be 0..8, got " + i64(count));
+    if (count > 0 && !calls) return fail(IT_ERR_NULL, "matmul group: calls is NULL");
+    for (int i = 0; i < count; ++i) {
+        const it_gemm_call &c = calls[i];
+        const it_status st = it_gemm_check(dtype_in, dtype_out, c.transA, c.transB, c.M, c.N, c.K, c.A, c.lda,
+                                           c.strideA, c.B, c.ldb, c.strideB, c.beta, c.C, c.ldc, c.strideC, c.batch,
+                                           c.epi);
+        if (st != IT_OK) return st;
+    }
+    if (!ctx) return fail(IT_ERR_NULL, "matmul: ctx is NULL");
+    // Consecutive calls of one layout with outputs form the groups; empty GEMMs are skipped.
+    it::GemmArgs args[8];
+    int n = 0;
+    bool ta = false, tb = false;
+    auto flush = [&]() -> it_status {
+        const it_status st = n ? it::launch_gemm_group(ctx, dtype_in, ta, tb, args, n, "") : IT_OK;
+        n = 0;
+        return st;
+    };
+    for (int i = 0; i < count; ++i) {
+        const it_gemm_call &c = calls[i];
+        if (c.M == 0 || c.N == 0 || c.batch == 0) continue;
+        const bool cta = c.transA == IT_OP_T, ctb = c.transB == IT_OP_T;
+        if (n && (cta != ta || ctb != tb)) {
+            const it_status st = flush();
+            if (st != IT_OK) return st;
+        }
+        ta = cta;
+        tb = ctb;
+        const it_status st = gemm_args(ctx, dtype_in, dtype_out, c.M, c.N, c.K, c.alpha, c.A, c.lda, c.strideA, c.B,
+                                       c.ldb, c.strideB, c.beta, c.C, c.ldc, c.strideC, c.batch, c.epi, args[n]);
+        if (st != IT_OK) return st;
+        ++n;
+    }
+    return flush();
 }
 
 it_status it_f32_to_bf16(it_context *ctx, const float *src, uint16_t *dst, int64_t n) {

@@ -1158,27 +1158,21 @@ __device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char 
     }
 }
 
-template <bool TA, bool TB, bool DUAL = false, int FB = 4>
-__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void gemm_bf16_dtl(const GemmArgs p) {
-    // DUAL (SwiGLU, Y = X.W^T only): the B stage's rows 0..127 are 128 gate-weight rows (loaded
-    // by waves 0-1) and rows 128..255 the same rows of the up weight (waves 2-3), so waves wn = 0
-    // accumulate gate and wn = 1 up for one 256 x 128 output tile; the epilogue pairs them.
-    // FB = 2: a 256 x 128 output tile (twice the tiles where 256 x 256 would leave CUs idle), with
-    // three stages of 48 KB.
+// One block of gemm_bf16_dtl: output tile `tile` (in map_tile order) of batch-and-split index z.
+// DUAL (SwiGLU, Y = X.W^T only): the B stage's rows 0..127 are 128 gate-weight rows (loaded by
+// waves 0-1) and rows 128..255 the same rows of the up weight (waves 2-3), so waves wn = 0
+// accumulate gate and wn = 1 up for one 256 x 128 output tile; the epilogue pairs them. FB = 2:
+// a 256 x 128 output tile (twice the tiles where 256 x 256 would leave CUs idle), with three
+// stages of 48 KB.
+template <bool TA, bool TB, bool DUAL, int FB>
+__device__ __forceinline__ void dtl_block(const GemmArgs &p, int tile, int64_t z, char *st0, char *st1, char *st2) {
     static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
     using T = uint16_t;
     constexpr int BM = 256, BN = FB * 64, BK = 64, F = 4;
-    constexpr int STAGE = (BM + (FB == 4 ? 256 : 128)) * BK * 2;
-    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
-    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
-    __shared__ __attribute__((aligned(1024))) char st2[FB == 2 ? STAGE : 16];  // FB = 2 only
-
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int tm, tn;
-    map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int64_t z = blockIdx.y;
+    map_tile(tile, p.tiles_m, p.tiles_n, tm, tn);
     const int64_t b = z % p.batch, split = z / p.batch;
     const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * (DUAL ? BN / 2 : BN);
@@ -1191,6 +1185,41 @@ void gemm_bf16_dtl(const GemmArgs p) {
     dtl_tile<TA, TB, DUAL, FB>(p, st0, st1, st2, A, B, ke - kb, ke > kb ? (int)((ke - kb) / BK) : 0, acc, wave,
                                lane);
     dtl_epilogue<DUAL, FB>(p, st0, st1, st2, acc, m0, n0, bo * p.sC_out + bi * p.sC_in, z, wave, lane);
+}
+
+template <bool TA, bool TB, bool DUAL = false, int FB = 4>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_dtl(const GemmArgs p) {
+    constexpr int STAGE = (256 + (FB == 4 ? 256 : 128)) * 64 * 2;
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st2[FB == 2 ? STAGE : 16];  // FB = 2 only
+    dtl_block<TA, TB, DUAL, FB>(p, blockIdx.x, blockIdx.y, st0, st1, st2);
+}
+
+// Several independent GEMMs of one layout in one launch of 256 x 256 direct-to-LDS tiles (batch 1,
+// no split-K): problem g takes blocks start[g] .. start[g + 1] - 1, each problem's range padded to
+// a multiple of 8 blocks (the padding blocks return at once) so that map_tile's XCD-aware order
+// holds within every problem.
+constexpr int GEMM_GROUP_MAX = 8;
+struct GemmGroupArgs {
+    GemmArgs g[GEMM_GROUP_MAX];
+    int start[GEMM_GROUP_MAX + 1];
+    int count;
+};
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_dtl_group(const GemmGroupArgs grp) {
+    constexpr int STAGE = 512 * 64 * 2;
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+    int gi = 0;
+    while (gi + 1 < grp.count && (int)blockIdx.x >= grp.start[gi + 1]) ++gi;
+    const GemmArgs &p = grp.g[gi];
+    const int tile = (int)blockIdx.x - grp.start[gi];
+    if (tile >= p.tiles_m * p.tiles_n) return;  // padding block
+    dtl_block<TA, TB, false, 4>(p, tile, 0, st0, st1, st0);
 }
 
 // Deterministic split-K reduction: partial sums are added in split order.
@@ -1380,7 +1409,8 @@ struct Plan {
 //     weight gradients), which is what split-K fixes by running more blocks at once;
 //   * split-K adds its partial-sum traffic and a reduction launch.
 // Estimated seconds, lowest wins.
-Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
+// est (optional): the chosen plan's estimated seconds.
+Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, double *est = nullptr) {
     struct Cand {
         int b, bn, occ;  // b x bn tiles (bn 0: square)
         double eff;
@@ -1451,6 +1481,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb) {
             }
         }
     }
+    if (est) *est = best_t;
     return best;
 }
 
@@ -1575,6 +1606,82 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
         it_status st = launch_splitk_reduce(ctx->stream, a);
         if (st != IT_OK) return st;
     }
+    if (ctx->profiling) profile_end(ctx, key, ev);
+    return IT_OK;
+}
+
+
+// Runs `count` independent GEMMs of one input dtype and layout on ctx->stream. As one launch of
+// gemm_bf16_dtl_group when each is a BF16 GEMM of batch 1 that the direct-to-LDS kernel takes as
+// whole 256 x 256 tiles with one split and a plain epilogue (bias, alpha/beta, BF16 or FP32
+// out), their tiles fit one round of CUs, and the planner's estimate for that round (every block
+// runs its whole K) beats the sum of its estimates for the separate launches; otherwise each goes
+// through launch_gemm, as separate calls would.
+it_status launch_gemm_group(it_context *ctx, it_dtype dtype_in, bool transA, bool transB, GemmArgs *args, int count,
+                            const char *profile_tag) {
+    static_assert(sizeof(GemmGroupArgs) <= 4096, "kernel arguments");
+    const bool bf16 = dtype_in == IT_BF16;
+    const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    bool fuse = bf16 && count >= 2 && count <= GEMM_GROUP_MAX;
+    int64_t blocks = 0;
+    double separate = 0.0;
+    int64_t kmax = 0;
+    for (int i = 0; fuse && i < count; ++i) {
+        GemmArgs &a = args[i];
+        a.splits = 1;
+        a.k_per_split = a.K;
+        a.tiles_m = (int)cdiv(a.M, 256);
+        a.tiles_n = (int)cdiv(a.N, 256);
+        fuse = a.batch == 1 && !a.dual && a.K > 0 && dtl_applicable(transA, transB, a, 256) &&
+               !gemv_applicable(a, bf16, transA, transB) && !gemv_kn_applicable(a, bf16, transA, transB);
+        blocks += cdiv((int64_t)a.tiles_m * a.tiles_n, 8) * 8;
+        double t = 0.0;
+        choose_plan(a, bf16, cus, transA, transB, &t);
+        separate += t;
+        kmax = std::max(kmax, a.K);
+    }
+    if (fuse && blocks <= cus) {
+        // one round, every block over its whole K (the planner's direct-to-LDS pricing)
+        const double step = 2.0 * 256 * 256 * 64 / (2.5e15 / 256.0 * 0.53);
+        const double grouped = 3e-6 + cdiv(kmax, 64) * std::max(step, 1.0e-6);
+        fuse = grouped < 0.97 * separate;
+    } else {
+        fuse = false;
+    }
+    if (!fuse) {
+        for (int i = 0; i < count; ++i) {
+            it_status st = launch_gemm(ctx, dtype_in, transA, transB, args[i], profile_tag);
+            if (st != IT_OK) return st;
+        }
+        return IT_OK;
+    }
+    GemmGroupArgs grp{};
+    grp.count = count;
+    int start = 0;
+    for (int i = 0; i < count; ++i) {
+        grp.g[i] = args[i];
+        grp.start[i] = start;
+        start += (int)(cdiv((int64_t)args[i].tiles_m * args[i].tiles_n, 8) * 8);
+    }
+    grp.start[count] = start;
+    std::string key;
+    hipEvent_t ev = nullptr;
+    if (ctx->profiling) {
+        key = std::string("gemm_bf16_") + (transA ? 'T' : 'N') + (transB ? 'T' : 'N') + "_256x256_dtl_group|" +
+              (profile_tag ? profile_tag : "");
+        for (int i = 0; i < count; ++i)
+            key += (i ? "+[" : "[") + std::to_string(args[i].M) + "," + std::to_string(args[i].N) + "," +
+                   std::to_string(args[i].K) + "]";
+        key += "x1 s1";
+        profile_begin(ctx, key, &ev);
+    }
+    const dim3 grid((unsigned)start);
+    if (!transA && transB) hipLaunchKernelGGL((gemm_bf16_dtl_group<false, true>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+    else if (!transA && !transB) hipLaunchKernelGGL((gemm_bf16_dtl_group<false, false>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+    else if (transA && !transB) hipLaunchKernelGGL((gemm_bf16_dtl_group<true, false>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+    else hipLaunchKernelGGL((gemm_bf16_dtl_group<true, true>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail_hip(e, "gemm group launch");
     if (ctx->profiling) profile_end(ctx, key, ev);
     return IT_OK;
 }

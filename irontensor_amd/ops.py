@@ -87,6 +87,39 @@ def gemm(a: Tensor, b: Tensor, *, trans_a: bool = False, trans_b: bool = False, 
     return out
 
 
+def gemm_group(calls, op: str = "matmul_group") -> None:
+    """Several independent 2D GEMMs in one it_gemm_group call: `calls` holds up to 8 tuples
+    (a, b, out, trans_a, trans_b), out = op(a) . op(b), all of one input and one output precision.
+    Where the library can, they run as one launch (BF16, whole 256 x 256 tiles, one round);
+    otherwise as separate GEMMs. No counterpart in the reference (its command batch issues each
+    GEMM separately); for callers holding several GEMMs at once, such as a layer's weight
+    gradients."""
+    if not calls:
+        return
+    if len(calls) > 8:
+        raise Panic(f"{op}: at most 8 GEMMs per group, got {len(calls)}")
+    a0, _, o0, _, _ = calls[0]
+    structs = []
+    for a, b, out, ta, tb in calls:
+        if a.precision() != a0.precision() or b.precision() != a0.precision():
+            raise PrecisionMismatch(op, _prec_name(a0.precision()), _prec_name(b.precision()))
+        if out.precision() != o0.precision():
+            raise PrecisionMismatch(op, _prec_name(o0.precision()), _prec_name(out.precision()))
+        sa, sb = a.shape(), b.shape()
+        if len(sa) != 2 or len(sb) != 2:
+            raise UnsupportedDimensions(op, "2D tensors", [len(sa), len(sb)])
+        M, K = (sa[1], sa[0]) if ta else (sa[0], sa[1])
+        K2, N = (sb[1], sb[0]) if tb else (sb[0], sb[1])
+        if K != K2:
+            raise InnerDimensionMismatch(op, sa, sb)
+        if out.shape() != [M, N]:
+            raise ShapeMismatch(op, str([M, N]), str(out.shape()))
+        structs.append(_lib.GemmCall(_lib.IT_OP_T if ta else _lib.IT_OP_N, _lib.IT_OP_T if tb else _lib.IT_OP_N,
+                                     M, N, K, 1.0, a.ptr, sa[1], 0, b.ptr, sb[1], 0, 0.0, out.ptr, N, 0, 1, None))
+    arr = (_lib.GemmCall * len(structs))(*structs)
+    check(a0.ctx.lib.it_gemm_group(a0.ctx.handle, int(a0.precision()), int(o0.precision()), len(structs), arr), op)
+
+
 # ------------------------------------------------------------------ FP32 matmul family
 
 def matmul_mps(a: Tensor, b: Tensor) -> Tensor:

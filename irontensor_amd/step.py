@@ -95,6 +95,8 @@ class GemmStep:
         # layer beats one per GEMM (dw_fork = "gemm").
         self.overlap = overlap_weight_grads
         self.dw_fork = "layer"
+        # A layer's weight gradients go to the library as one group (it_gemm_group).
+        self.group_weight_grads = True
         self._dw_queue = None
 
         def w(shape_, std=0.02):
@@ -169,18 +171,27 @@ class GemmStep:
         self.seed_of[t.ptr] = (self._seed, std)
         return t
 
+    def _call(self, A: Tensor, B: Tensor, Cout: Tensor, ta: bool, tb: bool, M, N, K, alpha=1.0,
+              epi: Optional[_lib.Epilogue] = None, a_off=0, lda=None) -> _lib.GemmCall:
+        """it_gemm's arguments for one GEMM of the step (batch 1, beta 0)."""
+        lda = lda if lda is not None else (A.shape()[-1])
+        eb = self.prec.byte_size()
+        return _lib.GemmCall(int(ta), int(tb), M, N, K, float(alpha), A.ptr + a_off * eb, lda, 0, B.ptr,
+                             B.shape()[-1], 0, 0.0, Cout.ptr, Cout.shape()[-1], 0, 1,
+                             C.pointer(epi) if epi is not None else None)
+
     def _gemm(self, name, A: Tensor, B: Tensor, Cout: Tensor, ta: bool, tb: bool, M, N, K,
               alpha=1.0, epi: Optional[_lib.Epilogue] = None, a_off=0, lda=None):
-        lda = lda if lda is not None else (A.shape()[-1])
-        ldb = B.shape()[-1]
-        ldc = Cout.shape()[-1]
-        eb = self.prec.byte_size()
-        st = self.lib.it_gemm(self.ctx.handle, int(self.prec), int(Cout.precision()),
-                              int(ta), int(tb), M, N, K, float(alpha),
-                              C.c_void_p(A.ptr + a_off * eb), lda, 0, C.c_void_p(B.ptr), ldb, 0,
-                              0.0, C.c_void_p(Cout.ptr), ldc, 0, 1,
+        c = self._call(A, B, Cout, ta, tb, M, N, K, alpha, epi, a_off, lda)
+        st = self.lib.it_gemm(self.ctx.handle, int(self.prec), int(Cout.precision()), c.transA, c.transB, M, N, K,
+                              c.alpha, c.A, c.lda, 0, c.B, c.ldb, 0, 0.0, c.C, c.ldc, 0, 1,
                               C.byref(epi) if epi is not None else None)
         check(st, name)
+        self._note(name, A, B, Cout, ta, tb, M, N, K, alpha, epi, a_off, lda)
+
+    def _note(self, name, A, B, Cout, ta, tb, M, N, K, alpha=1.0, epi=None, a_off=0, lda=None):
+        """The step's bookkeeping of one GEMM: its FLOPs and the first call of each shape."""
+        lda = lda if lda is not None else (A.shape()[-1])
         if self._record:
             mult = 2 if (epi is not None and epi.flags & _lib.IT_EPI_SWIGLU) else 1
             self.launches.append(_Launch(name, 2.0 * M * N * K * mult))
@@ -189,13 +200,13 @@ class GemmStep:
                 self._calls[key] = (name, A, B, Cout, ta, tb, M, N, K, alpha, epi, a_off, lda)
 
     def _dw(self, *args, **kw):
-        """A weight-gradient GEMM, on the side stream when overlapping (queued for the layer's
-        single fork when one is open)."""
-        if not self.overlap:
-            return self._gemm(*args, **kw)
+        """A weight-gradient GEMM: queued for the layer's group when one is open (issued together
+        at the end of the layer), else on the side stream when overlapping."""
         if self._dw_queue is not None:
             self._dw_queue.append((args, kw))
             return None
+        if not self.overlap:
+            return self._gemm(*args, **kw)
         check(self.lib.it_side_begin(self.ctx.handle), "side stream")
         try:
             self._gemm(*args, **kw)
@@ -203,15 +214,27 @@ class GemmStep:
             check(self.lib.it_side_end(self.ctx.handle), "side stream")
 
     def _dw_flush(self):
+        """The layer's queued weight gradients (on the side stream when overlapping), as one
+        it_gemm_group call (one launch where the library can group them, else one GEMM after the
+        other)."""
         q, self._dw_queue = self._dw_queue, None
         if not q:
             return
-        check(self.lib.it_side_begin(self.ctx.handle), "side stream")
+        if self.overlap:
+            check(self.lib.it_side_begin(self.ctx.handle), "side stream")
         try:
-            for args, kw in q:
-                self._gemm(*args, **kw)
+            if self.group_weight_grads and len({a[3].precision() for a, _ in q}) == 1:
+                calls = (_lib.GemmCall * len(q))(*[self._call(*a[1:], **kw) for a, kw in q])
+                check(self.lib.it_gemm_group(self.ctx.handle, int(self.prec), int(q[0][0][3].precision()), len(q),
+                                             calls), "weight gradients")
+                for args, kw in q:
+                    self._note(*args, **kw)
+            else:
+                for args, kw in q:
+                    self._gemm(*args, **kw)
         finally:
-            check(self.lib.it_side_end(self.ctx.handle), "side stream")
+            if self.overlap:
+                check(self.lib.it_side_end(self.ctx.handle), "side stream")
 
     def _layouts(self):
         s = self.s
@@ -254,7 +277,7 @@ class GemmStep:
     def backward_layer(self, l: int) -> None:
         s, P = self.s, self.prec
         T, H, F = s.tokens, s.hidden, s.ffn
-        if self.overlap and self.dw_fork == "layer":
+        if (self.overlap and self.dw_fork == "layer") or self.group_weight_grads:
             self._dw_queue = []
         # down: dHh = dZ.Wd (NN), dWd = dZ^T.Hh (TN)
         self._dw("down.dW", self.dZ, self.Hh[l], self.dWd[l], True, False, H, F, T)

@@ -103,6 +103,23 @@ def test_gemm_rejects_before_device_work():
     assert st == _lib.IT_ERR_NULL and "ctx" in _lib.last_error()
 
 
+def test_gemm_group_validates_every_call_first():
+    """it_gemm_group checks its count and each call as it_gemm does before touching the context
+    (a NULL context is reported only once every call is valid)."""
+    lib = _lib.load()
+    arr = (_lib.GemmCall * 9)()
+    st = lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 9, arr)
+    assert st == _lib.IT_ERR_INVALID and "count" in _lib.last_error()
+    assert lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 2, None) == _lib.IT_ERR_NULL
+    good = _lib.GemmCall(_lib.IT_OP_T, _lib.IT_OP_N, 4, 4, 4, 1.0, 16, 4, 0, 16, 4, 0, 0.0, 16, 4, 0, 1, None)
+    bad = _lib.GemmCall(_lib.IT_OP_T, _lib.IT_OP_N, 4, 4, 4, 1.0, 16, 2, 0, 16, 4, 0, 0.0, 16, 4, 0, 1, None)
+    st = lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 2, (_lib.GemmCall * 2)(good, bad))
+    assert st == _lib.IT_ERR_INVALID and "lda" in _lib.last_error()
+    st = lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 2, (_lib.GemmCall * 2)(good, good))
+    assert st == _lib.IT_ERR_NULL and "ctx" in _lib.last_error()
+    assert lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 0, None) == _lib.IT_ERR_NULL  # ctx checked last
+
+
 def test_null_context_calls_fail_cleanly():
     lib = _lib.load()
     assert lib.it_malloc(None, 16, C.byref(C.c_void_p())) == _lib.IT_ERR_NULL

@@ -1,0 +1,98 @@
+"""it_gemm_group (no reference counterpart: the reference's CommandBatch, src/command_batch.rs:166-181,
+issues each GEMM separately) on the GPU: the medium step's four weight gradients of one layer
+(dW = dY^T . X, K = 8192 tokens: [5632,1024], [3072,1024], [1024,2816], [1024,1024]) run as one
+grouped launch of 256 x 256 direct-to-LDS tiles with K unsplit; groups the library does not fuse
+(FP32, mixed layouts) run as the separate GEMMs would, bit for bit."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from irontensor_amd import profiler, synth
+from tests.numerics import BF16_FROB_TOL, FP32_TOL, frob_rel, normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+T = 8192
+DW = [(5632, 1024), (3072, 1024), (1024, 2816), (1024, 1024)]  # (M, N) of dW = dY^T . X
+
+
+def _keys(it, fn):
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    fn()
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    return keys
+
+
+def test_group_weight_gradients_exact(it):
+    """Small integers: every grouped product equals a float64 product bit for bit on sampled rows
+    (exact in any FP32 summation order), the group is one launch, and a second run repeats it."""
+    ops = []
+    for i, (m, n) in enumerate(DW):
+        dy = synth.small_ints(300 + i, (T, m), -2, 2)
+        x = synth.small_ints(310 + i, (T, n), -2, 2)
+        ops.append((dy, x, it.Tensor.from_f32_as_bf16(dy, dy.shape), it.Tensor.from_f32_as_bf16(x, x.shape),
+                    it.Tensor.zeros([m, n])))
+    calls = [(a, b, out, True, False) for _, _, a, b, out in ops]
+    keys = _keys(it, lambda: it.gemm_group(calls))
+    print(f"[group exact] {keys}", flush=True)
+    assert len(keys) == 1 and "_dtl_group" in keys[0], keys
+    first = [out.numpy() for *_, out in ops]
+    rng = np.random.default_rng(3)
+    for (dy, x, *_), got, (m, n) in zip(ops, first, DW):
+        rows = rng.choice(m, 48, replace=False)
+        exact = dy[:, rows].T.astype(np.float64) @ x.astype(np.float64)
+        assert np.array_equal(got[rows], exact.astype(np.float32)), (m, n)
+    it.gemm_group(calls)
+    for (*_, out), f in zip(ops, first):
+        assert np.array_equal(out.numpy(), f)
+
+
+def test_group_matches_separate_and_oracle(it, oracle):
+    """Gaussian operands: each grouped FP32 product within the FP32 contract of the oracle on the
+    same BF16 operands (sampled rows) and of the separate it_gemm call (which splits K), and within
+    the BF16 contract of the unrounded product; the grouped BF16 output is the RNE rounding of the
+    grouped FP32 output bit for bit (one accumulation, rounded once)."""
+    ops = []
+    for i, (m, n) in enumerate(DW):
+        dy, x = synth.normal(320 + i, (T, m)), synth.normal(330 + i, (T, n))
+        ops.append((dy, x, it.Tensor.from_f32_as_bf16(dy, dy.shape), it.Tensor.from_f32_as_bf16(x, x.shape)))
+    got = {}
+    for prec in (it.Precision.FP32, it.Precision.BF16):
+        outs = [it.Tensor.empty([m, n], prec) for m, n in DW]
+        keys = _keys(it, lambda: it.gemm_group([(a, b, o, True, False) for (_, _, a, b), o in zip(ops, outs)]))
+        assert len(keys) == 1 and "_dtl_group" in keys[0], keys
+        got[prec] = outs
+    rng = np.random.default_rng(4)
+    for (dy, x, a, b), o32, o16, (m, n) in zip(ops, got[it.Precision.FP32], got[it.Precision.BF16], DW):
+        g = o32.numpy()
+        sep = it.gemm(a, b, trans_a=True).numpy()
+        rows = rng.choice(m, 32, replace=False)
+        a_rows = np.ascontiguousarray(dy[:, rows].T)
+        ref16 = oracle.gemm_bf16(oracle.f32_to_bf16(a_rows), oracle.f32_to_bf16(x), False, False)
+        assert normwise_rel(g[rows], ref16) <= FP32_TOL, (m, n)
+        assert normwise_rel(g, sep) <= FP32_TOL, (m, n)
+        assert frob_rel(g[rows], oracle.gemm_f32(a_rows, x)) <= BF16_FROB_TOL, (m, n)
+        assert np.array_equal(o16.as_bf16_slice().reshape(m, n), oracle.f32_to_bf16(g)), (m, n)
+
+
+def test_group_fallbacks_equal_separate_calls(it):
+    """Groups the library does not fuse run as the separate GEMMs: FP32 weight gradients, and
+    BF16 GEMMs of two layouts, bit-identical to separate it_gemm calls."""
+    a32 = [it.Tensor.from_f32_slice(synth.normal(340 + i, (1024, 256 * (i + 1))), [1024, 256 * (i + 1)])
+           for i in range(3)]
+    x32 = it.Tensor.from_f32_slice(synth.normal(345, (1024, 384)), [1024, 384])
+    outs = [it.Tensor.zeros([256 * (i + 1), 384]) for i in range(3)]
+    keys = _keys(it, lambda: it.gemm_group([(a, x32, o, True, False) for a, o in zip(a32, outs)]))
+    assert not any("_group" in k for k in keys) and len(keys) == 3, keys
+    for a, o in zip(a32, outs):
+        assert np.array_equal(o.numpy(), it.gemm(a, x32, trans_a=True).numpy())
+    a16 = it.Tensor.from_f32_as_bf16(synth.normal(350, (2048, 1024)), [2048, 1024])
+    w16 = it.Tensor.from_f32_as_bf16(synth.normal(351, (1024, 1024)), [1024, 1024])
+    o1, o2 = it.Tensor.zeros([2048, 1024]), it.Tensor.zeros([2048, 1024])
+    it.gemm_group([(a16, w16, o1, False, True), (a16, w16, o2, False, False)])
+    assert np.array_equal(o1.numpy(), it.gemm(a16, w16, trans_b=True).numpy())
+    assert np.array_equal(o2.numpy(), it.gemm(a16, w16).numpy())

@@ -11,6 +11,8 @@ order (src/train/trainer/train_step.rs:39-236).
   recorded by the profiler) on 64+ sampled output rows: against the oracle on the same BF16
   operands (FP32 normwise 1e-5, or half a BF16 ulp + 1e-5 for BF16 outputs) and against the f32
   oracle on the unrounded seeded inputs (relative Frobenius 1e-2). tests/stepcheck.py does it.
+* A layer's four weight gradients, which the step issues as one it_gemm_group launch: each within
+  FP32 normwise 1e-5 of the same GEMM issued alone (the call the previous check verifies).
 """
 from __future__ import annotations
 
@@ -20,7 +22,7 @@ import numpy as np
 import pytest
 
 from irontensor_amd.step import MEDIUM, GemmStep
-from tests.numerics import BF16_FROB_TOL, frob_rel
+from tests.numerics import BF16_FROB_TOL, FP32_TOL, frob_rel, normwise_rel
 from tests.stepcheck import StepChecker
 
 pytestmark = pytest.mark.gpu
@@ -96,3 +98,28 @@ def test_medium_every_gemm_plan(it, oracle, med):
         plans[key] = chk.check_call(key)
     _log(f"[medium] {len(plans)} distinct GEMMs, plans: {sorted(set(plans.values()))}")
     assert len(plans) == 15
+
+
+def test_medium_grouped_weight_gradients(it, med):
+    st = med
+    ctx = it.Context.global_()
+    from irontensor_amd import profiler
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    st.enqueue()
+    ctx.sync()
+    keys = [k for k in profiler.stats(ctx) if "_dtl_group" in k]
+    profiler.enable(ctx, False)
+    _log(f"[medium] grouped weight-gradient launches: {keys}")
+    assert keys, "the step's weight gradients did not run as a group"
+    s, l = st.s, st.s.layers - 1  # the reissued calls are the first of each shape: the last layer's
+    T, H, F = s.tokens, s.hidden, s.ffn
+    outs = {(True, False, H, F, T): st.dWd[l], (True, False, 2 * F, H, T): st.dWgu[l],
+            (True, False, H, H, T): st.dWo[l], (True, False, 3 * H, H, T): st.dWqkv[l]}
+    grouped = {k: t.numpy() for k, t in outs.items()}
+    for k, t in outs.items():
+        st.reissue(*k)
+        ctx.sync()
+        err = normwise_rel(grouped[k], t.numpy())
+        _log(f"[medium] grouped vs single {k[2:]}: normwise {err:.2e}")
+        assert err <= FP32_TOL, k
