@@ -217,31 +217,21 @@ it_status it_gemm_group(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, 
         if (st != IT_OK) return st;
     }
     if (!ctx) return fail(IT_ERR_NULL, "matmul: ctx is NULL");
-    // Consecutive calls of one layout with outputs form the groups; empty GEMMs are skipped.
+    // Empty GEMMs are skipped; the library groups the rest where it pays.
     it::GemmArgs args[8];
+    bool ta[8], tb[8];
     int n = 0;
-    bool ta = false, tb = false;
-    auto flush = [&]() -> it_status {
-        const it_status st = n ? it::launch_gemm_group(ctx, dtype_in, ta, tb, args, n, "") : IT_OK;
-        n = 0;
-        return st;
-    };
     for (int i = 0; i < count; ++i) {
         const it_gemm_call &c = calls[i];
         if (c.M == 0 || c.N == 0 || c.batch == 0) continue;
-        const bool cta = c.transA == IT_OP_T, ctb = c.transB == IT_OP_T;
-        if (n && (cta != ta || ctb != tb)) {
-            const it_status st = flush();
-            if (st != IT_OK) return st;
-        }
-        ta = cta;
-        tb = ctb;
+        ta[n] = c.transA == IT_OP_T;
+        tb[n] = c.transB == IT_OP_T;
         const it_status st = gemm_args(ctx, dtype_in, dtype_out, c.M, c.N, c.K, c.alpha, c.A, c.lda, c.strideA, c.B,
                                        c.ldb, c.strideB, c.beta, c.C, c.ldc, c.strideC, c.batch, c.epi, args[n]);
         if (st != IT_OK) return st;
         ++n;
     }
-    return flush();
+    return it::launch_gemm_group(ctx, dtype_in, ta, tb, args, n, "");
 }
 
 it_status it_f32_to_bf16(it_context *ctx, const float *src, uint16_t *dst, int64_t n) {

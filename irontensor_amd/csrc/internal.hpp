@@ -181,10 +181,10 @@ struct GemmArgs {
 // Launches the MFMA GEMM for `dtype_in` (IT_F32 / IT_BF16). Chooses tile shape and split-K.
 it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool transB, GemmArgs args,
                       const char *profile_tag);
-// `count` independent GEMMs of one dtype and layout: one grouped launch where it pays (whole
-// 256 x 256 direct-to-LDS tiles, one round), else launch_gemm for each.
-it_status launch_gemm_group(it_context *ctx, it_dtype dtype_in, bool transA, bool transB, GemmArgs *args, int count,
-                            const char *profile_tag);
+// `count` (<= 8) independent GEMMs of one dtype (ta[i], tb[i]: their layouts): grouped launches
+// where they pay (kernels_gemm.hip), else launch_gemm for each.
+it_status launch_gemm_group(it_context *ctx, it_dtype dtype_in, const bool *ta, const bool *tb, GemmArgs *args,
+                            int count, const char *profile_tag);
 
 // Fused attention (kernels_flash.hip), head_dim 64. Per-head addressing of each operand:
 // (bh / heads) * bs + (bh % heads) * hs + row * rs + col (element strides).

@@ -901,11 +901,13 @@ struct DtlOperand {
 // s_waitcnt immediate: vmcnt(vm) lgkmcnt(lgkm), expcnt not waited on.
 constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8); }
 
-template <bool TA, bool TB, bool DUAL, int FB>
+template <bool TA, bool TB, bool DUAL, int FB, bool OPAQUE = (FB == 2)>
 __device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *__restrict__ st0, char *__restrict__ st1,
                                          char *__restrict__ st2, const uint16_t *A,
                                          const uint16_t *B, int64_t krange, int ntiles, f32x16 (&acc)[4][FB],
                                          int wave, int lane) {
+    // OPAQUE: the direct loads' LDS addresses hidden from the compiler (needed whenever the
+    // stages share one LDS object or are three: then only the explicit waits order the loads).
     // FB: 32-column B fragments per wave (4: 256 x 256 tile, 128 x 128 per wave, two 64 KB
     // stages; 2: 256 x 128 tile, 128 x 64 per wave, three 48 KB stages, so that loads run two
     // k-tiles ahead of a k-tile that takes half as long).
@@ -928,8 +930,8 @@ __device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *__restrict__ s
     const int last = ntiles - 1;
     auto issue = [&](int t, char *stage) {
         const int64_t kk = (int64_t)min(t, last) * BK;
-        oa.issue(stage, kk, wave, NS == 3);
-        ob.issue(stage + TILE, kk, wave, NS == 3);
+        oa.issue(stage, kk, wave, OPAQUE);
+        ob.issue(stage + TILE, kk, wave, OPAQUE);
     };
     u32x4 fa0[F], fb0[FB], fa1[F], fb1[FB];
     auto frags = [&](u32x4 (&fa)[F], u32x4 (&fb)[FB], const char *st, int ks) {
@@ -1164,7 +1166,7 @@ __device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char 
 // accumulate gate and wn = 1 up for one 256 x 128 output tile; the epilogue pairs them. FB = 2:
 // a 256 x 128 output tile (twice the tiles where 256 x 256 would leave CUs idle), with three
 // stages of 48 KB.
-template <bool TA, bool TB, bool DUAL, int FB>
+template <bool TA, bool TB, bool DUAL, int FB, bool OPAQUE = (FB == 2)>
 __device__ __forceinline__ void dtl_block(const GemmArgs &p, int tile, int64_t z, char *st0, char *st1, char *st2) {
     static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
     using T = uint16_t;
@@ -1182,8 +1184,8 @@ __device__ __forceinline__ void dtl_block(const GemmArgs &p, int tile, int64_t z
     const T *Bm = (const T *)(DUAL && wave >= 2 ? p.B2 : p.B);
     const T *B = Bm + bo * p.sB_out + bi * p.sB_in + (TB ? n0 * p.ldb + kb : kb * p.ldb + n0);
     f32x16 acc[F][FB];
-    dtl_tile<TA, TB, DUAL, FB>(p, st0, st1, st2, A, B, ke - kb, ke > kb ? (int)((ke - kb) / BK) : 0, acc, wave,
-                               lane);
+    dtl_tile<TA, TB, DUAL, FB, OPAQUE>(p, st0, st1, st2, A, B, ke - kb, ke > kb ? (int)((ke - kb) / BK) : 0, acc,
+                                       wave, lane);
     dtl_epilogue<DUAL, FB>(p, st0, st1, st2, acc, m0, n0, bo * p.sC_out + bi * p.sC_in, z, wave, lane);
 }
 
@@ -1611,46 +1613,79 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
 }
 
 
-// Runs `count` independent GEMMs of one input dtype and layout on ctx->stream. As one launch of
-// gemm_bf16_dtl_group when each is a BF16 GEMM of batch 1 that the direct-to-LDS kernel takes as
-// whole 256 x 256 tiles with one split and a plain epilogue (bias, alpha/beta, BF16 or FP32
-// out), their tiles fit one round of CUs, and the planner's estimate for that round (every block
-// runs its whole K) beats the sum of its estimates for the separate launches; otherwise each goes
-// through launch_gemm, as separate calls would.
-it_status launch_gemm_group(it_context *ctx, it_dtype dtype_in, bool transA, bool transB, GemmArgs *args, int count,
-                            const char *profile_tag) {
-    static_assert(sizeof(GemmGroupArgs) <= 4096, "kernel arguments");
+namespace {
+
+// Prepares a for a one-split 256 x 256 direct-to-LDS block in a group; false if it does not qualify.
+bool group_256(GemmArgs &a, bool bf16, bool ta, bool tb) {
+    a.splits = 1;
+    a.k_per_split = a.K;
+    a.tiles_m = (int)cdiv(a.M, 256);
+    a.tiles_n = (int)cdiv(a.N, 256);
+    return bf16 && a.batch == 1 && !a.dual && a.K > 0 && dtl_applicable(ta, tb, a, 256) &&
+           !gemv_applicable(a, bf16, ta, tb) && !gemv_kn_applicable(a, bf16, ta, tb);
+}
+
+int64_t padded_blocks(const GemmArgs &a) { return cdiv((int64_t)a.tiles_m * a.tiles_n, 8) * 8; }
+
+// The planner's pricing of a direct-to-LDS block that runs `k` of K: k-steps at the tile's rate or
+// the latency floor.
+double dtl_block_time(int64_t k, int bn, bool ta) {
+    const double cu_peak = 2.5e15 / 256.0;
+    const double eff = bn == 256 ? 0.53 : ta ? 0.42 : 0.52;
+    const double step = 2.0 * 256 * bn * 64 / (cu_peak * eff);
+    return cdiv(k, 64) * std::max(step, bn == 256 ? 1.0e-6 : 0.85e-6);
+}
+
+it_status launch_group_kernel(it_context *ctx, const GemmGroupArgs &grp, int blocks, bool ta, bool tb,
+                              const std::string &key) {
+    hipEvent_t ev = nullptr;
+    if (ctx->profiling) profile_begin(ctx, key, &ev);
+    const dim3 grid((unsigned)blocks);
+    if (!ta && tb) {
+        hipLaunchKernelGGL((gemm_bf16_dtl_group<false, true>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+    } else if (!ta && !tb) {
+        hipLaunchKernelGGL((gemm_bf16_dtl_group<false, false>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+    } else if (ta && !tb) {
+        hipLaunchKernelGGL((gemm_bf16_dtl_group<true, false>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+    } else {
+        hipLaunchKernelGGL((gemm_bf16_dtl_group<true, true>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail_hip(e, "gemm group launch");
+    if (ctx->profiling) profile_end(ctx, key, ev);
+    return IT_OK;
+}
+
+std::string group_key(const char *form, const GemmArgs *args, int count, const char *tag) {
+    std::string key = std::string("gemm_bf16_") + form + "|" + (tag ? tag : "");
+    for (int i = 0; i < count; ++i)
+        key += (i ? "+[" : "[") + std::to_string(args[i].M) + "," + std::to_string(args[i].N) + "," +
+               std::to_string(args[i].K) + "]";
+    return key + "x1 s1";
+}
+
+// Calls of one layout: one grouped launch where it pays, else launch_gemm each.
+it_status launch_same_layout(it_context *ctx, it_dtype dtype_in, bool ta, bool tb, GemmArgs *args, int count,
+                             const char *tag) {
     const bool bf16 = dtype_in == IT_BF16;
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    bool fuse = bf16 && count >= 2 && count <= GEMM_GROUP_MAX;
-    int64_t blocks = 0;
+    bool fuse = count >= 2;
+    int64_t blocks = 0, kmax = 0;
     double separate = 0.0;
-    int64_t kmax = 0;
     for (int i = 0; fuse && i < count; ++i) {
-        GemmArgs &a = args[i];
-        a.splits = 1;
-        a.k_per_split = a.K;
-        a.tiles_m = (int)cdiv(a.M, 256);
-        a.tiles_n = (int)cdiv(a.N, 256);
-        fuse = a.batch == 1 && !a.dual && a.K > 0 && dtl_applicable(transA, transB, a, 256) &&
-               !gemv_applicable(a, bf16, transA, transB) && !gemv_kn_applicable(a, bf16, transA, transB);
-        blocks += cdiv((int64_t)a.tiles_m * a.tiles_n, 8) * 8;
+        GemmArgs a = args[i];
+        fuse = group_256(a, bf16, ta, tb);
+        blocks += padded_blocks(a);
         double t = 0.0;
-        choose_plan(a, bf16, cus, transA, transB, &t);
+        choose_plan(args[i], bf16, cus, ta, tb, &t);
         separate += t;
         kmax = std::max(kmax, a.K);
     }
-    if (fuse && blocks <= cus) {
-        // one round, every block over its whole K (the planner's direct-to-LDS pricing)
-        const double step = 2.0 * 256 * 256 * 64 / (2.5e15 / 256.0 * 0.53);
-        const double grouped = 3e-6 + cdiv(kmax, 64) * std::max(step, 1.0e-6);
-        fuse = grouped < 0.97 * separate;
-    } else {
-        fuse = false;
-    }
+    // one round, every block over its whole K
+    fuse = fuse && blocks <= cus && 3e-6 + dtl_block_time(kmax, 256, ta) < 0.97 * separate;
     if (!fuse) {
         for (int i = 0; i < count; ++i) {
-            it_status st = launch_gemm(ctx, dtype_in, transA, transB, args[i], profile_tag);
+            const it_status st = launch_gemm(ctx, dtype_in, ta, tb, args[i], tag);
             if (st != IT_OK) return st;
         }
         return IT_OK;
@@ -1660,29 +1695,36 @@ it_status launch_gemm_group(it_context *ctx, it_dtype dtype_in, bool transA, boo
     int start = 0;
     for (int i = 0; i < count; ++i) {
         grp.g[i] = args[i];
+        group_256(grp.g[i], bf16, ta, tb);
         grp.start[i] = start;
-        start += (int)(cdiv((int64_t)args[i].tiles_m * args[i].tiles_n, 8) * 8);
+        start += (int)padded_blocks(grp.g[i]);
     }
     grp.start[count] = start;
-    std::string key;
-    hipEvent_t ev = nullptr;
-    if (ctx->profiling) {
-        key = std::string("gemm_bf16_") + (transA ? 'T' : 'N') + (transB ? 'T' : 'N') + "_256x256_dtl_group|" +
-              (profile_tag ? profile_tag : "");
-        for (int i = 0; i < count; ++i)
-            key += (i ? "+[" : "[") + std::to_string(args[i].M) + "," + std::to_string(args[i].N) + "," +
-                   std::to_string(args[i].K) + "]";
-        key += "x1 s1";
-        profile_begin(ctx, key, &ev);
+    const std::string form = std::string(1, ta ? 'T' : 'N') + (tb ? 'T' : 'N') + "_256x256_dtl_group";
+    return launch_group_kernel(ctx, grp, start, ta, tb,
+                               ctx->profiling ? group_key(form.c_str(), grp.g, count, tag) : std::string());
+}
+
+}  // namespace
+
+// Runs `count` independent GEMMs of one input dtype on ctx->stream (ta[i], tb[i]: their layouts),
+// each run of consecutive calls of one layout as one gemm_bf16_dtl_group launch when they are BF16
+// GEMMs of batch 1 that each take whole 256 x 256 direct-to-LDS tiles with one split and a plain
+// epilogue, their tiles fit one round of CUs, and the planner's estimate for that round (every
+// block running its whole K) beats the separate launches; else launch_gemm for each, as separate
+// calls would run.
+it_status launch_gemm_group(it_context *ctx, it_dtype dtype_in, const bool *ta, const bool *tb, GemmArgs *args,
+                            int count, const char *profile_tag) {
+    static_assert(sizeof(GemmGroupArgs) <= 4096, "kernel arguments");
+    if (count <= 0) return IT_OK;
+    if (count > GEMM_GROUP_MAX) return fail(IT_ERR_INVALID, "gemm group: more than 8 GEMMs");
+    for (int i = 0; i < count;) {
+        int j = i + 1;
+        while (j < count && ta[j] == ta[i] && tb[j] == tb[i]) ++j;
+        const it_status st = launch_same_layout(ctx, dtype_in, ta[i], tb[i], args + i, j - i, profile_tag);
+        if (st != IT_OK) return st;
+        i = j;
     }
-    const dim3 grid((unsigned)start);
-    if (!transA && transB) hipLaunchKernelGGL((gemm_bf16_dtl_group<false, true>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
-    else if (!transA && !transB) hipLaunchKernelGGL((gemm_bf16_dtl_group<false, false>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
-    else if (transA && !transB) hipLaunchKernelGGL((gemm_bf16_dtl_group<true, false>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
-    else hipLaunchKernelGGL((gemm_bf16_dtl_group<true, true>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail_hip(e, "gemm group launch");
-    if (ctx->profiling) profile_end(ctx, key, ev);
     return IT_OK;
 }
 
