@@ -4,9 +4,10 @@ Workload: every contraction of one TINY training step, for
 FP32 (4 layers, hidden 256, 4 heads x 64, SwiGLU FFN 688, untied vocab 16384, batch 16 x seq 256):
 115 dense-equivalent GEMMs = 195.82 GFLOP, issued by irontensor_amd.step.GemmStep as 51 GEMM
 launches (fused QKV and gate|up) plus the fused attention kernels (forward, and dK/dV + dQ
-backward, per layer), captured once into a HIP graph and replayed; the weight-gradient GEMMs run
-on a second stream beside the data-gradient chain. A "step" is one replay; inputs are resident in
-HBM before timing starts.
+backward, per layer), captured once into a HIP graph and replayed on one stream; each layer's four
+weight-gradient GEMMs run as one grouped launch (it_gemm_group). A "step" is one replay; inputs are
+resident in HBM before timing starts. The same step with the weight gradients on a second stream
+is timed beside it (config.ms_per_step_side_stream).
 
 Prints ONE JSON line (rank 0 = this process). Extra figures (configs 1, 3, 4 and 5: the FP32 QKV
 projection, BF16 attention, the medium BF16 step, the BF16 square and decode GEMMs) go under
@@ -43,12 +44,16 @@ def log(msg: str) -> None:
 
 
 def parse_key_flops(key: str) -> float:
-    """FLOPs of one launch from a profiler key '...|tag[M,N,K]xB s..' (x2 for the SwiGLU dual-B)."""
-    m = re.search(r"\[(\d+),(\d+),(\d+)\]x(\d+)", key)
-    if not m:
+    """FLOPs of one launch from a profiler key '...|tag[M,N,K]xB s..' (x2 for the SwiGLU dual-B); a
+    grouped launch's key lists every call, '...|tag[M,N,K]+[M,N,K]+...x1 s..', and counts their sum."""
+    body = key.split("|", 1)[-1]
+    m = re.search(r"\]x(\d+)", body)
+    trips = re.findall(r"\[(\d+),(\d+),(\d+)\]", body)
+    if not m or not trips:
         return 0.0
-    M, N, K, B = (int(g) for g in m.groups())
-    return 2.0 * M * N * K * B * (2 if "_swiglu" in key else 1)
+    B = int(m.group(1))
+    total = sum(2.0 * int(M) * int(N) * int(K) for M, N, K in trips)
+    return total * B * (2 if "_swiglu" in key else 1)
 
 
 def profiler_stats(ctx) -> dict:
@@ -326,7 +331,6 @@ def train_step_figures(it, timer, steps: int, warmup: int) -> dict:
         ctx.sync()
         wall_ms = (time.perf_counter() - t0) * 1e3 / steps
         loss1, gnorm = st.loss_value(), st.grad_norm()
-        st.overlap = False
         ctx.lib.it_profiler_reset(ctx.handle)
         ctx.lib.it_profiler_enable(ctx.handle, 1)
         st.enqueue()
@@ -347,7 +351,8 @@ def train_step_figures(it, timer, steps: int, warmup: int) -> dict:
             "eager_kernel_ms_by_group": {k: round(v, 4) for k, v in sorted(groups.items(), key=lambda kv: -kv[1])},
             "eager_kernel_ms_total": round(total, 4),
             "optimizer": "Lion lr 3e-4 betas (0.9, 0.99) wd 0.1, clip 1.0 (src/bin/benchmark.rs:124-129)",
-            "execution": "one hipGraph per step; weight gradients on a second stream; loss, norm and clip stay on the GPU"}
+            "execution": "one hipGraph per step on one stream; each layer's weight gradients as one grouped launch; "
+                         "loss, norm and clip stay on the GPU"}
 
 
 def extra_fusions(it, timer, iters: int = 10) -> dict:
@@ -460,9 +465,10 @@ def committed_traffic(key: str):
 
 
 def kernel_only(it, ctx, step, iters: int) -> int:
-    """Calibration copy, then each of the step's largest GEMMs (the LM-head forward, dX and dW, any
-    of which can be the dominant kernel) `iters` times in a row, for rocprofv3 --pmc passes. Prints
-    the order of the groups with their profiler keys, to map dispatches back to keys."""
+    """Calibration copy, then each of the step's largest GEMMs (the LM-head forward, dX and dW) and
+    the first layer's grouped weight gradients (any of which can be the dominant kernel) `iters`
+    times in a row, for rocprofv3 --pmc passes. Prints the order of the groups with their profiler
+    keys, to map dispatches back to keys."""
     from irontensor_amd import synth
     n = 1 << 26  # 256 MiB read, 128 MiB written
     src = _dev(it, 9, (n,))
@@ -485,6 +491,16 @@ def kernel_only(it, ctx, step, iters: int) -> int:
         ctx.lib.it_profiler_enable(ctx.handle, 0)
         (key, st), = stats.items()
         groups.append({"key": key, "step_gemm": name, "launches": iters,
+                       "avg_us_events": round(st["total_ms"] / st["calls"] * 1e3, 2)})
+    # The first layer's weight gradients as the step groups them (one it_gemm_group call).
+    ctx.lib.it_profiler_reset(ctx.handle)
+    ctx.lib.it_profiler_enable(ctx.handle, 1)
+    for _ in range(iters):
+        names = step.reissue_group()
+    stats = profiler_stats(ctx)
+    ctx.lib.it_profiler_enable(ctx.handle, 0)
+    for key, st in stats.items():
+        groups.append({"key": key, "step_gemm": "+".join(names), "launches": st["calls"],
                        "avg_us_events": round(st["total_ms"] / st["calls"] * 1e3, 2)})
     print(json.dumps({"calibration": {"kernel": "f32_to_bf16_kernel", "elements": n, "read_bytes": 4 * n,
                                       "write_bytes": 2 * n, "launches": 5},
@@ -673,17 +689,18 @@ def main() -> int:
     log(f"[bench] timed {args.steps} steps: wall {ms_per_step:.3f} ms/step, events "
         f"{gpu_ms / args.steps:.3f} ms/step")
 
-    # Per-kernel durations: the same steps run eagerly with hipEvents around every launch, on one
-    # stream (with the weight gradients overlapped, a kernel's events would also time its neighbour).
-    step.overlap = False
+    # Per-kernel durations: the same steps run eagerly on the same one stream with hipEvents around
+    # every launch.
     ctx.lib.it_profiler_reset(ctx.handle)
     ctx.lib.it_profiler_enable(ctx.handle, 1)
     for _ in range(args.steps):
         step.enqueue()
     stats = profiler_stats(ctx)
     ctx.lib.it_profiler_enable(ctx.handle, 0)
-    # The same step on one stream (no side-stream fork), graph-replayed and timed the same way.
+    # The same step with each layer's weight-gradient group on the context's side stream, beside
+    # the data-gradient chain, graph-replayed and timed the same way.
     step.close()
+    step.overlap = True
     step.enqueue()
     step.capture()
     for _ in range(args.warmup):
@@ -693,10 +710,10 @@ def main() -> int:
     for _ in range(args.steps):
         step.replay()
     ctx.sync()
-    ms_single = (time.perf_counter() - t1) * 1e3 / args.steps
-    log(f"[bench] single-stream replay {ms_single:.3f} ms/step")
+    ms_side = (time.perf_counter() - t1) * 1e3 / args.steps
+    log(f"[bench] side-stream replay {ms_side:.3f} ms/step")
     step.close()
-    step.overlap = True
+    step.overlap = False
     gemm_ms = sum(v["total_ms"] for v in stats.values()) / args.steps
     dom_key, dom = max(stats.items(), key=lambda kv: kv[1]["total_ms"])
     avg_ms = dom["total_ms"] / dom["calls"]
@@ -729,10 +746,11 @@ def main() -> int:
             "workload": "TINY training step, all contractions fwd+bwd (BASELINE configs[1])",
             "layers": 4, "hidden": 256, "heads": 4, "head_dim": 64, "ffn": 688, "vocab": 16384,
             "tied_lm_head": False, "batch": 16, "seq": 256, "gflop_per_step": round(total_flops / 1e9, 2),
-            "gemm_launches": len(step.launches), "execution": "hipGraph replay; weight gradients on a second stream",
+            "gemm_launches": len(step.launches),
+            "execution": "hipGraph replay on one stream; each layer's weight gradients as one grouped launch",
             "frac_fp32_mfma_peak": round(total_flops / (ms_per_step * 1e-3) / 1e12 / PEAK_TFLOPS["f32"], 4),
-            "ms_per_step_single_stream": round(ms_single, 4),
-            "tflops_single_stream": round(total_flops / (ms_single * 1e-3) / 1e12, 3),
+            "ms_per_step_side_stream": round(ms_side, 4),
+            "tflops_side_stream": round(total_flops / (ms_side * 1e-3) / 1e12, 3),
             "attention_gflop_dense_equiv": round(attn_flops / 1e9, 2),
             "attention_gflop_skipped_by_causal": round(attn_skipped / 1e9, 2),
             "note_flops": "value counts attention as dense-equivalent GEMMs (BASELINE's definition); the causal "

@@ -336,9 +336,17 @@ namespace sg {
 constexpr int MFMA = 0x008, VMEM_READ = 0x020, DS_READ = 0x100, DS_WRITE = 0x200;
 }
 
+// LDS bytes of one gemm_mfma block (two stages of the A and B tiles).
+template <typename T, bool TA, bool TB, int BM, int BN>
+constexpr int mfma_smem_bytes() {
+    return 2 * (Operand<T, !TA, BM>::STAGE_BYTES + Operand<T, TB, BN>::STAGE_BYTES);
+}
+
+// One block of gemm_mfma: output tile `tile` (in map_tile order) of batch-and-split index z, with
+// `smem` of mfma_smem_bytes().
 template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL, int LM, bool KS = false, int PF = 1,
           bool XF = false>
-__global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
+__device__ __forceinline__ void gemm_mfma_block(const GemmArgs &p, int tile, int64_t z, char *smem) {
     static_assert(WM * WN == 4, "4 waves per block");
     constexpr int BK = ET<T>::BK;
     constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
@@ -352,13 +360,11 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
     static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
     constexpr int SA = OA::STAGE_BYTES, SB = OB::STAGE_BYTES;
     constexpr int STAGE = SA + SB;
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     int tm, tn;
-    map_tile(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int64_t z = blockIdx.y;
+    map_tile(tile, p.tiles_m, p.tiles_n, tm, tn);
     const int64_t b = z % p.batch, split = z / p.batch;
     const int64_t bo = b / p.batch_inner, bi = b % p.batch_inner;
     const T *A = (const T *)p.A + bo * p.sA_out + bi * p.sA_in;
@@ -590,6 +596,13 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
             __syncthreads();
         }
     }
+}
+
+template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL, int LM, bool KS = false, int PF = 1,
+          bool XF = false>
+__global__ __launch_bounds__(NTHREADS) void gemm_mfma(const GemmArgs p) {
+    __shared__ __attribute__((aligned(16))) char smem[mfma_smem_bytes<T, TA, TB, BM, BN>()];
+    gemm_mfma_block<T, TA, TB, BM, BN, WM, WN, DUAL, LM, KS, PF, XF>(p, blockIdx.x, blockIdx.y, smem);
 }
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -1199,29 +1212,89 @@ void gemm_bf16_dtl(const GemmArgs p) {
     dtl_block<TA, TB, DUAL, FB>(p, blockIdx.x, blockIdx.y, st0, st1, st2);
 }
 
-// Several independent GEMMs of one layout in one launch of 256 x 256 direct-to-LDS tiles (batch 1,
-// no split-K): problem g takes blocks start[g] .. start[g + 1] - 1, each problem's range padded to
-// a multiple of 8 blocks (the padding blocks return at once) so that map_tile's XCD-aware order
-// holds within every problem.
+// Several independent GEMMs of one layout in one launch. Workgroup w runs on XCD w % 8, and each
+// XCD has its own L2, so the blocks are scheduled per XCD: XCD x runs blocks j = 0 .. xn[x] - 1
+// (workgroup j * 8 + x), an equal share of the group's tiles x splits, as contiguous chunks. Chunk c
+// gives blocks jstart.. of its XCD the tiles t0, t0 + 1, ... (grouped raster order) of split `split`
+// of problem gi, until the next chunk of that XCD starts. A problem's split then sits on one XCD
+// (or two, where a share ends inside it), and its operand panels are fetched into one L2 instead of
+// eight.
 constexpr int GEMM_GROUP_MAX = 8;
+constexpr int GROUP_CHUNKS = 96;
+struct GroupChunk {
+    uint16_t jstart;
+    uint8_t gi, split;
+    uint16_t t0, unused;
+};
 struct GemmGroupArgs {
     GemmArgs g[GEMM_GROUP_MAX];
-    int start[GEMM_GROUP_MAX + 1];
+    int64_t rstart[GEMM_GROUP_MAX + 1];  // FP32 groups: first 4-element vector of each split-K sum
     int count;
+    uint16_t xn[8];                      // blocks of XCD x
+    uint16_t xstart[9];                  // its chunks: chunk[xstart[x]] .. chunk[xstart[x + 1] - 1]
+    GroupChunk chunk[GROUP_CHUNKS];
 };
 
+// The map_tile index whose tile is number r of the grouped raster order (map_tile's XCD remap
+// undone: the group's schedule has already placed the block on its XCD).
+__device__ __forceinline__ int raster_pid(int r, int total) {
+    if (total % 8 != 0) return r;
+    const int q = total / 8;
+    return (r % q) * 8 + r / q;
+}
+
+// This block's problem, split and map_tile index under the group's XCD schedule; false for a block
+// past its XCD's share.
+__device__ __forceinline__ bool group_block(const GemmGroupArgs &grp, int &gi, int &split, int &tile) {
+    const int x = (int)blockIdx.x & 7, j = (int)blockIdx.x >> 3;
+    if (j >= grp.xn[x]) return false;
+    int c = grp.xstart[x];
+    while (c + 1 < grp.xstart[x + 1] && grp.chunk[c + 1].jstart <= j) ++c;
+    gi = grp.chunk[c].gi;
+    split = grp.chunk[c].split;
+    const GemmArgs &p = grp.g[gi];
+    tile = raster_pid(grp.chunk[c].t0 + (j - grp.chunk[c].jstart), p.tiles_m * p.tiles_n);
+    return true;
+}
+
+// BF16: 256 x 256 direct-to-LDS tiles, batch 1, no split-K, one round of CUs.
 template <bool TA, bool TB>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_dtl_group(const GemmGroupArgs grp) {
     constexpr int STAGE = 512 * 64 * 2;
     __shared__ __attribute__((aligned(1024))) char st0[STAGE];
     __shared__ __attribute__((aligned(1024))) char st1[STAGE];
-    int gi = 0;
-    while (gi + 1 < grp.count && (int)blockIdx.x >= grp.start[gi + 1]) ++gi;
-    const GemmArgs &p = grp.g[gi];
-    const int tile = (int)blockIdx.x - grp.start[gi];
-    if (tile >= p.tiles_m * p.tiles_n) return;  // padding block
-    dtl_block<TA, TB, false, 4>(p, tile, 0, st0, st1, st0);
+    int gi, split, tile;
+    if (!group_block(grp, gi, split, tile)) return;
+    dtl_block<TA, TB, false, 4>(grp.g[gi], tile, 0, st0, st1, st0);
+}
+
+// FP32: 64 x 64 tiles, batch 1, one split count for the group. Split-K partial sums go to each
+// problem's own region; splitk_reduce4_group then sums every problem's in one launch.
+template <bool TA, bool TB, int LM>
+__global__ __launch_bounds__(NTHREADS) void gemm_f32_group(const GemmGroupArgs grp) {
+    __shared__ __attribute__((aligned(16))) char smem[mfma_smem_bytes<float, TA, TB, 64, 64>()];
+    int gi, split, tile;
+    if (!group_block(grp, gi, split, tile)) return;
+    gemm_mfma_block<float, TA, TB, 64, 64, 2, 2, false, LM, false, 2>(grp.g[gi], tile, split, smem);
+}
+
+// The split-K sums of an FP32 group (N % 4 == 0 for every problem with splits): vector e of the
+// group belongs to problem g when rstart[g] <= e < rstart[g + 1]; each sums its splits in order, as
+// splitk_reduce4 does.
+__global__ __launch_bounds__(256) void splitk_reduce4_group(const GemmGroupArgs grp) {
+    const int64_t total4 = grp.rstart[grp.count];
+    for (int64_t e4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e4 < total4;
+         e4 += (int64_t)gridDim.x * blockDim.x) {
+        int gi = 0;
+        while (gi + 1 < grp.count && e4 >= grp.rstart[gi + 1]) ++gi;
+        const GemmArgs &p = grp.g[gi];
+        const int64_t mn = p.M * p.N, e = (e4 - grp.rstart[gi]) * 4;
+        const int64_t row = e / p.N, col = e % p.N;
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < p.splits; ++sp) s += *(const f32x4 *)(p.partial + (int64_t)sp * mn + e);
+        finish4<false, true>(p, s, row, col, 0, 0);
+    }
 }
 
 // Deterministic split-K reduction: partial sums are added in split order.
@@ -1625,7 +1698,46 @@ bool group_256(GemmArgs &a, bool bf16, bool ta, bool tb) {
            !gemv_applicable(a, bf16, ta, tb) && !gemv_kn_applicable(a, bf16, ta, tb);
 }
 
-int64_t padded_blocks(const GemmArgs &a) { return cdiv((int64_t)a.tiles_m * a.tiles_n, 8) * 8; }
+// The group's XCD schedule (GemmGroupArgs): the blocks of every problem (tiles x splits, in call
+// and split order) cut into eight equal shares, one per XCD. Returns the grid size, or 0 when the
+// schedule does not fit the table (the caller then launches the calls separately).
+int xcd_schedule(GemmGroupArgs &grp) {
+    int64_t total = 0;
+    for (int i = 0; i < grp.count; ++i) {
+        const int64_t tiles = (int64_t)grp.g[i].tiles_m * grp.g[i].tiles_n;
+        if (tiles > 65535 || grp.g[i].splits > 255) return 0;
+        total += tiles * grp.g[i].splits;
+    }
+    const int64_t per = cdiv(total, 8);
+    if (total == 0 || per > 65535) return 0;
+    int x = 0, nch = 0;
+    int64_t filled = 0;
+    grp.xstart[0] = 0;
+    for (int i = 0; i < grp.count; ++i) {
+        const int64_t tiles = (int64_t)grp.g[i].tiles_m * grp.g[i].tiles_n;
+        for (int sp = 0; sp < grp.g[i].splits; ++sp)
+            for (int64_t t = 0; t < tiles;) {
+                if (filled == per) {  // this XCD's share is full: the next one starts
+                    if (x == 7) return 0;
+                    grp.xn[x++] = (uint16_t)per;
+                    grp.xstart[x] = (uint16_t)nch;
+                    filled = 0;
+                }
+                if (nch == GROUP_CHUNKS) return 0;
+                grp.chunk[nch++] = GroupChunk{(uint16_t)filled, (uint8_t)i, (uint8_t)sp, (uint16_t)t, 0};
+                const int64_t take = std::min(tiles - t, per - filled);
+                t += take;
+                filled += take;
+            }
+    }
+    grp.xn[x] = (uint16_t)filled;
+    for (int y = x + 1; y < 8; ++y) {
+        grp.xn[y] = 0;
+        grp.xstart[y] = (uint16_t)nch;
+    }
+    grp.xstart[8] = (uint16_t)nch;
+    return (int)(8 * per);
+}
 
 // The planner's pricing of a direct-to-LDS block that runs `k` of K: k-steps at the tile's rate or
 // the latency floor.
@@ -1664,10 +1776,135 @@ std::string group_key(const char *form, const GemmArgs *args, int count, const c
     return key + "x1 s1";
 }
 
+// FP32 calls of one layout: one gemm_f32_group launch (64 x 64 tiles, one split count for the
+// group) and one splitk_reduce4_group where the planner's model prices them below the separate
+// plans; false if they do not qualify or do not pay (nothing launched then).
+bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int count, const char *tag,
+                      it_status *status) {
+    constexpr int bk = ET<float>::BK;
+    const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    if (count < 2) return false;
+    double separate = 0.0;
+    for (int i = 0; i < count; ++i) {
+        const GemmArgs &a = args[i];
+        if (a.batch != 1 || a.dual || a.causal != CAUSAL_NONE || a.kmode != KMODE_FULL || a.swiglu_bwd ||
+            a.xent_stats || a.a_kscale || a.K <= 0 || a.N % 4 != 0 || a.no_split || gemv_applicable(a, false, ta, tb))
+            return false;
+        double t = 0.0;
+        const Plan pl = choose_plan(a, false, cus, ta, tb, &t);
+        if (pl.bm != 64) return false;  // the group runs 64 x 64 tiles only
+        separate += t;
+    }
+    // The planner's model of the group at one split count s: 64 x 64 tiles, up to 4 blocks per CU.
+    const double cu_peak = 157.3e12 / 256.0, eff0 = 0.60;
+    double best_t = 1e30;
+    int best_s = 0;
+    for (int s = 1; s <= 32; ++s) {
+        int64_t blocks = 0, ksteps = 0;
+        double traffic = 0.0;
+        bool ok = true;
+        for (int i = 0; i < count && ok; ++i) {
+            const GemmArgs &a = args[i];
+            const int64_t kps = cdiv(cdiv(a.K, s), bk) * bk;
+            ok = s == 1 || kps >= 4 * bk;
+            const int64_t splits = s > 1 ? cdiv(a.K, kps) : 1;
+            blocks += cdiv(a.M, 64) * cdiv(a.N, 64) * splits;
+            ksteps = std::max(ksteps, cdiv(kps, bk));
+            if (splits > 1) traffic += 2.0 * splits * a.M * a.N * 4.0;
+        }
+        if (!ok) break;
+        const int64_t per_cu = cdiv(blocks, cus), conc = std::min<int64_t>(per_cu, 4), rounds = cdiv(per_cu, 4);
+        const double eff = conc == 1 ? 0.9 * eff0 : eff0;
+        const double step = 2.0 * 64 * 64 * bk / (cu_peak * eff);
+        double t = rounds * (3e-6 + ksteps * std::max(conc * step, 0.5e-6));
+        if (traffic > 0.0) t += traffic / 4e12 + 4e-6;
+        if (t < best_t) {
+            best_t = t;
+            best_s = s;
+        }
+    }
+#ifdef IT_TUNING
+    // Planner sweeps only (a tuning build): IT_GROUP_SPLITS forces the group's split count.
+    if (const char *env = std::getenv("IT_GROUP_SPLITS")) {
+        best_s = std::max(1, std::min(32, std::atoi(env)));
+        best_t = 0.0;
+    }
+#endif
+    if (!best_s || best_t >= 0.97 * separate) return false;
+    GemmGroupArgs grp{};
+    grp.count = count;
+    int64_t r4 = 0, scratch = 0;
+    bool exact = true, masked = true;
+    for (int i = 0; i < count; ++i) {
+        GemmArgs &a = grp.g[i];
+        a = args[i];
+        const int64_t kps = cdiv(cdiv(a.K, best_s), bk) * bk;
+        a.splits = best_s > 1 ? (int)cdiv(a.K, kps) : 1;
+        a.k_per_split = best_s > 1 ? kps : cdiv(a.K, bk) * bk;
+        a.tiles_m = (int)cdiv(a.M, 64);
+        a.tiles_n = (int)cdiv(a.N, 64);
+        grp.rstart[i] = r4;
+        if (a.splits > 1) {
+            r4 += a.M * a.N / 4;
+            scratch += (int64_t)a.splits * a.M * a.N;
+        }
+        exact = exact && tiles_exact(a, 64, 64, bk);
+        masked = masked && vectors_exact<float>(a, ta, tb);
+    }
+    grp.rstart[count] = r4;
+    const int grid_blocks = xcd_schedule(grp);
+    if (!grid_blocks) return false;
+    if (scratch > 0) {
+        void *ws = nullptr;
+        *status = ensure_scratch(ctx, (size_t)scratch * sizeof(float), &ws);
+        if (*status != IT_OK) return true;
+        float *part = (float *)ws;
+        for (int i = 0; i < count; ++i)
+            if (grp.g[i].splits > 1) {
+                grp.g[i].partial = part;
+                part += (int64_t)grp.g[i].splits * grp.g[i].M * grp.g[i].N;
+            }
+    }
+    std::string key;
+    hipEvent_t ev = nullptr;
+    if (ctx->profiling) {
+        key = std::string("gemm_f32_") + (ta ? 'T' : 'N') + (tb ? 'T' : 'N') + "_64x64_group|" + (tag ? tag : "");
+        for (int i = 0; i < count; ++i)
+            key += (i ? "+[" : "[") + std::to_string(args[i].M) + "," + std::to_string(args[i].N) + "," +
+                   std::to_string(args[i].K) + "]";
+        key += "x1 s" + std::to_string(best_s);
+        profile_begin(ctx, key, &ev);
+    }
+    const dim3 grid((unsigned)grid_blocks);
+    auto go = [&](auto lm) {
+        constexpr int LM = decltype(lm)::value;
+        if (!ta && tb) hipLaunchKernelGGL((gemm_f32_group<false, true, LM>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+        else if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_group<false, false, LM>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+        else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_group<true, false, LM>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+        else hipLaunchKernelGGL((gemm_f32_group<true, true, LM>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
+    };
+    if (exact) go(std::integral_constant<int, LOAD_EXACT>{});
+    else if (masked) go(std::integral_constant<int, LOAD_MASKED>{});
+    else go(std::integral_constant<int, LOAD_CHECKED>{});
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && r4 > 0) {
+        const int64_t blocks = std::min<int64_t>(cdiv(r4, 256), 65536);
+        hipLaunchKernelGGL(splitk_reduce4_group, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, grp);
+        e = hipGetLastError();
+    }
+    *status = e == hipSuccess ? IT_OK : fail_hip(e, "gemm group launch");
+    if (ctx->profiling && *status == IT_OK) profile_end(ctx, key, ev);
+    return true;
+}
+
 // Calls of one layout: one grouped launch where it pays, else launch_gemm each.
 it_status launch_same_layout(it_context *ctx, it_dtype dtype_in, bool ta, bool tb, GemmArgs *args, int count,
                              const char *tag) {
     const bool bf16 = dtype_in == IT_BF16;
+    if (!bf16) {
+        it_status st = IT_OK;
+        if (launch_f32_group(ctx, ta, tb, args, count, tag, &st)) return st;
+    }
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     bool fuse = count >= 2;
     int64_t blocks = 0, kmax = 0;
@@ -1675,7 +1912,7 @@ it_status launch_same_layout(it_context *ctx, it_dtype dtype_in, bool ta, bool t
     for (int i = 0; fuse && i < count; ++i) {
         GemmArgs a = args[i];
         fuse = group_256(a, bf16, ta, tb);
-        blocks += padded_blocks(a);
+        blocks += (int64_t)a.tiles_m * a.tiles_n;
         double t = 0.0;
         choose_plan(args[i], bf16, cus, ta, tb, &t);
         separate += t;
@@ -1692,16 +1929,20 @@ it_status launch_same_layout(it_context *ctx, it_dtype dtype_in, bool ta, bool t
     }
     GemmGroupArgs grp{};
     grp.count = count;
-    int start = 0;
     for (int i = 0; i < count; ++i) {
         grp.g[i] = args[i];
         group_256(grp.g[i], bf16, ta, tb);
-        grp.start[i] = start;
-        start += (int)padded_blocks(grp.g[i]);
     }
-    grp.start[count] = start;
+    const int grid = xcd_schedule(grp);
+    if (!grid) {
+        for (int i = 0; i < count; ++i) {
+            const it_status st = launch_gemm(ctx, dtype_in, ta, tb, args[i], tag);
+            if (st != IT_OK) return st;
+        }
+        return IT_OK;
+    }
     const std::string form = std::string(1, ta ? 'T' : 'N') + (tb ? 'T' : 'N') + "_256x256_dtl_group";
-    return launch_group_kernel(ctx, grp, start, ta, tb,
+    return launch_group_kernel(ctx, grp, grid, ta, tb,
                                ctx->profiling ? group_key(form.c_str(), grp.g, count, tag) : std::string());
 }
 

@@ -90,8 +90,9 @@ def gemm(a: Tensor, b: Tensor, *, trans_a: bool = False, trans_b: bool = False, 
 def gemm_group(calls, op: str = "matmul_group") -> None:
     """Several independent 2D GEMMs in one it_gemm_group call: `calls` holds up to 8 tuples
     (a, b, out, trans_a, trans_b), out = op(a) . op(b), all of one input and one output precision.
-    Where the library can, they run as one launch (BF16, whole 256 x 256 tiles, one round);
-    otherwise as separate GEMMs. No counterpart in the reference (its command batch issues each
+    Calls of one layout run as one launch where the library can (BF16: whole 256 x 256 tiles in
+    one round; FP32: 64 x 64 tiles with one split count for the group and one grouped reduction,
+    when that is priced below the separate plans); otherwise as separate GEMMs. No counterpart in the reference (its command batch issues each
     GEMM separately); for callers holding several GEMMs at once, such as a layer's weight
     gradients."""
     if not calls:

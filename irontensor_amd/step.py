@@ -73,7 +73,7 @@ class GemmStep:
 
     def __init__(self, shape: ModelShape, precision: Precision = Precision.FP32,
                  ctx: Optional[Context] = None, seed: int = 1234, fused_attention: Optional[bool] = None,
-                 ffn_bias: bool = False, overlap_weight_grads: bool = True):
+                 ffn_bias: bool = False, overlap_weight_grads: bool = False):
         if shape.heads * shape.head_dim != shape.hidden:
             raise ValueError("heads * head_dim must equal hidden")
         self.s = shape
@@ -89,15 +89,17 @@ class GemmStep:
         # seed_of maps each one's device address to (seed, std), so a check can regenerate any
         # element on the host (synth.normal_at).
         self.seed_of: dict = {}
-        # Weight gradients run on the context's side stream, beside the data-gradient chain. A
-        # layer's four are issued together, once its last upstream gradient (dQKV) is ready: each
-        # fork of the side stream idles the GPU for microseconds inside the graph, so one fork per
-        # layer beats one per GEMM (dw_fork = "gemm").
+        # A layer's four weight gradients are issued together, once its last upstream gradient
+        # (dQKV) is ready, and go to the library as one group (it_gemm_group): one launch that
+        # fills the GPU, so they run on the main stream by default. With overlap_weight_grads they
+        # run on the context's side stream instead, beside the data-gradient chain (one fork per
+        # layer: each fork idles the GPU for microseconds inside the graph; dw_fork = "gemm" forks
+        # per GEMM).
         self.overlap = overlap_weight_grads
         self.dw_fork = "layer"
-        # A layer's weight gradients go to the library as one group (it_gemm_group).
         self.group_weight_grads = True
         self._dw_queue = None
+        self._first_group = None
 
         def w(shape_, std=0.02):
             return self._tensor(shape_, std)
@@ -224,9 +226,9 @@ class GemmStep:
             check(self.lib.it_side_begin(self.ctx.handle), "side stream")
         try:
             if self.group_weight_grads and len({a[3].precision() for a, _ in q}) == 1:
-                calls = (_lib.GemmCall * len(q))(*[self._call(*a[1:], **kw) for a, kw in q])
-                check(self.lib.it_gemm_group(self.ctx.handle, int(self.prec), int(q[0][0][3].precision()), len(q),
-                                             calls), "weight gradients")
+                self._issue_group(q)
+                if self._record and self._first_group is None:
+                    self._first_group = q
                 for args, kw in q:
                     self._note(*args, **kw)
             else:
@@ -235,6 +237,20 @@ class GemmStep:
         finally:
             if self.overlap:
                 check(self.lib.it_side_end(self.ctx.handle), "side stream")
+
+    def _issue_group(self, q) -> None:
+        calls = (_lib.GemmCall * len(q))(*[self._call(*a[1:], **kw) for a, kw in q])
+        check(self.lib.it_gemm_group(self.ctx.handle, int(self.prec), int(q[0][0][3].precision()), len(q), calls),
+              "weight gradients")
+
+    def reissue_group(self) -> List[str]:
+        """Launches again the first layer's weight-gradient group as issued in the step (one
+        it_gemm_group call, for profiling it in isolation); returns the names of its GEMMs.
+        enqueue() must have run once with grouped weight gradients."""
+        if self._first_group is None:
+            raise RuntimeError("no weight-gradient group was issued")
+        self._issue_group(self._first_group)
+        return [a[0] for a, _ in self._first_group]
 
     def _layouts(self):
         s = self.s

@@ -19,11 +19,14 @@ attention kernels), and the row/elementwise ops of kernels_train.hip. The MI355X
     rebuild the gradient from the logits on their way into LDS (IT_EPI_XENT_A): 268 MB less at
     TINY, but slower (the rebuild runs once per output tile column: cross entropy 111 -> 43 us,
     the dX and dW GEMMs 298 -> 418 and 287 -> 342 us on MI355X), so it is off by default;
-  * weight-gradient GEMMs run on the side stream beside the data-gradient chain; every buffer they
-    read is per layer, so the main stream never overwrites one before the side stream has read it.
-    A layer's four are issued together once its last input (the RoPE backward) is ready: each fork
-    of the side stream costs several microseconds of idle GPU inside the graph, so one fork per
-    layer (dw_fork="layer", 2.80 ms per TINY step) beats one per GEMM ("gemm", 2.85 ms);
+  * a layer's four weight-gradient GEMMs are issued together once their last input (the RoPE
+    backward) is ready, as one it_gemm_group call (one launch with one split-K reduction where the
+    library's model prices that below four separate plans). Every buffer they read is per layer,
+    so the main stream never overwrites one before they have read it. They run on the main stream
+    by default; overlap_weight_grads puts them on the side stream beside the data-gradient chain,
+    forked once per layer (dw_fork="layer": each fork costs several microseconds of idle GPU
+    inside the graph, so that beat one fork per GEMM, "gemm", 2.80 against 2.85 ms per TINY step
+    before the grouping);
   * the gradient norm, the clip factor and the learning rate stay on the device (Lion reads them
     from memory), so a step has no host synchronisation and captures into one HIP graph.
 
@@ -53,8 +56,8 @@ class TrainStep:
     def __init__(self, shape: ModelShape = TINY, ctx: Optional[Context] = None, seed: int = 1234,
                  lr: float = 3e-4, beta1: float = 0.9, beta2: float = 0.99, weight_decay: float = 0.1,
                  max_grad_norm: float = 1.0, eps: float = 1e-5, rope_base: float = 10000.0,
-                 overlap_weight_grads: bool = True, fused_attention: Optional[bool] = None,
-                 xent_operand: bool = False, dw_fork: str = "layer"):
+                 overlap_weight_grads: bool = False, fused_attention: Optional[bool] = None,
+                 xent_operand: bool = False, dw_fork: str = "layer", group_weight_grads: bool = True):
         s = shape
         if s.heads * s.head_dim != s.hidden:
             raise ValueError("heads * head_dim must equal hidden")
@@ -66,6 +69,7 @@ class TrainStep:
         self.lr, self.beta1, self.beta2, self.wd = float(lr), float(beta1), float(beta2), float(weight_decay)
         self.max_grad_norm = float(max_grad_norm)
         self.overlap = overlap_weight_grads
+        self.group_weight_grads = bool(group_weight_grads)
         self.fused = (s.head_dim == 64) if fused_attention is None else bool(fused_attention)
         self.xent_operand = bool(xent_operand)
         if dw_fork not in ("gemm", "layer"):
@@ -186,6 +190,13 @@ class TrainStep:
         check(self.lib.it_memcpy_h2d(self.h, C.c_void_p(self.lr_dev.ptr), v.ctypes.data_as(C.c_void_p), 4), "lr")
 
     # ---------------------------------------------------------------- launch helpers
+    @staticmethod
+    def _call(A: Tensor, B: Tensor, Cout: Tensor, ta: bool, tb: bool, M, N, K,
+              epi: Optional[_lib.Epilogue] = None) -> _lib.GemmCall:
+        """it_gemm's arguments for one FP32 GEMM of the step (batch 1, alpha 1, beta 0)."""
+        return _lib.GemmCall(int(ta), int(tb), M, N, K, 1.0, A.ptr, A.shape()[-1], 0, B.ptr, B.shape()[-1], 0,
+                             0.0, Cout.ptr, Cout.shape()[-1], 0, 1, C.pointer(epi) if epi is not None else None)
+
     def _gemm(self, name, A: Tensor, B: Tensor, Cout: Tensor, ta: bool, tb: bool, M, N, K,
               epi: Optional[_lib.Epilogue] = None):
         st = self.lib.it_gemm(self.h, 0, 0, int(ta), int(tb), M, N, K, 1.0, C.c_void_p(A.ptr), A.shape()[-1], 0,
@@ -194,13 +205,14 @@ class TrainStep:
         check(st, name)
 
     def _dw(self, *args, **kw):
-        """A weight-gradient GEMM: on the side stream, forked from the main stream here
-        (dw_fork="gemm") or queued and issued with the rest of its layer's (dw_fork="layer")."""
-        if not self.overlap:
-            return self._gemm(*args, **kw)
+        """A weight-gradient GEMM: queued and issued with the rest of its layer's when a queue is
+        open (group_weight_grads, or dw_fork="layer" on the side stream), else issued here (on
+        the side stream, forked from the main stream, when overlapping)."""
         if self._dw_queue is not None:
             self._dw_queue.append((args, kw))
             return None
+        if not self.overlap:
+            return self._gemm(*args, **kw)
         check(self.lib.it_side_begin(self.h), "side stream")
         try:
             self._gemm(*args, **kw)
@@ -208,15 +220,23 @@ class TrainStep:
             check(self.lib.it_side_end(self.h), "side stream")
 
     def _dw_flush(self):
+        """The layer's queued weight gradients (on the side stream when overlapping): one
+        it_gemm_group call with group_weight_grads, else one GEMM after the other."""
         q, self._dw_queue = self._dw_queue, None
         if not q:
             return
-        check(self.lib.it_side_begin(self.h), "side stream")
+        if self.overlap:
+            check(self.lib.it_side_begin(self.h), "side stream")
         try:
-            for args, kw in q:
-                self._gemm(*args, **kw)
+            if self.group_weight_grads:
+                calls = (_lib.GemmCall * len(q))(*[self._call(*a[1:], **kw) for a, kw in q])
+                check(self.lib.it_gemm_group(self.h, 0, 0, len(q), calls), "weight gradients")
+            else:
+                for args, kw in q:
+                    self._gemm(*args, **kw)
         finally:
-            check(self.lib.it_side_end(self.h), "side stream")
+            if self.overlap:
+                check(self.lib.it_side_end(self.h), "side stream")
 
     def _norm(self, x: Tensor, res: Optional[Tensor], gamma: Tensor, sum_out: Optional[Tensor], y: Tensor):
         T, H = self.s.tokens, self.s.hidden
@@ -282,7 +302,7 @@ class TrainStep:
         s = self.s
         T, H, F = s.tokens, s.hidden, s.ffn
         g = self.g_out[l + 1]
-        if self.overlap and self.dw_fork == "layer":
+        if (self.overlap and self.dw_fork == "layer") or self.group_weight_grads:
             self._dw_queue = []
         # FFN: down projection, SwiGLU, gate|up projection, ffn norm (+ residual)
         self._dw("down.dW", g, self.Hh[l], self.dWd[l], True, False, H, F, T)

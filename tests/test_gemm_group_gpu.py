@@ -79,20 +79,57 @@ def test_group_matches_separate_and_oracle(it, oracle):
         assert np.array_equal(o16.as_bf16_slice().reshape(m, n), oracle.f32_to_bf16(g)), (m, n)
 
 
+TINY_DW = [(688 * 2, 256), (256, 688), (768, 256), (256, 256)]  # TINY's weight gradients, K = 4096 tokens
+
+
+def test_group_f32_weight_gradients(it, oracle):
+    """FP32: the TINY step's four weight gradients of a layer ([1376,256], [256,688], [768,256],
+    [256,256], K = 4096) as one grouped launch of 64 x 64 tiles and one grouped split-K sum: exact
+    on small integers (sampled rows against float64), repeatable, and on Gaussian data within the
+    FP32 contract of the oracle and of the separate it_gemm calls."""
+    k = 4096
+    ints, gauss = [], []
+    for i, (m, n) in enumerate(TINY_DW):
+        dy, x = synth.small_ints(400 + i, (k, m), -2, 2), synth.small_ints(410 + i, (k, n), -2, 2)
+        ints.append((dy, x, it.Tensor.from_f32_slice(dy, dy.shape), it.Tensor.from_f32_slice(x, x.shape),
+                     it.Tensor.zeros([m, n])))
+        gy, gx = synth.normal(420 + i, (k, m)), synth.normal(430 + i, (k, n))
+        gauss.append((gy, gx, it.Tensor.from_f32_slice(gy, gy.shape), it.Tensor.from_f32_slice(gx, gx.shape),
+                      it.Tensor.zeros([m, n])))
+    calls = [(a, b, o, True, False) for _, _, a, b, o in ints]
+    keys = _keys(it, lambda: it.gemm_group(calls))
+    print(f"[group f32] {keys}", flush=True)
+    assert len(keys) == 1 and "f32_TN_64x64_group" in keys[0], keys
+    first = [o.numpy() for *_, o in ints]
+    rng = np.random.default_rng(6)
+    for (dy, x, *_), got in zip(ints, first):
+        rows = rng.choice(got.shape[0], 48, replace=False)
+        exact = dy[:, rows].T.astype(np.float64) @ x.astype(np.float64)
+        assert np.array_equal(got[rows], exact.astype(np.float32)), got.shape
+    it.gemm_group(calls)
+    for (*_, o), f in zip(ints, first):
+        assert np.array_equal(o.numpy(), f)
+    it.gemm_group([(a, b, o, True, False) for _, _, a, b, o in gauss])
+    for gy, gx, a, b, o in gauss:
+        got = o.numpy()
+        assert normwise_rel(got, it.gemm(a, b, trans_a=True).numpy()) <= FP32_TOL
+        rows = rng.choice(got.shape[0], 32, replace=False)
+        ref = oracle.gemm_f32(np.ascontiguousarray(gy[:, rows].T), gx)
+        assert normwise_rel(got[rows], ref) <= FP32_TOL
+
+
 def test_group_fallbacks_equal_separate_calls(it):
-    """Groups the library does not fuse run as the separate GEMMs: FP32 weight gradients, and
-    BF16 GEMMs of two layouts, bit-identical to separate it_gemm calls."""
-    a32 = [it.Tensor.from_f32_slice(synth.normal(340 + i, (1024, 256 * (i + 1))), [1024, 256 * (i + 1)])
-           for i in range(3)]
-    x32 = it.Tensor.from_f32_slice(synth.normal(345, (1024, 384)), [1024, 384])
-    outs = [it.Tensor.zeros([256 * (i + 1), 384]) for i in range(3)]
-    keys = _keys(it, lambda: it.gemm_group([(a, x32, o, True, False) for a, o in zip(a32, outs)]))
-    assert not any("_group" in k for k in keys) and len(keys) == 3, keys
-    for a, o in zip(a32, outs):
-        assert np.array_equal(o.numpy(), it.gemm(a, x32, trans_a=True).numpy())
-    a16 = it.Tensor.from_f32_as_bf16(synth.normal(350, (2048, 1024)), [2048, 1024])
-    w16 = it.Tensor.from_f32_as_bf16(synth.normal(351, (1024, 1024)), [1024, 1024])
-    o1, o2 = it.Tensor.zeros([2048, 1024]), it.Tensor.zeros([2048, 1024])
-    it.gemm_group([(a16, w16, o1, False, True), (a16, w16, o2, False, False)])
+    """Groups the library does not fuse run as the separate GEMMs, bit for bit: BF16 GEMMs whose
+    tiles exceed one round of CUs, and BF16 GEMMs of two layouts."""
+    a16 = it.Tensor.from_f32_as_bf16(synth.normal(350, (4096, 1024)), [4096, 1024])
+    w16 = it.Tensor.from_f32_as_bf16(synth.normal(351, (4096, 1024)), [4096, 1024])
+    o1, o2 = it.Tensor.zeros([4096, 4096]), it.Tensor.zeros([4096, 4096])
+    keys = _keys(it, lambda: it.gemm_group([(a16, w16, o1, False, True), (w16, a16, o2, False, True)]))
+    assert keys and not any("_group" in k for k in keys), keys  # one key: both launches have one shape
     assert np.array_equal(o1.numpy(), it.gemm(a16, w16, trans_b=True).numpy())
-    assert np.array_equal(o2.numpy(), it.gemm(a16, w16).numpy())
+    assert np.array_equal(o2.numpy(), it.gemm(w16, a16, trans_b=True).numpy())
+    b16 = it.Tensor.from_f32_as_bf16(synth.normal(352, (1024, 1024)), [1024, 1024])
+    o3, o4 = it.Tensor.zeros([4096, 1024]), it.Tensor.zeros([4096, 1024])
+    it.gemm_group([(a16, b16, o3, False, True), (a16, b16, o4, False, False)])
+    assert np.array_equal(o3.numpy(), it.gemm(a16, b16, trans_b=True).numpy())
+    assert np.array_equal(o4.numpy(), it.gemm(a16, b16).numpy())

@@ -123,12 +123,12 @@ def test_medium_grouped_weight_gradients(it, med):
         err = normwise_rel(grouped[k], t.numpy())
         _log(f"[medium] grouped vs single {k[2:]}: normwise {err:.2e}")
         assert err <= FP32_TOL, k
-    # On one stream the group runs on the main stream: the same kernel, so the same bits.
-    st.overlap = False
+    # On the side stream (overlap_weight_grads) the group is the same kernel, so the same bits.
+    st.overlap = True
     try:
         st.enqueue()
         ctx.sync()
         for k, t in outs.items():
             assert np.array_equal(t.numpy(), grouped[k]), k
     finally:
-        st.overlap = True
+        st.overlap = False
