@@ -17,6 +17,7 @@
 // BF16 operands accumulate in FP32; P and dS are rounded to BF16 before their MFMA. When a
 // fragment comes from accumulators (P, dS), a BF16 lane group g holds keys {4g..4g+3} and
 // {16+4g..16+4g+3} of a 32-key chunk, and the LDS operand it meets is read with the same split.
+#include <algorithm>
 #include <cmath>
 
 #include "internal.hpp"
@@ -125,10 +126,11 @@ struct Unit4 {
 // 0-1 move tensor 0 and waves 2-3 tensor 1. Each tensor goes to LDS row-major, transposed or both
 // (an offset < 0 skips a layout). Optionally two per-row FP32 vectors (aux) ride along, scaled, for
 // rows blk*64 + tid (tid < 64), into `aux_off`.
-template <typename T>
+template <typename T, int NT = NTH>
 struct TilePair {
     static constexpr int PER_TILE = TR * HD / (4 * FE<T>::VEC);
-    static constexpr int SLOTS = 2 * PER_TILE / NTH;
+    static constexpr int SLOTS = 2 * PER_TILE >= NT ? 2 * PER_TILE / NT : 1;
+    static constexpr bool ALL = 2 * PER_TILE >= NT;  // every thread moves units
     const T *m[2];
     int64_t rs[2];
     int rows[2];
@@ -149,6 +151,7 @@ struct TilePair {
         float *x = SET ? x1 : x0;
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s) {
+            if (!ALL && tid >= 2 * PER_TILE) break;
             const int t = tensor(s);
             r[s].load(m[t], rs[t], blk * TR, rows[t], unit(), off_cols[t] >= 0);
         }
@@ -164,6 +167,7 @@ struct TilePair {
         const float *x = SET ? x1 : x0;
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s) {
+            if (!ALL && tid >= 2 * PER_TILE) break;
             const int t = tensor(s);
             const bool rg_fast = off_cols[t] >= 0;
             if (off_rows[t] >= 0) r[s].store_rows(stage + off_rows[t], unit(), rg_fast);
@@ -179,8 +183,8 @@ struct TilePair {
 // Runs body(t, stage) for t = 0..n-1 on row blocks b0 + t, block t's tiles in LDS stage t % 2.
 // Block t+2 is loaded as body t starts and written to LDS after body t+1, so its loads have two
 // blocks of compute to land.
-template <typename T, typename Body>
-__device__ __forceinline__ void pipelined(TilePair<T> &tp, char *smem, int stage_bytes, int b0, int n, Body body) {
+template <typename TP, typename Body>
+__device__ __forceinline__ void pipelined(TP &tp, char *smem, int stage_bytes, int b0, int n, Body body) {
     if (n > 0) {
         tp.template load<0>(b0);
         tp.template store<0>(smem);
@@ -261,13 +265,38 @@ __device__ __forceinline__ void grid_tile(int &tile, int64_t &bh) {
 
 // ------------------------------------------------------------------ forward
 
-template <typename T>
-__global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
+// WG wave groups: with WG = 2 a block runs 8 waves, and wave w's 16 rows are shared by waves w and
+// w + 4, each taking two of every tile's four 16-column blocks (grp = wave / 4 picks which). The
+// two groups read the same LDS tiles; their partial results meet through LDS at the end, group 1's
+// added to group 0's in a fixed order. A launch whose blocks fit one round on the CUs thereby runs
+// twice the waves, each with half the work per tile.
+constexpr int group_of(int wave8) { return wave8 >> 2; }
+
+// Group 1 hands `n` floats per lane to group 0 through LDS ([wave][n][lane], conflict-free); call
+// after the tile loop's final barrier, by every thread. Returns false for group 1 (done).
+template <int N>
+__device__ __forceinline__ bool hand_over(char *smem, int grp, int wave, int lane, float (&v)[N]) {
+    float *x = (float *)smem + wave * N * 64 + lane;
+    if (grp == 1) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i * 64] = v[i];
+    }
+    __syncthreads();
+    if (grp == 1) return false;
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = x[i * 64];
+    return true;
+}
+
+template <typename T, int WG>
+__global__ __launch_bounds__(NTH * WG) void flash_fwd(const FlashArgs p) {
     constexpr int KT = tile_bytes<T>();      // K tile [keys][d]
     constexpr int STAGE = 2 * KT;            // + V^T tile [d][keys]
     constexpr int NC = HD / FE<T>::KC;       // d chunks
+    constexpr int MBG = 4 / WG;              // 16-key blocks per group and tile
+    constexpr int PCG = TR / FE<T>::KC / WG; // P chunks per group and tile
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, grp = group_of(tid >> 6);
     const int ql = lane & 15, g = lane >> 4;
     // Causal: the last query block sees every key block, so query blocks go out last-first.
     int qb;
@@ -297,7 +326,7 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
 
     const int kblocks = (p.skv + TR - 1) / TR;
     const int nkb = p.causal ? min(kblocks, qb + 1) : kblocks;
-    TilePair<T> tp;
+    TilePair<T, NTH * WG> tp;
     tp.tid = tid;
     tp.m[0] = K;  // K row-major
     tp.m[1] = V;  // V transposed
@@ -309,34 +338,35 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
     tp.off_cols[1] = KT;
     pipelined(tp, smem, STAGE, 0, nkb, [&](int kb, const char *kt) {
         const char *vt = kt + KT;
-        // S^T blocks: keys 16mb + 4g + r of this tile, query q.
-        f32x4 s[4];
+        // S^T blocks: keys 16mb + 4g + r of this tile (mb = grp * MBG + i), query q.
+        f32x4 s[MBG];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-            s[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < MBG; ++i) {
+            const int mb = grp * MBG + i;
+            s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < NC; ++c) mma16<T>(s[mb], frag_c<T>(kt, mb * 16 + ql, c, g), qf[c]);
+            for (int c = 0; c < NC; ++c) mma16<T>(s[i], frag_c<T>(kt, mb * 16 + ql, c, g), qf[c]);
         }
         // Scores to the log2 domain; keys past the diagonal (causal) or past seq_kv are -inf. Only
         // the last key block of a row block can hold such keys.
         float mx = -INFINITY;
         if (kb == nkb - 1 && (p.causal || p.skv % TR != 0)) {
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int i = 0; i < MBG; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int key = kb * TR + mb * 16 + g * 4 + r;
+                    const int key = kb * TR + (grp * MBG + i) * 16 + g * 4 + r;
                     const bool dead = key >= p.skv || (p.causal && key > q);
-                    s[mb][r] = dead ? -INFINITY : s[mb][r] * c2;
-                    mx = fmaxf(mx, s[mb][r]);
+                    s[i][r] = dead ? -INFINITY : s[i][r] * c2;
+                    mx = fmaxf(mx, s[i][r]);
                 }
         } else {
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int i = 0; i < MBG; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    s[mb][r] *= c2;
-                    mx = fmaxf(mx, s[mb][r]);
+                    s[i][r] *= c2;
+                    mx = fmaxf(mx, s[i][r]);
                 }
         }
         const float mnew = fmaxf(m, xmax(mx));
@@ -344,23 +374,46 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
         const float alpha = exp2_fast(m - msafe);
         float ls = 0.f;
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+        for (int i = 0; i < MBG; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = exp2_fast(s[mb][r] - msafe);
-                s[mb][r] = e;
+                const float e = exp2_fast(s[i][r] - msafe);
+                s[i][r] = e;
                 ls += e;
             }
         l = l * alpha + xsum(ls);
         m = mnew;
 #pragma unroll
         for (int d = 0; d < 4; ++d) o[d] *= alpha;
-        // O^T (d x q) += V^T (d x keys) . P^T (keys x q)
+        // O^T (d x q) += V^T (d x keys) . P^T (keys x q), over this group's keys
 #pragma unroll
         for (int d = 0; d < 4; ++d)
 #pragma unroll
-            for (int c = 0; c < TR / FE<T>::KC; ++c) mma16<T>(o[d], frag_s<T>(vt, d * 16 + ql, c, g), frag_acc<T>(s, c));
+            for (int c = 0; c < PCG; ++c)
+                mma16<T>(o[d], frag_s<T>(vt, d * 16 + ql, grp * PCG + c, g), frag_acc<T>(s, c));
     });
+    if constexpr (WG == 2) {
+        // Each group ran the online softmax over its own keys: merge (m, l, O) at the larger max.
+        float v[18];
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[d * 4 + r] = o[d][r];
+        v[16] = m;
+        v[17] = l;
+        float mine[18];
+#pragma unroll
+        for (int i = 0; i < 18; ++i) mine[i] = v[i];
+        if (!hand_over<18>(smem, grp, wave, lane, v)) return;
+        const float m1 = v[16], mn = fmaxf(m, m1), ms = mn == -INFINITY ? 0.f : mn;
+        const float a0 = exp2_fast(m - ms), a1 = exp2_fast(m1 - ms);
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[d][r] = mine[d * 4 + r] * a0 + v[d * 4 + r] * a1;
+        l = l * a0 + v[17] * a1;
+        m = mn;
+    }
     if (qok) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
@@ -373,15 +426,17 @@ __global__ __launch_bounds__(NTH) void flash_fwd(const FlashArgs p) {
 // ------------------------------------------------------------------ backward
 
 
-// dK, dV for 64 keys per block (16 per wave), looping over the query blocks that see them.
-template <typename T>
-__global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
+// dK, dV for 64 keys per block (16 per wave), looping over the query blocks that see them. WG = 2:
+// each wave group takes half of every query tile's rows (see flash_fwd).
+template <typename T, int WG>
+__global__ __launch_bounds__(NTH * WG) void flash_bwd_dkdv(const FlashArgs p) {
     constexpr int T_ = tile_bytes<T>();
     constexpr int STAGE = 4 * T_ + 2 * TR * 4;  // Q, Q^T, dO, dO^T tiles + lse, dlt rows
     constexpr int NC = HD / FE<T>::KC;
-    constexpr int NQ = TR / FE<T>::KC;  // q chunks per tile
+    constexpr int NQG = TR / FE<T>::KC / WG;  // q chunks per group and tile
+    constexpr int MBG = 4 / WG;               // 16-query blocks per group and tile
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, grp = group_of(tid >> 6);
     const int ql = lane & 15, g = lane >> 4;
     // Causal: key block 0 is seen by every query block, so key blocks go out first-first.
     int kb;
@@ -414,7 +469,7 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
     const int qb0 = p.causal ? kb : 0;
     // Q and dO, each needed row-major (S, dP) and transposed (dK, dV); the rows' LSE (as log2) and
     // rowsum(dO * O) ride along.
-    TilePair<T> tp;
+    TilePair<T, NTH * WG> tp;
     tp.tid = tid;
     tp.m[0] = Q;
     tp.m[1] = dO;
@@ -434,15 +489,17 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
         const int qb = qb0 + t;
         const char *qt = st, *qtt = st + T_, *dot = st + 2 * T_, *dott = st + 3 * T_;
         const float *ls = (const float *)(st + 4 * T_), *dl = ls + TR;
-        // S = Q.K^T and dP = dO.V^T: rows q = 16mb + 4g + r of the tile, column = this key.
-        f32x4 sp[4], dp[4];
+        // S = Q.K^T and dP = dO.V^T: rows q = 16mb + 4g + r of the tile (mb = grp * MBG + i),
+        // column = this key.
+        f32x4 sp[MBG], dp[MBG];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-            sp[mb] = dp[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < MBG; ++i) {
+            const int mb = grp * MBG + i;
+            sp[i] = dp[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                mma16<T>(sp[mb], frag_c<T>(qt, mb * 16 + ql, c, g), kf[c]);
-                mma16<T>(dp[mb], frag_c<T>(dot, mb * 16 + ql, c, g), vf[c]);
+                mma16<T>(sp[i], frag_c<T>(qt, mb * 16 + ql, c, g), kf[c]);
+                mma16<T>(dp[i], frag_c<T>(dot, mb * 16 + ql, c, g), vf[c]);
             }
         }
         // P = exp2(S * scale * log2(e) - LSE2). Rows past seq_q need no mask: their Q and dO rows
@@ -453,29 +510,47 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
         // blocks run the exponentials without a compare and select per probability.
         if (p.causal && qb == kb) {
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int i = 0; i < MBG; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    if (key > qb * TR + mb * 16 + g * 4 + r) sp[mb][r] = -INFINITY;
+                    if (key > qb * TR + (grp * MBG + i) * 16 + g * 4 + r) sp[i][r] = -INFINITY;
         }
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+        for (int i = 0; i < MBG; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int ql_ = mb * 16 + g * 4 + r;
-                const float pr = exp2_fast(sp[mb][r] * c2 - ls[ql_]);
-                sp[mb][r] = pr;
-                dp[mb][r] = pr * (dp[mb][r] - dl[ql_]);
+                const int ql_ = (grp * MBG + i) * 16 + g * 4 + r;
+                const float pr = exp2_fast(sp[i][r] * c2 - ls[ql_]);
+                sp[i][r] = pr;
+                dp[i][r] = pr * (dp[i][r] - dl[ql_]);
             }
-        // dV (keys x d) += P^T (keys x q) . dO (q x d);  dK += dS^T . Q
+        // dV (keys x d) += P^T (keys x q) . dO (q x d);  dK += dS^T . Q, over this group's queries
 #pragma unroll
         for (int n = 0; n < 4; ++n)
 #pragma unroll
-            for (int c = 0; c < NQ; ++c) {
-                mma16<T>(dv[n], frag_acc<T>(sp, c), frag_s<T>(dott, n * 16 + ql, c, g));
-                mma16<T>(dk[n], frag_acc<T>(dp, c), frag_s<T>(qtt, n * 16 + ql, c, g));
+            for (int c = 0; c < NQG; ++c) {
+                mma16<T>(dv[n], frag_acc<T>(sp, c), frag_s<T>(dott, n * 16 + ql, grp * NQG + c, g));
+                mma16<T>(dk[n], frag_acc<T>(dp, c), frag_s<T>(qtt, n * 16 + ql, grp * NQG + c, g));
             }
     });
+    if constexpr (WG == 2) {
+        float v[32];
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                v[n * 4 + r] = dk[n][r];
+                v[16 + n * 4 + r] = dv[n][r];
+            }
+        if (!hand_over<32>(smem, grp, wave, lane, v)) return;
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                dk[n][r] += v[n * 4 + r];
+                dv[n][r] += v[16 + n * 4 + r];
+            }
+    }
     // Lane l holds rows (keys) 16*wave + 4g + r and column d = 16n + l%16.
     const Head hdk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs};
     float *dK = p.dK + hdk.base(bh), *dV = p.dV + hdk.base(bh);
@@ -491,15 +566,17 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dkdv(const FlashArgs p) {
     }
 }
 
-// dQ for 64 queries per block (16 per wave), looping over the key blocks they see.
-template <typename T>
-__global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
+// dQ for 64 queries per block (16 per wave), looping over the key blocks they see. WG = 2: each
+// wave group takes half of every key tile's rows (see flash_fwd).
+template <typename T, int WG>
+__global__ __launch_bounds__(NTH * WG) void flash_bwd_dq(const FlashArgs p) {
     constexpr int T_ = tile_bytes<T>();
     constexpr int STAGE = 3 * T_;  // K, V, K^T
     constexpr int NC = HD / FE<T>::KC;
-    constexpr int NK = TR / FE<T>::KC;
+    constexpr int NKG = TR / FE<T>::KC / WG;  // key chunks per group and tile
+    constexpr int MBG = 4 / WG;               // 16-key blocks per group and tile
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, grp = group_of(tid >> 6);
     const int ql = lane & 15, g = lane >> 4;
     int qb;
     int64_t bh;
@@ -552,7 +629,7 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
         }
         dl += __shfl_xor(dl, 16, 64);
         dl += __shfl_xor(dl, 32, 64);
-        if (g == 0 && qok) p.dlt[bh * p.sq + q] = dl;
+        if (g == 0 && qok && grp == 0) p.dlt[bh * p.sq + q] = dl;
     }
     f32x4 dq[4];
 #pragma unroll
@@ -561,7 +638,7 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
     const int kblocks = (p.skv + TR - 1) / TR;
     const int nkb = p.causal ? min(kblocks, qb + 1) : kblocks;
     // K row-major (S^T) and transposed (dQ^T), V row-major (dP^T).
-    TilePair<T> tp;
+    TilePair<T, NTH * WG> tp;
     tp.tid = tid;
     tp.m[0] = K;
     tp.m[1] = V;
@@ -573,15 +650,17 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
     tp.off_cols[1] = -1;
     pipelined(tp, smem, STAGE, 0, nkb, [&](int kb, const char *kt) {
         const char *vt = kt + T_, *ktt = kt + 2 * T_;
-        // S^T = K.Q^T and dP^T = V.dO^T: rows = keys 16mb + 4g + r, column = this query.
-        f32x4 sp[4], dp[4];
+        // S^T = K.Q^T and dP^T = V.dO^T: rows = keys 16mb + 4g + r (mb = grp * MBG + i), column =
+        // this query.
+        f32x4 sp[MBG], dp[MBG];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-            sp[mb] = dp[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < MBG; ++i) {
+            const int mb = grp * MBG + i;
+            sp[i] = dp[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                mma16<T>(sp[mb], frag_c<T>(kt, mb * 16 + ql, c, g), qf[c]);
-                mma16<T>(dp[mb], frag_c<T>(vt, mb * 16 + ql, c, g), of[c]);
+                mma16<T>(sp[i], frag_c<T>(kt, mb * 16 + ql, c, g), qf[c]);
+                mma16<T>(dp[i], frag_c<T>(vt, mb * 16 + ql, c, g), of[c]);
             }
         }
         // Queries past seq_q are not stored. The causal diagonal block masks keys above the query,
@@ -591,23 +670,36 @@ __global__ __launch_bounds__(NTH) void flash_bwd_dq(const FlashArgs p) {
         // blocks take.
         if ((p.causal && kb == qb) || (kb == nkb - 1 && p.skv % TR != 0)) {
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int i = 0; i < MBG; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int key = kb * TR + mb * 16 + g * 4 + r;
-                    if (key >= p.skv || (p.causal && key > q)) sp[mb][r] = -INFINITY;
+                    const int key = kb * TR + (grp * MBG + i) * 16 + g * 4 + r;
+                    if (key >= p.skv || (p.causal && key > q)) sp[i][r] = -INFINITY;
                 }
         }
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+        for (int i = 0; i < MBG; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) dp[mb][r] = exp2_fast(sp[mb][r] * c2 - lse2) * (dp[mb][r] - dl);
-        // dQ^T (d x q) += K^T (d x keys) . dS^T (keys x q)
+            for (int r = 0; r < 4; ++r) dp[i][r] = exp2_fast(sp[i][r] * c2 - lse2) * (dp[i][r] - dl);
+        // dQ^T (d x q) += K^T (d x keys) . dS^T (keys x q), over this group's keys
 #pragma unroll
         for (int d = 0; d < 4; ++d)
 #pragma unroll
-            for (int c = 0; c < NK; ++c) mma16<T>(dq[d], frag_s<T>(ktt, d * 16 + ql, c, g), frag_acc<T>(dp, c));
+            for (int c = 0; c < NKG; ++c)
+                mma16<T>(dq[d], frag_s<T>(ktt, d * 16 + ql, grp * NKG + c, g), frag_acc<T>(dp, c));
     });
+    if constexpr (WG == 2) {
+        float v[16];
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[d * 4 + r] = dq[d][r];
+        if (!hand_over<16>(smem, grp, wave, lane, v)) return;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dq[d][r] += v[d * 4 + r];
+    }
     if (qok) {
         float *dQ = p.dQ + hq.base(bh) + (int64_t)q * p.q_rs;
 #pragma unroll
@@ -632,15 +724,32 @@ bool flash_supported(const FlashArgs &p, int elem_bytes, bool backward) {
     return r;
 }
 
+// Grids of at most this many blocks (one round on MI355X's 256 CUs) run the two-group form: with
+// one block per CU, each of a block's 16-row jobs then runs as two waves.
+constexpr int64_t SPLIT_MAX_BLOCKS = 256;
+
+template <typename T, int WG>
+void fwd_launch(hipStream_t s, const FlashArgs &p, dim3 grid) {
+    hipLaunchKernelGGL((flash_fwd<T, WG>), grid, dim3(NTH * WG), 0, s, p);
+}
+
+template <typename T, int WG>
+void bwd_launch(hipStream_t s, const FlashArgs &p, int64_t qblocks, int64_t kblocks) {
+    // dQ first: it also computes dlt = rowsum(dO * O) for its queries, which dK/dV reads.
+    hipLaunchKernelGGL((flash_bwd_dq<T, WG>), dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH * WG), 0, s, p);
+    hipLaunchKernelGGL((flash_bwd_dkdv<T, WG>), dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH * WG), 0, s, p);
+}
+
 it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16) {
     if (bf16 && flash2_applicable(p, false)) return launch_flash2_fwd(s, p);
     const int64_t qblocks = (p.sq + TR - 1) / TR;
     if (qblocks > 0x7fffffff || p.bh > 65535) return fail(IT_ERR_DIMS, "flash attention: grid too large");
-    dim3 grid((unsigned)qblocks, (unsigned)p.bh);
+    const dim3 grid((unsigned)qblocks, (unsigned)p.bh);
+    const bool split = qblocks * p.bh <= SPLIT_MAX_BLOCKS;
     if (bf16)
-        hipLaunchKernelGGL(flash_fwd<uint16_t>, grid, dim3(NTH), 0, s, p);
+        split ? fwd_launch<uint16_t, 2>(s, p, grid) : fwd_launch<uint16_t, 1>(s, p, grid);
     else
-        hipLaunchKernelGGL(flash_fwd<float>, grid, dim3(NTH), 0, s, p);
+        split ? fwd_launch<float, 2>(s, p, grid) : fwd_launch<float, 1>(s, p, grid);
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
 }
@@ -650,14 +759,11 @@ it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16) {
     const int64_t qblocks = (p.sq + TR - 1) / TR, kblocks = (p.skv + TR - 1) / TR;
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || p.bh > 65535)
         return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
-    // dQ first: it also computes dlt = rowsum(dO * O) for its queries, which dK/dV reads.
-    if (bf16) {
-        hipLaunchKernelGGL(flash_bwd_dq<uint16_t>, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
-        hipLaunchKernelGGL(flash_bwd_dkdv<uint16_t>, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
-    } else {
-        hipLaunchKernelGGL(flash_bwd_dq<float>, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
-        hipLaunchKernelGGL(flash_bwd_dkdv<float>, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
-    }
+    const bool split = std::max(qblocks, kblocks) * p.bh <= SPLIT_MAX_BLOCKS;
+    if (bf16)
+        split ? bwd_launch<uint16_t, 2>(s, p, qblocks, kblocks) : bwd_launch<uint16_t, 1>(s, p, qblocks, kblocks);
+    else
+        split ? bwd_launch<float, 2>(s, p, qblocks, kblocks) : bwd_launch<float, 1>(s, p, qblocks, kblocks);
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
 }

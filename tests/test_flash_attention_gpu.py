@@ -96,10 +96,12 @@ def test_flash_forward_bhsd_o_and_lse(it, oracle, causal):
 
 
 @pytest.mark.parametrize("b,h,s,causal", [(2, 4, 16, True), (2, 3, 200, True), (1, 2, 130, False),
-                                          (4, 4, 256, True)])
+                                          (4, 4, 256, True), (4, 8, 640, True)])
 def test_flash_backward_f32(it, oracle, b, h, s, causal):
     """(2,4,16) is the shape family of src/train/helpers.rs:435-494 at head_dim 64; (4,4,256) is a
-    quarter of one TINY layer; 200 and 130 leave partial tiles."""
+    quarter of one TINY layer; 200 and 130 leave partial tiles. Grids of up to 256 blocks run each
+    block's 16-row jobs as two waves that split every tile; (4,8,640) has 320 blocks and runs the
+    one-wave form."""
     print(f"[flash bwd f32] {b}x{h}x{s} causal={causal}", flush=True)
     q, k, v, do = (synth.normal(10 + i, (b, h, s, D)) for i in range(4))
     tq, tk, tv, tdo = (_t(it, x) for x in (q, k, v, do))
