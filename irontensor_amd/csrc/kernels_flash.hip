@@ -428,20 +428,18 @@ __global__ __launch_bounds__(NTH * WG) void flash_fwd(const FlashArgs p) {
 
 // dK, dV for 64 keys per block (16 per wave), looping over the query blocks that see them. WG = 2:
 // each wave group takes half of every query tile's rows (see flash_fwd).
+template <typename T>
+constexpr int dkdv_lds() { return 2 * (4 * tile_bytes<T>() + 2 * TR * 4); }
+
 template <typename T, int WG>
-__global__ __launch_bounds__(NTH * WG) void flash_bwd_dkdv(const FlashArgs p) {
+__device__ __forceinline__ void dkdv_block(const FlashArgs &p, int kb, int64_t bh, char *smem) {
     constexpr int T_ = tile_bytes<T>();
     constexpr int STAGE = 4 * T_ + 2 * TR * 4;  // Q, Q^T, dO, dO^T tiles + lse, dlt rows
     constexpr int NC = HD / FE<T>::KC;
     constexpr int NQG = TR / FE<T>::KC / WG;  // q chunks per group and tile
     constexpr int MBG = 4 / WG;               // 16-query blocks per group and tile
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, grp = group_of(tid >> 6);
     const int ql = lane & 15, g = lane >> 4;
-    // Causal: key block 0 is seen by every query block, so key blocks go out first-first.
-    int kb;
-    int64_t bh;
-    grid_tile(kb, bh);
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         hd{p.heads, p.do_bs, p.do_hs, p.do_rs};
     const T *Q = (const T *)p.Q + hq.base(bh);
@@ -566,22 +564,32 @@ __global__ __launch_bounds__(NTH * WG) void flash_bwd_dkdv(const FlashArgs p) {
     }
 }
 
+template <typename T, int WG>
+__global__ __launch_bounds__(NTH * WG) void flash_bwd_dkdv(const FlashArgs p) {
+    __shared__ __attribute__((aligned(16))) char smem[dkdv_lds<T>()];
+    // Causal: key block 0 is seen by every query block, so key blocks go out first-first.
+    int kb;
+    int64_t bh;
+    grid_tile(kb, bh);
+    dkdv_block<T, WG>(p, kb, bh, smem);
+}
+
 // dQ for 64 queries per block (16 per wave), looping over the key blocks they see. WG = 2: each
 // wave group takes half of every key tile's rows (see flash_fwd).
-template <typename T, int WG>
-__global__ __launch_bounds__(NTH * WG) void flash_bwd_dq(const FlashArgs p) {
+template <typename T>
+constexpr int dq_lds() { return 2 * 3 * tile_bytes<T>(); }
+
+// DLT_IN: rowsum(dO * O) comes from p.dlt (written by flash_bwd_dlt); else computed here from the
+// dO fragments and written to p.dlt for the dK/dV kernel.
+template <typename T, int WG, bool DLT_IN>
+__device__ __forceinline__ void dq_block(const FlashArgs &p, int qb, int64_t bh, char *smem) {
     constexpr int T_ = tile_bytes<T>();
     constexpr int STAGE = 3 * T_;  // K, V, K^T
     constexpr int NC = HD / FE<T>::KC;
     constexpr int NKG = TR / FE<T>::KC / WG;  // key chunks per group and tile
     constexpr int MBG = 4 / WG;               // 16-key blocks per group and tile
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, grp = group_of(tid >> 6);
     const int ql = lane & 15, g = lane >> 4;
-    int qb;
-    int64_t bh;
-    grid_tile(qb, bh);
-    if (p.causal) qb = (int)gridDim.x - 1 - qb;  // heaviest first
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         hd{p.heads, p.do_bs, p.do_hs, p.do_rs};
     const T *Q = (const T *)p.Q + hq.base(bh);
@@ -605,7 +613,9 @@ __global__ __launch_bounds__(NTH * WG) void flash_bwd_dq(const FlashArgs p) {
     // lanes of a query hold 16 of its 64 columns each. Written for the dK/dV kernel, which runs
     // after this one.
     float dl = 0.f;
-    {
+    if constexpr (DLT_IN) {
+        dl = qok ? p.dlt[bh * p.sq + q] : 0.f;
+    } else {
         const Head ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
         const float *Orow = p.O + ho.base(bh) + (qok ? (int64_t)q * p.o_rs : 0);
 #pragma unroll
@@ -707,6 +717,54 @@ __global__ __launch_bounds__(NTH * WG) void flash_bwd_dq(const FlashArgs p) {
     }
 }
 
+template <typename T, int WG>
+__global__ __launch_bounds__(NTH * WG) void flash_bwd_dq(const FlashArgs p) {
+    __shared__ __attribute__((aligned(16))) char smem[dq_lds<T>()];
+    int qb;
+    int64_t bh;
+    grid_tile(qb, bh);
+    if (p.causal) qb = (int)gridDim.x - 1 - qb;  // heaviest first
+    dq_block<T, WG, false>(p, qb, bh, smem);
+}
+
+// rowsum(dO * O) of every query row into p.dlt, 16 lanes per row (4 columns each), for
+// flash_bwd_fused, whose dK/dV part reads rows that other blocks' dQ parts cover.
+template <typename T>
+__global__ __launch_bounds__(256) void flash_bwd_dlt(const FlashArgs p) {
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int c = threadIdx.x & 15;
+    if (row >= p.bh * p.sq) return;  // whole 16-lane groups leave together
+    const int64_t bh = row / p.sq, q = row % p.sq;
+    const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
+    const f32x4 o = *(const f32x4 *)(p.O + ho.base(bh) + q * p.o_rs + 4 * c);
+    f32x4 d;
+    if constexpr (sizeof(T) == 4) {
+        d = *(const f32x4 *)((const float *)p.dO + hd.base(bh) + q * p.do_rs + 4 * c);
+    } else {
+        const u32x2 h = *(const u32x2 *)((const uint16_t *)p.dO + hd.base(bh) + q * p.do_rs + 4 * c);
+        d = f32x4{__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u), __uint_as_float(h[1] << 16),
+                  __uint_as_float(h[1] & 0xffff0000u)};
+    }
+    float s = d[0] * o[0] + d[1] * o[1] + d[2] * o[2] + d[3] * o[3];
+#pragma unroll
+    for (int w = 1; w < 16; w <<= 1) s += __shfl_xor(s, w, 64);
+    if (c == 0) p.dlt[bh * p.sq + q] = s;
+}
+
+// The backward for grids with as many key blocks as query blocks: block j computes dQ of query
+// block j, then dK and dV of key block j. Under the causal mask the two parts' tile counts are
+// j + 1 and blocks - j, so every block does the same work (one kernel of balanced blocks in place
+// of two kernels whose slowest blocks each take every tile).
+template <typename T, int WG>
+__global__ __launch_bounds__(NTH * WG) void flash_bwd_fused(const FlashArgs p) {
+    __shared__ __attribute__((aligned(16))) char smem[dkdv_lds<T>() > dq_lds<T>() ? dkdv_lds<T>() : dq_lds<T>()];
+    const int j = (int)blockIdx.x;
+    const int64_t bh = blockIdx.y;
+    dq_block<T, WG, true>(p, j, bh, smem);
+    __syncthreads();  // the dQ part's last LDS reads (its hand-over) before the dK/dV part's writes
+    dkdv_block<T, WG>(p, j, bh, smem);
+}
+
 }  // namespace
 
 bool flash_supported(const FlashArgs &p, int elem_bytes, bool backward) {
@@ -735,6 +793,14 @@ void fwd_launch(hipStream_t s, const FlashArgs &p, dim3 grid) {
 
 template <typename T, int WG>
 void bwd_launch(hipStream_t s, const FlashArgs &p, int64_t qblocks, int64_t kblocks) {
+    if (qblocks == kblocks) {
+        // rowsum(dO * O) for every row first, then one kernel of balanced dQ + dK/dV blocks.
+        const int64_t rows = p.bh * p.sq;
+        hipLaunchKernelGGL(flash_bwd_dlt<T>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, p);
+        hipLaunchKernelGGL((flash_bwd_fused<T, WG>), dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH * WG), 0, s,
+                           p);
+        return;
+    }
     // dQ first: it also computes dlt = rowsum(dO * O) for its queries, which dK/dV reads.
     hipLaunchKernelGGL((flash_bwd_dq<T, WG>), dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH * WG), 0, s, p);
     hipLaunchKernelGGL((flash_bwd_dkdv<T, WG>), dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH * WG), 0, s, p);
