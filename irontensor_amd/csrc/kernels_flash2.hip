@@ -346,16 +346,14 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void f
 
 // ------------------------------------------------------------------ backward: dQ (and rowsum(dO * O))
 
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_dq(const FlashArgs p) {
-    __shared__ __attribute__((aligned(1024))) char st0[2 * TB];  // K tile, V tile
-    __shared__ __attribute__((aligned(1024))) char st1[2 * TB];
+// One dQ block: query rows qb * RB .. + RB - 1 of head bh, LDS stages st0 and st1 of 2 TB bytes.
+// ROWS_IN: -rowsum(dO * O) and -LSE log2 e come from the workspace (written by flash2_bwd_rows);
+// else they are computed here and written there for the dK/dV kernel.
+template <bool ROWS_IN>
+__device__ __forceinline__ void dq2_block(const FlashArgs &p, int qb, int64_t bh, char *st0, char *st1) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5;
-    int qb;
-    int64_t bh;
-    grid_tile(qb, bh);
-    if (p.causal) qb = (int)gridDim.x - 1 - qb;
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
     const uint16_t *Q = (const uint16_t *)p.Q + hq.base(bh);
@@ -380,7 +378,9 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
     // 32 of its 64 d each). For the dK/dV kernel, which runs after this one, the workspace gets
     // -rowsum at dlt[row] and -LSE log2 e at dlt[bh seq + row].
     float dl = 0.f;
-    {
+    if constexpr (ROWS_IN) {
+        dl = qok ? -p.dlt[bh * p.sq + q] : 0.f;
+    } else {
         const float *Orow = p.O + ho.base(bh) + (qok ? (int64_t)q * p.o_rs : 0);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
@@ -397,7 +397,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
         dl += __shfl_xor(dl, 32, 64);
     }
     const float nl2 = qok ? -p.lse[bh * p.sq + q] * LOG2E : 0.f;
-    if (h == 0 && qok) {
+    if (!ROWS_IN && h == 0 && qok) {
         p.dlt[bh * p.sq + q] = -dl;
         p.dlt[p.bh * p.sq + bh * p.sq + q] = nl2;
     }
@@ -463,18 +463,25 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
     }
 }
 
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_dq(const FlashArgs p) {
+    __shared__ __attribute__((aligned(1024))) char st0[2 * TB];  // K tile, V tile
+    __shared__ __attribute__((aligned(1024))) char st1[2 * TB];
+    int qb;
+    int64_t bh;
+    grid_tile(qb, bh);
+    if (p.causal) qb = (int)gridDim.x - 1 - qb;
+    dq2_block<false>(p, qb, bh, st0, st1);
+}
+
 // ------------------------------------------------------------------ backward: dK, dV
 
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_dkdv(const FlashArgs p) {
-    constexpr int STAGE = 2 * TB + 2 * TR * 4;  // Q tile, dO tile, -LSE log2 e and -rowsum(dO * O) rows
-    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
-    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+constexpr int DKDV2_STAGE = 2 * TB + 2 * TR * 4;  // Q tile, dO tile, -LSE log2 e and -rowsum(dO * O) rows
+
+// One dK/dV block: keys kb * RB .. + RB - 1 of head bh, LDS stages st0 and st1 of DKDV2_STAGE bytes.
+__device__ __forceinline__ void dkdv2_block(const FlashArgs &p, int kb, int64_t bh, char *st0, char *st1) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5;
-    int kb;
-    int64_t bh;
-    grid_tile(kb, bh);  // causal: key block 0 is seen by every query block, so it goes out first
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         hd{p.heads, p.do_bs, p.do_hs, p.do_rs};
     const uint16_t *Q = (const uint16_t *)p.Q + hq.base(bh);
@@ -584,6 +591,49 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
     }
 }
 
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_dkdv(const FlashArgs p) {
+    __shared__ __attribute__((aligned(1024))) char st0[DKDV2_STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[DKDV2_STAGE];
+    int kb;
+    int64_t bh;
+    grid_tile(kb, bh);  // causal: key block 0 is seen by every query block, so it goes out first
+    dkdv2_block(p, kb, bh, st0, st1);
+}
+
+// The workspace rows of every query: -rowsum(dO * O) at dlt[row] and -LSE log2 e at
+// dlt[bh seq + row], 16 lanes per row (4 columns each), for flash2_bwd_fused.
+__global__ __launch_bounds__(256) void flash2_bwd_rows(const FlashArgs p) {
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int c = threadIdx.x & 15;
+    if (row >= p.bh * p.sq) return;  // whole 16-lane groups leave together
+    const int64_t bh = row / p.sq, q = row % p.sq;
+    const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
+    const f32x4 o = *(const f32x4 *)(p.O + ho.base(bh) + q * p.o_rs + 4 * c);
+    const u32x2 g = *(const u32x2 *)((const uint16_t *)p.dO + hd.base(bh) + q * p.do_rs + 4 * c);
+    float s = __uint_as_float(g[0] << 16) * o[0] + __uint_as_float(g[0] & 0xffff0000u) * o[1] +
+              __uint_as_float(g[1] << 16) * o[2] + __uint_as_float(g[1] & 0xffff0000u) * o[3];
+#pragma unroll
+    for (int w = 1; w < 16; w <<= 1) s += __shfl_xor(s, w, 64);
+    if (c == 0) {
+        p.dlt[row] = -s;
+        p.dlt[p.bh * p.sq + row] = -p.lse[row] * LOG2E;
+    }
+}
+
+// The backward for grids with as many key blocks as query blocks: block j computes dQ of query
+// block j, then dK and dV of key block j. Under the causal mask the two parts' tile counts add up
+// to the same number for every block.
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_fused(const FlashArgs p) {
+    __shared__ __attribute__((aligned(1024))) char st0[DKDV2_STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[DKDV2_STAGE];
+    int j;
+    int64_t bh;
+    grid_tile(j, bh);
+    dq2_block<true>(p, j, bh, st0, st1);
+    __syncthreads();  // the dQ part's last LDS reads before the dK/dV part's first writes
+    dkdv2_block(p, j, bh, st0, st1);
+}
+
 }  // namespace
 
 // The BF16 kernels above need 16-byte aligned operand rows (checked by flash_supported) and 32-bit
@@ -607,9 +657,16 @@ it_status launch_flash2_bwd(hipStream_t s, const FlashArgs &p) {
     const int64_t qblocks = (p.sq + RB - 1) / RB, kblocks = (p.skv + RB - 1) / RB;
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || p.bh > 65535)
         return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
-    // dQ first: it also writes rowsum(dO * O), which the dK/dV kernel reads.
-    hipLaunchKernelGGL(flash2_bwd_dq, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
-    hipLaunchKernelGGL(flash2_bwd_dkdv, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+    if (qblocks == kblocks) {
+        // The workspace rows of every query first, then one kernel of balanced dQ + dK/dV blocks.
+        const int64_t rows = p.bh * p.sq;
+        hipLaunchKernelGGL(flash2_bwd_rows, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(flash2_bwd_fused, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+    } else {
+        // dQ first: it also writes rowsum(dO * O), which the dK/dV kernel reads.
+        hipLaunchKernelGGL(flash2_bwd_dq, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+        hipLaunchKernelGGL(flash2_bwd_dkdv, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
+    }
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
 }
