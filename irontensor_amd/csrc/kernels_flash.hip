@@ -272,11 +272,12 @@ __device__ __forceinline__ void grid_tile(int &tile, int64_t &bh) {
 // twice the waves, each with half the work per tile.
 constexpr int group_of(int wave8) { return wave8 >> 2; }
 
-// Group 1 hands `n` floats per lane to group 0 through LDS ([wave][n][lane], conflict-free); call
-// after the tile loop's final barrier, by every thread. Returns false for group 1 (done).
+// Group 1 hands `n` floats per lane to group 0 through LDS ([job][n][lane], conflict-free), each
+// wave at the slot of its 16-row job; call after the tile loop's final barrier, by every thread.
+// Returns false for group 1 (done).
 template <int N>
-__device__ __forceinline__ bool hand_over(char *smem, int grp, int wave, int lane, float (&v)[N]) {
-    float *x = (float *)smem + wave * N * 64 + lane;
+__device__ __forceinline__ bool hand_over(char *smem, int grp, int job, int lane, float (&v)[N]) {
+    float *x = (float *)smem + job * N * 64 + lane;
     if (grp == 1) {
 #pragma unroll
         for (int i = 0; i < N; ++i) x[i * 64] = v[i];
@@ -298,11 +299,30 @@ __global__ __launch_bounds__(NTH * WG) void flash_fwd(const FlashArgs p) {
     __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, grp = group_of(tid >> 6);
     const int ql = lane & 15, g = lane >> 4;
-    // Causal: the last query block sees every key block, so query blocks go out last-first.
-    int qb;
+    int x;
     int64_t bh;
-    grid_tile(qb, bh);
-    if (p.causal) qb = (int)gridDim.x - 1 - qb;
+    grid_tile(x, bh);
+    const int nq = (int)gridDim.x, kblocks = (p.skv + TR - 1) / TR;
+    // The block's 64 rows are four 16-row jobs: jobs 0-1 rows ra.., jobs 2-3 rows rz.. . Plain:
+    // one query block (causal: last-first, as the last query block sees every key block). Causal
+    // with two groups: rows 32h.. of query blocks i and nq - 1 - i (block x = 2i + h; the middle
+    // block of an odd count takes both halves of its own), and group 1's wave w takes job
+    // (w + 2) & 3, so each SIMD holds one wave of each query block: (i + 1 + nq - i) / 2 key tiles
+    // of work on every SIMD instead of up to nq.
+    const bool paired = WG == 2 && p.causal;
+    const int job = paired && grp == 1 ? (wave + 2) & 3 : wave;
+    int qa, qz, ra, rz;
+    if (paired && x < nq / 2 * 2) {
+        qa = x >> 1;
+        qz = nq - 1 - qa;
+        ra = qa * TR + (x & 1) * 32;
+        rz = qz * TR + (x & 1) * 32;
+    } else {
+        qa = qz = paired ? nq / 2 : (p.causal ? nq - 1 - x : x);
+        ra = qa * TR;
+        rz = ra + 32;
+    }
+    const int qb = job < 2 ? qa : qz;
     const Head hq{p.heads, p.q_bs, p.q_hs, p.q_rs}, hk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs},
         ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
     const T *Q = (const T *)p.Q + hq.base(bh);
@@ -310,7 +330,7 @@ __global__ __launch_bounds__(NTH * WG) void flash_fwd(const FlashArgs p) {
     const T *V = (const T *)p.V + hk.base(bh);
     float *O = (float *)p.O + ho.base(bh);
     const float c2 = p.scale * LOG2E;
-    const int q = qb * TR + wave * 16 + ql;  // this lane's query
+    const int q = (job < 2 ? ra : rz) + (job & 1) * 16 + ql;  // this lane's query
     const bool qok = q < p.sq;
 
     u32x4 qf[NC];
@@ -324,8 +344,8 @@ __global__ __launch_bounds__(NTH * WG) void flash_fwd(const FlashArgs p) {
     for (int d = 0; d < 4; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
 
-    const int kblocks = (p.skv + TR - 1) / TR;
-    const int nkb = p.causal ? min(kblocks, qb + 1) : kblocks;
+    const int nkb = p.causal ? min(kblocks, qb + 1) : kblocks;               // this wave's key blocks
+    const int nkb_all = p.causal ? min(kblocks, max(qa, qz) + 1) : kblocks;  // the block's
     TilePair<T, NTH * WG> tp;
     tp.tid = tid;
     tp.m[0] = K;  // K row-major
@@ -336,7 +356,8 @@ __global__ __launch_bounds__(NTH * WG) void flash_fwd(const FlashArgs p) {
     tp.off_cols[0] = -1;
     tp.off_rows[1] = -1;
     tp.off_cols[1] = KT;
-    pipelined(tp, smem, STAGE, 0, nkb, [&](int kb, const char *kt) {
+    pipelined(tp, smem, STAGE, 0, nkb_all, [&](int kb, const char *kt) {
+        if (kb >= nkb) return;  // past this wave's causal range (wave-uniform)
         const char *vt = kt + KT;
         // S^T blocks: keys 16mb + 4g + r of this tile (mb = grp * MBG + i), query q.
         f32x4 s[MBG];
@@ -404,7 +425,7 @@ __global__ __launch_bounds__(NTH * WG) void flash_fwd(const FlashArgs p) {
         float mine[18];
 #pragma unroll
         for (int i = 0; i < 18; ++i) mine[i] = v[i];
-        if (!hand_over<18>(smem, grp, wave, lane, v)) return;
+        if (!hand_over<18>(smem, grp, job, lane, v)) return;
         const float m1 = v[16], mn = fmaxf(m, m1), ms = mn == -INFINITY ? 0.f : mn;
         const float a0 = exp2_fast(m - ms), a1 = exp2_fast(m1 - ms);
 #pragma unroll
