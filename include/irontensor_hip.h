@@ -184,10 +184,13 @@ typedef struct it_gemm_call {
  * returned before anything is launched). No counterpart in the reference, whose CommandBatch
  * (src/command_batch.rs:166-181) gathers a step's dispatches into one command buffer but issues
  * each GEMM as its own dispatch; for callers holding several GEMMs at once (a layer's weight
- * gradients). When every call is a BF16 GEMM of batch 1 in one layout on whole 256 x 256 tiles
- * with a plain epilogue and their tiles fit one round of the GPU, they run as one launch with K
- * unsplit (results can differ in the last bits from separate calls that split K); otherwise each
- * runs exactly as it_gemm would. The outputs must not overlap each other's inputs. */
+ * gradients). Each run of consecutive calls of one layout can become one launch: BF16 GEMMs of
+ * batch 1 on whole 256 x 256 tiles with a plain epilogue whose tiles fit one round of the GPU run
+ * with K unsplit; FP32 GEMMs of batch 1 with a plain epilogue, N % 4 == 0, that it_gemm would run
+ * on 64 x 64 tiles run at one split count for the run and one grouped split-K sum, when that is
+ * priced below the separate calls. Grouped results can differ in the last bits from separate
+ * calls (another split of K); everything else runs exactly as it_gemm would. The outputs must not
+ * overlap each other's inputs. */
 it_status it_gemm_group(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, int count,
                         const it_gemm_call *calls);
 
