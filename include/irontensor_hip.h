@@ -329,7 +329,7 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
  *   - O and lse (the forward's outputs) are required, since the forward is not recomputed
  *     (IT_ERR_NULL otherwise);
  *   - its one workspace, two floats per query row (rowsum(dO * O) and the row's LSE in the form the
- *     dK/dV kernel reads; 8 bytes per row), lives in a static device array of
+ *     dK/dV part reads; 8 bytes per row), lives in a static device array of
  *     IT_NOALLOC_SCRATCH_BYTES (8 MiB) that each GPU the library runs on holds until the process
  *     ends, so bh * seq may be at most 1048576 rows (IT_ERR_DIMS otherwise, before any device work);
  *   - every call on a GPU shares that GPU's array: calls that overlap on one GPU (other streams or

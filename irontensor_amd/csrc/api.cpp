@@ -660,8 +660,8 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
                                   q_layout, kv_layout, o_layout, dO, Q, K, V, O, lse, dQ, dK, dV, &g, &f, &empty);
     if (st != IT_OK || empty) return st;
     const size_t rows = (size_t)bh * (size_t)seq;
-    // Workspace: when the forward is recomputed, O [rows, 64] and lse [rows]; then the two row arrays
-    // the dQ kernel leaves for the dK/dV kernel, dlt [2 rows].
+    // Workspace: when the forward is recomputed, O [rows, 64] and lse [rows]; then the row arrays
+    // the backward's row pass writes for its dQ + dK/dV kernel, dlt [2 rows].
     const size_t bytes = rows * 4 * (O ? 2 : 64 + 1 + 2);
     void *ws = nullptr;
     if ((st = it::ensure_attn_scratch(ctx, bytes, &ws)) != IT_OK) return st;
@@ -698,7 +698,7 @@ it_status it_flash_attention_backward_noalloc(it_context *ctx, it_dtype dtype, i
                                               float *dQ, float *dK, float *dV) {
     const char *op = "flash_attention_backward_noalloc";
     // The static workspace holds two floats per query row (rowsum(dO * O), and the LSE in the form
-    // the dK/dV kernel reads) for at most max_rows rows; checked first, so a call it cannot hold is
+    // the dK/dV part reads) for at most max_rows rows; checked first, so a call it cannot hold is
     // refused before anything else is looked at.
     const int64_t max_rows = (int64_t)(IT_NOALLOC_SCRATCH_BYTES / (2 * sizeof(float)));
     if (bh > 0 && seq > 0 && bh > max_rows / seq)
@@ -717,7 +717,7 @@ it_status it_flash_attention_backward_noalloc(it_context *ctx, it_dtype dtype, i
     if (!ws) return fail(IT_ERR_NO_DEVICE, std::string(op) + ": no static workspace on device " + i64(ctx->device));
     f.O = const_cast<float *>(O);
     f.lse = const_cast<float *>(lse);
-    f.dlt = (float *)ws;  // every row the dK/dV kernel reads is written first by the dQ kernel
+    f.dlt = (float *)ws;  // every row the backward reads is written first by its row pass
     return it::launch_flash_bwd(ctx->stream, f, dtype == IT_BF16);
 }
 

@@ -585,24 +585,13 @@ __device__ __forceinline__ void dkdv_block(const FlashArgs &p, int kb, int64_t b
     }
 }
 
-template <typename T, int WG>
-__global__ __launch_bounds__(NTH * WG) void flash_bwd_dkdv(const FlashArgs p) {
-    __shared__ __attribute__((aligned(16))) char smem[dkdv_lds<T>()];
-    // Causal: key block 0 is seen by every query block, so key blocks go out first-first.
-    int kb;
-    int64_t bh;
-    grid_tile(kb, bh);
-    dkdv_block<T, WG>(p, kb, bh, smem);
-}
 
 // dQ for 64 queries per block (16 per wave), looping over the key blocks they see. WG = 2: each
 // wave group takes half of every key tile's rows (see flash_fwd).
 template <typename T>
 constexpr int dq_lds() { return 2 * 3 * tile_bytes<T>(); }
 
-// DLT_IN: rowsum(dO * O) comes from p.dlt (written by flash_bwd_dlt); else computed here from the
-// dO fragments and written to p.dlt for the dK/dV kernel.
-template <typename T, int WG, bool DLT_IN>
+template <typename T, int WG>
 __device__ __forceinline__ void dq_block(const FlashArgs &p, int qb, int64_t bh, char *smem) {
     constexpr int T_ = tile_bytes<T>();
     constexpr int STAGE = 3 * T_;  // K, V, K^T
@@ -630,38 +619,8 @@ __device__ __forceinline__ void dq_block(const FlashArgs &p, int qb, int64_t bh,
         qf[c] = qok ? a : u32x4{0u, 0u, 0u, 0u};
         of[c] = qok ? b : u32x4{0u, 0u, 0u, 0u};
     }
-    // dlt[q] = rowsum(dO * O) for this block's queries, from the dO fragments just loaded: the 4
-    // lanes of a query hold 16 of its 64 columns each. Written for the dK/dV kernel, which runs
-    // after this one.
-    float dl = 0.f;
-    if constexpr (DLT_IN) {
-        dl = qok ? p.dlt[bh * p.sq + q] : 0.f;
-    } else {
-        const Head ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
-        const float *Orow = p.O + ho.base(bh) + (qok ? (int64_t)q * p.o_rs : 0);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            constexpr int V = FE<T>::VEC;
-            const int d0 = c * FE<T>::KC + g * V;
-#pragma unroll
-            for (int h = 0; h < V; h += 4) {
-                const f32x4 o = qok ? *(const f32x4 *)(Orow + d0 + h) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float gv;
-                    if constexpr (sizeof(T) == 4)
-                        gv = __uint_as_float(of[c][h + e]);
-                    else
-                        gv = __uint_as_float((h + e) & 1 ? of[c][(h + e) >> 1] & 0xffff0000u
-                                                         : of[c][(h + e) >> 1] << 16);
-                    dl += gv * o[e];
-                }
-            }
-        }
-        dl += __shfl_xor(dl, 16, 64);
-        dl += __shfl_xor(dl, 32, 64);
-        if (g == 0 && qok && grp == 0) p.dlt[bh * p.sq + q] = dl;
-    }
+    // rowsum(dO * O) of this query, written by flash_bwd_dlt.
+    const float dl = qok ? p.dlt[bh * p.sq + q] : 0.f;
     f32x4 dq[4];
 #pragma unroll
     for (int d = 0; d < 4; ++d) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -738,15 +697,6 @@ __device__ __forceinline__ void dq_block(const FlashArgs &p, int qb, int64_t bh,
     }
 }
 
-template <typename T, int WG>
-__global__ __launch_bounds__(NTH * WG) void flash_bwd_dq(const FlashArgs p) {
-    __shared__ __attribute__((aligned(16))) char smem[dq_lds<T>()];
-    int qb;
-    int64_t bh;
-    grid_tile(qb, bh);
-    if (p.causal) qb = (int)gridDim.x - 1 - qb;  // heaviest first
-    dq_block<T, WG, false>(p, qb, bh, smem);
-}
 
 // rowsum(dO * O) of every query row into p.dlt, 16 lanes per row (4 columns each), for
 // flash_bwd_fused, whose dK/dV part reads rows that other blocks' dQ parts cover.
@@ -781,7 +731,7 @@ __global__ __launch_bounds__(NTH * WG) void flash_bwd_fused(const FlashArgs p) {
     __shared__ __attribute__((aligned(16))) char smem[dkdv_lds<T>() > dq_lds<T>() ? dkdv_lds<T>() : dq_lds<T>()];
     const int j = (int)blockIdx.x;
     const int64_t bh = blockIdx.y;
-    dq_block<T, WG, true>(p, j, bh, smem);
+    dq_block<T, WG>(p, j, bh, smem);
     __syncthreads();  // the dQ part's last LDS reads (its hand-over) before the dK/dV part's writes
     dkdv_block<T, WG>(p, j, bh, smem);
 }
@@ -813,18 +763,11 @@ void fwd_launch(hipStream_t s, const FlashArgs &p, dim3 grid) {
 }
 
 template <typename T, int WG>
-void bwd_launch(hipStream_t s, const FlashArgs &p, int64_t qblocks, int64_t kblocks) {
-    if (qblocks == kblocks) {
-        // rowsum(dO * O) for every row first, then one kernel of balanced dQ + dK/dV blocks.
-        const int64_t rows = p.bh * p.sq;
-        hipLaunchKernelGGL(flash_bwd_dlt<T>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, p);
-        hipLaunchKernelGGL((flash_bwd_fused<T, WG>), dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH * WG), 0, s,
-                           p);
-        return;
-    }
-    // dQ first: it also computes dlt = rowsum(dO * O) for its queries, which dK/dV reads.
-    hipLaunchKernelGGL((flash_bwd_dq<T, WG>), dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH * WG), 0, s, p);
-    hipLaunchKernelGGL((flash_bwd_dkdv<T, WG>), dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH * WG), 0, s, p);
+void bwd_launch(hipStream_t s, const FlashArgs &p, int64_t blocks) {
+    // rowsum(dO * O) for every row first, then one kernel of balanced dQ + dK/dV blocks.
+    const int64_t rows = p.bh * p.sq;
+    hipLaunchKernelGGL(flash_bwd_dlt<T>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((flash_bwd_fused<T, WG>), dim3((unsigned)blocks, (unsigned)p.bh), dim3(NTH * WG), 0, s, p);
 }
 
 it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16) {
@@ -842,15 +785,16 @@ it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16) {
 }
 
 it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16) {
+    // The backward entry points take one sequence length for queries and keys.
+    if (p.sq != p.skv) return fail(IT_ERR_SHAPE, "flash attention backward: query and key lengths differ");
     if (bf16 && flash2_applicable(p, true)) return launch_flash2_bwd(s, p);
-    const int64_t qblocks = (p.sq + TR - 1) / TR, kblocks = (p.skv + TR - 1) / TR;
-    if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || p.bh > 65535)
-        return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
-    const bool split = std::max(qblocks, kblocks) * p.bh <= SPLIT_MAX_BLOCKS;
+    const int64_t blocks = (p.sq + TR - 1) / TR;
+    if (blocks > 0x7fffffff || p.bh > 65535) return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
+    const bool split = blocks * p.bh <= SPLIT_MAX_BLOCKS;
     if (bf16)
-        split ? bwd_launch<uint16_t, 2>(s, p, qblocks, kblocks) : bwd_launch<uint16_t, 1>(s, p, qblocks, kblocks);
+        split ? bwd_launch<uint16_t, 2>(s, p, blocks) : bwd_launch<uint16_t, 1>(s, p, blocks);
     else
-        split ? bwd_launch<float, 2>(s, p, qblocks, kblocks) : bwd_launch<float, 1>(s, p, qblocks, kblocks);
+        split ? bwd_launch<float, 2>(s, p, blocks) : bwd_launch<float, 1>(s, p, blocks);
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
 }

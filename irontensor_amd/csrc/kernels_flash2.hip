@@ -346,10 +346,8 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void f
 
 // ------------------------------------------------------------------ backward: dQ (and rowsum(dO * O))
 
-// One dQ block: query rows qb * RB .. + RB - 1 of head bh, LDS stages st0 and st1 of 2 TB bytes.
-// ROWS_IN: -rowsum(dO * O) and -LSE log2 e come from the workspace (written by flash2_bwd_rows);
-// else they are computed here and written there for the dK/dV kernel.
-template <bool ROWS_IN>
+// One dQ block: query rows qb * RB .. + RB - 1 of head bh, LDS stages st0 and st1 of 2 TB bytes;
+// -rowsum(dO * O) of its queries comes from the workspace (written by flash2_bwd_rows).
 __device__ __forceinline__ void dq2_block(const FlashArgs &p, int qb, int64_t bh, char *st0, char *st1) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -374,33 +372,9 @@ __device__ __forceinline__ void dq2_block(const FlashArgs &p, int qb, int64_t bh
         qf[ks] = qok ? a : u32x4{0u, 0u, 0u, 0u};
         of[ks] = qok ? b : u32x4{0u, 0u, 0u, 0u};
     }
-    // rowsum(dO * O) for this query from the dO fragments just loaded (the two lanes of a query hold
-    // 32 of its 64 d each). For the dK/dV kernel, which runs after this one, the workspace gets
-    // -rowsum at dlt[row] and -LSE log2 e at dlt[bh seq + row].
-    float dl = 0.f;
-    if constexpr (ROWS_IN) {
-        dl = qok ? -p.dlt[bh * p.sq + q] : 0.f;
-    } else {
-        const float *Orow = p.O + ho.base(bh) + (qok ? (int64_t)q * p.o_rs : 0);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-            for (int e4 = 0; e4 < 2; ++e4) {
-                const f32x4 ov = qok ? *(const f32x4 *)(Orow + 16 * ks + 8 * h + 4 * e4) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t w = of[ks][2 * e4 + (e >> 1)];
-                    const float gv = __uint_as_float(e & 1 ? w & 0xffff0000u : w << 16);
-                    dl += gv * ov[e];
-                }
-            }
-        dl += __shfl_xor(dl, 32, 64);
-    }
+    // rowsum(dO * O) of this query, stored negated by flash2_bwd_rows.
+    const float dl = qok ? -p.dlt[bh * p.sq + q] : 0.f;
     const float nl2 = qok ? -p.lse[bh * p.sq + q] * LOG2E : 0.f;
-    if (!ROWS_IN && h == 0 && qok) {
-        p.dlt[bh * p.sq + q] = -dl;
-        p.dlt[p.bh * p.sq + bh * p.sq + q] = nl2;
-    }
     // dP^T accumulates from -rowsum (the same for all 16 rows of a lane's column), so the MFMA
     // leaves dP - rowsum(dO * O) and dS = P (dP - rowsum) is one multiply.
     const float ndl = -dl;
@@ -463,15 +437,6 @@ __device__ __forceinline__ void dq2_block(const FlashArgs &p, int qb, int64_t bh
     }
 }
 
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_dq(const FlashArgs p) {
-    __shared__ __attribute__((aligned(1024))) char st0[2 * TB];  // K tile, V tile
-    __shared__ __attribute__((aligned(1024))) char st1[2 * TB];
-    int qb;
-    int64_t bh;
-    grid_tile(qb, bh);
-    if (p.causal) qb = (int)gridDim.x - 1 - qb;
-    dq2_block<false>(p, qb, bh, st0, st1);
-}
 
 // ------------------------------------------------------------------ backward: dK, dV
 
@@ -508,7 +473,7 @@ __device__ __forceinline__ void dkdv2_block(const FlashArgs &p, int kb, int64_t 
     Stream sq_, sd;
     sq_.init(Q, p.q_rs, p.sq, wave, lane);
     sd.init(dO, p.do_rs, p.sq, wave, lane);
-    RowStream rl, rd;  // rows the dQ kernel left in the workspace
+    RowStream rl, rd;  // rows flash2_bwd_rows left in the workspace
     rl.init(p.dlt + p.bh * p.sq + bh * p.sq, p.sq);
     rd.init(p.dlt + bh * p.sq, p.sq);
     stream_tiles(st0, st1, qblocks - qb0, [&](char *st, int t) {
@@ -591,14 +556,6 @@ __device__ __forceinline__ void dkdv2_block(const FlashArgs &p, int kb, int64_t 
     }
 }
 
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_dkdv(const FlashArgs p) {
-    __shared__ __attribute__((aligned(1024))) char st0[DKDV2_STAGE];
-    __shared__ __attribute__((aligned(1024))) char st1[DKDV2_STAGE];
-    int kb;
-    int64_t bh;
-    grid_tile(kb, bh);  // causal: key block 0 is seen by every query block, so it goes out first
-    dkdv2_block(p, kb, bh, st0, st1);
-}
 
 // The workspace rows of every query: -rowsum(dO * O) at dlt[row] and -LSE log2 e at
 // dlt[bh seq + row], 16 lanes per row (4 columns each), for flash2_bwd_fused.
@@ -629,7 +586,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void f
     int j;
     int64_t bh;
     grid_tile(j, bh);
-    dq2_block<true>(p, j, bh, st0, st1);
+    dq2_block(p, j, bh, st0, st1);
     __syncthreads();  // the dQ part's last LDS reads before the dK/dV part's first writes
     dkdv2_block(p, j, bh, st0, st1);
 }
@@ -654,19 +611,12 @@ it_status launch_flash2_fwd(hipStream_t s, const FlashArgs &p) {
 }
 
 it_status launch_flash2_bwd(hipStream_t s, const FlashArgs &p) {
-    const int64_t qblocks = (p.sq + RB - 1) / RB, kblocks = (p.skv + RB - 1) / RB;
-    if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || p.bh > 65535)
-        return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
-    if (qblocks == kblocks) {
-        // The workspace rows of every query first, then one kernel of balanced dQ + dK/dV blocks.
-        const int64_t rows = p.bh * p.sq;
-        hipLaunchKernelGGL(flash2_bwd_rows, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, p);
-        hipLaunchKernelGGL(flash2_bwd_fused, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
-    } else {
-        // dQ first: it also writes rowsum(dO * O), which the dK/dV kernel reads.
-        hipLaunchKernelGGL(flash2_bwd_dq, dim3((unsigned)qblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
-        hipLaunchKernelGGL(flash2_bwd_dkdv, dim3((unsigned)kblocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
-    }
+    const int64_t blocks = (p.sq + RB - 1) / RB;  // query blocks = key blocks (equal lengths)
+    if (blocks > 0x7fffffff || p.bh > 65535) return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
+    // The workspace rows of every query first, then one kernel of balanced dQ + dK/dV blocks.
+    const int64_t rows = p.bh * p.sq;
+    hipLaunchKernelGGL(flash2_bwd_rows, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(flash2_bwd_fused, dim3((unsigned)blocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
 }

@@ -1,6 +1,6 @@
 // Device-resident workspace for the entry point that allocates nothing,
-// it_flash_attention_backward_noalloc: the rowsum(dO * O) values its dQ kernel writes and its dK/dV
-// kernel reads (4 bytes per query row) live in `scratch`, a static device array of
+// it_flash_attention_backward_noalloc: the per-row values its row pass writes and its dQ + dK/dV
+// kernel reads (rowsum(dO * O), and for BF16 the row's LSE; 4 bytes each per query row) live in `scratch`, a static device array of
 // IT_NOALLOC_SCRATCH_BYTES. Every GPU the library runs on holds its own copy, at its own address,
 // until the process ends. In host code `scratch` names a host-side stand-in, not device memory, so
 // its device address is looked up once per device (it_init, with the device current) and only that
