@@ -2,10 +2,11 @@
 
 Workload: every contraction of one TINY training step, forward and backward,
 FP32 (4 layers, hidden 256, 4 heads x 64, SwiGLU FFN 688, untied vocab 16384, batch 16 x seq 256):
-115 dense-equivalent GEMMs = 195.82 GFLOP, issued by irontensor_amd.step.GemmStep as 51 GEMM
-launches (fused QKV and gate|up) plus the fused attention kernels (forward, and dK/dV + dQ
-backward, per layer), captured once into a HIP graph and replayed on one stream; each layer's four
-weight-gradient GEMMs run as one grouped launch (it_gemm_group). A "step" is one replay; inputs are
+115 dense-equivalent GEMMs = 195.82 GFLOP, issued by irontensor_amd.step.GemmStep as 51 GEMMs
+(fused QKV and gate|up) in 39 launches (each layer's four weight-gradient GEMMs as one grouped
+launch, it_gemm_group) plus the fused attention kernels (forward, and the one-kernel dQ + dK/dV
+backward after its row pass, per layer), captured once into a HIP graph and replayed on one
+stream. A "step" is one replay; inputs are
 resident in HBM before timing starts. The same step with the weight gradients on a second stream
 is timed beside it (config.ms_per_step_side_stream).
 
