@@ -1796,10 +1796,12 @@ bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int cou
         separate += t;
     }
     // The planner's model of the group at one split count s: 64 x 64 tiles, up to 4 blocks per CU.
+    // The XCD schedule takes at most count * s + 7 chunks (a chunk per GEMM and split, plus one
+    // more where an XCD's share ends inside one), so s stays where that fits the table.
     const double cu_peak = 157.3e12 / 256.0, eff0 = 0.60;
     double best_t = 1e30;
     int best_s = 0;
-    for (int s = 1; s <= 32; ++s) {
+    for (int s = 1; s <= 32 && count * s + 7 <= GROUP_CHUNKS; ++s) {
         int64_t blocks = 0, ksteps = 0;
         double traffic = 0.0;
         bool ok = true;

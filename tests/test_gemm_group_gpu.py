@@ -133,3 +133,27 @@ def test_group_fallbacks_equal_separate_calls(it):
     it.gemm_group([(a16, b16, o3, False, True), (a16, b16, o4, False, False)])
     assert np.array_equal(o3.numpy(), it.gemm(a16, b16, trans_b=True).numpy())
     assert np.array_equal(o4.numpy(), it.gemm(a16, b16).numpy())
+
+
+def test_group_f32_many_small_gemms_long_k(it):
+    """Eight FP32 TN GEMMs with few output tiles and K = 16384 (the group's split count is capped so
+    its per-XCD schedule fits the kernel arguments): one grouped launch, exact on small integers
+    (every element against float64), repeatable."""
+    k = 16384
+    shapes = [(64, 128), (128, 64), (64, 64), (192, 64), (64, 256), (128, 128), (64, 64), (256, 64)]
+    ops = []
+    for i, (m, n) in enumerate(shapes):
+        a, b = synth.small_ints(500 + i, (k, m), -2, 2), synth.small_ints(520 + i, (k, n), -2, 2)
+        ops.append((a, b, it.Tensor.from_f32_slice(a, a.shape), it.Tensor.from_f32_slice(b, b.shape),
+                    it.Tensor.zeros([m, n])))
+    calls = [(ta, tb, o, True, False) for _, _, ta, tb, o in ops]
+    keys = _keys(it, lambda: it.gemm_group(calls))
+    print(f"[group f32 long k] {keys}", flush=True)
+    assert len(keys) == 1 and "f32_TN_64x64_group" in keys[0], keys
+    first = [o.numpy() for *_, o in ops]
+    for (a, b, *_), got in zip(ops, first):
+        exact = a.T.astype(np.float64) @ b.astype(np.float64)
+        assert np.array_equal(got, exact.astype(np.float32)), got.shape
+    it.gemm_group(calls)
+    for (*_, o), f in zip(ops, first):
+        assert np.array_equal(o.numpy(), f)
