@@ -698,27 +698,33 @@ __device__ __forceinline__ void dq_block(const FlashArgs &p, int qb, int64_t bh,
 }
 
 
-// rowsum(dO * O) of every query row into p.dlt, 16 lanes per row (4 columns each), for
+// rowsum(dO * O) of every query row into p.dlt, 8 lanes per row (8 columns each), for
 // flash_bwd_fused, whose dK/dV part reads rows that other blocks' dQ parts cover.
 template <typename T>
 __global__ __launch_bounds__(256) void flash_bwd_dlt(const FlashArgs p) {
-    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int c = threadIdx.x & 15;
-    if (row >= p.bh * p.sq) return;  // whole 16-lane groups leave together
+    const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    const int c = threadIdx.x & 7;
+    if (row >= p.bh * p.sq) return;  // whole 8-lane groups leave together
     const int64_t bh = row / p.sq, q = row % p.sq;
     const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
-    const f32x4 o = *(const f32x4 *)(p.O + ho.base(bh) + q * p.o_rs + 4 * c);
-    f32x4 d;
+    const float *o = p.O + ho.base(bh) + q * p.o_rs + 8 * c;
+    const f32x4 o0 = *(const f32x4 *)o, o1 = *(const f32x4 *)(o + 4);
+    f32x4 d0, d1;
     if constexpr (sizeof(T) == 4) {
-        d = *(const f32x4 *)((const float *)p.dO + hd.base(bh) + q * p.do_rs + 4 * c);
+        const float *d = (const float *)p.dO + hd.base(bh) + q * p.do_rs + 8 * c;
+        d0 = *(const f32x4 *)d;
+        d1 = *(const f32x4 *)(d + 4);
     } else {
-        const u32x2 h = *(const u32x2 *)((const uint16_t *)p.dO + hd.base(bh) + q * p.do_rs + 4 * c);
-        d = f32x4{__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u), __uint_as_float(h[1] << 16),
-                  __uint_as_float(h[1] & 0xffff0000u)};
+        const u32x4 h = *(const u32x4 *)((const uint16_t *)p.dO + hd.base(bh) + q * p.do_rs + 8 * c);
+        d0 = f32x4{__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u), __uint_as_float(h[1] << 16),
+                   __uint_as_float(h[1] & 0xffff0000u)};
+        d1 = f32x4{__uint_as_float(h[2] << 16), __uint_as_float(h[2] & 0xffff0000u), __uint_as_float(h[3] << 16),
+                   __uint_as_float(h[3] & 0xffff0000u)};
     }
-    float s = d[0] * o[0] + d[1] * o[1] + d[2] * o[2] + d[3] * o[3];
+    float s = d0[0] * o0[0] + d0[1] * o0[1] + d0[2] * o0[2] + d0[3] * o0[3] + d1[0] * o1[0] + d1[1] * o1[1] +
+              d1[2] * o1[2] + d1[3] * o1[3];
 #pragma unroll
-    for (int w = 1; w < 16; w <<= 1) s += __shfl_xor(s, w, 64);
+    for (int w = 1; w < 8; w <<= 1) s += __shfl_xor(s, w, 64);
     if (c == 0) p.dlt[bh * p.sq + q] = s;
 }
 
@@ -766,7 +772,7 @@ template <typename T, int WG>
 void bwd_launch(hipStream_t s, const FlashArgs &p, int64_t blocks) {
     // rowsum(dO * O) for every row first, then one kernel of balanced dQ + dK/dV blocks.
     const int64_t rows = p.bh * p.sq;
-    hipLaunchKernelGGL(flash_bwd_dlt<T>, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(flash_bwd_dlt<T>, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, p);
     hipLaunchKernelGGL((flash_bwd_fused<T, WG>), dim3((unsigned)blocks, (unsigned)p.bh), dim3(NTH * WG), 0, s, p);
 }
 

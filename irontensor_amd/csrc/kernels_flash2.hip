@@ -558,19 +558,23 @@ __device__ __forceinline__ void dkdv2_block(const FlashArgs &p, int kb, int64_t 
 
 
 // The workspace rows of every query: -rowsum(dO * O) at dlt[row] and -LSE log2 e at
-// dlt[bh seq + row], 16 lanes per row (4 columns each), for flash2_bwd_fused.
+// dlt[bh seq + row], 8 lanes per row (8 columns each: 32 bytes of O, 16 of dO), for
+// flash2_bwd_fused.
 __global__ __launch_bounds__(256) void flash2_bwd_rows(const FlashArgs p) {
-    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int c = threadIdx.x & 15;
-    if (row >= p.bh * p.sq) return;  // whole 16-lane groups leave together
+    const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    const int c = threadIdx.x & 7;
+    if (row >= p.bh * p.sq) return;  // whole 8-lane groups leave together
     const int64_t bh = row / p.sq, q = row % p.sq;
     const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
-    const f32x4 o = *(const f32x4 *)(p.O + ho.base(bh) + q * p.o_rs + 4 * c);
-    const u32x2 g = *(const u32x2 *)((const uint16_t *)p.dO + hd.base(bh) + q * p.do_rs + 4 * c);
-    float s = __uint_as_float(g[0] << 16) * o[0] + __uint_as_float(g[0] & 0xffff0000u) * o[1] +
-              __uint_as_float(g[1] << 16) * o[2] + __uint_as_float(g[1] & 0xffff0000u) * o[3];
+    const float *o = p.O + ho.base(bh) + q * p.o_rs + 8 * c;
+    const f32x4 o0 = *(const f32x4 *)o, o1 = *(const f32x4 *)(o + 4);
+    const u32x4 g = *(const u32x4 *)((const uint16_t *)p.dO + hd.base(bh) + q * p.do_rs + 8 * c);
+    auto lo = [](uint32_t w) { return __uint_as_float(w << 16); };
+    auto hi = [](uint32_t w) { return __uint_as_float(w & 0xffff0000u); };
+    float s = lo(g[0]) * o0[0] + hi(g[0]) * o0[1] + lo(g[1]) * o0[2] + hi(g[1]) * o0[3] + lo(g[2]) * o1[0] +
+              hi(g[2]) * o1[1] + lo(g[3]) * o1[2] + hi(g[3]) * o1[3];
 #pragma unroll
-    for (int w = 1; w < 16; w <<= 1) s += __shfl_xor(s, w, 64);
+    for (int w = 1; w < 8; w <<= 1) s += __shfl_xor(s, w, 64);
     if (c == 0) {
         p.dlt[row] = -s;
         p.dlt[p.bh * p.sq + row] = -p.lse[row] * LOG2E;
@@ -615,7 +619,7 @@ it_status launch_flash2_bwd(hipStream_t s, const FlashArgs &p) {
     if (blocks > 0x7fffffff || p.bh > 65535) return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
     // The workspace rows of every query first, then one kernel of balanced dQ + dK/dV blocks.
     const int64_t rows = p.bh * p.sq;
-    hipLaunchKernelGGL(flash2_bwd_rows, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(flash2_bwd_rows, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s, p);
     hipLaunchKernelGGL(flash2_bwd_fused, dim3((unsigned)blocks, (unsigned)p.bh), dim3(NTH), 0, s, p);
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
