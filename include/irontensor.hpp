@@ -494,8 +494,9 @@ inline Tensor attention(const Tensor &q, const Tensor &k, const Tensor &v, bool 
     return out;
 }
 
-// ops::attention fused for head_dim 64 (no [seq, seq] buffers); same checks as attention().
-inline Tensor flash_attention(const Tensor &q, const Tensor &k, const Tensor &v, bool causal) {
+// ops::attention on [B,S,H,D], fused for head_dim 64 (no [seq, seq] buffers; other head_dim up to
+// 128 run the materialised contractions); same checks as attention().
+inline Tensor flash_attention_bshd(const Tensor &q, const Tensor &k, const Tensor &v, bool causal) {
     detail::require(q.is_f32() && k.is_f32() && v.is_f32(), "assertion `left == right` failed: attention requires FP32");
     detail::require(q.shape().size() == 4, "Q must be 4D [batch, seq, heads, dim]");
     detail::require(k.shape().size() == 4, "K must be 4D [batch, seq, heads, dim]");
@@ -514,6 +515,30 @@ inline Tensor flash_attention(const Tensor &q, const Tensor &k, const Tensor &v,
                                      (int64_t)skv, (int64_t)d, 1.f / std::sqrt((float)d), causal ? 1 : 0, &lq,
                                      &lkv, &lq, q.data(), k.data(), v.data(), (float *)out.data(), nullptr),
           "attention");
+    return out;
+}
+
+// flash_attention (src/ops/flash_attention.rs:76-193, re-exported at src/ops/mod.rs:36): attention
+// on [batch, heads, seq, head_dim] FP32 tensors of one shape, scale 1/sqrt(head_dim), head_dim <= 128;
+// same assertions and messages; zeros at seq 0. head_dim 64 runs the fused kernels, other sizes the
+// materialised contractions.
+inline Tensor flash_attention(const Tensor &q, const Tensor &k, const Tensor &v, bool causal) {
+    detail::require(q.is_f32(), "assertion `left == right` failed: Q must be FP32");
+    detail::require(k.is_f32(), "assertion `left == right` failed: K must be FP32");
+    detail::require(v.is_f32(), "assertion `left == right` failed: V must be FP32");
+    detail::require(q.shape().size() == 4, "Q must be 4D [batch, heads, seq, head_dim]");
+    detail::require(k.shape().size() == 4, "K must be 4D [batch, heads, seq, head_dim]");
+    detail::require(v.shape().size() == 4, "V must be 4D [batch, heads, seq, head_dim]");
+    detail::require(q.shape() == k.shape(), "Q and K must have same shape");
+    detail::require(q.shape() == v.shape(), "Q and V must have same shape");
+    const size_t b = q.shape()[0], h = q.shape()[1], s = q.shape()[2], d = q.shape()[3];
+    detail::require(d <= 128, "head_dim must be <= 128");
+    if (b * h * s * d == 0) return Tensor::zeros({b, h, s, d}, Precision::FP32);
+    Tensor out = Tensor::empty({b, h, s, d}, Precision::FP32);
+    check(it_flash_attention_forward(Context::global().handle(), IT_F32, (int64_t)(b * h), (int64_t)s, (int64_t)s,
+                                     (int64_t)d, 1.f / std::sqrt((float)d), causal ? 1 : 0, nullptr, nullptr,
+                                     nullptr, q.data(), k.data(), v.data(), (float *)out.data(), nullptr),
+          "flash_attention");
     return out;
 }
 

@@ -65,6 +65,10 @@ it_status it_malloc(it_context *ctx, size_t bytes, void **out_ptr);
 it_status it_free(it_context *ctx, void *ptr);
 /* Bytes currently handed out (gpu_memory_allocated, src/device.rs:43-71). */
 size_t it_mem_allocated(it_context *ctx);
+/* Bytes of library-owned scratch (split-K partial sums, attention workspaces), including blocks
+ * retired while graphs that may use them are alive (see it_graph_launch). The reference allocates
+ * per op and has no such pool. */
+size_t it_mem_scratch(it_context *ctx);
 /* Returns cached blocks to the device. */
 it_status it_empty_cache(it_context *ctx);
 
@@ -189,8 +193,9 @@ typedef struct it_gemm_call {
  * with K unsplit; FP32 GEMMs of batch 1 with a plain epilogue, N % 4 == 0, that it_gemm would run
  * on 64 x 64 tiles run at one split count for the run and one grouped split-K sum, when that is
  * priced below the separate calls. Grouped results can differ in the last bits from separate
- * calls (another split of K); everything else runs exactly as it_gemm would. The outputs must not
- * overlap each other's inputs. */
+ * calls (another split of K); everything else runs exactly as it_gemm would. No call's outputs
+ * (C, and gate_out / up_out of IT_EPI_SWIGLU) may overlap another call's operands or outputs, as
+ * byte ranges with the strides included (IT_ERR_INVALID otherwise, before anything is launched). */
 it_status it_gemm_group(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, int count,
                         const it_gemm_call *calls);
 
@@ -307,8 +312,18 @@ it_status it_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int
  * per key block and dQ per query block, without atomics, so results are deterministic.
  * IT_BF16 rounds P and dS to BF16 before their MFMA, as the materialised form stores them.
  *
- * Requires head_dim == 64 and 16-byte aligned operands whose strides are multiples of 16 bytes
- * (IT_ERR_DIMS otherwise); causal requires seq_q == seq_kv.
+ * head_dim 64 runs the fused kernels, which need 16-byte aligned operands whose strides are
+ * multiples of 16 bytes (IT_ERR_DIMS otherwise) and a finite scale > 0 (IT_ERR_INVALID).
+ * Any other head_dim up to 128 (the limit of src/ops/flash_attention.rs:98; IT_ERR_DIMS above it)
+ * runs the materialised contractions of it_attention_forward / it_attention_backward with their
+ * [BH, seq_q, seq_kv] buffers in library-owned scratch (2 * bh * seq_q * seq_kv * sizeof(f32) for
+ * the forward, twice that for the backward; grown once per shape, not during capture); there lse
+ * must be NULL, the backward's O and lse must be NULL (it always recomputes), and the forward
+ * needs seq_kv > 0. causal requires seq_q == seq_kv.
+ * The reference's flash_attention(q, k, v, causal) on [batch, heads, seq, head_dim] FP32 tensors
+ * (src/ops/flash_attention.rs:76-193, re-exported at src/ops/mod.rs:36) is
+ * it_flash_attention_forward(ctx, IT_F32, batch * heads, seq, seq, head_dim, 1 / sqrt(head_dim),
+ * causal, NULL, NULL, NULL, q, k, v, out, NULL).
  */
 it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
                                      int64_t seq_kv, int64_t head_dim, float scale, int causal,
@@ -479,8 +494,15 @@ typedef struct it_graph it_graph;
 it_status it_capture_begin(it_context *ctx);
 /* Ends the capture and instantiates the graph. */
 it_status it_capture_end(it_context *ctx, it_graph **out_graph);
-/* Replays the graph on the context's stream. */
+/* Replays the graph on the context's stream. A graph keeps the device addresses it was captured
+ * with: the caller's buffers must outlive it; the library's own scratch does (a scratch block that a
+ * later, larger eager call replaces is retired, not freed, while any graph of the context lives).
+ * Replays are asynchronous like other stream work (the reference's commit_async,
+ * src/command_batch.rs:228-272). */
 it_status it_graph_launch(it_context *ctx, it_graph *graph);
+/* Waits for the context's streams, then destroys the graph; when it was the context's last live
+ * graph, frees the scratch blocks retired meanwhile. A graph may also be destroyed after
+ * it_shutdown of its context. */
 it_status it_graph_destroy(it_graph *graph);
 
 /* ---------------------------------------------------------------- profiling (src/profile) */

@@ -7,7 +7,7 @@ from .errors import (DeviceError, EmptyTensor, InnerDimensionMismatch, InvalidVa
                      PrecisionMismatch, ShapeMismatch, TensorError, UnsupportedDimensions)
 from .tensor import Context, Precision, Tensor, bf16_to_f32, device_count, f32_to_bf16
 from .ops import (Linear, attention, attention_backward_recompute, attention_forward_bhsd,
-                  ensure_fp32, flash_attention, flash_attention_backward,
+                  ensure_fp32, flash_attention, flash_attention_backward, flash_attention_bshd,
                   flash_attention_forward_bhsd, gemm, gemm_group, linear, linear_backward, linear_forward, matmul,
                   matmul_backward, matmul_backward_a, matmul_backward_b, matmul_bf16,
                   matmul_bf16_batched, matmul_custom, matmul_mps, matmul_mps_nt, matmul_mps_tn,

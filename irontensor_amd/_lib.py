@@ -102,6 +102,7 @@ _SIGNATURES = {
     "it_malloc": (c_int, [c_void_p, C.c_size_t, C.POINTER(c_void_p)]),
     "it_free": (c_int, [c_void_p, c_void_p]),
     "it_mem_allocated": (C.c_size_t, [c_void_p]),
+    "it_mem_scratch": (C.c_size_t, [c_void_p]),
     "it_empty_cache": (c_int, [c_void_p]),
     "it_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_void_p, C.c_size_t]),
     "it_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_void_p, C.c_size_t]),

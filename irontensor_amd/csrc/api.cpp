@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "internal.hpp"
 
@@ -216,6 +217,50 @@ it_status it_gemm_group(it_context *ctx, it_dtype dtype_in, it_dtype dtype_out, 
                                            c.epi);
         if (st != IT_OK) return st;
     }
+    // One launch may run the calls concurrently: no call's outputs may touch another call's
+    // operands or outputs (byte ranges, strides included; broadcast operands count once).
+    struct Range {
+        uintptr_t lo, hi;
+    };
+    auto extent = [](const void *p, int64_t batch, int64_t stride, int64_t rows, int64_t ld, int64_t cols,
+                     int64_t eb) {
+        const uintptr_t lo = (uintptr_t)p;
+        return Range{lo, lo + (uintptr_t)(((batch - 1) * stride + (rows - 1) * ld + cols) * eb)};
+    };
+    const int64_t eb_in = dtype_in == IT_BF16 ? 2 : 4, eb_out = dtype_out == IT_BF16 ? 2 : 4;
+    std::vector<Range> outs[8], ins[8];
+    for (int i = 0; i < count; ++i) {
+        const it_gemm_call &c = calls[i];
+        if (c.M == 0 || c.N == 0 || c.batch == 0) continue;
+        const uint32_t fl = c.epi ? c.epi->flags : 0u;
+        const int64_t cols = (fl & IT_EPI_SWIGLU_BWD) ? 2 * c.N : c.N;
+        outs[i].push_back(extent(c.C, c.batch, c.strideC, c.M, c.ldc, cols, eb_out));
+        if ((fl & IT_EPI_SWIGLU) && c.epi->gate_out)
+            outs[i].push_back(extent(c.epi->gate_out, c.batch, c.strideC, c.M, c.ldc, c.N, eb_out));
+        if ((fl & IT_EPI_SWIGLU) && c.epi->up_out)
+            outs[i].push_back(extent(c.epi->up_out, c.batch, c.strideC, c.M, c.ldc, c.N, eb_out));
+        if (c.K > 0) {
+            const bool ta = c.transA == IT_OP_T, tb = c.transB == IT_OP_T;
+            ins[i].push_back(extent(c.A, c.batch, c.strideA, ta ? c.K : c.M, c.lda, ta ? c.M : c.K, eb_in));
+            ins[i].push_back(extent(c.B, c.batch, c.strideB, tb ? c.N : c.K, c.ldb, tb ? c.K : c.N, eb_in));
+            if ((fl & IT_EPI_SWIGLU) && c.epi->B2)
+                ins[i].push_back(extent(c.epi->B2, c.batch, c.strideB, tb ? c.N : c.K, c.ldb, tb ? c.K : c.N, eb_in));
+        }
+    }
+    for (int i = 0; i < count; ++i)
+        for (int j = 0; j < count; ++j) {
+            if (i == j) continue;
+            for (const Range &o : outs[i]) {
+                auto hit = [&](const std::vector<Range> &v) {
+                    for (const Range &r : v)
+                        if (o.lo < r.hi && r.lo < o.hi) return true;
+                    return false;
+                };
+                if (hit(ins[j]) || hit(outs[j]))
+                    return fail(IT_ERR_INVALID, "matmul group: the output of call " + i64(i) +
+                                                    " overlaps the operands or outputs of call " + i64(j));
+            }
+        }
     if (!ctx) return fail(IT_ERR_NULL, "matmul: ctx is NULL");
     // Empty GEMMs are skipped; the library groups the rest where it pays.
     it::GemmArgs args[8];
@@ -557,6 +602,28 @@ std::string flash_key(const char *what, bool bf16, const AttnGeom &g, int causal
            ",sq=" + i64(g.Sq) + ",skv=" + i64(g.Skv) + "]";
 }
 
+// The fused kernels hold a 64-wide head in registers. Other head sizes up to the reference flash
+// op's limit (src/ops/flash_attention.rs:98) run the materialised contractions, with their
+// [BH, Sq, Skv] score buffers in library-owned scratch.
+constexpr int64_t FLASH_MAX_HEAD_DIM = 128;
+
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+it_status flash_head_dim_ok(const char *op, int64_t head_dim) {
+    if (head_dim > FLASH_MAX_HEAD_DIM)
+        return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, head_dim must be <= " +
+                                     i64(FLASH_MAX_HEAD_DIM) + ", got " + i64(head_dim));
+    return IT_OK;
+}
+
+// Checks scale for the fused kernels: the BF16 forward takes each row's maximum of the unscaled
+// scores and scales it afterwards, which is the maximum of the scaled scores only for scale > 0.
+it_status flash_scale_ok(const char *op, float scale) {
+    if (!(scale > 0.f) || !std::isfinite(scale))
+        return fail(IT_ERR_INVALID, std::string(op) + ": scale must be finite and > 0, got " + std::to_string(scale));
+    return IT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -573,9 +640,26 @@ it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh
     if (causal && seq_q != seq_kv)
         return fail(IT_ERR_SHAPE, "flash_attention: shape mismatch, expected seq_q == seq_kv for causal, got " +
                                       i64(seq_q) + " and " + i64(seq_kv));
-    if (head_dim != 64)
-        return fail(IT_ERR_DIMS, "flash_attention: unsupported dimensions, head_dim must be 64, got " +
-                                     i64(head_dim));
+    if ((st = flash_head_dim_ok("flash_attention", head_dim)) != IT_OK) return st;
+    if (head_dim != 64) {
+        if (lse)
+            return fail(IT_ERR_DIMS, "flash_attention: unsupported dimensions, lse is written for head_dim 64 "
+                                     "only, got " + i64(head_dim));
+        if (bh == 0 || seq_q == 0 || head_dim == 0) return IT_OK;
+        if (seq_kv == 0)
+            return fail(IT_ERR_DIMS, "flash_attention: unsupported dimensions, seq_kv == 0 needs head_dim 64, got " +
+                                         i64(head_dim));
+        // Materialised: Sc [BH,Sq,Skv] f32 then P in dtype, both in scratch.
+        const size_t n = (size_t)bh * (size_t)seq_q * (size_t)seq_kv;
+        const size_t eb = dtype == IT_BF16 ? 2 : 4;
+        void *ws = nullptr;
+        if ((st = it::ensure_attn_scratch(ctx, round256(n * 4) + n * eb, &ws)) != IT_OK) return st;
+        float *sc = (float *)ws;
+        void *p = (char *)ws + round256(n * 4);
+        return it_attention_forward(ctx, dtype, bh, seq_q, seq_kv, head_dim, scale, causal, q_layout, kv_layout,
+                                    o_layout, Q, K, V, sc, p, O);
+    }
+    if ((st = flash_scale_ok("flash_attention", scale)) != IT_OK) return st;
     if (bh == 0 || seq_q == 0) return IT_OK;
     if (!Q || !O || (seq_kv > 0 && (!K || !V))) return fail(IT_ERR_NULL, "flash_attention: NULL buffer");
     it::FlashArgs f = flash_args(g, scale, causal);
@@ -617,6 +701,7 @@ it_status flash_bwd_args(const char *op, it_context *ctx, it_dtype dtype, int64_
     if (head_dim != 64)
         return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, head_dim must be 64, got " +
                                      i64(head_dim));
+    if ((st = flash_scale_ok(op, scale)) != IT_OK) return st;
     if ((O == nullptr) != (lse == nullptr))
         return fail(IT_ERR_INVALID, std::string(op) + ": pass both O and lse, or neither");
     if (bh == 0 || seq == 0) {
@@ -656,8 +741,29 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
     AttnGeom g;
     it::FlashArgs f;
     bool empty = false;
-    it_status st = flash_bwd_args("flash_attention_backward", ctx, dtype, bh, seq, head_dim, scale, causal,
-                                  q_layout, kv_layout, o_layout, dO, Q, K, V, O, lse, dQ, dK, dV, &g, &f, &empty);
+    it_status st;
+    if (head_dim != 64) {
+        const char *op = "flash_attention_backward";
+        if ((st = check_attention(op, ctx, dtype, bh, seq, seq, head_dim, q_layout, kv_layout, o_layout, &g)) != IT_OK)
+            return st;
+        if ((st = flash_head_dim_ok(op, head_dim)) != IT_OK) return st;
+        if (O || lse)
+            return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, O and lse are read for head_dim "
+                                                       "64 only (pass NULL to recompute), got " + i64(head_dim));
+        if (bh == 0 || seq == 0 || head_dim == 0) return IT_OK;
+        // Materialised recompute: Sc, dP f32 and P, dS in dtype, [BH, seq, seq] each, in scratch.
+        const size_t n = (size_t)bh * (size_t)seq * (size_t)seq;
+        const size_t eb = dtype == IT_BF16 ? 2 : 4;
+        const size_t f32b = round256(n * 4), lowb = round256(n * eb);
+        void *ws = nullptr;
+        if ((st = it::ensure_attn_scratch(ctx, 2 * f32b + 2 * lowb, &ws)) != IT_OK) return st;
+        char *base = (char *)ws;
+        return it_attention_backward(ctx, dtype, bh, seq, head_dim, scale, causal, q_layout, kv_layout, o_layout,
+                                     dO, Q, K, V, (float *)base, base + f32b, (float *)(base + f32b + lowb),
+                                     base + 2 * f32b + lowb, dQ, dK, dV);
+    }
+    st = flash_bwd_args("flash_attention_backward", ctx, dtype, bh, seq, head_dim, scale, causal,
+                        q_layout, kv_layout, o_layout, dO, Q, K, V, O, lse, dQ, dK, dV, &g, &f, &empty);
     if (st != IT_OK || empty) return st;
     const size_t rows = (size_t)bh * (size_t)seq;
     // Workspace: when the forward is recomputed, O [rows, 64] and lse [rows]; then the row arrays

@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <map>
 #include <mutex>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -65,6 +66,11 @@ struct it_context {
     size_t scratch_bytes[2] = {0, 0};
     void *attn_scratch[2] = {nullptr, nullptr};
     size_t attn_scratch_bytes[2] = {0, 0};
+    // Scratch blocks replaced by a larger one while graphs captured on this context were alive: a
+    // graph keeps the addresses it was captured with, so the old block stays allocated until the
+    // last such graph is destroyed (or the context shuts down).
+    std::vector<std::pair<void *, size_t>> retired;
+    std::set<it_graph *> graphs;  // graphs captured here and not yet destroyed
     // Arrival counters of kernels whose last block finishes a shared output (the decode kernel's
     // k splits), zeroed once at allocation; every launch leaves them zero.
     int *counters[2] = {nullptr, nullptr};
@@ -90,6 +96,7 @@ struct it_event {
 struct it_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    it_context *ctx = nullptr;  // the capturing context; NULL once it has shut down
 };
 
 namespace it {

@@ -273,12 +273,15 @@ __global__ __launch_bounds__(GK_THREADS) void gemv_bf16_kn(const GemmArgs p, int
     __syncthreads();
     int *cnt = counters + blockIdx.x * p.batch + b;
     if (tid == 0) {
-        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Release: the block's partial (stored by every wave before the barrier above) is visible
+        // at device scope before its arrival counts; acquire: the last block sees every partial.
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         last = old == p.splits - 1;
         if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last || !mine) return;
+    __atomic_thread_fence(__ATOMIC_ACQUIRE);  // ordered after thread 0's acquire by the barrier
     f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
     for (int sp = 0; sp < p.splits; ++sp) {
@@ -294,15 +297,6 @@ __global__ __launch_bounds__(GK_THREADS) void gemv_bf16_kn(const GemmArgs p, int
 
 int64_t gemv_kn_strips(const GemmArgs &a) { return (a.N + GK_STRIP - 1) / GK_STRIP; }
 
-bool gemv_kn_applicable(const GemmArgs &a, bool bf16, bool transA, bool transB) {
-    return bf16 && !transB && a.M >= 1 && a.M <= 16 && !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL &&
-           !a.swiglu_bwd && !a.xent_stats && !a.a_kscale && !a.rope_table && a.K % 32 == 0 && a.N % 8 == 0 &&
-           a.ldb % 8 == 0 && a.b_vec_ok && (transA || (a.a_vec_ok && a.lda % 8 == 0)) &&
-           gemv_kn_strips(a) * a.batch <= COUNTERS && a.batch * a.M * a.N <= (1ll << 24);
-}
-
-// (The partial sums stay under 2^31 bytes: batch * M * N <= 2^24 and at most 32 splits; the TN
-// form may need more splits for its LDS slice of X: K / 128 of them at most for M = 16.)
 // The fewest k splits the TN form's LDS slice of X allows.
 int gemv_kn_min_splits(const GemmArgs &a, bool transA) {
     int64_t ks = 1;
@@ -320,6 +314,16 @@ int gemv_kn_splits(const GemmArgs &a, bool transA) {
     ks = std::min<int64_t>({ks, std::max<int64_t>(1, a.K / 512), 32});
     while (ks > 1 && ks * a.batch > 65535) --ks;
     return (int)std::max<int64_t>(ks, gemv_kn_min_splits(a, transA));
+}
+
+// The partial sums are addressed with 32-bit byte offsets: splits * batch * M * N * 4 < 2^31 (the TN
+// form may need more than 32 splits for its LDS slice of X).
+bool gemv_kn_applicable(const GemmArgs &a, bool bf16, bool transA, bool transB) {
+    return bf16 && !transB && a.M >= 1 && a.M <= 16 && !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL &&
+           !a.swiglu_bwd && !a.xent_stats && !a.a_kscale && !a.rope_table && a.K % 32 == 0 && a.N % 8 == 0 &&
+           a.ldb % 8 == 0 && a.b_vec_ok && (transA || (a.a_vec_ok && a.lda % 8 == 0)) &&
+           gemv_kn_strips(a) * a.batch <= COUNTERS && a.batch * a.M * a.N <= (1ll << 24) &&
+           (int64_t)gemv_kn_splits(a, transA) * a.batch * a.M * a.N * 4 < (1ll << 31);
 }
 
 it_status launch_gemv_kn(hipStream_t s, bool transA, const GemmArgs &a, int *counters) {

@@ -50,8 +50,14 @@ static it_status grow(it_context *ctx, void *&buf, size_t &have, size_t bytes, v
                                         " bytes needed during graph capture: run the work once before capturing");
     if (have < bytes) {
         if (buf) {
-            if (const it_status st_ = sync_all(ctx); st_ != IT_OK) return st_;
-            IT_HIP_TRY(hipFree(buf));
+            if (!ctx->graphs.empty()) {
+                // A live graph may have been captured with this block: keep it until the last
+                // graph is destroyed.
+                ctx->retired.emplace_back(buf, have);
+            } else {
+                if (const it_status st_ = sync_all(ctx); st_ != IT_OK) return st_;
+                IT_HIP_TRY(hipFree(buf));
+            }
             buf = nullptr;
             have = 0;
         }
@@ -212,6 +218,8 @@ it_status it_shutdown(it_context *ctx) {
     for (auto &kv : ctx->cache) (void)hipFree(kv.second);
     for (auto &kv : ctx->live) (void)hipFree(kv.first);
     for (auto &kv : ctx->rope_tables) (void)hipFree(kv.second);
+    for (it_graph *g : ctx->graphs) g->ctx = nullptr;  // graphs may still be destroyed afterwards
+    for (auto &r : ctx->retired) (void)hipFree(r.first);
     for (int i = 0; i < 2; ++i) {
         if (ctx->scratch[i]) (void)hipFree(ctx->scratch[i]);
         if (ctx->attn_scratch[i]) (void)hipFree(ctx->attn_scratch[i]);
@@ -282,6 +290,14 @@ it_status it_free(it_context *ctx, void *ptr) {
 }
 
 size_t it_mem_allocated(it_context *ctx) { return ctx ? ctx->bytes_live : 0; }
+
+size_t it_mem_scratch(it_context *ctx) {
+    if (!ctx) return 0;
+    size_t total = 0;
+    for (int i = 0; i < 2; ++i) total += ctx->scratch_bytes[i] + ctx->attn_scratch_bytes[i];
+    for (auto &r : ctx->retired) total += r.second;
+    return total;
+}
 
 it_status it_empty_cache(it_context *ctx) {
     if (!ctx) return fail(IT_ERR_NULL, "it_empty_cache: ctx is NULL");
@@ -433,6 +449,8 @@ it_status it_capture_end(it_context *ctx, it_graph **out_graph) {
         delete g;
         return it::fail_hip(e, "hipStreamEndCapture/hipGraphInstantiate");
     }
+    g->ctx = ctx;
+    ctx->graphs.insert(g);
     *out_graph = g;
     return IT_OK;
 }
@@ -445,10 +463,22 @@ it_status it_graph_launch(it_context *ctx, it_graph *graph) {
 
 it_status it_graph_destroy(it_graph *graph) {
     if (!graph) return IT_OK;
+    it_context *ctx = graph->ctx;
+    it_status st = IT_OK;
+    if (ctx) {
+        // A replay may still be running: the graph's resources go once the streams have drained.
+        (void)hipSetDevice(ctx->device);
+        st = it::sync_all(ctx);
+        ctx->graphs.erase(graph);
+    }
     if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
     if (graph->graph) (void)hipGraphDestroy(graph->graph);
     delete graph;
-    return IT_OK;
+    if (ctx && ctx->graphs.empty() && st == IT_OK) {
+        for (auto &r : ctx->retired) (void)hipFree(r.first);
+        ctx->retired.clear();
+    }
+    return st;
 }
 
 it_status it_profiler_enable(it_context *ctx, int enable) {

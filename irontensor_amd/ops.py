@@ -464,9 +464,37 @@ def attention_backward_recompute(grad_output: Tensor, q: Tensor, k: Tensor, v: T
 
 
 def flash_attention(q: Tensor, k: Tensor, v: Tensor, causal: bool) -> Tensor:
-    """ops::attention (src/ops/attention.rs:286-377) on [B,S,H,D] FP32 tensors, fused for D = 64:
-    the scores never leave the chip (online softmax over 64-key blocks). Same checks and panics as
-    `attention`."""
+    """flash_attention (src/ops/flash_attention.rs:76-193, re-exported at src/ops/mod.rs:36 and
+    src/lib.rs:32): softmax(Q.K^T / sqrt(head_dim), causal).V on [batch, heads, seq, head_dim] FP32
+    tensors of one shape, head_dim <= 128, with the reference's assertions and messages; zeros at
+    seq 0. head_dim 64 runs the fused kernels (the scores never leave the chip); other head sizes
+    run the materialised contractions inside the same C entry point."""
+    for name, t in (("Q", q), ("K", k), ("V", v)):
+        if t.precision() is not _P.FP32:
+            raise Panic(f"assertion `left == right` failed: {name} must be FP32")
+    for name, t in (("Q", q), ("K", k), ("V", v)):
+        if len(t.shape()) != 4:
+            raise Panic(f"{name} must be 4D [batch, heads, seq, head_dim]")
+    if q.shape() != k.shape():
+        raise Panic("Q and K must have same shape")
+    if q.shape() != v.shape():
+        raise Panic("Q and V must have same shape")
+    b, h, s, d = q.shape()
+    if d > 128:
+        raise Panic("head_dim must be <= 128")
+    if b * h * s * d == 0:
+        return Tensor.zeros([b, h, s, d], _P.FP32, q.ctx)
+    out = Tensor.empty([b, h, s, d], _P.FP32, q.ctx)
+    check(q.ctx.lib.it_flash_attention_forward(q.ctx.handle, _lib.IT_F32, b * h, s, s, d, 1.0 / math.sqrt(d),
+                                               int(causal), None, None, None, _vp(q), _vp(k), _vp(v),
+                                               _vp(out), None), "flash_attention")
+    return out
+
+
+def flash_attention_bshd(q: Tensor, k: Tensor, v: Tensor, causal: bool) -> Tensor:
+    """ops::attention (src/ops/attention.rs:286-377) on [B,S,H,D] FP32 tensors through the fused entry
+    point: for D = 64 the scores never leave the chip (online softmax over 64-key blocks); other
+    D up to 128 run the materialised contractions. Same checks and panics as `attention`."""
     for t in (q, k, v):
         if t.precision() is not _P.FP32:
             raise Panic("assertion `left == right` failed: attention requires FP32")

@@ -200,8 +200,8 @@ static void gpu_tests() {
         const size_t b = 1, s = 70, h = 2, d = 64;
         std::vector<float> q(b * s * h * d, 0.0f), v(b * s * h * d);
         for (size_t i = 0; i < v.size(); ++i) v[i] = (float)((i * 37) % 101) * 0.01f - 0.5f;
-        auto o = flash_attention(Tensor::from_f32_slice(q, {b, s, h, d}), Tensor::from_f32_slice(v, {b, s, h, d}),
-                                 Tensor::from_f32_slice(v, {b, s, h, d}), true).as_f32_slice();
+        auto o = flash_attention_bshd(Tensor::from_f32_slice(q, {b, s, h, d}), Tensor::from_f32_slice(v, {b, s, h, d}),
+                                      Tensor::from_f32_slice(v, {b, s, h, d}), true).as_f32_slice();
         for (size_t r = 0; r < s; ++r)
             for (size_t hh = 0; hh < h; ++hh)
                 for (size_t c = 0; c < d; ++c) {
@@ -210,9 +210,32 @@ static void gpu_tests() {
                     mean /= (double)(r + 1);
                     CHECK(std::fabs(o[(r * h + hh) * d + c] - mean) < 1e-5);
                 }
-        Tensor small = Tensor::zeros({1, 4, 1, 32}, Precision::FP32);
-        expect_throw<InvalidValue>([&] { flash_attention(small, small, small, false); });
     });
+    // flash_attention (src/ops/flash_attention.rs:76-98) on [batch, heads, seq, head_dim]: Q = 0 gives
+    // causal prefix means of V at a fused (64) and a materialised (32) head size; its assertions.
+    for (size_t d : {size_t(64), size_t(32)})
+        run(("flash_attention_bhsd_d" + std::to_string(d)).c_str(), [d] {
+            const size_t b = 1, h = 2, s = 70;
+            std::vector<float> q(b * h * s * d, 0.0f), v(b * h * s * d);
+            for (size_t i = 0; i < v.size(); ++i) v[i] = (float)((i * 37) % 101) * 0.01f - 0.5f;
+            auto o = flash_attention(Tensor::from_f32_slice(q, {b, h, s, d}), Tensor::from_f32_slice(v, {b, h, s, d}),
+                                     Tensor::from_f32_slice(v, {b, h, s, d}), true).as_f32_slice();
+            for (size_t hh = 0; hh < h; ++hh)
+                for (size_t r = 0; r < s; ++r)
+                    for (size_t c = 0; c < d; ++c) {
+                        double mean = 0;
+                        for (size_t j = 0; j <= r; ++j) mean += v[(hh * s + j) * d + c];
+                        mean /= (double)(r + 1);
+                        CHECK(std::fabs(o[(hh * s + r) * d + c] - mean) < 1e-5);
+                    }
+            Tensor big = Tensor::zeros({1, 1, 4, 129}, Precision::FP32);
+            expect_throw<Panic>([&] { flash_attention(big, big, big, false); });
+            Tensor a = Tensor::zeros({1, 2, 4, d}, Precision::FP32), c = Tensor::zeros({1, 2, 5, d}, Precision::FP32);
+            expect_throw<Panic>([&] { flash_attention(a, c, a, false); });
+            auto z = flash_attention(Tensor::zeros({1, 2, 0, d}, Precision::FP32), Tensor::zeros({1, 2, 0, d}, Precision::FP32),
+                                     Tensor::zeros({1, 2, 0, d}, Precision::FP32), true);
+            CHECK(z.shape() == std::vector<size_t>({1, 2, 0, d}));
+        });
     run("flash_attention_backward_zero_grad", [] {  // dO = 0 gives dQ = dK = dV = 0 exactly
         const size_t b = 1, h = 2, n = 100, d = 64;
         std::vector<float> x(b * h * n * d);

@@ -115,8 +115,20 @@ def test_gemm_group_validates_every_call_first():
     bad = _lib.GemmCall(_lib.IT_OP_T, _lib.IT_OP_N, 4, 4, 4, 1.0, 16, 2, 0, 16, 4, 0, 0.0, 16, 4, 0, 1, None)
     st = lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 2, (_lib.GemmCall * 2)(good, bad))
     assert st == _lib.IT_ERR_INVALID and "lda" in _lib.last_error()
-    st = lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 2, (_lib.GemmCall * 2)(good, good))
+    other = _lib.GemmCall(_lib.IT_OP_T, _lib.IT_OP_N, 4, 4, 4, 1.0, 4096, 4, 0, 8192, 4, 0, 0.0, 12288, 4, 0, 1,
+                          None)
+    st = lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 2, (_lib.GemmCall * 2)(good, other))
     assert st == _lib.IT_ERR_NULL and "ctx" in _lib.last_error()
+    # One call's output may not overlap another call's operands or output (the group may run them
+    # in one launch): the same buffers twice, and an output that lands inside the next call's B.
+    st = lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 2, (_lib.GemmCall * 2)(good, good))
+    assert st == _lib.IT_ERR_INVALID and "overlaps" in _lib.last_error()
+    into_b = _lib.GemmCall(_lib.IT_OP_T, _lib.IT_OP_N, 4, 4, 4, 1.0, 4096, 4, 0, 8192, 4, 0, 0.0, 8200, 4, 0, 1, None)
+    st = lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 2, (_lib.GemmCall * 2)(other, into_b))
+    assert st == _lib.IT_ERR_INVALID and "call 1 overlaps the operands or outputs of call 0" in _lib.last_error()
+    st = lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 2, (_lib.GemmCall * 2)(other, _lib.GemmCall(
+        _lib.IT_OP_T, _lib.IT_OP_N, 4, 4, 4, 1.0, 4096, 4, 0, 8192, 4, 0, 0.0, 12288 + 64, 4, 0, 1, None)))
+    assert st == _lib.IT_ERR_NULL  # C ranges [12288, 12352) and [12352, 12416) only touch
     assert lib.it_gemm_group(None, _lib.IT_BF16, _lib.IT_F32, 0, None) == _lib.IT_ERR_NULL  # ctx checked last
 
 

@@ -57,6 +57,17 @@ def test_step_lm_head_gemms_against_oracle(it, oracle, step):
         chk.check_call(key)
 
 
+def test_tiny_every_gemm_plan(it, oracle, step):
+    """Every distinct GEMM of the TINY step at its step shape and in the plan
+    the step runs it with, on 64+ sampled output rows against the oracle's FP32 loop (normwise 1e-5):
+    the fused QKV projection with its RoPE epilogue input, Wo, the SwiGLU up-projection, down, the
+    four data gradients, the four weight gradients and the three LM-head GEMMs."""
+    chk = StepChecker(it, oracle, step, rows=64, log=lambda m: print(m, flush=True))
+    plans = {key: chk.check_call(key) for key in list(step._calls)}
+    print(f"[tiny] {len(plans)} distinct GEMMs, plans: {sorted(set(plans.values()))}", flush=True)
+    assert len(plans) == 15
+
+
 def test_step_graph_replay_matches_eager(it, step):
     names = ["logits", "dE", "dHf", "dQKV", "dX"]
     eager = {n: getattr(step, n).numpy() for n in names}

@@ -58,6 +58,32 @@ def test_train_step_matches_oracle(it, oracle, fused, xent):
         assert np.array_equal(m1.numpy(), rm)
 
 
+def test_train_step_tiny_matches_oracle(it, oracle):
+    """One complete TrainStep at the TINY shape (4 layers, H 256, 4 x 64,
+    F 688, vocab 16384, 16 x 256 tokens) against the oracle's step on the same parameters and batch:
+    loss within 1e-5 relative, every gradient within normwise 1e-4, the global norm within 1e-5.
+    The oracle step runs the restated reference loops on the host's threads (about 20 s)."""
+    from irontensor_amd.train import TrainStep
+    from oracle import train_step as ts
+    print("[case] TINY train step vs oracle", flush=True)
+    st = TrainStep(TINY, seed=9)
+    p0 = _oracle_params(st)
+    st.step()
+    it.Context.global_().sync()
+    loss, grads, _ = ts.gradients(p0, st.ids_host, st.targets_host, TINY)
+    print(f"[tiny step] loss {st.loss_value():.6f} oracle {loss:.6f}", flush=True)
+    assert abs(st.loss_value() - loss) <= 1e-5 * abs(loss)
+    worst = 0.0
+    for i, (g, r) in enumerate(zip(st.grads, ts.param_list(grads))):
+        err = normwise_rel(g.numpy(), r)
+        worst = max(worst, err)
+        assert err <= GRAD_TOL, i
+    ref_norm = float(np.sqrt(sum(float(np.sum(r.astype(np.float64) ** 2)) for r in ts.param_list(grads))))
+    norm, _ = st.norm_clip.numpy()
+    print(f"[tiny step] worst gradient normwise {worst:.2e}; norm {norm:.6f} oracle {ref_norm:.6f}", flush=True)
+    assert abs(norm - ref_norm) <= 1e-5 * ref_norm
+
+
 def test_train_step_graph_and_side_stream_bit_identical(it):
     """Two steps: eager on one stream vs eager then graph replay with the side stream."""
     from irontensor_amd.train import TrainStep

@@ -52,32 +52,40 @@ def test_noalloc_matches_existing_entry(it, prec):
             assert np.array_equal(g.numpy(), r.numpy()), (prec, b, h, s, "d" + name)
 
 
-def test_noalloc_under_graph_capture(it):
+@pytest.mark.parametrize("prec", ["bf16", "f32"])
+def test_noalloc_under_graph_capture(it, prec):
     """Captured without any eager call first (nothing to size, nothing allocated), replayed three
-    times with eager work between the replays; every replay equals the existing entry's result."""
+    times; between the replays an eager no-alloc call of another size writes other rows into the
+    same static array. Every replay equals the existing entry's result."""
     b, h, s = 4, 8, 384
-    q, k, v, do, o, lse = _inputs(it, "bf16", b, h, s, 760)
+    q, k, v, do, o, lse = _inputs(it, prec, b, h, s, 760)
     ref = [t.numpy() for t in it.flash_attention_backward(do, q, k, v, causal=True, scale=0.125, o=o, lse=lse)]
     got = [it.Tensor.empty([b, h, s, D]) for _ in range(3)]
     ctx = it.Context.global_()
     ctx.sync()
+    _log(f"[noalloc capture] {prec} b={b} h={h} s={s}")
     assert ctx.lib.it_capture_begin(ctx.handle) == 0
-    st = _noalloc(it, "bf16", q, k, v, do, o, lse, *got)
+    st = _noalloc(it, prec, q, k, v, do, o, lse, *got)
     graph = C.c_void_p()
     assert ctx.lib.it_capture_end(ctx.handle, C.byref(graph)) == 0, _lib.last_error()
     assert st == 0, _lib.last_error()
     try:
-        other = _inputs(it, "bf16", 2, 2, 130, 770)
+        other = _inputs(it, prec, 2, 2, 130, 770)
+        other_ref = [t.numpy() for t in it.flash_attention_backward(
+            other[3], *other[:3], causal=True, scale=0.125, o=other[4], lse=other[5])]
+        other_got = [it.Tensor.empty([2, 2, 130, D]) for _ in range(3)]
         for rep in range(3):
             for t in got:
                 t_zero = np.zeros(t.numel(), np.float32)
                 ctx.lib.it_memcpy_h2d(ctx.handle, C.c_void_p(t.ptr), t_zero.ctypes.data_as(C.c_void_p), t_zero.nbytes)
-            # eager work between replays, on the same static workspace
-            it.flash_attention_backward(*other[3:4], *other[:3], causal=True, scale=0.125, o=other[4], lse=other[5])
+            # an eager no-alloc call of another size between replays, on the same static array
+            assert _noalloc(it, prec, *other[:3], other[3], other[4], other[5], *other_got) == 0, _lib.last_error()
             assert ctx.lib.it_graph_launch(ctx.handle, graph) == 0
             ctx.sync()
             for name, g, r in zip("QKV", got, ref):
                 assert np.array_equal(g.numpy(), r), (rep, "d" + name)
+            for name, g, r in zip("QKV", other_got, other_ref):
+                assert np.array_equal(g.numpy(), r), (rep, "other d" + name)
     finally:
         ctx.lib.it_graph_destroy(graph)
 
