@@ -157,3 +157,30 @@ def test_group_f32_many_small_gemms_long_k(it):
     it.gemm_group(calls)
     for (*_, o), f in zip(ops, first):
         assert np.array_equal(o.numpy(), f)
+
+
+def test_group_f32_ragged(it, oracle):
+    """FP32 TN GEMMs with ragged edges (M and N not multiples of the 64 x 64 tile, K not a multiple
+    of the 32-wide k-tile): one grouped launch with bounds-checked loads; exact on small integers
+    (every element against float64), and on Gaussian data within the FP32 contract of the oracle."""
+    k = 4000
+    shapes = [(100, 68), (130, 200), (250, 60), (70, 36)]
+    ints, gauss = [], []
+    for i, (m, n) in enumerate(shapes):
+        a, b = synth.small_ints(600 + i, (k, m), -2, 2), synth.small_ints(610 + i, (k, n), -2, 2)
+        ints.append((a, b, it.Tensor.from_f32_slice(a, a.shape), it.Tensor.from_f32_slice(b, b.shape),
+                     it.Tensor.zeros([m, n])))
+        ga, gb = synth.normal(620 + i, (k, m)), synth.normal(630 + i, (k, n))
+        gauss.append((ga, gb, it.Tensor.from_f32_slice(ga, ga.shape), it.Tensor.from_f32_slice(gb, gb.shape),
+                      it.Tensor.zeros([m, n])))
+    calls = [(ta, tb, o, True, False) for _, _, ta, tb, o in ints]
+    keys = _keys(it, lambda: it.gemm_group(calls))
+    print(f"[group f32 ragged] {keys}", flush=True)
+    assert len(keys) == 1 and "f32_TN_64x64_group" in keys[0], keys
+    for a, b, *_, o in ints:
+        exact = a.T.astype(np.float64) @ b.astype(np.float64)
+        assert np.array_equal(o.numpy(), exact.astype(np.float32)), o.shape()
+    it.gemm_group([(ta, tb, o, True, False) for _, _, ta, tb, o in gauss])
+    for ga, gb, *_, o in gauss:
+        ref = oracle.gemm_f32(np.ascontiguousarray(ga.T), gb)
+        assert normwise_rel(o.numpy(), ref) <= FP32_TOL, o.shape()
