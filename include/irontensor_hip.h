@@ -336,6 +336,26 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
                                       const it_attn_layout *o_layout, const void *dO, const void *Q,
                                       const void *K, const void *V, const float *O, const float *lse,
                                       float *dQ, float *dK, float *dV);
+/*
+ * The two calls above with the output dtype chosen: out_dtype IT_F32 is them exactly; IT_BF16
+ * (BF16 operands and head_dim 64 only: IT_ERR_PRECISION / IT_ERR_DIMS otherwise) writes O, and dQ,
+ * dK, dV, as BF16 rounded to nearest even from the FP32 results, with the same element strides,
+ * and the backward then reads a BF16 O (16-byte aligned, strides multiples of 8 elements). lse
+ * stays FP32. This is the reference trainer's data path in BF16 mode, where the attention output
+ * feeds the output projection and dQ / dK / dV feed the Q/K/V projections' backward
+ * (src/train/forward.rs:138-146, src/train/backward.rs:100-147), without an FP32 round trip.
+ */
+it_status it_flash_attention_forward_ex(it_context *ctx, it_dtype dtype, it_dtype out_dtype, int64_t bh,
+                                        int64_t seq_q, int64_t seq_kv, int64_t head_dim, float scale, int causal,
+                                        const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                        const it_attn_layout *o_layout, const void *Q, const void *K,
+                                        const void *V, void *O, float *lse);
+it_status it_flash_attention_backward_ex(it_context *ctx, it_dtype dtype, it_dtype out_dtype, int64_t bh,
+                                         int64_t seq, int64_t head_dim, float scale, int causal,
+                                         const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                         const it_attn_layout *o_layout, const void *dO, const void *Q,
+                                         const void *K, const void *V, const void *O, const float *lse,
+                                         void *dQ, void *dK, void *dV);
 
 /*
  * it_flash_attention_backward without any device allocation. No counterpart in the reference: it is
@@ -514,6 +534,13 @@ it_status it_profiler_reset(it_context *ctx);
 /* Writes a JSON object {"<kernel>|<shape key>": {"calls": n, "total_ms": t}, ...} (syncs first).
  * Returns IT_ERR_INVALID with *needed set when buf_len is too small. */
 it_status it_profiler_report(it_context *ctx, char *buf, size_t buf_len, size_t *needed);
+/* The same launches as matmul statistics by shape, as Profiler::record_matmul_shape keys them
+ * (src/ops/mps_gemm.rs:22-30,421-422; src/profile/report.rs:198-230): a JSON object
+ * {"[4096,256]x[768,256]^T": {"count": n, "total_ms": t}, ...} over every GEMM launch, whatever
+ * its plan: A as stored, "[M,K]" or "[K,M]^T", then "x", then B as stored, "[K,N]" or "[N,K]^T".
+ * A grouped launch (it_gemm_group) counts once for each of its GEMMs, its time shared among them
+ * in proportion to their FLOPs. Same buffer protocol as it_profiler_report. */
+it_status it_profiler_report_shapes(it_context *ctx, char *buf, size_t buf_len, size_t *needed);
 
 #ifdef __cplusplus
 }

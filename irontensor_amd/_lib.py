@@ -145,6 +145,14 @@ _SIGNATURES = {
                                             C.POINTER(AttnLayout), C.POINTER(AttnLayout),
                                             C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "it_flash_attention_forward_ex": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_float, c_int,
+                                              C.POINTER(AttnLayout), C.POINTER(AttnLayout),
+                                              C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
+                                              c_void_p, c_void_p]),
+    "it_flash_attention_backward_ex": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_i64, c_float, c_int,
+                                               C.POINTER(AttnLayout), C.POINTER(AttnLayout),
+                                               C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
+                                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "it_flash_attention_backward_noalloc": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_float, c_int,
                                                     C.POINTER(AttnLayout), C.POINTER(AttnLayout),
                                                     C.POINTER(AttnLayout), c_void_p, c_void_p, c_void_p,
@@ -183,6 +191,7 @@ _SIGNATURES = {
     "it_profiler_enable": (c_int, [c_void_p, c_int]),
     "it_profiler_reset": (c_int, [c_void_p]),
     "it_profiler_report": (c_int, [c_void_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "it_profiler_report_shapes": (c_int, [c_void_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
 }
 
 _lib = None

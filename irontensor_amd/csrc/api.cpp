@@ -624,19 +624,40 @@ it_status flash_scale_ok(const char *op, float scale) {
     return IT_OK;
 }
 
+// Output dtype of the fused entry points: FP32, or BF16 from the BF16 fused kernels (BF16 operands,
+// head_dim 64).
+it_status flash_out_dtype_ok(const char *op, it_dtype dtype, it_dtype out_dtype, int64_t head_dim) {
+    if (out_dtype != IT_F32 && out_dtype != IT_BF16)
+        return fail(IT_ERR_PRECISION, std::string(op) + ": precision mismatch, expected FP32 or BF16 output, got " +
+                                          dtype_name(out_dtype));
+    if (out_dtype == IT_BF16 && dtype != IT_BF16)
+        return fail(IT_ERR_PRECISION, std::string(op) + ": precision mismatch, a BF16 output needs BF16 operands, got " +
+                                          dtype_name(dtype));
+    if (out_dtype == IT_BF16 && head_dim != 64)
+        return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, a BF16 output needs head_dim 64, got " +
+                                     i64(head_dim));
+    return IT_OK;
+}
+
+// A BF16 O is read 8 values (16 bytes) at a time by the backward's row pass.
+bool o16_ok(const void *O, const it_attn_layout &l) {
+    return (uintptr_t)O % 16 == 0 && l.batch_stride % 8 == 0 && l.head_stride % 8 == 0 && l.row_stride % 8 == 0;
+}
+
 }  // namespace
 
 extern "C" {
 
-it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
-                                     int64_t seq_kv, int64_t head_dim, float scale, int causal,
-                                     const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
-                                     const it_attn_layout *o_layout, const void *Q, const void *K,
-                                     const void *V, float *O, float *lse) {
+it_status it_flash_attention_forward_ex(it_context *ctx, it_dtype dtype, it_dtype out_dtype, int64_t bh,
+                                        int64_t seq_q, int64_t seq_kv, int64_t head_dim, float scale, int causal,
+                                        const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                        const it_attn_layout *o_layout, const void *Q, const void *K,
+                                        const void *V, void *O, float *lse) {
     AttnGeom g;
     it_status st = check_attention("flash_attention", ctx, dtype, bh, seq_q, seq_kv, head_dim, q_layout,
                                    kv_layout, o_layout, &g);
     if (st != IT_OK) return st;
+    if ((st = flash_out_dtype_ok("flash_attention", dtype, out_dtype, head_dim)) != IT_OK) return st;
     if (causal && seq_q != seq_kv)
         return fail(IT_ERR_SHAPE, "flash_attention: shape mismatch, expected seq_q == seq_kv for causal, got " +
                                       i64(seq_q) + " and " + i64(seq_kv));
@@ -657,7 +678,7 @@ it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh
         float *sc = (float *)ws;
         void *p = (char *)ws + round256(n * 4);
         return it_attention_forward(ctx, dtype, bh, seq_q, seq_kv, head_dim, scale, causal, q_layout, kv_layout,
-                                    o_layout, Q, K, V, sc, p, O);
+                                    o_layout, Q, K, V, sc, p, (float *)O);
     }
     if ((st = flash_scale_ok("flash_attention", scale)) != IT_OK) return st;
     if (bh == 0 || seq_q == 0) return IT_OK;
@@ -669,8 +690,9 @@ it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh
     f.V = seq_kv > 0 ? V : Q;
     f.O = O;
     f.lse = lse;
+    f.o_bf16 = out_dtype == IT_BF16;
     const int eb = dtype == IT_BF16 ? 2 : 4;
-    if (!it::flash_supported(f, eb, false))
+    if (!it::flash_supported(f, eb, false) || (f.o_bf16 && !o16_ok(O, g.o_lay)))
         return fail(IT_ERR_DIMS, "flash_attention: unsupported dimensions, operands must be 16-byte aligned "
                                  "with strides that are multiples of 16 bytes");
     hipEvent_t ev = nullptr;
@@ -684,20 +706,30 @@ it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh
     return st;
 }
 
+it_status it_flash_attention_forward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq_q,
+                                     int64_t seq_kv, int64_t head_dim, float scale, int causal,
+                                     const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                     const it_attn_layout *o_layout, const void *Q, const void *K,
+                                     const void *V, float *O, float *lse) {
+    return it_flash_attention_forward_ex(ctx, dtype, IT_F32, bh, seq_q, seq_kv, head_dim, scale, causal, q_layout,
+                                         kv_layout, o_layout, Q, K, V, O, lse);
+}
+
 }  // extern "C"
 
 namespace {
 
 // Validates a fused-backward call and fills its kernel arguments (everything but O, lse and dlt).
 // *empty is set when there is nothing to compute.
-it_status flash_bwd_args(const char *op, it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
-                         int64_t head_dim, float scale, int causal, const it_attn_layout *q_layout,
+it_status flash_bwd_args(const char *op, it_context *ctx, it_dtype dtype, it_dtype out_dtype, int64_t bh,
+                         int64_t seq, int64_t head_dim, float scale, int causal, const it_attn_layout *q_layout,
                          const it_attn_layout *kv_layout, const it_attn_layout *o_layout, const void *dO,
-                         const void *Q, const void *K, const void *V, const float *O, const float *lse, float *dQ,
-                         float *dK, float *dV, AttnGeom *g, it::FlashArgs *f, bool *empty) {
+                         const void *Q, const void *K, const void *V, const void *O, const float *lse, void *dQ,
+                         void *dK, void *dV, AttnGeom *g, it::FlashArgs *f, bool *empty) {
     *empty = false;
     it_status st = check_attention(op, ctx, dtype, bh, seq, seq, head_dim, q_layout, kv_layout, o_layout, g);
     if (st != IT_OK) return st;
+    if ((st = flash_out_dtype_ok(op, dtype, out_dtype, head_dim)) != IT_OK) return st;
     if (head_dim != 64)
         return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, head_dim must be 64, got " +
                                      i64(head_dim));
@@ -717,14 +749,17 @@ it_status flash_bwd_args(const char *op, it_context *ctx, it_dtype dtype, int64_
     f->dQ = dQ;
     f->dK = dK;
     f->dV = dV;
+    f->grad_bf16 = out_dtype == IT_BF16;
+    f->o_bf16 = O && out_dtype == IT_BF16;
     const int eb = dtype == IT_BF16 ? 2 : 4;
     if (!it::flash_supported(*f, eb, true))
         return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, operands must be 16-byte "
                                                    "aligned with strides that are multiples of 16 bytes");
-    if (O && ((uintptr_t)O % 16 != 0 || g->o_lay.batch_stride % 4 || g->o_lay.head_stride % 4 ||
-              g->o_lay.row_stride % 4))
+    if (O && (f->o_bf16 ? !o16_ok(O, g->o_lay)
+                        : ((uintptr_t)O % 16 != 0 || g->o_lay.batch_stride % 4 || g->o_lay.head_stride % 4 ||
+                           g->o_lay.row_stride % 4)))
         return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, O must be 16-byte aligned "
-                                                   "with strides that are multiples of 4");
+                                                   "with strides that are multiples of 16 bytes");
     return IT_OK;
 }
 
@@ -732,12 +767,12 @@ it_status flash_bwd_args(const char *op, it_context *ctx, it_dtype dtype, int64_
 
 extern "C" {
 
-it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
-                                      int64_t head_dim, float scale, int causal,
-                                      const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
-                                      const it_attn_layout *o_layout, const void *dO, const void *Q,
-                                      const void *K, const void *V, const float *O, const float *lse,
-                                      float *dQ, float *dK, float *dV) {
+it_status it_flash_attention_backward_ex(it_context *ctx, it_dtype dtype, it_dtype out_dtype, int64_t bh,
+                                         int64_t seq, int64_t head_dim, float scale, int causal,
+                                         const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                         const it_attn_layout *o_layout, const void *dO, const void *Q,
+                                         const void *K, const void *V, const void *O, const float *lse,
+                                         void *dQ, void *dK, void *dV) {
     AttnGeom g;
     it::FlashArgs f;
     bool empty = false;
@@ -746,6 +781,7 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
         const char *op = "flash_attention_backward";
         if ((st = check_attention(op, ctx, dtype, bh, seq, seq, head_dim, q_layout, kv_layout, o_layout, &g)) != IT_OK)
             return st;
+        if ((st = flash_out_dtype_ok(op, dtype, out_dtype, head_dim)) != IT_OK) return st;
         if ((st = flash_head_dim_ok(op, head_dim)) != IT_OK) return st;
         if (O || lse)
             return fail(IT_ERR_DIMS, std::string(op) + ": unsupported dimensions, O and lse are read for head_dim "
@@ -760,9 +796,9 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
         char *base = (char *)ws;
         return it_attention_backward(ctx, dtype, bh, seq, head_dim, scale, causal, q_layout, kv_layout, o_layout,
                                      dO, Q, K, V, (float *)base, base + f32b, (float *)(base + f32b + lowb),
-                                     base + 2 * f32b + lowb, dQ, dK, dV);
+                                     base + 2 * f32b + lowb, (float *)dQ, (float *)dK, (float *)dV);
     }
-    st = flash_bwd_args("flash_attention_backward", ctx, dtype, bh, seq, head_dim, scale, causal,
+    st = flash_bwd_args("flash_attention_backward", ctx, dtype, out_dtype, bh, seq, head_dim, scale, causal,
                         q_layout, kv_layout, o_layout, dO, Q, K, V, O, lse, dQ, dK, dV, &g, &f, &empty);
     if (st != IT_OK || empty) return st;
     const size_t rows = (size_t)bh * (size_t)seq;
@@ -780,11 +816,11 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
         it::profile_begin(ctx, key, &ev);
     }
     if (O) {
-        f.O = const_cast<float *>(O);
+        f.O = const_cast<void *>(O);
         f.lse = const_cast<float *>(lse);
     } else {
-        f.O = (float *)ws;  // 256-byte aligned, so its float4 stores are aligned
-        f.lse = f.O + rows * 64;
+        f.O = ws;  // 256-byte aligned, so its float4 stores are aligned; f32 (o_bf16 is 0)
+        f.lse = (float *)ws + rows * 64;
         // Recomputed O is [bh, seq, 64] contiguous.
         f.o_bs = f.heads * seq * 64;
         f.o_hs = seq * 64;
@@ -794,6 +830,16 @@ it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t b
     if (st == IT_OK) st = it::launch_flash_bwd(ctx->stream, f, bf16);
     if (ctx->profiling) it::profile_end(ctx, key, ev);
     return st;
+}
+
+it_status it_flash_attention_backward(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
+                                      int64_t head_dim, float scale, int causal,
+                                      const it_attn_layout *q_layout, const it_attn_layout *kv_layout,
+                                      const it_attn_layout *o_layout, const void *dO, const void *Q,
+                                      const void *K, const void *V, const float *O, const float *lse,
+                                      float *dQ, float *dK, float *dV) {
+    return it_flash_attention_backward_ex(ctx, dtype, IT_F32, bh, seq, head_dim, scale, causal, q_layout, kv_layout,
+                                          o_layout, dO, Q, K, V, O, lse, dQ, dK, dV);
 }
 
 it_status it_flash_attention_backward_noalloc(it_context *ctx, it_dtype dtype, int64_t bh, int64_t seq,
@@ -816,8 +862,8 @@ it_status it_flash_attention_backward_noalloc(it_context *ctx, it_dtype dtype, i
     AttnGeom g;
     it::FlashArgs f;
     bool empty = false;
-    it_status st = flash_bwd_args(op, ctx, dtype, bh, seq, head_dim, scale, causal, q_layout, kv_layout, o_layout,
-                                  dO, Q, K, V, O, lse, dQ, dK, dV, &g, &f, &empty);
+    it_status st = flash_bwd_args(op, ctx, dtype, IT_F32, bh, seq, head_dim, scale, causal, q_layout, kv_layout,
+                                  o_layout, dO, Q, K, V, O, lse, dQ, dK, dV, &g, &f, &empty);
     if (st != IT_OK || empty) return st;
     void *ws = it::noalloc_scratch(ctx->device);
     if (!ws) return fail(IT_ERR_NO_DEVICE, std::string(op) + ": no static workspace on device " + i64(ctx->device));

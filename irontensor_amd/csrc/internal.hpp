@@ -197,11 +197,12 @@ it_status launch_gemm_group(it_context *ctx, it_dtype dtype_in, const bool *ta, 
 // (bh / heads) * bs + (bh % heads) * hs + row * rs + col (element strides).
 struct FlashArgs {
     const void *Q, *K, *V, *dO;  // operand dtype
-    float *O;                    // forward output / backward input (f32)
+    void *O;                     // forward output / backward input (f32, or BF16 with o_bf16)
     float *lse, *dlt;            // [bh][sq] row log-sum-exp; dlt: workspace of 2 [bh][sq] row arrays
                                  // (FP32 kernels: rowsum(dO * O) in the first; BF16 kernels:
                                  // -rowsum(dO * O), then -LSE log2 e)
-    float *dQ, *dK, *dV;         // f32 gradients
+    void *dQ, *dK, *dV;          // gradients (f32, or BF16 with grad_bf16)
+    int o_bf16, grad_bf16;       // BF16 O / gradients (RNE): the BF16 (flash2) kernels only
     int64_t bh, sq, skv, head_dim, heads;
     int64_t q_bs, q_hs, q_rs;     // Q and dQ
     int64_t kv_bs, kv_hs, kv_rs;  // K, V, dK, dV

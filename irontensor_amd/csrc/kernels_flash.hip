@@ -572,7 +572,7 @@ __device__ __forceinline__ void dkdv_block(const FlashArgs &p, int kb, int64_t b
     }
     // Lane l holds rows (keys) 16*wave + 4g + r and column d = 16n + l%16.
     const Head hdk{p.heads, p.kv_bs, p.kv_hs, p.kv_rs};
-    float *dK = p.dK + hdk.base(bh), *dV = p.dV + hdk.base(bh);
+    float *dK = (float *)p.dK + hdk.base(bh), *dV = (float *)p.dV + hdk.base(bh);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int k = kb * TR + wave * 16 + g * 4 + r;
@@ -691,7 +691,7 @@ __device__ __forceinline__ void dq_block(const FlashArgs &p, int qb, int64_t bh,
             for (int r = 0; r < 4; ++r) dq[d][r] += v[d * 4 + r];
     }
     if (qok) {
-        float *dQ = p.dQ + hq.base(bh) + (int64_t)q * p.q_rs;
+        float *dQ = (float *)p.dQ + hq.base(bh) + (int64_t)q * p.q_rs;
 #pragma unroll
         for (int d = 0; d < 4; ++d) *(f32x4 *)(dQ + d * 16 + g * 4) = dq[d] * p.scale;
     }
@@ -707,7 +707,7 @@ __global__ __launch_bounds__(256) void flash_bwd_dlt(const FlashArgs p) {
     if (row >= p.bh * p.sq) return;  // whole 8-lane groups leave together
     const int64_t bh = row / p.sq, q = row % p.sq;
     const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
-    const float *o = p.O + ho.base(bh) + q * p.o_rs + 8 * c;
+    const float *o = (const float *)p.O + ho.base(bh) + q * p.o_rs + 8 * c;
     const f32x4 o0 = *(const f32x4 *)o, o1 = *(const f32x4 *)(o + 4);
     f32x4 d0, d1;
     if constexpr (sizeof(T) == 4) {
@@ -778,6 +778,7 @@ void bwd_launch(hipStream_t s, const FlashArgs &p, int64_t blocks) {
 
 it_status launch_flash_fwd(hipStream_t s, const FlashArgs &p, bool bf16) {
     if (bf16 && flash2_applicable(p, false)) return launch_flash2_fwd(s, p);
+    if (p.o_bf16) return fail(IT_ERR_DIMS, "flash attention: a BF16 O needs the BF16 kernels' 2 GiB row limits");
     const int64_t qblocks = (p.sq + TR - 1) / TR;
     if (qblocks > 0x7fffffff || p.bh > 65535) return fail(IT_ERR_DIMS, "flash attention: grid too large");
     const dim3 grid((unsigned)qblocks, (unsigned)p.bh);
@@ -794,6 +795,8 @@ it_status launch_flash_bwd(hipStream_t s, const FlashArgs &p, bool bf16) {
     // The backward entry points take one sequence length for queries and keys.
     if (p.sq != p.skv) return fail(IT_ERR_SHAPE, "flash attention backward: query and key lengths differ");
     if (bf16 && flash2_applicable(p, true)) return launch_flash2_bwd(s, p);
+    if (p.o_bf16 || p.grad_bf16)
+        return fail(IT_ERR_DIMS, "flash attention backward: BF16 O or gradients need the BF16 kernels' 2 GiB row limits");
     const int64_t blocks = (p.sq + TR - 1) / TR;
     if (blocks > 0x7fffffff || p.bh > 65535) return fail(IT_ERR_DIMS, "flash attention backward: grid too large");
     const bool split = blocks * p.bh <= SPLIT_MAX_BLOCKS;

@@ -21,7 +21,9 @@
 //     exp2(s * scale * log2 e - m) (one FMA and one v_exp_f32 each), and the output is rescaled only
 //     when the running max grows by more than 8 (log2 units: probabilities then stay below 2^8 and
 //     the final division by the row sum cancels the factor); P is rounded to BF16 before its MFMA.
-// The backward is deterministic (dQ and dK/dV from two kernels, no atomics).
+// The backward is deterministic (dQ and dK/dV from two kernels, no atomics). O (written by the
+// forward, read by the backward's row pass) and dQ, dK, dV are FP32, or BF16 (round to nearest
+// even) when the caller asks for BF16 outputs.
 #include <cmath>
 
 #include "internal.hpp"
@@ -181,6 +183,14 @@ struct Head {
 
 __device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
 
+// Four consecutive output values at element `idx` of an f32 or (bf16: RNE) BF16 array.
+__device__ __forceinline__ void store4(void *base, int64_t idx, f32x4 v, int bf16) {
+    if (bf16)
+        *(u32x2 *)((uint16_t *)base + idx) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    else
+        *(f32x4 *)((float *)base + idx) = v;
+}
+
 // Workgroup (x, y) takes tile lin / heads-count of head lin % heads-count, lin = y * gridDim.x + x,
 // so the first workgroups dispatched hold the costliest causal tile of every head.
 __device__ __forceinline__ void grid_tile(int &tile, int64_t &bh) {
@@ -332,14 +342,14 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void f
     const float l = o[2][0] + __shfl_xor(o[2][0], 32, 64);
     if (qok) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
-        float *O = (float *)p.O + ho.base(bh) + (int64_t)q * p.o_rs;
+        const int64_t orow = ho.base(bh) + (int64_t)q * p.o_rs;
         // o[dh][j]: d = 32dh + 8 (j / 4) + 4h + j % 4
 #pragma unroll
         for (int dh = 0; dh < 2; ++dh)
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj)
-                *(f32x4 *)(O + 32 * dh + 8 * jj + 4 * h) =
-                    f32x4{o[dh][4 * jj], o[dh][4 * jj + 1], o[dh][4 * jj + 2], o[dh][4 * jj + 3]} * inv;
+                store4(p.O, orow + 32 * dh + 8 * jj + 4 * h,
+                       f32x4{o[dh][4 * jj], o[dh][4 * jj + 1], o[dh][4 * jj + 2], o[dh][4 * jj + 3]} * inv, p.o_bf16);
         if (h == 0 && p.lse) p.lse[bh * p.sq + q] = (m + __log2f(l)) * LN2;  // natural-log LSE
     }
 }
@@ -427,13 +437,14 @@ __device__ __forceinline__ void dq2_block(const FlashArgs &p, int qb, int64_t bh
             for (int c = 0; c < 4; ++c) dq[dh] = mfma32(frag_tr(kt, 32 * dh, 16 * c, lane), df[c], dq[dh]);
     });
     if (qok) {
-        float *dQ = p.dQ + hq.base(bh) + (int64_t)q * p.q_rs;
+        const int64_t row = hq.base(bh) + (int64_t)q * p.q_rs;
 #pragma unroll
         for (int dh = 0; dh < 2; ++dh)
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj)
-                *(f32x4 *)(dQ + 32 * dh + 8 * jj + 4 * h) =
-                    f32x4{dq[dh][4 * jj], dq[dh][4 * jj + 1], dq[dh][4 * jj + 2], dq[dh][4 * jj + 3]} * p.scale;
+                store4(p.dQ, row + 32 * dh + 8 * jj + 4 * h,
+                       f32x4{dq[dh][4 * jj], dq[dh][4 * jj + 1], dq[dh][4 * jj + 2], dq[dh][4 * jj + 3]} * p.scale,
+                       p.grad_bf16);
     }
 }
 
@@ -542,16 +553,17 @@ __device__ __forceinline__ void dkdv2_block(const FlashArgs &p, int kb, int64_t 
         }
     });
     if (kok) {
-        float *dK = p.dK + hk.base(bh) + (int64_t)key * p.kv_rs;
-        float *dV = p.dV + hk.base(bh) + (int64_t)key * p.kv_rs;
+        const int64_t row = hk.base(bh) + (int64_t)key * p.kv_rs;
 #pragma unroll
         for (int dh = 0; dh < 2; ++dh)
 #pragma unroll
             for (int jj = 0; jj < 4; ++jj) {
                 const int d = 32 * dh + 8 * jj + 4 * h;
-                *(f32x4 *)(dK + d) =
-                    f32x4{dk[dh][4 * jj], dk[dh][4 * jj + 1], dk[dh][4 * jj + 2], dk[dh][4 * jj + 3]} * p.scale;
-                *(f32x4 *)(dV + d) = f32x4{dv[dh][4 * jj], dv[dh][4 * jj + 1], dv[dh][4 * jj + 2], dv[dh][4 * jj + 3]};
+                store4(p.dK, row + d,
+                       f32x4{dk[dh][4 * jj], dk[dh][4 * jj + 1], dk[dh][4 * jj + 2], dk[dh][4 * jj + 3]} * p.scale,
+                       p.grad_bf16);
+                store4(p.dV, row + d, f32x4{dv[dh][4 * jj], dv[dh][4 * jj + 1], dv[dh][4 * jj + 2], dv[dh][4 * jj + 3]},
+                       p.grad_bf16);
             }
     }
 }
@@ -566,11 +578,19 @@ __global__ __launch_bounds__(256) void flash2_bwd_rows(const FlashArgs p) {
     if (row >= p.bh * p.sq) return;  // whole 8-lane groups leave together
     const int64_t bh = row / p.sq, q = row % p.sq;
     const Head hd{p.heads, p.do_bs, p.do_hs, p.do_rs}, ho{p.heads, p.o_bs, p.o_hs, p.o_rs};
-    const float *o = p.O + ho.base(bh) + q * p.o_rs + 8 * c;
-    const f32x4 o0 = *(const f32x4 *)o, o1 = *(const f32x4 *)(o + 4);
-    const u32x4 g = *(const u32x4 *)((const uint16_t *)p.dO + hd.base(bh) + q * p.do_rs + 8 * c);
     auto lo = [](uint32_t w) { return __uint_as_float(w << 16); };
     auto hi = [](uint32_t w) { return __uint_as_float(w & 0xffff0000u); };
+    const int64_t oi = ho.base(bh) + q * p.o_rs + 8 * c;
+    f32x4 o0, o1;
+    if (p.o_bf16) {
+        const u32x4 ob = *(const u32x4 *)((const uint16_t *)p.O + oi);
+        o0 = f32x4{lo(ob[0]), hi(ob[0]), lo(ob[1]), hi(ob[1])};
+        o1 = f32x4{lo(ob[2]), hi(ob[2]), lo(ob[3]), hi(ob[3])};
+    } else {
+        o0 = *(const f32x4 *)((const float *)p.O + oi);
+        o1 = *(const f32x4 *)((const float *)p.O + oi + 4);
+    }
+    const u32x4 g = *(const u32x4 *)((const uint16_t *)p.dO + hd.base(bh) + q * p.do_rs + 8 * c);
     float s = lo(g[0]) * o0[0] + hi(g[0]) * o0[1] + lo(g[1]) * o0[2] + hi(g[1]) * o0[3] + lo(g[2]) * o1[0] +
               hi(g[2]) * o1[1] + lo(g[3]) * o1[2] + hi(g[3]) * o1[3];
 #pragma unroll

@@ -517,3 +517,79 @@ it_status it_profiler_report(it_context *ctx, char *buf, size_t buf_len, size_t 
 }
 
 }  // extern "C"
+
+namespace {
+
+// The GEMMs of one profiler key "gemm_<dtype>_<AB>_<plan>|<tag>[M,N,K](+[M,N,K])*x<batch> s<splits>"
+// (or gemv_...): layout letters and shapes; false for other kernels (attention, training ops).
+struct KeyGemm {
+    bool ta, tb;
+    long long m, n, k;
+};
+
+bool parse_gemm_key(const std::string &key, std::vector<KeyGemm> &out) {
+    out.clear();
+    if (key.rfind("gemm_", 0) != 0 && key.rfind("gemv_", 0) != 0) return false;
+    const size_t u1 = key.find('_'), u2 = key.find('_', u1 + 1);
+    if (u2 == std::string::npos || u2 + 2 >= key.size()) return false;
+    const char a = key[u2 + 1], b = key[u2 + 2];
+    const size_t bar = key.find('|');
+    if (bar == std::string::npos) return false;
+    size_t pos = key.find('[', bar);
+    while (pos != std::string::npos) {
+        KeyGemm g{a == 'T', b == 'T', 0, 0, 0};
+        if (std::sscanf(key.c_str() + pos, "[%lld,%lld,%lld]", &g.m, &g.n, &g.k) != 3) return false;
+        out.push_back(g);
+        const size_t close = key.find(']', pos);
+        if (close == std::string::npos || close + 1 >= key.size() || key[close + 1] != '+') break;
+        pos = close + 2;
+    }
+    return !out.empty();
+}
+
+}  // namespace
+
+extern "C" {
+
+it_status it_profiler_report_shapes(it_context *ctx, char *buf, size_t buf_len, size_t *needed) {
+    if (!ctx) return fail(IT_ERR_NULL, "it_profiler_report_shapes: ctx is NULL");
+    it_status st = it::profile_drain(ctx);
+    if (st != IT_OK) return st;
+    std::map<std::string, it::ProfileStat> shapes;
+    std::vector<KeyGemm> gs;
+    for (auto &kv : ctx->stats) {
+        if (!parse_gemm_key(kv.first, gs)) continue;
+        double flops = 0.0;
+        for (const KeyGemm &g : gs) flops += (double)g.m * g.n * g.k;
+        for (const KeyGemm &g : gs) {
+            // The stored operands as the reference names them: A [M,K] or, transposed, [K,M]^T;
+            // B [K,N] or [N,K]^T (src/ops/mps_gemm.rs:22-30,421-422).
+            const long long a0 = g.ta ? g.k : g.m, a1 = g.ta ? g.m : g.k;
+            const long long b0 = g.tb ? g.n : g.k, b1 = g.tb ? g.k : g.n;
+            const std::string shape = "[" + std::to_string(a0) + "," + std::to_string(a1) + "]" + (g.ta ? "^T" : "") +
+                                      "x[" + std::to_string(b0) + "," + std::to_string(b1) + "]" + (g.tb ? "^T" : "");
+            auto &d = shapes[shape];
+            d.calls += kv.second.calls;
+            d.total_ms += flops > 0.0 ? kv.second.total_ms * ((double)g.m * g.n * g.k / flops)
+                                      : kv.second.total_ms / (double)gs.size();
+        }
+    }
+    std::string out = "{";
+    bool first = true;
+    for (auto &kv : shapes) {
+        char tmp[128];
+        std::snprintf(tmp, sizeof(tmp), "{\"count\": %lld, \"total_ms\": %.6f}", (long long)kv.second.calls,
+                      kv.second.total_ms);
+        if (!first) out += ", ";
+        first = false;
+        out += "\"" + kv.first + "\": " + tmp;
+    }
+    out += "}";
+    if (needed) *needed = out.size() + 1;
+    if (!buf || buf_len < out.size() + 1)
+        return fail(IT_ERR_INVALID, "it_profiler_report_shapes: buffer too small");
+    std::memcpy(buf, out.c_str(), out.size() + 1);
+    return IT_OK;
+}
+
+}  // extern "C"

@@ -526,8 +526,10 @@ def flash_attention_bshd(q: Tensor, k: Tensor, v: Tensor, causal: bool) -> Tenso
 
 
 def flash_attention_forward_bhsd(q: Tensor, k: Tensor, v: Tensor, causal: bool = True,
-                                 scale: Optional[float] = None) -> Tuple[Tensor, Tensor]:
-    """Fused forward on [B,H,S,D] (D = 64, FP32 or BF16). Returns (O f32, lse f32 [B*H, S])."""
+                                 scale: Optional[float] = None,
+                                 out_precision: Precision = _P.FP32) -> Tuple[Tensor, Tensor]:
+    """Fused forward on [B,H,S,D] (D = 64, FP32 or BF16). Returns (O, lse f32 [B*H, S]); O is FP32,
+    or BF16 with out_precision=BF16 (BF16 operands only)."""
     b, h, sq, d = q.shape()
     skv = k.shape()[2]
     prec = q.precision()
@@ -535,22 +537,25 @@ def flash_attention_forward_bhsd(q: Tensor, k: Tensor, v: Tensor, causal: bool =
         if t.precision() is not prec:
             raise PrecisionMismatch("flash_attention", _prec_name(prec), _prec_name(t.precision()))
     scale = 1.0 / math.sqrt(d) if scale is None else scale
-    o = Tensor.empty([b, h, sq, d], _P.FP32, q.ctx)
+    o = Tensor.empty([b, h, sq, d], out_precision, q.ctx)
     lse = Tensor.empty([b * h, sq], _P.FP32, q.ctx)
     lq, lkv = _layout_bhsd(sq, d), _layout_bhsd(skv, d)
-    check(q.ctx.lib.it_flash_attention_forward(q.ctx.handle, int(prec), b * h, sq, skv, d, float(scale),
-                                               int(causal), C.byref(lq), C.byref(lkv), C.byref(lq),
-                                               _vp(q), _vp(k), _vp(v), _vp(o), _vp(lse)),
+    check(q.ctx.lib.it_flash_attention_forward_ex(q.ctx.handle, int(prec), int(out_precision), b * h, sq, skv, d,
+                                                  float(scale), int(causal), C.byref(lq), C.byref(lkv),
+                                                  C.byref(lq), _vp(q), _vp(k), _vp(v), _vp(o), _vp(lse)),
           "flash_attention")
     return o, lse
 
 
 def flash_attention_backward(grad_output: Tensor, q: Tensor, k: Tensor, v: Tensor, causal: bool = True,
                              scale: Optional[float] = None, o: Optional[Tensor] = None,
-                             lse: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
-    """attention_backward_recompute (src/train/helpers.rs:120-193) fused, on [B,H,S,D] with D = 64.
-    With `o` and `lse` from flash_attention_forward_bhsd the forward is not recomputed. Returns
-    (dQ, dK, dV), FP32; deterministic (no atomics)."""
+                             lse: Optional[Tensor] = None,
+                             out_precision: Precision = _P.FP32) -> Tuple[Tensor, Tensor, Tensor]:
+    """attention_backward_recompute (src/train/helpers.rs:120-193) fused, on [B,H,S,D] (D = 64 fused;
+    other D up to 128 recompute the materialised contractions). With `o` and `lse` from
+    flash_attention_forward_bhsd (same out_precision) the forward is not recomputed. Returns
+    (dQ, dK, dV), FP32 or, with out_precision=BF16 (BF16 operands, D = 64), BF16; deterministic (no
+    atomics)."""
     b, h, s, d = q.shape()
     prec = q.precision()
     for t in (grad_output, k, v):
@@ -562,15 +567,16 @@ def flash_attention_backward(grad_output: Tensor, q: Tensor, k: Tensor, v: Tenso
         raise InvalidValue("flash_attention_backward", "pass both o and lse, or neither")
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     ctx = q.ctx
-    dq = Tensor.empty([b, h, s, d], _P.FP32, ctx)
-    dk = Tensor.empty([b, h, s, d], _P.FP32, ctx)
-    dv = Tensor.empty([b, h, s, d], _P.FP32, ctx)
+    dq = Tensor.empty([b, h, s, d], out_precision, ctx)
+    dk = Tensor.empty([b, h, s, d], out_precision, ctx)
+    dv = Tensor.empty([b, h, s, d], out_precision, ctx)
     lay = _layout_bhsd(s, d)
-    check(ctx.lib.it_flash_attention_backward(ctx.handle, int(prec), b * h, s, d, float(scale), int(causal),
-                                              C.byref(lay), None, None, _vp(grad_output), _vp(q), _vp(k),
-                                              _vp(v), _vp(o) if o is not None else None,
-                                              _vp(lse) if lse is not None else None,
-                                              _vp(dq), _vp(dk), _vp(dv)), "attention_backward")
+    check(ctx.lib.it_flash_attention_backward_ex(ctx.handle, int(prec), int(out_precision), b * h, s, d,
+                                                 float(scale), int(causal), C.byref(lay), None, None,
+                                                 _vp(grad_output), _vp(q), _vp(k), _vp(v),
+                                                 _vp(o) if o is not None else None,
+                                                 _vp(lse) if lse is not None else None,
+                                                 _vp(dq), _vp(dk), _vp(dv)), "attention_backward")
     return dq, dk, dv
 
 

@@ -123,8 +123,14 @@ class GemmStep:
         self.X = [act([T, H]) for _ in range(L)]       # attention-norm output
         self.X2 = [act([T, H]) for _ in range(L)]      # ffn-norm output
         self.QKV = [empty([T, 3 * H]) for _ in range(L)]
-        self.O = [empty([T, H], Precision.FP32) for _ in range(L)]
-        self.Oin = self.O if P is Precision.FP32 else [act([T, H]) for _ in range(L)]
+        # The attention output feeds the output projection and dQ|dK|dV the QKV projection's
+        # backward (src/train/forward.rs:138-146, src/train/backward.rs:100-147). In BF16 the fused
+        # kernels write them as BF16 (it_flash_attention_*_ex); the materialised form writes FP32,
+        # so with it a BF16 step's two projections read seeded BF16 stand-ins instead.
+        self.fused = (s.head_dim == 64) if fused_attention is None else bool(fused_attention)
+        self.attn_out = P if (self.fused or P is Precision.FP32) else Precision.FP32
+        self.O = [empty([T, H], self.attn_out) for _ in range(L)]
+        self.Oin = self.O if self.attn_out is P else [act([T, H]) for _ in range(L)]
         self.Y = [empty([T, H]) for _ in range(L)]
         self.G = [empty([T, F]) for _ in range(L)]
         self.U = [empty([T, F]) for _ in range(L)]
@@ -145,7 +151,7 @@ class GemmStep:
         self.dOp = empty([T, H], Precision.FP32)
         # One dQKV per layer: a layer's qkv.dW (side stream) may still read it while the next layer's
         # attention backward (main stream) writes its own.
-        self.dQKV_layers = [empty([T, 3 * H], Precision.FP32) for _ in range(L)]
+        self.dQKV_layers = [empty([T, 3 * H], self.attn_out) for _ in range(L)]
         self.dQKV = self.dQKV_layers[0]
         self.dX = empty([T, H], Precision.FP32)
         self.dWd = [empty([H, F], Precision.FP32) for _ in range(L)]
@@ -154,7 +160,6 @@ class GemmStep:
         self.dWqkv = [empty([3 * H, H], Precision.FP32) for _ in range(L)]
         # Attention: the fused kernels keep each layer's row log-sum-exp for the backward; the
         # materialised form needs [BH, S, S] workspaces, shared by all layers.
-        self.fused = (s.head_dim == 64) if fused_attention is None else bool(fused_attention)
         if self.fused:
             self.lse = [empty([bh, s.seq], Precision.FP32) for _ in range(L)]
         else:
@@ -268,8 +273,8 @@ class GemmStep:
         base = self.QKV[l].ptr
         q, k, v = (C.c_void_p(base + i * H * eb) for i in range(3))
         if self.fused:
-            st = self.lib.it_flash_attention_forward(
-                self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.seq, s.head_dim,
+            st = self.lib.it_flash_attention_forward_ex(
+                self.ctx.handle, int(P), int(self.attn_out), s.batch * s.heads, s.seq, s.seq, s.head_dim,
                 1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o), q, k, v,
                 C.c_void_p(self.O[l].ptr), C.c_void_p(self.lse[l].ptr))
         else:
@@ -304,16 +309,16 @@ class GemmStep:
         # Wo: dO = dY.Wo (NN), dWo = dY^T.O (TN)
         self._dw("wo.dW", self.dY, self.Oin[l], self.dWo[l], True, False, H, H, T)
         self._gemm("wo.dX", self.dY, self.Wo[l], self.dOp, False, False, T, H, H)
-        # attention_backward_recompute into the dQKV buffer (f32, same [B,S,3,H,D] layout)
+        # attention_backward_recompute into the layer's dQKV buffer (same [B,S,3,H,D] layout as QKV)
         qkv, o = self._layouts()
         eb = P.byte_size()
         base = self.QKV[l].ptr
         dbase = self.dQKV_layers[l].ptr
         q, k, v = (C.c_void_p(base + i * H * eb) for i in range(3))
-        dq, dk, dv = (C.c_void_p(dbase + i * H * 4) for i in range(3))
+        dq, dk, dv = (C.c_void_p(dbase + i * H * self.attn_out.byte_size()) for i in range(3))
         if self.fused:
-            st = self.lib.it_flash_attention_backward(
-                self.ctx.handle, int(P), s.batch * s.heads, s.seq, s.head_dim,
+            st = self.lib.it_flash_attention_backward_ex(
+                self.ctx.handle, int(P), int(self.attn_out), s.batch * s.heads, s.seq, s.head_dim,
                 1.0 / math.sqrt(s.head_dim), 1, C.byref(qkv), C.byref(qkv), C.byref(o),
                 C.c_void_p(self.dO.ptr), q, k, v, C.c_void_p(self.O[l].ptr),
                 C.c_void_p(self.lse[l].ptr), dq, dk, dv)
@@ -327,9 +332,9 @@ class GemmStep:
         if self._record:
             attn = 2.0 * s.batch * s.heads * s.seq * s.seq * s.head_dim
             self.launches += [_Launch(n, attn) for n in ("attn.S", "attn.dV", "attn.dP", "attn.dQ", "attn.dK")]
-        # QKV: dX = dQKV.Wqkv (NN), dWqkv = dQKV^T.X (TN). dQKV is f32; in BF16 mode the
-        # projection backward reads the seeded BF16 gradient stand-in instead.
-        dqkv = self.dQKV_layers[l] if P is Precision.FP32 else self._dqkv_bf16()
+        # QKV: dX = dQKV.Wqkv (NN), dWqkv = dQKV^T.X (TN), reading the attention backward's dQ|dK|dV
+        # (the materialised form's FP32 gradient leaves a BF16 step a seeded BF16 stand-in).
+        dqkv = self.dQKV_layers[l] if self.attn_out is P else self._dqkv_bf16()
         self._dw("qkv.dW", dqkv, self.X[l], self.dWqkv[l], True, False, 3 * H, H, T)
         self._dw_flush()
         self._gemm("qkv.dX", dqkv, self.Wqkv[l], self.dX, False, False, T, H, 3 * H)

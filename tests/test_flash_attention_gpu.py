@@ -363,3 +363,44 @@ def test_flash_bf16_bshd_strided(it, oracle, causal):
     refs = oracle.attention_bwd_bhsd(tb(do), tb(q), tb(k), tb(v), 0.125, causal)
     for name, g, r in zip("QKV", grads, refs):
         assert frob_rel(tb(g.numpy()), r) <= BF16_FROB_TOL, name
+
+
+# ----------------------------------------- BF16 outputs (it_flash_attention_forward_ex / backward_ex)
+
+@pytest.mark.parametrize("s,causal", [(1024, True), (200, False)])
+def test_flash_bf16_outputs(it, oracle, s, causal):
+    """BF16 O and dQ, dK, dV: the forward's BF16 O is the round-to-nearest-even of its FP32 O bit for
+    bit; the recomputing backward's BF16 gradients are those of its FP32 gradients bit for bit; the
+    backward reading the BF16 O stays within the BF16 contract of the oracle."""
+    from irontensor_amd import bf16_to_f32, f32_to_bf16
+    b, h = 2, 4
+    B16 = it.Precision.BF16
+    q, k, v, do = (synth.normal(700 + s + i, (b, h, s, D)) for i in range(4))
+    tq, tk, tv, tdo = (_bf(it, x) for x in (q, k, v, do))
+    o32, lse32 = it.flash_attention_forward_bhsd(tq, tk, tv, causal=causal, scale=0.125)
+    o16, lse16 = it.flash_attention_forward_bhsd(tq, tk, tv, causal=causal, scale=0.125, out_precision=B16)
+    assert o16.precision() is B16
+    assert np.array_equal(o16.as_bf16_slice(), f32_to_bf16(o32.numpy()).ravel())
+    assert np.array_equal(lse16.numpy(), lse32.numpy())
+    g32 = it.flash_attention_backward(tdo, tq, tk, tv, causal=causal, scale=0.125)
+    g16 = it.flash_attention_backward(tdo, tq, tk, tv, causal=causal, scale=0.125, out_precision=B16)
+    for name, x, y in zip("QKV", g32, g16):
+        assert np.array_equal(y.as_bf16_slice(), f32_to_bf16(x.numpy()).ravel()), name
+    chained = it.flash_attention_backward(tdo, tq, tk, tv, causal=causal, scale=0.125, o=o16, lse=lse16,
+                                          out_precision=B16)
+    ro, _ = oracle.attention_fwd_bhsd(q, k, v, 0.125, causal)
+    assert frob_rel(bf16_to_f32(o16.as_bf16_slice()).reshape(ro.shape), ro) <= BF16_FROB_TOL
+    refs = oracle.attention_bwd_bhsd(do, q, k, v, 0.125, causal)
+    for name, g, r in zip("QKV", chained, refs):
+        assert g.precision() is B16
+        assert frob_rel(g.numpy(), r) <= BF16_FROB_TOL, name
+
+
+def test_flash_bf16_output_refusals(it):
+    """A BF16 output needs BF16 operands and head_dim 64."""
+    x32 = _t(it, synth.normal(12, (1, 2, 64, 64)))
+    with pytest.raises(it.TensorError, match="BF16 output needs BF16 operands"):
+        it.flash_attention_forward_bhsd(x32, x32, x32, out_precision=it.Precision.BF16)
+    x16 = _bf(it, synth.normal(13, (1, 2, 64, 32)))
+    with pytest.raises(it.TensorError, match="head_dim 64"):
+        it.flash_attention_backward(x16, x16, x16, x16, out_precision=it.Precision.BF16)
