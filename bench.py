@@ -82,6 +82,33 @@ class Timer:
         return float(ms.value)
 
 
+class StepEvents:
+    """One hipEvent before each of `n` steps and one after the last, on the library's stream: the
+    per-step durations of a timed run without extra synchronisation inside it."""
+
+    def __init__(self, ctx, n: int):
+        self.ctx = ctx
+        self.ev = [C.c_void_p() for _ in range(n + 1)]
+        for e in self.ev:
+            ctx.lib.it_event_create(ctx.handle, C.byref(e))
+
+    def mark(self, i: int) -> None:
+        self.ctx.lib.it_event_record(self.ctx.handle, self.ev[i])
+
+    def durations_ms(self) -> list:
+        self.ctx.lib.it_event_sync(self.ev[-1])
+        out = []
+        for a, b in zip(self.ev, self.ev[1:]):
+            ms = C.c_float()
+            self.ctx.lib.it_event_elapsed_ms(a, b, C.byref(ms))
+            out.append(float(ms.value))
+        return out
+
+    def close(self) -> None:
+        for e in self.ev:
+            self.ctx.lib.it_event_destroy(e)
+
+
 def time_gemm(it, timer, a, b, out, trans_a, trans_b, iters, warm=3) -> float:
     for _ in range(warm):
         it.gemm(a, b, trans_a=trans_a, trans_b=trans_b, out=out)
@@ -231,36 +258,44 @@ def bf16_square(it, timer, sizes) -> dict:
     return out
 
 
-def vs_library(it, timer, n: int = 4096, iters: int = 20) -> dict:
-    """The BF16 n^3 GEMM against AMD's library in the same process: torch.mm on two contiguous BF16
-    [n, n] tensors (served by hipBLASLt), then this library's NN, NT and TN forms; three batches of
-    `iters` launches each, TFLOP/s per batch. For same-box A/B kernel traces and counter passes."""
+def vs_library(it, timer, sizes=((4096, 20), (8192, 6))) -> dict:
+    """The BF16 n^3 GEMM against AMD's library in the same process: torch.mm on BF16 [n, n] tensors
+    (served by hipBLASLt) in the NN, NT and TN layouts (the transposed operand a 2-D transposed view,
+    which the library reads in place), then this library's NN, NT and TN forms on its own seeded
+    operands; three batches of `iters` launches each, TFLOP/s per batch. BF16 out."""
     import torch
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0)
-    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
-    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
-    for _ in range(5):
-        torch.mm(a, b)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    tf = lambda ms: round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)  # noqa: E731
-    out = {"hipblaslt_torch_mm_NN": []}
-    for _ in range(3):
-        e0.record()
-        for _ in range(iters):
-            torch.mm(a, b)
-        e1.record()
-        torch.cuda.synchronize()
-        out["hipblaslt_torch_mm_NN"].append(tf(e0.elapsed_time(e1) / iters))
-    del a, b
     P = it.Precision
-    A, B = _dev(it, 3, (n, n), prec=P.BF16), _dev(it, 4, (n, n), prec=P.BF16)
-    Cm = it.Tensor.empty([n, n], P.BF16)
-    for lay, (ta, tb) in (("NN", (False, False)), ("NT", (False, True)), ("TN", (True, False))):
-        out[f"this_{lay}"] = [tf(time_gemm(it, timer, A, B, Cm, ta, tb, iters, warm=3)) for _ in range(3)]
-    return {f"bf16_{n}_vs_library_tflops": out}
+    res = {}
+    for n, iters in sizes:
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        a = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
+        b = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        tf = lambda ms: round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)  # noqa: E731
+        out = {}
+        for lay, (x, y) in (("NN", (a, b)), ("NT", (a, b.t())), ("TN", (a.t(), b))):
+            for _ in range(3):
+                torch.mm(x, y)
+            torch.cuda.synchronize()
+            out[f"hipblaslt_torch_mm_{lay}"] = []
+            for _ in range(3):
+                e0.record()
+                for _ in range(iters):
+                    torch.mm(x, y)
+                e1.record()
+                torch.cuda.synchronize()
+                out[f"hipblaslt_torch_mm_{lay}"].append(tf(e0.elapsed_time(e1) / iters))
+        del a, b
+        torch.cuda.empty_cache()
+        A, B = _dev(it, 3, (n, n), prec=P.BF16), _dev(it, 4, (n, n), prec=P.BF16)
+        Cm = it.Tensor.empty([n, n], P.BF16)
+        for lay, (ta, tb) in (("NN", (False, False)), ("NT", (False, True)), ("TN", (True, False))):
+            out[f"this_{lay}"] = [tf(time_gemm(it, timer, A, B, Cm, ta, tb, iters, warm=3)) for _ in range(3)]
+        del A, B, Cm
+        res[f"bf16_{n}_vs_library_tflops"] = out
+    return res
 
 
 def extra_sweep(it, timer) -> dict:
@@ -656,7 +691,8 @@ def main() -> int:
         print(json.dumps(attention_only(it, Timer(ctx), args.steps)), flush=True)
         return 0
     if args.vs_library:
-        print(json.dumps(vs_library(it, Timer(ctx), iters=args.steps)), flush=True)
+        print(json.dumps(vs_library(it, Timer(ctx), sizes=((4096, args.steps), (8192, max(2, args.steps // 4))))),
+              flush=True)
         return 0
     if args.decode:
         print(json.dumps(decode_shapes(it, Timer(ctx), rounds=max(1, args.steps))), flush=True)
@@ -679,16 +715,22 @@ def main() -> int:
         step.replay()
     ctx.sync()
     timer = Timer(ctx)
+    marks = StepEvents(ctx, args.steps)
     t0 = time.perf_counter()
     timer.start()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        marks.mark(i)
         step.replay()
+    marks.mark(args.steps)
     gpu_ms = timer.stop_ms()
     ctx.sync()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
+    step_ms = marks.durations_ms()
+    marks.close()
+    ms_median = float(np.median(step_ms))
     log(f"[bench] timed {args.steps} steps: wall {ms_per_step:.3f} ms/step, events "
-        f"{gpu_ms / args.steps:.3f} ms/step")
+        f"{gpu_ms / args.steps:.3f} ms/step, median step {ms_median:.3f} ms")
 
     # Per-kernel durations: the same steps run eagerly on the same one stream with hipEvents around
     # every launch.
@@ -738,6 +780,8 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step_median": round(ms_median, 4),
+        "ms_per_step_min_max": [round(min(step_ms), 4), round(max(step_ms), 4)],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -914,20 +914,23 @@ struct DtlOperand {
 // s_waitcnt immediate: vmcnt(vm) lgkmcnt(lgkm), expcnt not waited on.
 constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8); }
 
-template <bool TA, bool TB, bool DUAL, int FB, bool OPAQUE = (FB == 2)>
+template <bool TA, bool TB, bool DUAL, int FB, bool OPAQUE = (FB == 2), int FA = 4, int NSX = 0>
 __device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *__restrict__ st0, char *__restrict__ st1,
-                                         char *__restrict__ st2, const uint16_t *A,
-                                         const uint16_t *B, int64_t krange, int ntiles, f32x16 (&acc)[4][FB],
+                                         char *__restrict__ st2, char *__restrict__ st3, const uint16_t *A,
+                                         const uint16_t *B, int64_t krange, int ntiles, f32x16 (&acc)[FA][FB],
                                          int wave, int lane) {
     // OPAQUE: the direct loads' LDS addresses hidden from the compiler (needed whenever the
-    // stages share one LDS object or are three: then only the explicit waits order the loads).
-    // FB: 32-column B fragments per wave (4: 256 x 256 tile, 128 x 128 per wave, two 64 KB
-    // stages; 2: 256 x 128 tile, 128 x 64 per wave, three 48 KB stages, so that loads run two
-    // k-tiles ahead of a k-tile that takes half as long).
-    constexpr int BN = FB * 64, BK = 64, WT = 128, F = 4;
-    constexpr int NS = FB == 2 ? 3 : 2;
-    constexpr int TILE = 256 * BK * 2;
-    using OA = DtlOperand<!TA>;
+    // stages share one LDS object or are three or more: then only the explicit waits order the
+    // loads). FA / FB: 32-row A / 32-column B fragments per wave. FA = 4, FB = 4: 256 x 256 tile,
+    // 128 x 128 per wave, two 64 KB stages; FA = 4, FB = 2: 256 x 128 tile, 128 x 64 per wave,
+    // three 48 KB stages, so that loads run two k-tiles ahead of a k-tile that takes half as long;
+    // FA = 2, FB = 2: 128 x 128 tile, 64 x 64 per wave, NSX stages of 32 KB (a k-tile is a quarter
+    // of the 256 x 256 one: more stages keep the same load latency covered).
+    constexpr int BN = FB * 64, BK = 64, WT = FA * 32, F = FA;
+    constexpr int NS = NSX ? NSX : FB == 2 ? 3 : 2;
+    static_assert(NS >= 2 && NS <= 4 && (NS == 2 || OPAQUE), "two to four stages; three or more need OPAQUE");
+    constexpr int TILE = FA * 64 * BK * 2;
+    using OA = DtlOperand<!TA, FA * 64>;
     using OB = DtlOperand<TB, BN>;
     const int wm = wave >> 1, wn = wave & 1;
     const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -962,9 +965,9 @@ __device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *__restrict__ s
                     __builtin_bit_cast(bf16x8, fa[i]), __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
     };
     // DS reads per MFMA pair (a k-step's fragment set is F + FB fragments, an mn-contiguous one
-    // two reads each; the k-step has 2 FB MFMA pairs), and load instructions per pair in the
+    // two reads each; the k-step has F FB / 2 MFMA pairs), and load instructions per pair in the
     // k-step that issues them.
-    constexpr int PAIRS = 2 * FB;
+    constexpr int PAIRS = F * FB / 2;
     constexpr int DSR = (F * (TA ? 2 : 1) + FB * (TB ? 1 : 2) + PAIRS - 1) / PAIRS;
     constexpr int VMR = (OA::NI + OB::NI + PAIRS - 1) / PAIRS;
     // Load instructions a wave issues per k-tile: with three stages the wait before the barrier
@@ -1021,7 +1024,7 @@ __device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *__restrict__ s
             body(st0, st1, t);
             body(st1, st0, t + 1);
         }
-    } else {
+    } else if constexpr (NS == 3) {
         issue(0, st0);
         issue(1, st1);
         __builtin_amdgcn_s_waitcnt(waitcnt_imm(NLOAD, 15));  // tile 0 landed
@@ -1037,6 +1040,24 @@ __device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *__restrict__ s
             body(st2, st0, t + 2);
             if (t + 3 >= ntiles) break;
         }
+    } else {
+        issue(0, st0);
+        issue(1, st1);
+        issue(2, st2);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * NLOAD, 15));  // tile 0 landed
+        __syncthreads();
+        issue(3, st3);
+        frags(fa0, fb0, st0, 0);
+        for (int t = 0;; t += 4) {
+            body(st0, st1, t);
+            if (t + 1 >= ntiles) break;
+            body(st1, st2, t + 1);
+            if (t + 2 >= ntiles) break;
+            body(st2, st3, t + 2);
+            if (t + 3 >= ntiles) break;
+            body(st3, st0, t + 3);
+            if (t + 4 >= ntiles) break;
+        }
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the loads into dead stages have landed
 }
@@ -1050,18 +1071,24 @@ __device__ __forceinline__ void dtl_tile(const GemmArgs &p, char *__restrict__ s
 // write instruction touches (4 apart) then fall in different banks. In the SwiGLU form the gate
 // wave (wn = 0) and the up wave (wn = 1) of a row half stage the same output columns and then
 // finish 64 rows each of the pair.
-template <bool DUAL, int FB>
+template <bool DUAL, int FB, int FA = 4>
 __device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char *st1, char *st2,
-                                             const f32x16 (&acc)[4][FB], int64_t m0, int64_t n0, int64_t coff,
+                                             const f32x16 (&acc)[FA][FB], int64_t m0, int64_t n0, int64_t coff,
                                              int64_t z, int wave, int lane) {
-    static_assert(!DUAL || FB == 4, "the SwiGLU form pairs 128-column gate and up waves");
-    constexpr int WT = 128, F = 4, STAGE = FB == 4 ? 2 * 256 * 64 * 2 : (256 + 128) * 64 * 2;
+    static_assert(!DUAL || (FB == 4 && FA == 4), "the SwiGLU form pairs 128-column gate and up waves");
+    constexpr int WT = FA * 32, F = FA, NH = FA / 2;  // NH: 64-row halves per wave
+    constexpr int STAGE = FA == 2 ? 2 * 128 * 64 * 2 : FB == 4 ? 2 * 256 * 64 * 2 : (256 + 128) * 64 * 2;
     constexpr int EC2 = 64, EP2 = EC2 * 4, HALF = 64 * EP2;
-    static_assert(FB == 4 ? 4 * HALF <= STAGE : 3 * HALF <= STAGE, "epilogue staging fits in the stages");
+    static_assert(FA == 2 ? 2 * HALF <= STAGE : FB == 4 ? 4 * HALF <= STAGE : 3 * HALF <= STAGE,
+                  "epilogue staging fits in the stages");
     const int wm = wave >> 1, wn = wave & 1;
     __syncthreads();
-    char *lo, *hi;  // this wave's staging for rows 0-63 and 64-127 of its 128
-    if constexpr (FB == 4) {
+    char *lo, *hi;  // this wave's staging for rows 0-63 and 64-127 of its 128 (FA = 2: 64 rows, lo)
+    if constexpr (FA == 2) {
+        // st0 and st1 are consecutive stages: four 16 KB halves in their 64 KB
+        lo = (wave < 2 ? st0 : st1) + (wave & 1) * HALF;
+        hi = lo;
+    } else if constexpr (FB == 4) {
         lo = (wave < 2 ? st0 : st1) + (wave & 1) * (2 * HALF);
         hi = lo + HALF;
     } else {
@@ -1138,7 +1165,7 @@ __device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char 
                 return *(const f32x4 *)((h ? hi : lo) + (4 * it + (lane >> 4)) * EP2 + ((cl ^ ((it & 1) << 5)) * 4));
             };
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+            for (int h = 0; h < NH; ++h) {
                 const int64_t row0 = m0 + wm * WT + h * 64 + (lane >> 4);
                 if (p.splits > 1) {
                     // split-K partial sums: plain f32 rows of N
@@ -1179,11 +1206,12 @@ __device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char 
 // accumulate gate and wn = 1 up for one 256 x 128 output tile; the epilogue pairs them. FB = 2:
 // a 256 x 128 output tile (twice the tiles where 256 x 256 would leave CUs idle), with three
 // stages of 48 KB.
-template <bool TA, bool TB, bool DUAL, int FB, bool OPAQUE = (FB == 2)>
-__device__ __forceinline__ void dtl_block(const GemmArgs &p, int tile, int64_t z, char *st0, char *st1, char *st2) {
+template <bool TA, bool TB, bool DUAL, int FB, bool OPAQUE = (FB == 2), int FA = 4, int NS = 0>
+__device__ __forceinline__ void dtl_block(const GemmArgs &p, int tile, int64_t z, char *st0, char *st1, char *st2,
+                                          char *st3 = nullptr) {
     static_assert(!DUAL || (!TA && TB), "SwiGLU is Y = X.W^T");
     using T = uint16_t;
-    constexpr int BM = 256, BN = FB * 64, BK = 64, F = 4;
+    constexpr int BM = FA * 64, BN = FB * 64, BK = 64, F = FA;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int tm, tn;
@@ -1197,9 +1225,9 @@ __device__ __forceinline__ void dtl_block(const GemmArgs &p, int tile, int64_t z
     const T *Bm = (const T *)(DUAL && wave >= 2 ? p.B2 : p.B);
     const T *B = Bm + bo * p.sB_out + bi * p.sB_in + (TB ? n0 * p.ldb + kb : kb * p.ldb + n0);
     f32x16 acc[F][FB];
-    dtl_tile<TA, TB, DUAL, FB, OPAQUE>(p, st0, st1, st2, A, B, ke - kb, ke > kb ? (int)((ke - kb) / BK) : 0, acc,
-                                       wave, lane);
-    dtl_epilogue<DUAL, FB>(p, st0, st1, st2, acc, m0, n0, bo * p.sC_out + bi * p.sC_in, z, wave, lane);
+    dtl_tile<TA, TB, DUAL, FB, OPAQUE, FA, NS>(p, st0, st1, st2, st3, A, B, ke - kb,
+                                               ke > kb ? (int)((ke - kb) / BK) : 0, acc, wave, lane);
+    dtl_epilogue<DUAL, FB, FA>(p, st0, st1, st2, acc, m0, n0, bo * p.sC_out + bi * p.sC_in, z, wave, lane);
 }
 
 template <bool TA, bool TB, bool DUAL = false, int FB = 4>
@@ -1210,6 +1238,18 @@ void gemm_bf16_dtl(const GemmArgs p) {
     __shared__ __attribute__((aligned(1024))) char st1[STAGE];
     __shared__ __attribute__((aligned(1024))) char st2[FB == 2 ? STAGE : 16];  // FB = 2 only
     dtl_block<TA, TB, DUAL, FB>(p, blockIdx.x, blockIdx.y, st0, st1, st2);
+}
+
+// 128 x 128 tiles (64 x 64 per wave), DTL128_STAGES stages of 32 KB in one LDS object: for shapes
+// whose 256-wide tiles would leave CUs idle (2048^3: 256 tiles, one per CU, where 256 x 256 gives 64).
+constexpr int DTL128_STAGES = 4;
+template <bool TA, bool TB>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_bf16_dtl128(const GemmArgs p) {
+    constexpr int STAGE = 2 * 128 * 64 * 2;
+    __shared__ __attribute__((aligned(1024))) char st[DTL128_STAGES * STAGE];
+    dtl_block<TA, TB, false, 2, true, 2, DTL128_STAGES>(p, blockIdx.x, blockIdx.y, st, st + STAGE, st + 2 * STAGE,
+                                                        st + (DTL128_STAGES > 3 ? 3 : 0) * STAGE);
 }
 
 // Several independent GEMMs of one layout in one launch. Workgroup w runs on XCD w % 8, and each
@@ -1362,6 +1402,26 @@ bool dtl_applicable(bool ta, bool tb, const GemmArgs &a, int bn = 256) {
            fits(!ta, a.lda) && fits(tb, a.ldb) && a.K * 2 < (1ll << 31);
 }
 
+// The 128 x 128 direct-to-LDS kernel: whole tiles, any number of 64-wide k-tiles per split, and
+// 32-bit buffer offsets (a k-contiguous operand's 128 rows, or an mn-contiguous one's k range, within
+// 2 GiB).
+bool dtl128_applicable(bool ta, bool tb, const GemmArgs &a) {
+    auto fits = [&](bool kcontig, int64_t ld) {
+        return kcontig ? ld * 2 * 128 < (1ll << 31) : a.k_per_split * ld * 2 < (1ll << 31);
+    };
+    return !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.swiglu_bwd && !a.xent_stats &&
+           !a.a_kscale && tiles_exact(a, 128, 128, ET<uint16_t>::BK) && a.k_per_split % ET<uint16_t>::BK == 0 &&
+           fits(!ta, a.lda) && fits(tb, a.ldb) && a.K * 2 < (1ll << 31);
+}
+
+hipError_t launch_bf16_dtl128(bool ta, bool tb, const GemmArgs &a, dim3 grid, hipStream_t s) {
+    if (!ta && tb) hipLaunchKernelGGL((gemm_bf16_dtl128<false, true>), grid, dim3(NTHREADS), 0, s, a);
+    else if (!ta && !tb) hipLaunchKernelGGL((gemm_bf16_dtl128<false, false>), grid, dim3(NTHREADS), 0, s, a);
+    else if (ta && !tb) hipLaunchKernelGGL((gemm_bf16_dtl128<true, false>), grid, dim3(NTHREADS), 0, s, a);
+    else hipLaunchKernelGGL((gemm_bf16_dtl128<true, true>), grid, dim3(NTHREADS), 0, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_bf16_256(bool ta, bool tb, int bn, const GemmArgs &a, dim3 grid, hipStream_t s) {
     if (bn == 128) {  // the planner offers 256 x 128 only where the direct-to-LDS kernel applies
         if (!dtl_applicable(ta, tb, a, 128)) return hipErrorInvalidConfiguration;
@@ -1497,6 +1557,11 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
     // 256 x 128, whose waves read 50% more LDS per MFMA (two transposed reads per fragment of a
     // transposed A: lower still), and whose third stage lowers the memory-latency floor.
     constexpr double DTL_EFF = 0.53, DTL_HALF_FLOOR = 0.85e-6;
+    // The 128 x 128 direct-to-LDS tile (four stages: three k-tiles of loads in flight). Measured
+    // (2048^3, one tile per CU): NT 23.6 us; NN and TN, whose transposed fragments take two reads
+    // each, 35-36 us, slower than their 256 x 128 split plans.
+    const double DTL128_EFF = !ta && tb ? 0.35 : 0.22;
+    constexpr double DTL128_FLOOR = 0.35e-6;
     const double DTL_HALF_EFF = ta ? 0.42 : 0.52;
     const Cand *cands = bf16 ? b16c : f32c;
     const int ncand = bf16 ? 4 : 2;
@@ -1529,19 +1594,26 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
             const int64_t splits = s > 1 ? cdiv(a.K, kps) : 1;
             const int64_t blocks = tiles * splits;
             const int64_t per_cu = cdiv(blocks, cus);
-            const int64_t conc = std::min<int64_t>(per_cu, cd.occ);
-            const int64_t rounds = cdiv(per_cu, cd.occ);
+            // The 128 x 128 BF16 tile runs on the direct-to-LDS kernel where it applies (one block
+            // per CU: its stages take 128 KB of LDS).
+            GemmArgs d = a;
+            d.k_per_split = kps;
+            const bool d128 = bf16 && cd.b == 128 && dtl128_applicable(ta, tb, d);
+            const int occ = d128 ? 1 : cd.occ;
+            const int64_t conc = std::min<int64_t>(per_cu, occ);
+            const int64_t rounds = cdiv(per_cu, occ);
             const int64_t ksteps = std::max<int64_t>(1, cdiv(kps, bk));
             // A lone block on a CU whose tile could run two at once hides less latency.
-            double eff = conc == 1 && cd.occ > 1 ? 0.9 * cd.eff : cd.eff;
-            if (bf16 && cd.b == 256) {
-                GemmArgs d = a;
-                d.k_per_split = kps;
-                if (dtl_applicable(ta, tb, d, a.dual ? 256 : bn)) eff = bn == 128 && !a.dual ? DTL_HALF_EFF : DTL_EFF;
+            double eff = conc == 1 && occ > 1 ? 0.9 * cd.eff : cd.eff;
+            double floor = cd.bn == 128 ? DTL_HALF_FLOOR : step_floor;
+            if (bf16 && cd.b == 256 && dtl_applicable(ta, tb, d, a.dual ? 256 : bn))
+                eff = bn == 128 && !a.dual ? DTL_HALF_EFF : DTL_EFF;
+            if (d128) {
+                eff = DTL128_EFF;
+                floor = DTL128_FLOOR;
             }
             if (eff <= 0.0) continue;
             const double step = (a.dual ? 4.0 : 2.0) * cd.b * bn * bk / (cu_peak * eff);
-            const double floor = cd.bn == 128 ? DTL_HALF_FLOOR : step_floor;
             double t = rounds * (round_overhead + ksteps * std::max(conc * step, floor));
             if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
             // Near ties (3%) keep the earlier, larger and less split plan, except that between two
@@ -1651,7 +1723,8 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
         if (st != IT_OK) return st;
         a.partial = (float *)ws;
     }
-    const bool dtl = cfg.bm == 256 && dtl_applicable(transA, transB, a, a.dual ? 256 : cfg.bn);
+    const bool dtl128 = bf16 && cfg.bm == 128 && cfg.bn == 128 && dtl128_applicable(transA, transB, a);
+    const bool dtl = dtl128 || (cfg.bm == 256 && dtl_applicable(transA, transB, a, a.dual ? 256 : cfg.bn));
 
     const int64_t gx = (int64_t)a.tiles_m * a.tiles_n;
     const int64_t gy = a.batch * splits;
@@ -1674,6 +1747,7 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
         profile_begin(ctx, key, &ev);
     }
     hipError_t e = cfg.bm == 256 ? launch_bf16_256(transA, transB, a.dual ? 256 : cfg.bn, a, grid, ctx->stream)
+                   : dtl128      ? launch_bf16_dtl128(transA, transB, a, grid, ctx->stream)
                    : bf16        ? launch_typed<uint16_t>(transA, transB, a.dual, cfg, a, grid, ctx->stream)
                                  : launch_typed<float>(transA, transB, a.dual, cfg, a, grid, ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "gemm_mfma launch");

@@ -151,3 +151,29 @@ def test_fill_normal_is_the_host_stream(it, prec):
     assert ctx.lib.it_fill_normal(ctx.handle, 0, 350, 12345, 1001, 0.02, C.c_void_p(part.ptr)) == 0
     ref = synth.normal_at(350, np.arange(12345, 12345 + 1001), std=0.02)
     assert np.max(np.abs(part.numpy().view(np.int32).astype(np.int64) - ref.view(np.int32))) <= 1
+
+
+def test_profiler_matmul_by_shape(it):
+    """The library profiler's GEMM launches keyed as the reference's Profiler::record_matmul_shape
+    keys them (src/ops/mps_gemm.rs:22-30,421-422): A and B as stored, "^T" on a transposed operand;
+    a grouped launch counts once per GEMM."""
+    from irontensor_amd import profiler
+    ctx = it.Context.global_()
+    x = it.Tensor.from_f32_slice(synth.normal(1, (4096, 256)), [4096, 256])
+    w = it.Tensor.from_f32_slice(synth.normal(2, (768, 256), std=0.02), [768, 256])
+    a = it.Tensor.from_f32_slice(synth.normal(3, (64, 32)), [64, 32])
+    b = it.Tensor.from_f32_slice(synth.normal(4, (32, 48)), [32, 48])
+    dy = it.Tensor.from_f32_slice(synth.normal(5, (4096, 768)), [4096, 768])
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    it.matmul_mps_nt(x, w)
+    it.matmul_mps_nt(x, w)
+    it.matmul(a, b)
+    it.matmul_mps_tn(dy, x)
+    shapes = profiler.matmul_by_shape(ctx)
+    profiler.enable(ctx, False)
+    print(f"[profiler shapes] {shapes}", flush=True)
+    assert shapes["[4096,256]x[768,256]^T"]["count"] == 2
+    assert shapes["[64,32]x[32,48]"]["count"] == 1
+    assert shapes["[4096,768]^Tx[4096,256]"]["count"] == 1
+    assert all(v["total_ms"] > 0 for v in shapes.values())

@@ -554,7 +554,7 @@ def test_bf16_uneven_tile_counts_exact(it, ta, tb, m, n, k):
     assert np.array_equal(c.numpy(), again.numpy())
 
 
-@pytest.mark.parametrize("ta,tb,m,n,k", [(0, 0, 4096, 1152, 1024), (0, 1, 2048, 1152, 2048), (1, 0, 1024, 896, 4096),
+@pytest.mark.parametrize("ta,tb,m,n,k", [(0, 0, 4096, 1152, 1024), (0, 1, 4096, 1152, 2048), (1, 0, 1024, 896, 4096),
                                          (1, 1, 4096, 1152, 256), (0, 0, 8192, 1024, 1024), (1, 0, 1024, 1024, 8192)])
 def test_bf16_dtl_256x128_exact(it, ta, tb, m, n, k):
     """The 256 x 128 direct-to-LDS tile (each wave 128 x 64; B staged as 128 rows) in every
@@ -665,3 +665,25 @@ def test_bf16_large_tile_epilogues(it, oracle):
                 trans_b=True, bias=it.Tensor.from_f32_slice(bias, bias.shape))
     ref = (a.astype(np.float64) @ b.astype(np.float64).T) + bias
     assert normwise_rel(y.numpy(), ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 1024, 1024), (2048, 2048, 2048), (1152, 640, 1344)])
+def test_bf16_nt_128_tile_exact(it, m, n, k):
+    """BF16 Y = X.W^T at shapes the planner runs on the 128 x 128 direct-to-LDS tile (four LDS
+    stages; 1344 = 21 k-tiles, an odd count): exact on small integers against an int64 product."""
+    from irontensor_amd import profiler
+    x = synth.small_ints(800 + m, (m, k), -3, 3)
+    w = synth.small_ints(801 + n, (n, k), -3, 3)
+    tx, tw = it.Tensor.from_f32_as_bf16(x, x.shape), it.Tensor.from_f32_as_bf16(w, w.shape)
+    out = it.Tensor.zeros([m, n])
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    it.gemm(tx, tw, trans_b=True, out=out)
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    print(f"[bf16 nt 128] {keys}", flush=True)
+    if (m, n) != (1152, 640):
+        assert "128x128_dtl" in keys[0], keys
+    ref = x.astype(np.int64) @ w.T.astype(np.int64)
+    assert np.array_equal(out.numpy(), ref.astype(np.float32))
