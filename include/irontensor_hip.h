@@ -25,7 +25,15 @@
 extern "C" {
 #endif
 
-typedef enum it_status {
+/* The enums have int as their underlying type in C++ as well (IT_ENUM_INT), so that any int a C
+ * caller passes is a valid value there and is refused by the argument checks, not undefined. */
+#ifdef __cplusplus
+#define IT_ENUM_INT : int
+#else
+#define IT_ENUM_INT
+#endif
+
+typedef enum it_status IT_ENUM_INT {
     IT_OK = 0,
     IT_ERR_INNER_DIM = 1,   /* TensorError::InnerDimensionMismatch (src/error.rs:28-33) */
     IT_ERR_SHAPE = 2,       /* TensorError::ShapeMismatch (src/error.rs:9-14) */
@@ -39,8 +47,8 @@ typedef enum it_status {
     IT_ERR_NOT_READY = 10   /* it_event_query: work not finished yet (not a failure) */
 } it_status;
 
-typedef enum it_dtype { IT_F32 = 0, IT_F16 = 1, IT_BF16 = 2 } it_dtype;
-typedef enum it_op { IT_OP_N = 0, IT_OP_T = 1 } it_op;
+typedef enum it_dtype IT_ENUM_INT { IT_F32 = 0, IT_F16 = 1, IT_BF16 = 2 } it_dtype;
+typedef enum it_op IT_ENUM_INT { IT_OP_N = 0, IT_OP_T = 1 } it_op;
 
 typedef struct it_context it_context;
 typedef struct it_event it_event;

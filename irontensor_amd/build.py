@@ -81,6 +81,60 @@ def build_cpp_tests() -> Path:
     return CPP_TEST_BIN
 
 
+SAN_DIR = ROOT / "tests" / "cpp" / "_build" / "sanitize"
+CLANG = os.environ.get("CLANGXX", "/opt/rocm/llvm/bin/clang++")
+SAN_FLAGS = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-fno-omit-frame-pointer", "-g"]
+
+
+def _clang_rt_dir() -> str:
+    """Directory of clang's sanitizer runtimes (libclang_rt.asan-x86_64.so)."""
+    res = subprocess.run([CLANG, "-print-file-name=libclang_rt.asan-x86_64.so"], stdout=subprocess.PIPE, text=True)
+    path = Path(res.stdout.strip())
+    if not path.is_file():
+        hits = sorted(Path(CLANG).resolve().parents[1].glob("lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+        path = hits[-1] if hits else path
+    return str(path.parent)
+
+
+def build_sanitized_host() -> Path:
+    """The library's host code (runtime, argument checks, dispatch: the .cpp sources) under
+    AddressSanitizer + UndefinedBehaviorSanitizer, linked with the kernel objects of the last
+    build_library(), and the C++ host-API test against it: for `test_host_api --cpu`, which needs
+    no GPU. Returns the test binary."""
+    if not all((BUILD / (n + ".o")).exists() for n in SOURCES if n.endswith(".hip")):
+        build_library()
+    SAN_DIR.mkdir(parents=True, exist_ok=True)
+    procs, objs = [], []
+    for name in SOURCES:
+        if name.endswith(".hip"):
+            objs.append(BUILD / (name + ".o"))
+            continue
+        obj = SAN_DIR / (name + ".o")
+        objs.append(obj)
+        cmd = [CLANG, "-std=c++17", "-O1", "-fPIC", *SAN_FLAGS, "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+               f"-I{ROOT / 'include'}", f"-I{CSRC}", "-c", str(CSRC / name), "-o", str(obj)]
+        procs.append((name, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    for name, p in procs:
+        out, _ = p.communicate()
+        if p.returncode != 0:
+            raise RuntimeError(f"sanitized build of {name} failed:\n{out}")
+    lib = SAN_DIR / "libirontensor_hip.so"
+    res = subprocess.run([CLANG, "-shared", "-fPIC", *SAN_FLAGS, "-shared-libsan", "-o", str(lib), *map(str, objs),
+                          "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"],
+                         stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"sanitized link failed:\n{res.stdout}")
+    exe = SAN_DIR / "test_host_api"
+    res = subprocess.run([CLANG, "-std=c++17", "-O1", *SAN_FLAGS, "-shared-libsan", f"-I{ROOT / 'include'}",
+                          str(CPP_TEST_SRC), "-o", str(exe), f"-L{SAN_DIR}", "-lirontensor_hip",
+                          f"-Wl,-rpath,{SAN_DIR}", "-Wl,-rpath,/opt/rocm/lib",
+                          f"-Wl,-rpath,{_clang_rt_dir()}"],
+                         stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"sanitized C++ test build failed:\n{res.stdout}")
+    return exe
+
+
 if __name__ == "__main__":
     print(build_library(verbose=True))
     print(build_cpp_tests())
