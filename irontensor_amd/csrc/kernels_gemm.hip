@@ -83,7 +83,14 @@ __device__ __forceinline__ u32x4 load_vec(const T *base, int64_t off, bool row_o
 //   LOAD_MASKED  16-byte vectors are aligned and never straddle an edge, so a vector is either
 //                wholly in bounds or wholly out: branch-free load of a safe address + select;
 //   LOAD_CHECKED anything else: per-element bounds checks.
-enum LoadMode : int { LOAD_EXACT = 0, LOAD_MASKED = 1, LOAD_CHECKED = 2 };
+//   LOAD_RSRC    (FP32, 16-byte vectors as LOAD_MASKED, K a multiple of the k-tile where an operand
+//                is k-contiguous) buffer loads through a descriptor that ends where the operand's
+//                valid rows (k-contiguous) or k (mn-contiguous) end, from 32-bit offsets formed once
+//                per block: the hardware's range check returns zeros past that end, with no
+//                per-load address arithmetic or selects. An mn-contiguous operand's columns past
+//                M (or N) read whatever follows within the buffer; they reach only output rows
+//                (columns) past M (N), which the epilogue never stores.
+enum LoadMode : int { LOAD_EXACT = 0, LOAD_MASKED = 1, LOAD_CHECKED = 2, LOAD_RSRC = 3 };
 
 template <int MODE, typename T>
 __device__ __forceinline__ u32x4 load_mode(const T *base, int64_t off, bool row_ok, int64_t c,
@@ -299,6 +306,45 @@ struct Operand {
     }
 };
 
+// LOAD_RSRC addressing of one FP32 operand tile (Operand<float, KCONTIG, ROWS>'s items): the
+// descriptor and each item's byte offset at k-tile 0; a k-tile adds k0 * kstride bytes.
+template <bool KCONTIG, int ROWS>
+struct RsrcLoad {
+    using O = Operand<float, KCONTIG, ROWS>;
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t voff[O::ITERS];
+    uint32_t kstride;
+
+    // base: the operand of this batch item; records: its valid bytes (rows * ld * 4 k-contiguous,
+    // K * ld * 4 otherwise); r0: the tile's first row.
+    __device__ __forceinline__ void init(const float *base, int64_t ld, int64_t r0, int64_t records, int tid) {
+        const int n = records > 0x7fffffff ? 0x7fffffff : (int)records;
+        rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, n, 0x00020000);
+        kstride = KCONTIG ? 4u : (uint32_t)(ld * 4);
+#pragma unroll
+        for (int it = 0; it < O::ITERS; ++it) {
+            const int item = tid + it * NTHREADS;
+            if constexpr (KCONTIG) {
+                const int rr = item / (O::BK / O::VEC), kc = item % (O::BK / O::VEC);
+                voff[it] = (uint32_t)(((r0 + rr) * ld + kc * O::VEC) * 4);
+            } else {
+                const int kk = item / (ROWS / O::VEC), rc = item % (ROWS / O::VEC);
+                voff[it] = (uint32_t)((kk * ld + r0 + rc * O::VEC) * 4);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void load(O &o, int64_t k0, int tid) const {
+        const uint32_t koff = (uint32_t)k0 * kstride;
+#pragma unroll
+        for (int it = 0; it < O::ITERS; ++it) {
+            const int item = tid + it * NTHREADS;
+            if (O::ITEMS % NTHREADS != 0 && item >= O::ITEMS) continue;
+            o.reg[it][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[it] + koff, 0, 0));
+        }
+    }
+};
+
 template <typename T>
 __device__ __forceinline__ void mma(f32x4 &acc, const u32x4 &a, const u32x4 &b) {
     if constexpr (sizeof(T) == 4) {
@@ -398,6 +444,14 @@ __device__ __forceinline__ void gemm_mfma_block(const GemmArgs &p, int tile, int
 
     // Register staging sets: PF of them, so the loads of tile t+PF are issued during tile t.
     OA oa[PF];
+    constexpr bool RSRC = LM == LOAD_RSRC;
+    static_assert(!RSRC || (sizeof(T) == 4 && !DUAL && !KS && !XF), "LOAD_RSRC: plain FP32 tiles");
+    RsrcLoad<!TA, BM> ra;
+    RsrcLoad<TB, BN> rb;
+    if constexpr (RSRC) {
+        ra.init((const float *)A, p.lda, m0, TA ? p.K * p.lda * 4 : p.M * p.lda * 4, tid);
+        rb.init((const float *)B, p.ldb, n0, TB ? p.N * p.ldb * 4 : p.K * p.ldb * 4, tid);
+    }
     // SwiGLU (DUAL): the B tile's rows 0..BN/2-1 are gate-weight rows and BN/2..BN-1 the same up-
     // weight rows, so waves wn = 0 / 1 accumulate gate / up of one BM x BN/2 output tile and the
     // loop is the ordinary one.
@@ -407,11 +461,16 @@ __device__ __forceinline__ void gemm_mfma_block(const GemmArgs &p, int tile, int
 #pragma unroll
         for (int q = 0; q < PF; ++q)
             if (q == set) {
-                oa[q].template load<LM>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
-                if constexpr (KS) oa[q].load_kscale(p.a_kscale, k0, ke, tid);
-                if constexpr (XF) oa[q].load_xent(p.xent_stats, p.xent_tgt, m0, k0, p.M, ke, tid);
-                ob[q].template load<LM>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
-                if constexpr (DUAL) ob2[q].template load<LM>(B2, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
+                if constexpr (RSRC) {
+                    ra.load(oa[q], k0, tid);
+                    rb.load(ob[q], k0, tid);
+                } else {
+                    oa[q].template load<LM>(A, p.lda, m0, k0, p.M, ke, p.a_vec_ok, tid);
+                    if constexpr (KS) oa[q].load_kscale(p.a_kscale, k0, ke, tid);
+                    if constexpr (XF) oa[q].load_xent(p.xent_stats, p.xent_tgt, m0, k0, p.M, ke, tid);
+                    ob[q].template load<LM>(B, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
+                    if constexpr (DUAL) ob2[q].template load<LM>(B2, p.ldb, n0, k0, p.N, ke, p.b_vec_ok, tid);
+                }
             }
     };
     // KS: per-thread partial sums of squares of its A rows, over the k-tiles written to LDS.
@@ -1465,14 +1524,50 @@ bool vectors_exact(const GemmArgs &a, bool ta, bool tb) {
     return a.a_vec_ok && a.b_vec_ok && a.K % VEC == 0 && (!ta || a.M % VEC == 0) && (tb || a.N % VEC == 0);
 }
 
+// LOAD_RSRC (FP32): 16-byte vectors as LOAD_MASKED, no k tail inside a k-contiguous operand's rows
+// (K a multiple of the k-tile), and each operand's valid bytes within a 32-bit range.
+bool rsrc_ok(const GemmArgs &a, bool ta, bool tb) {
+    const bool kcontig = !ta || tb;
+    return vectors_exact<float>(a, ta, tb) && (!kcontig || a.K % ET<float>::BK == 0) &&
+           (ta ? a.K : a.M) * a.lda * 4 < (1ll << 31) && (tb ? a.N : a.K) * a.ldb * 4 < (1ll << 31);
+}
+
+// The load mode of a plain tile: exact, buffer-descriptor (FP32), masked or checked.
+template <typename T>
+int load_mode_for(const GemmArgs &a, bool ta, bool tb, int bm, int bn) {
+    int mode = tiles_exact(a, bm, bn, ET<T>::BK)                        ? LOAD_EXACT
+               : sizeof(T) == 4 && rsrc_ok(a, ta, tb)                     ? LOAD_RSRC
+               : vectors_exact<T>(a, ta, tb)                              ? LOAD_MASKED
+                                                                          : LOAD_CHECKED;
+#ifdef IT_TUNING
+    // Planner sweeps only: IT_LOAD_MODE=masked|rsrc forces one of the two where both apply.
+    if (const char *env = std::getenv("IT_LOAD_MODE")) {
+        const std::string m(env);
+        if (sizeof(T) == 4 && m == "rsrc" && rsrc_ok(a, ta, tb)) mode = LOAD_RSRC;
+        if (m == "masked" && mode == LOAD_RSRC) mode = LOAD_MASKED;
+    }
+#endif
+    return mode;
+}
+
 template <typename T, bool TA, bool TB, bool DUAL>
 hipError_t launch_cfg(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
-    if (tiles_exact(a, cfg.bm, DUAL ? cfg.bn / 2 : cfg.bn, ET<T>::BK))
+    const int mode = DUAL ? (tiles_exact(a, cfg.bm, cfg.bn / 2, ET<T>::BK) ? LOAD_EXACT
+                             : vectors_exact<T>(a, TA, TB)                  ? LOAD_MASKED
+                                                                            : LOAD_CHECKED)
+                          : load_mode_for<T>(a, TA, TB, cfg.bm, cfg.bn);
+    if (mode == LOAD_EXACT)
         launch_cfg_lm<T, TA, TB, DUAL, LOAD_EXACT>(cfg, a, grid, s);
-    else if (vectors_exact<T>(a, TA, TB))
+    else if (mode == LOAD_MASKED)
         launch_cfg_lm<T, TA, TB, DUAL, LOAD_MASKED>(cfg, a, grid, s);
-    else
+    else if constexpr (sizeof(T) == 4 && !DUAL) {
+        if (mode == LOAD_RSRC)
+            launch_cfg_lm<T, TA, TB, DUAL, LOAD_RSRC>(cfg, a, grid, s);
+        else
+            launch_cfg_lm<T, TA, TB, DUAL, LOAD_CHECKED>(cfg, a, grid, s);
+    } else {
         launch_cfg_lm<T, TA, TB, DUAL, LOAD_CHECKED>(cfg, a, grid, s);
+    }
     return hipGetLastError();
 }
 
@@ -1910,7 +2005,7 @@ bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int cou
     GemmGroupArgs grp{};
     grp.count = count;
     int64_t r4 = 0, scratch = 0;
-    bool exact = true, masked = true;
+    bool exact = true, masked = true, rsrc = true;
     for (int i = 0; i < count; ++i) {
         GemmArgs &a = grp.g[i];
         a = args[i];
@@ -1926,6 +2021,7 @@ bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int cou
         }
         exact = exact && tiles_exact(a, 64, 64, bk);
         masked = masked && vectors_exact<float>(a, ta, tb);
+        rsrc = rsrc && load_mode_for<float>(a, ta, tb, 64, 64) != LOAD_MASKED && rsrc_ok(a, ta, tb);
     }
     grp.rstart[count] = r4;
     const int grid_blocks = xcd_schedule(grp);
@@ -1960,6 +2056,7 @@ bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int cou
         else hipLaunchKernelGGL((gemm_f32_group<true, true, LM>), grid, dim3(NTHREADS), 0, ctx->stream, grp);
     };
     if (exact) go(std::integral_constant<int, LOAD_EXACT>{});
+    else if (rsrc) go(std::integral_constant<int, LOAD_RSRC>{});
     else if (masked) go(std::integral_constant<int, LOAD_MASKED>{});
     else go(std::integral_constant<int, LOAD_CHECKED>{});
     hipError_t e = hipGetLastError();
