@@ -87,9 +87,11 @@ __device__ __forceinline__ u32x4 load_vec(const T *base, int64_t off, bool row_o
 //                is k-contiguous) buffer loads through a descriptor that ends where the operand's
 //                valid rows (k-contiguous) or k (mn-contiguous) end, from 32-bit offsets formed once
 //                per block: the hardware's range check returns zeros past that end, with no
-//                per-load address arithmetic or selects. An mn-contiguous operand's columns past
-//                M (or N) read whatever follows within the buffer; they reach only output rows
-//                (columns) past M (N), which the epilogue never stores.
+//                per-load address arithmetic or selects. The descriptor spans exactly the
+//                operand's elements (first to last, not whole row strides, which can reach past the
+//                allocation for a strided head). An mn-contiguous operand's columns past M (or N)
+//                read the next row's elements, or zeros past the last element; they reach only
+//                output rows (columns) past M (N), which the epilogue never stores.
 enum LoadMode : int { LOAD_EXACT = 0, LOAD_MASKED = 1, LOAD_CHECKED = 2, LOAD_RSRC = 3 };
 
 template <int MODE, typename T>
@@ -315,8 +317,9 @@ struct RsrcLoad {
     uint32_t voff[O::ITERS];
     uint32_t kstride;
 
-    // base: the operand of this batch item; records: its valid bytes (rows * ld * 4 k-contiguous,
-    // K * ld * 4 otherwise); r0: the tile's first row.
+    // base: the operand of this batch item; records: its extent in bytes, ((rows - 1) * ld + K) * 4
+    // k-contiguous, ((K - 1) * ld + rows) * 4 otherwise (exactly the operand's span: a row stride past
+    // the last element may leave the allocation); r0: the tile's first row.
     __device__ __forceinline__ void init(const float *base, int64_t ld, int64_t r0, int64_t records, int tid) {
         const int n = records > 0x7fffffff ? 0x7fffffff : (int)records;
         rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, n, 0x00020000);
@@ -449,8 +452,8 @@ __device__ __forceinline__ void gemm_mfma_block(const GemmArgs &p, int tile, int
     RsrcLoad<!TA, BM> ra;
     RsrcLoad<TB, BN> rb;
     if constexpr (RSRC) {
-        ra.init((const float *)A, p.lda, m0, TA ? p.K * p.lda * 4 : p.M * p.lda * 4, tid);
-        rb.init((const float *)B, p.ldb, n0, TB ? p.N * p.ldb * 4 : p.K * p.ldb * 4, tid);
+        ra.init((const float *)A, p.lda, m0, (TA ? (p.K - 1) * p.lda + p.M : (p.M - 1) * p.lda + p.K) * 4, tid);
+        rb.init((const float *)B, p.ldb, n0, (TB ? (p.N - 1) * p.ldb + p.K : (p.K - 1) * p.ldb + p.N) * 4, tid);
     }
     // SwiGLU (DUAL): the B tile's rows 0..BN/2-1 are gate-weight rows and BN/2..BN-1 the same up-
     // weight rows, so waves wn = 0 / 1 accumulate gate / up of one BM x BN/2 output tile and the
