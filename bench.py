@@ -174,7 +174,58 @@ def extra_attention(it, timer) -> dict:
                      "tflops_useful": round(tf * useful, 1),
                      "frac_bf16_peak_useful": round(tf * useful / PEAK_TFLOPS["bf16"], 4)}
     res["useful_fraction"] = round(useful, 5)
+    res["torch_sdpa_same_run"] = (sdpa_library(b, h, s, d, unit * useful) if TORCH_STATE["ready"]
+                                  else {"skipped": TORCH_STATE["error"] or "torch not initialised first"})
     return {"config3_bf16_attention_16x8x1024x64_causal": res}
+
+
+def sdpa_library(b: int, h: int, s: int, d: int, useful_unit: float) -> dict:
+    """PyTorch's fused attention on the same box and in the same process, for comparison: causal
+    scaled_dot_product_attention (scale 1/8) on BF16 [b, h, s, d] with the flash and the
+    memory-efficient backends only (the math backend, batched BF16 products on a transposed K, is
+    never selected). Forward timed alone, backward as forward + backward minus forward; TFLOP/s on
+    the same useful-FLOP count as the fused kernels (2 and 5 GEMMs of 2*B*H*S*S*D times the
+    causal fraction)."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(0)
+    q, k, v, do = (torch.randn(b, h, s, d, device="cuda:0", dtype=torch.bfloat16, generator=g) for _ in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, iters):
+        fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    out = {}
+    for name, backend in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        try:
+            with sdpa_kernel([backend]):
+                fwd = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.125)  # noqa: E731
+
+                def fwd_bwd():
+                    q.grad = k.grad = v.grad = None
+                    fwd().backward(do)
+
+                f_ms = timed(fwd, 10)
+                b_ms = timed(fwd_bwd, 5) - f_ms
+            out[name] = {"forward_ms": round(f_ms, 4), "forward_tflops_useful": round(2 * useful_unit / f_ms / 1e9, 1),
+                         "backward_ms": round(b_ms, 4),
+                         "backward_tflops_useful": round(5 * useful_unit / b_ms / 1e9, 1)}
+        except RuntimeError as e:  # the backend is not built for this device
+            out[name] = f"unavailable: {str(e)[:160]}"
+    del q, k, v, do
+    torch.cuda.empty_cache()
+    return out
 
 
 def attention_only(it, timer, reps: int) -> dict:
@@ -663,8 +714,8 @@ def main() -> int:
               "(irontensor_amd/libirontensor_hip.so), unset it", file=sys.stderr)
         return 2
 
-    if args.vs_library or not (args.no_extra or args.kernel_only or args.train_only or args.bf16_square
-                               or args.attention or args.medium_step or args.decode):
+    if args.vs_library or args.attention or not (args.no_extra or args.kernel_only or args.train_only
+                                                 or args.bf16_square or args.medium_step or args.decode):
         init_torch_first()
         if args.vs_library and not TORCH_STATE["ready"]:
             print(f"bench.py: torch could not take the device: {TORCH_STATE['error']}", file=sys.stderr)
@@ -688,7 +739,11 @@ def main() -> int:
               flush=True)
         return 0
     if args.attention:
-        print(json.dumps(attention_only(it, Timer(ctx), args.steps)), flush=True)
+        out = attention_only(it, Timer(ctx), args.steps)
+        if TORCH_STATE["ready"]:
+            out["torch_sdpa_bf16_16x8x1024x64_causal"] = sdpa_library(16, 8, 1024, 64,
+                                                                      2.0 * 16 * 8 * 1024 ** 2 * 64 * 1025 / 2048)
+        print(json.dumps(out), flush=True)
         return 0
     if args.vs_library:
         print(json.dumps(vs_library(it, Timer(ctx), sizes=((4096, args.steps), (8192, max(2, args.steps // 4))))),

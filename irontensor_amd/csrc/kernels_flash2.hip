@@ -17,10 +17,11 @@
 //     from the accumulators as B operands; the LDS operand they meet (V^T, K^T, dO^T, Q^T) is read
 //     transposed with the same k order: lane group h = l / 32 holds rows 4h..4h+3 and 8+4h..8+4h+3
 //     of each 16-row chunk.
-//   * Forward softmax: the row max is taken on the raw scores, probabilities are
-//     exp2(s * scale * log2 e - m) (one FMA and one v_exp_f32 each), and the output is rescaled only
-//     when the running max grows by more than 8 (log2 units: probabilities then stay below 2^8 and
-//     the final division by the row sum cancels the factor); P is rounded to BF16 before its MFMA.
+//   * Forward softmax, per 32-key half tile: the row max is taken on the raw scores, probabilities
+//     are exp2(s * scale * log2 e - m) (one FMA and one v_exp_f32 each), and the output and row sum
+//     are rescaled only when the running max grows by more than 8 (log2 units: probabilities then
+//     stay below 2^8 and the final division by the row sum cancels the factor); the row sum adds
+//     the FP32 probabilities, and P is rounded to BF16 before its MFMA.
 // The backward is deterministic (dQ and dK/dV from two kernels, no atomics). O (written by the
 // forward, read by the backward's row pass) and dQ, dK, dV are FP32, or BF16 (round to nearest
 // even) when the caller asks for BF16 outputs.
@@ -57,37 +58,19 @@ __device__ __forceinline__ f32x16 zero16() {
     return f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 }
 
-// Row-major fragment: lane l reads row r0 + l % 32, d = 16 ks + 8 (l / 32) .. +7.
-__device__ __forceinline__ u32x4 frag_rm(const char *tile, int r0, int ks, int lane) {
-    const int r = r0 + (lane & 31);
-    const int c = 2 * ks + (lane >> 5);
-    return *(const u32x4 *)(tile + r * 128 + ((c ^ swz(r)) << 4));
-}
-
-// Transposed fragment: lane l gets column c0 + l % 32 at tile rows k0 + 4h + 0..3 and
-// k0 + 8 + 4h + 0..3 (h = l / 32). ds_read_tr16_b64 hands lane i of a 16-lane group the 4 rows
-// its group points at (lane j of the group points at row j / 4, columns 4 (j % 4) .. +3).
-__device__ __forceinline__ u32x4 frag_tr(const char *tile, int c0, int k0, int lane) {
-    const int g = lane >> 4, j = lane & 15;
-    const int col = c0 + 16 * (g & 1) + 4 * (j & 3);
-    const int r1 = k0 + 4 * (g >> 1) + (j >> 2);
-    const int chunk = col >> 3, half = (j & 1) << 3;
-    const int r2 = r1 + 8;
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_s16x4_t *)(tile + r1 * 128 + ((chunk ^ swz(r1)) << 4) + half));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_s16x4_t *)(tile + r2 * 128 + ((chunk ^ swz(r2)) << 4) + half));
-    const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
-    return u32x4{a[0], a[1], b[0], b[1]};
-}
-
-// Per-lane LDS byte offsets of the fragment reads, computed once per kernel: the swizzle depends
-// only on row bits 1..3, so the row block (a multiple of 16 rows), the k chunk of a transposed
-// read and the stage are compile-time offsets added to these (ds_read immediates). Kept opaque
-// so the compiler holds them in 8 registers instead of recomputing the swizzle for every read.
+// Fragment reads of a 64-row tile (128 bytes per row, swizzled as above):
+//   row-major    lane l reads row r0 + l % 32, d = 16 ks + 8 (l / 32) .. +7 (one ds_read_b128);
+//   transposed   lane l gets column c0 + l % 32 at tile rows k0 + 4h + 0..3 and k0 + 8 + 4h + 0..3
+//                (h = l / 32), from two ds_read_tr16_b64: that instruction hands lane i of a 16-lane
+//                group the 4 rows its group points at (lane j of the group points at row j / 4,
+//                columns 4 (j % 4) .. +3).
+// Per-lane LDS byte offsets of these reads are computed once per kernel: the swizzle depends only on
+// row bits 1..3, so the row block (a multiple of 16 rows), the k chunk of a transposed read and the
+// stage are compile-time offsets added to them (ds_read immediates). Kept opaque so the compiler
+// holds them in 8 registers instead of hoisting a swizzled address per read out of the loop.
 struct FragOff {
-    uint32_t rm[4];     // frag_rm at r0 = 0, ks = 0..3
-    uint32_t tr[2][2];  // frag_tr at c0 = 32 dh, k0 = 0: rows r1 (lo) and r1 + 8 (hi)
+    uint32_t rm[4];     // row-major at r0 = 0, ks = 0..3
+    uint32_t tr[2][2];  // transposed at c0 = 32 dh, k0 = 0: rows r1 (lo) and r1 + 8 (hi)
 };
 
 __device__ __forceinline__ FragOff frag_offsets(int lane) {
@@ -110,12 +93,12 @@ __device__ __forceinline__ FragOff frag_offsets(int lane) {
     return f;
 }
 
-// frag_rm(tile, r0, ks, lane) with r0 a multiple of 16.
+// Row-major fragment at row r0 (a multiple of 16), k step ks.
 __device__ __forceinline__ u32x4 frag_rm_o(const char *tile, const FragOff &f, int r0, int ks) {
     return *(const u32x4 *)(tile + r0 * 128 + f.rm[ks]);
 }
 
-// frag_tr(tile, c0, k0, lane) with c0 = 0 or 32 and k0 a multiple of 16.
+// Transposed fragment at column c0 (0 or 32), row k0 (a multiple of 16).
 __device__ __forceinline__ u32x4 frag_tr_o(const char *tile, const FragOff &f, int c0, int k0) {
     const int dh = c0 >> 5;
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(tile + k0 * 128 + f.tr[dh][0]));
@@ -124,11 +107,8 @@ __device__ __forceinline__ u32x4 frag_tr_o(const char *tile, const FragOff &f, i
     return u32x4{a[0], a[1], b[0], b[1]};
 }
 
-// B operand for key (or query) chunk c from a 32x32 accumulator pair: values j = 8 (c % 2) .. +7 of
-// block c / 2, rounded to BF16.
-__device__ __forceinline__ u32x4 pack_chunk(const f32x16 (&s)[2], int c) {
-    const f32x16 &v = s[c >> 1];
-    const int j0 = 8 * (c & 1);
+// B operand from accumulator values j0 .. j0 + 7 of a 32x32 block (a 16-row chunk), rounded to BF16.
+__device__ __forceinline__ u32x4 pack8(const f32x16 &v, int j0) {
     return u32x4{pack_bf16x2(v[j0], v[j0 + 1]), pack_bf16x2(v[j0 + 2], v[j0 + 3]), pack_bf16x2(v[j0 + 4], v[j0 + 5]),
                  pack_bf16x2(v[j0 + 6], v[j0 + 7])};
 }
@@ -238,10 +218,12 @@ __device__ __forceinline__ float pair_max(float x) {
 
 // ------------------------------------------------------------------ forward
 
-// Three waves per SIMD (168 registers): the forward's max -> exp -> P.V chain is serial within a wave,
-// and a third wave hides more of it than software pipelining within the wave (which needs registers
-// for two score tiles and so allows only two).
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void flash2_fwd(const FlashArgs p) {
+// Four waves per SIMD (at most 128 registers): the forward's max -> exp -> P.V chain is serial within
+// a wave, so each 64-key tile is taken as two 32-key halves (one 16-register score block live, not
+// two) and the row sum is added on the VALU instead of through an extra MFMA per chunk; four blocks
+// of 32 KB LDS fit a CU. Measured against three waves with whole-tile softmax and the MFMA row sum:
+// config 3 causal forward 36.4 -> 33.7 us.
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void flash2_fwd(const FlashArgs p) {
     __shared__ __attribute__((aligned(1024))) char st0[2 * TB];  // K tile, V tile
     __shared__ __attribute__((aligned(1024))) char st1[2 * TB];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -268,13 +250,10 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void f
         const u32x4 v = ld16(Q + (qok ? (int64_t)q * p.q_rs + 16 * ks + 8 * h : 0));
         qf[ks] = qok ? v : u32x4{0u, 0u, 0u, 0u};
     }
-    // o[0], o[1]: O^T rows d 0..31, 32..63; o[2]: row 0 accumulates the row sum of P through the
-    // same MFMAs (A = a ones row), so the softmax denominator costs no VALU adds and uses the same
-    // BF16-rounded probabilities as the numerator.
-    f32x16 o[3] = {zero16(), zero16(), zero16()};
+    // o[0], o[1]: O^T rows d 0..31, 32..63.
+    f32x16 o[2] = {zero16(), zero16()};
     float m = -INFINITY;  // running max (log2 units) used by the probabilities
-    const uint32_t one2 = (lane & 31) == 0 ? 0x3f803f80u : 0u;  // BF16 1.0 pair in row 0 only
-    const u32x4 ones = {one2, one2, one2, one2};
+    float lsum = 0.f;     // this lane's share (its 32 of each tile's 64 keys) of the row sum
 
     const int kblocks = (int)((p.skv + TR - 1) / TR);
     const int nkb = p.causal ? min(kblocks, (qb * RB + RB - 1) / TR + 1) : kblocks;
@@ -287,59 +266,53 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void f
         sv.issue(st + TB, t, wave);
     }, [&](int t, const char *st) {
         const char *kt = st, *vt = st + TB;
-        // S^T (keys x queries): block kh holds keys 32kh + 8 (j / 4) + 4h + j % 4 of query q.
-        f32x16 s[2] = {zero16(), zero16()};
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) s[kh] = mfma32(frag_rm_o(kt, fo, 32 * kh, ks), qf[ks], s[kh]);
-        // Keys past seq_kv, and (causal) keys past the query, are -inf. Only blocks that reach past
-        // the first query of this workgroup or past seq_kv hold such keys.
         const int k0 = t * TR;
-        if ((p.causal && k0 + TR - 1 > qb * RB) || k0 + TR > skv) {
-            // a key is dead past seq_kv, or (causal) past the query
-            const int lim = p.causal ? min(skv - 1, q) : skv - 1;
+        const bool edge = (p.causal && k0 + TR - 1 > qb * RB) || k0 + TR > skv;
+        const int lim = p.causal ? min(skv - 1, q) : skv - 1;
+        // Two halves of 32 keys: S^T block (keys 32kh + 8 (j / 4) + 4h + j % 4 of query q),
+        // softmax, then its share of O^T += V^T . P^T.
 #pragma unroll
-            for (int kh = 0; kh < 2; ++kh)
+        for (int kh = 0; kh < 2; ++kh) {
+            f32x16 sh = zero16();
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) sh = mfma32(frag_rm_o(kt, fo, 32 * kh, ks), qf[ks], sh);
+            if (edge) {
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     const int key = k0 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
-                    s[kh][j] = key > lim ? -INFINITY : s[kh][j];
+                    sh[j] = key > lim ? -INFINITY : sh[j];
                 }
+            }
+            float m4[4] = {sh[0], sh[1], sh[2], sh[3]};
+#pragma unroll
+            for (int j = 4; j < 16; ++j) m4[j & 3] = vmax(m4[j & 3], sh[j]);
+            const float mx = pair_max(vmax(vmax(m4[0], m4[1]), vmax(m4[2], m4[3]))) * c2;
+            if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE) != 0) {
+                const float mn = fmaxf(m, mx);
+                const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+                o[0] *= alpha;
+                o[1] *= alpha;
+                lsum *= alpha;
+                m = mn;
+            }
+            const float nm = m == -INFINITY ? 0.f : -m;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sh[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sh[j], c2, nm));
+            float ls4[4] = {sh[0], sh[1], sh[2], sh[3]};
+#pragma unroll
+            for (int j = 4; j < 16; ++j) ls4[j & 3] += sh[j];
+            lsum += (ls4[0] + ls4[1]) + (ls4[2] + ls4[3]);
+            u32x4 pf[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                pf[c] = pack8(sh, 8 * c);
+#pragma unroll
+            for (int dh = 0; dh < 2; ++dh)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) o[dh] = mfma32(frag_tr_o(vt, fo, 32 * dh, 16 * (2 * kh + c)), pf[c], o[dh]);
         }
-        // Four independent max and sum chains: a single chain serialises on VALU latency; the lane
-        // pair's max with a permlane swap.
-        float m4[4] = {s[0][0], s[0][1], s[0][2], s[0][3]};
-#pragma unroll
-        for (int j = 4; j < 32; ++j) m4[j & 3] = vmax(m4[j & 3], s[j >> 4][j & 15]);
-        const float mx = pair_max(vmax(vmax(m4[0], m4[1]), vmax(m4[2], m4[3]))) * c2;
-        // Rescale only when some row's max grew by more than RESCALE (wave-uniform branch).
-        if (__builtin_amdgcn_ballot_w64(mx > m + RESCALE) != 0) {
-            const float mn = fmaxf(m, mx);
-            const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
-            o[0] *= alpha;
-            o[1] *= alpha;
-            o[2][0] *= alpha;  // the row sum (the block's other entries stay zero)
-            m = mn;
-        }
-        const float nm = m == -INFINITY ? 0.f : -m;
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) s[kh][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][j], c2, nm));
-        // O^T (d x queries) += V^T (d x keys) . P^T (keys x queries), and the row sums
-        u32x4 pf[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) pf[c] = pack_chunk(s, c);
-#pragma unroll
-        for (int dh = 0; dh < 2; ++dh)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) o[dh] = mfma32(frag_tr_o(vt, fo, 32 * dh, 16 * c), pf[c], o[dh]);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o[2] = mfma32(ones, pf[c], o[2]);
     });
-    // Row 0 of the sum block sits in lanes l < 32 (element 0); lanes l >= 32 hold row 4, zero.
-    const float l = o[2][0] + __shfl_xor(o[2][0], 32, 64);
+    const float l = lsum + __shfl_xor(lsum, 32, 64);
     if (qok) {
         const float inv = l > 0.f ? 1.f / l : 0.f;
         const int64_t orow = ho.base(bh) + (int64_t)q * p.o_rs;
@@ -396,45 +369,43 @@ __device__ __forceinline__ void dq2_block(const FlashArgs &p, int qb, int64_t bh
     Stream sk, sv;
     sk.init(K, p.kv_rs, p.skv, wave, lane);
     sv.init(V, p.kv_rs, p.skv, wave, lane);
+    const FragOff fo = frag_offsets(lane);
     stream_tiles(st0, st1, nkb, [&](char *st, int t) {
         sk.issue(st, t, wave);
         sv.issue(st + TB, t, wave);
     }, [&](int t, const char *st) {
         const char *kt = st, *vt = st + TB;
-        // S^T = K.Q^T and dP^T = V.dO^T: block kh holds keys 32kh + 8 (j / 4) + 4h + j % 4.
-        f32x16 s[2] = {zero16(), zero16()}, dp[2] = {ndl16, ndl16};
+        // One 32-key half of the tile at a time: S^T = K.Q^T and dP^T = V.dO^T (block of keys
+        // 32kh + 8 (j / 4) + 4h + j % 4), P^T = exp2(S^T scale log2 e - LSE log2 e), zero past the
+        // query (causal) and past seq_kv (K and V rows there are zero, but an unmasked probability
+        // could overflow into 0 * inf): masked scores become -inf before the exponential, in a
+        // wave-uniform branch taken only by the tiles that hold such keys. dS^T = P^T (dP^T - rowsum)
+        // then feeds dQ^T (d x queries) += K^T (d x keys) . dS^T (keys x queries).
+        const int k0 = t * TR;
+        const bool edge = (p.causal && k0 + TR - 1 > qb * RB) || k0 + TR > skv;
+        const int lim = p.causal ? min(skv - 1, q) : skv - 1;
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
+        for (int kh = 0; kh < 2; ++kh) {
+            f32x16 sh = zero16(), dph = ndl16;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                s[kh] = mfma32(frag_rm(kt, 32 * kh, ks, lane), qf[ks], s[kh]);
-                dp[kh] = mfma32(frag_rm(vt, 32 * kh, ks, lane), of[ks], dp[kh]);
+                sh = mfma32(frag_rm_o(kt, fo, 32 * kh, ks), qf[ks], sh);
+                dph = mfma32(frag_rm_o(vt, fo, 32 * kh, ks), of[ks], dph);
             }
-        // P^T = exp2(S^T scale log2 e - LSE log2 e), zero past the query (causal) and past seq_kv
-        // (K and V rows there are zero, but an unmasked probability could overflow into 0 * inf).
-        // Masked scores become -inf before the exponential (exp2(-inf) = 0), in a wave-uniform
-        // branch taken only by the tiles that hold such keys.
-        const int k0 = t * TR;
-        if ((p.causal && k0 + TR - 1 > qb * RB) || k0 + TR > skv) {
-            const int lim = p.causal ? min(skv - 1, q) : skv - 1;
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh)
+            if (edge) {
 #pragma unroll
                 for (int j = 0; j < 16; ++j)
-                    s[kh][j] = k0 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3) > lim ? -INFINITY : s[kh][j];
+                    sh[j] = k0 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3) > lim ? -INFINITY : sh[j];
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) dph[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sh[j], c2, nl2)) * dph[j];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const u32x4 df = pack8(dph, 8 * c);
+#pragma unroll
+                for (int dh = 0; dh < 2; ++dh) dq[dh] = mfma32(frag_tr_o(kt, fo, 32 * dh, 16 * (2 * kh + c)), df, dq[dh]);
+            }
         }
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) dp[kh][j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][j], c2, nl2)) * dp[kh][j];
-        // dQ^T (d x queries) += K^T (d x keys) . dS^T (keys x queries)
-        u32x4 df[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) df[c] = pack_chunk(dp, c);
-#pragma unroll
-        for (int dh = 0; dh < 2; ++dh)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) dq[dh] = mfma32(frag_tr(kt, 32 * dh, 16 * c, lane), df[c], dq[dh]);
     });
     if (qok) {
         const int64_t row = hq.base(bh) + (int64_t)q * p.q_rs;
@@ -487,6 +458,7 @@ __device__ __forceinline__ void dkdv2_block(const FlashArgs &p, int kb, int64_t 
     RowStream rl, rd;  // rows flash2_bwd_rows left in the workspace
     rl.init(p.dlt + p.bh * p.sq + bh * p.sq, p.sq);
     rd.init(p.dlt + bh * p.sq, p.sq);
+    const FragOff fo = frag_offsets(lane);
     stream_tiles(st0, st1, qblocks - qb0, [&](char *st, int t) {
         sq_.issue(st, qb0 + t, wave);
         sd.issue(st + TB, qb0 + t, wave);
@@ -513,8 +485,8 @@ __device__ __forceinline__ void dkdv2_block(const FlashArgs &p, int kb, int64_t 
             }
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                sv = mfma32(frag_rm(qt, 32 * qh, ks, lane), kf[ks], sv);
-                dpv = mfma32(frag_rm(dot, 32 * qh, ks, lane), vf[ks], dpv);
+                sv = mfma32(frag_rm_o(qt, fo, 32 * qh, ks), kf[ks], sv);
+                dpv = mfma32(frag_rm_o(dot, fo, 32 * qh, ks), vf[ks], dpv);
             }
             // P = exp2(S scale log2 e - LSE log2 e), zero for queries before this key (causal: the
             // score becomes -inf in a wave-uniform branch that only diagonal tiles take); rows past
@@ -539,15 +511,11 @@ __device__ __forceinline__ void dkdv2_block(const FlashArgs &p, int kb, int64_t 
             // dV^T (d x keys) += dO^T (d x queries) . P;  dK^T += Q^T . dS  (query chunks 2qh, 2qh + 1)
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
-                const u32x4 pf = u32x4{pack_bf16x2(sv[8 * cc], sv[8 * cc + 1]), pack_bf16x2(sv[8 * cc + 2], sv[8 * cc + 3]),
-                                       pack_bf16x2(sv[8 * cc + 4], sv[8 * cc + 5]), pack_bf16x2(sv[8 * cc + 6], sv[8 * cc + 7])};
-                const u32x4 df = u32x4{pack_bf16x2(dpv[8 * cc], dpv[8 * cc + 1]), pack_bf16x2(dpv[8 * cc + 2], dpv[8 * cc + 3]),
-                                       pack_bf16x2(dpv[8 * cc + 4], dpv[8 * cc + 5]),
-                                       pack_bf16x2(dpv[8 * cc + 6], dpv[8 * cc + 7])};
+                const u32x4 pf = pack8(sv, 8 * cc), df = pack8(dpv, 8 * cc);
 #pragma unroll
                 for (int dh = 0; dh < 2; ++dh) {
-                    dv[dh] = mfma32(frag_tr(dot, 32 * dh, 16 * (2 * qh + cc), lane), pf, dv[dh]);
-                    dk[dh] = mfma32(frag_tr(qt, 32 * dh, 16 * (2 * qh + cc), lane), df, dk[dh]);
+                    dv[dh] = mfma32(frag_tr_o(dot, fo, 32 * dh, 16 * (2 * qh + cc)), pf, dv[dh]);
+                    dk[dh] = mfma32(frag_tr_o(qt, fo, 32 * dh, 16 * (2 * qh + cc)), df, dk[dh]);
                 }
             }
         }
@@ -603,8 +571,10 @@ __global__ __launch_bounds__(256) void flash2_bwd_rows(const FlashArgs p) {
 
 // The backward for grids with as many key blocks as query blocks: block j computes dQ of query
 // block j, then dK and dV of key block j. Under the causal mask the two parts' tile counts add up
-// to the same number for every block.
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash2_bwd_fused(const FlashArgs p) {
+// to the same number for every block. Three waves per SIMD (168 registers; 32-key or 32-query halves
+// and per-lane fragment offsets keep both parts within them): config 3 causal backward 105 -> 101 us,
+// non-causal 173 -> 158 us against two waves.
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(3))) void flash2_bwd_fused(const FlashArgs p) {
     __shared__ __attribute__((aligned(1024))) char st0[DKDV2_STAGE];
     __shared__ __attribute__((aligned(1024))) char st1[DKDV2_STAGE];
     int j;
