@@ -526,7 +526,8 @@ it_status it_capture_end(it_context *ctx, it_graph **out_graph);
  * with: the caller's buffers must outlive it; the library's own scratch does (a scratch block that a
  * later, larger eager call replaces is retired, not freed, while any graph of the context lives).
  * Replays are asynchronous like other stream work (the reference's commit_async,
- * src/command_batch.rs:228-272). */
+ * src/command_batch.rs:228-272). A graph replays only on the context that captured it
+ * (IT_ERR_INVALID otherwise). */
 it_status it_graph_launch(it_context *ctx, it_graph *graph);
 /* Waits for the context's streams, then destroys the graph; when it was the context's last live
  * graph, frees the scratch blocks retired meanwhile. A graph may also be destroyed after

@@ -457,6 +457,8 @@ it_status it_capture_end(it_context *ctx, it_graph **out_graph) {
 
 it_status it_graph_launch(it_context *ctx, it_graph *graph) {
     if (!ctx || !graph) return fail(IT_ERR_NULL, "it_graph_launch: NULL argument");
+    // The graph's buffers (scratch included) belong to the context that captured it.
+    if (graph->ctx != ctx) return fail(IT_ERR_INVALID, "it_graph_launch: graph was captured on another context");
     IT_HIP_TRY(hipGraphLaunch(graph->exec, ctx->main_stream));
     return IT_OK;
 }

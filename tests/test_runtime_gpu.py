@@ -67,3 +67,29 @@ def test_graph_survives_scratch_grow(it):
     finally:
         lib.it_shutdown(ctx.handle)
         ctx.handle = None
+
+
+def test_graph_replays_only_on_its_context(it):
+    """A graph holds its context's buffers and scratch, so another context may not replay it."""
+    a, b = it.Context(0), it.Context(0)
+    lib = a.lib
+    try:
+        t = it.Tensor.from_f32_slice(np.ones(1024, dtype=np.float32), [1024], a)
+        a.sync()
+        assert lib.it_capture_begin(a.handle) == 0
+        st = lib.it_zero(a.handle, C.c_void_p(t.ptr), t.byte_size())
+        graph = C.c_void_p()
+        assert lib.it_capture_end(a.handle, C.byref(graph)) == 0, _lib.last_error()
+        assert st == 0, _lib.last_error()
+        try:
+            assert lib.it_graph_launch(b.handle, graph) == _lib.IT_ERR_INVALID
+            assert "another context" in _lib.last_error()
+            assert lib.it_graph_launch(a.handle, graph) == 0, _lib.last_error()
+            a.sync()
+            assert not t.numpy().any()
+        finally:
+            assert lib.it_graph_destroy(graph) == 0
+    finally:
+        for c in (a, b):
+            lib.it_shutdown(c.handle)
+            c.handle = None
