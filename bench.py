@@ -703,7 +703,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "(the kernels run one GPU's shard; sharding across GPUs is not built)", file=sys.stderr)
         return 2
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: launched with WORLD_SIZE > 1; this build runs on one GPU only", file=sys.stderr)

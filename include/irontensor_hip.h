@@ -1,9 +1,9 @@
 /*
  * irontensor_hip.h -- C ABI of the MI355X (gfx950) matmul path for IronTensor.
  *
- * This is the drop-in boundary that IronTensor's Rust ops API binds through `extern "C"` (the Rust
- * side is shown in INTEGRATION.md). Everything is plain pointers and sizes: no Rust, C++ or torch
- * types cross it.
+ * This is the drop-in boundary that IronTensor's Rust ops API binds through `extern "C"` (a
+ * build.rs that compiles this library with hipcc, one `extern "C"` block and thin wrappers in the ops
+ * modules). Everything is plain pointers and sizes: no Rust, C++ or torch types cross it.
  *
  * Conventions
  *   - Every function returns it_status (0 == IT_OK). On failure a thread-local message is left in
