@@ -309,7 +309,7 @@ def bf16_square(it, timer, sizes) -> dict:
     return out
 
 
-def vs_library(it, timer, sizes=((4096, 20), (8192, 6))) -> dict:
+def vs_library(it, timer, sizes=((1024, 50), (2048, 30), (4096, 20), (8192, 6))) -> dict:
     """The BF16 n^3 GEMM against AMD's library in the same process: torch.mm on BF16 [n, n] tensors
     (served by hipBLASLt) in the NN, NT and TN layouts (the transposed operand a 2-D transposed view,
     which the library reads in place), then this library's NN, NT and TN forms on its own seeded
@@ -746,8 +746,8 @@ def main() -> int:
         print(json.dumps(out), flush=True)
         return 0
     if args.vs_library:
-        print(json.dumps(vs_library(it, Timer(ctx), sizes=((4096, args.steps), (8192, max(2, args.steps // 4))))),
-              flush=True)
+        print(json.dumps(vs_library(it, Timer(ctx), sizes=((1024, 2 * args.steps), (2048, args.steps), (4096, args.steps),
+                                                            (8192, max(2, args.steps // 4))))), flush=True)
         return 0
     if args.decode:
         print(json.dumps(decode_shapes(it, Timer(ctx), rounds=max(1, args.steps))), flush=True)

@@ -1650,7 +1650,11 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
     };
     const Cand f32c[] = {{128, 0, 2, 0.50}, {64, 0, 4, 0.60}};
     // 256 x 128 exists only as the direct-to-LDS kernel (eff 0: skipped where that does not apply).
-    const Cand b16c[] = {{256, 0, 1, 0.40}, {256, 128, 1, 0.0}, {128, 0, 2, 0.20}, {64, 0, 4, 0.20}};
+    // The register-staged 64 x 64 BF16 tile transposes [k][mn] operands in registers on the way to
+    // LDS: measured (1536^3, 2048^3) about 0.24 of the per-CU rate with no transpose (NT), 0.20 with
+    // B transposed (NN) and 0.15-0.19 with A transposed.
+    const double e64 = ta ? 0.15 : tb ? 0.24 : 0.20;
+    const Cand b16c[] = {{256, 0, 1, 0.40}, {256, 128, 1, 0.0}, {128, 0, 2, 0.20}, {64, 0, 4, e64}};
     // The direct-to-LDS kernel (whole tiles, an even number of k-tiles per split): 256 x 256, and
     // 256 x 128, whose waves read 50% more LDS per MFMA (two transposed reads per fragment of a
     // transposed A: lower still), and whose third stage lowers the memory-latency floor.
@@ -1667,6 +1671,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
     const double cu_peak = (bf16 ? 2.5e15 : 157.3e12) / 256.0;  // FLOP/s per CU
     const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = 4e12;
     const double step_floor = bf16 ? 1.0e-6 : 0.5e-6;
+    constexpr double F64_FLOOR_NT = 0.4e-6, F64_FLOOR_NN = 0.6e-6, F64_FLOOR_TA = 1.05e-6;
     const bool can_split = !a.dual && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && !a.no_split;
     Plan best{64, 64, 1, 0};
     double best_t = 1e30;
@@ -1704,6 +1709,10 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
             // A lone block on a CU whose tile could run two at once hides less latency.
             double eff = conc == 1 && occ > 1 ? 0.9 * cd.eff : cd.eff;
             double floor = cd.bn == 128 ? DTL_HALF_FLOOR : step_floor;
+            // The register-staged BF16 64 x 64 tile with one block per CU (1024^3: 16 k-steps on 256
+            // CUs) measured 0.4 / 0.6 / 0.85 us per k-step for NT / NN / transposed A (9.6 / 13.0 /
+            // 16.4 us), not the 1 us floor of the larger tiles' loads.
+            if (bf16 && cd.b == 64 && !cd.bn) floor = ta ? F64_FLOOR_TA : tb ? F64_FLOOR_NT : F64_FLOOR_NN;
             if (bf16 && cd.b == 256 && dtl_applicable(ta, tb, d, a.dual ? 256 : bn))
                 eff = bn == 128 && !a.dual ? DTL_HALF_EFF : DTL_EFF;
             if (d128) {
