@@ -4,14 +4,24 @@
 // src/ops/mps_gemm.rs:213-314); the greedy-decode shapes of the benchmark (M in {1, 4, 16},
 // K 4096, N 11008) are HBM-bound: every W element is read once and used M times.
 //
-// Design: a 256-thread block owns 16 * GV_NB output columns (rows of W) and splits K over its 4
-// waves. Each wave streams its share of those W rows straight from HBM as the B operand of
-// v_mfma_f32_16x16x32_bf16 (lane l: W row n0 + l%16, 8 consecutive k at 8*(l/16)), eight 16-byte
-// loads in flight per lane and column block, with X (tiny, cache-resident) as the A operand (row
-// l%16; lanes past M load nothing and feed zeros). No LDS staging: each W byte is loaded once, by
-// the lane that feeds it to the MFMA. The four partial tiles are summed through LDS and the
-// epilogue writes the M valid rows. One column block per wave measured fastest at M = 1 and 4
-// (two blocks per wave halve the X requests but halve the number of blocks).
+// Design: a 256-thread block owns 16 output columns (rows of W) and splits K over its 4 waves.
+// Each wave streams its share of those W rows from HBM and feeds them to
+// v_mfma_f32_16x16x32_bf16 as the B operand, with X (tiny, cache-resident) as the A operand.
+//
+// The operand layout wants lane l to hold row l%16, 8 consecutive k at 8*(l/16). Loaded that way,
+// consecutive lanes read different rows, and the loads run at the speed of the lanes' addresses,
+// not of the lines they touch: measured 28.3 us at M = 16 (K 4096, N 11008), against 20.4 us for the
+// same loads issued with consecutive lanes on consecutive 16-byte chunks. So the loads come in pairs
+// over a 64-wide k block, lane l reading row l/8 (first load) or 8 + l/8 (second), chunk l%8: each
+// instruction reads 8 whole 128-byte lines, 8 consecutive lanes per line. Each pair goes through a
+// 4 KB LDS slot of the wave (XOR-swizzled, no bank conflicts) into the operand layout of k 0-31 and
+// 32-63 of the block; the wave's LDS accesses complete in order, so no barrier is needed. The loads
+// are buffer loads whose range check zero-fills rows past N or M and chunks past the wave's k
+// range, all issued before the first use (16 per lane and iteration at M > 8, 12 otherwise). The
+// four partial tiles are summed through LDS in wave order and the epilogue writes the M valid rows.
+// Measured at K 4096, N 11008 with cold weights: 18.7 / 19.8 / 20.6 us at M = 1 / 4 / 16 (the direct
+// layout: 20.6 / 22.0 / 28.3 us). Two or four column blocks per wave sharing the X fragments
+// measured slower: half or a quarter of the blocks.
 #include <algorithm>
 
 #include "epilogue.hpp"
@@ -22,9 +32,8 @@ namespace it {
 namespace {
 
 constexpr int GV_THREADS = 256;
-constexpr int GV_UNROLL = 8;   // 32-wide k chunks per wave per iteration
+constexpr int GV_UNROLL = 8;   // 32-wide k chunks per wave per iteration (4 pairs of loads)
 constexpr int GV_KCHUNK = 32;
-constexpr int GV_NB = 1;       // 16-column blocks per wave (they would share the X fragments)
 
 // Weights are streamed once per call. The [K, N] kernel loads them nontemporally (measured 4-8%
 // faster with cold weights); the [N, K] kernel measured 2-4% slower that way and loads them plainly.
@@ -34,65 +43,95 @@ __device__ __forceinline__ float out_load(const void *C, int64_t idx, bool bf16)
     return bf16 ? bf16_to_f32(((const uint16_t *)C)[idx]) : ((const float *)C)[idx];
 }
 
+// Byte offset that a buffer load's range check turns into zeros without touching memory.
+constexpr uint32_t GV_OOB = 0x80000000u;
+
+// LDS slot (in 16-byte units) of row rr (0-7) and k chunk c (0-7) of one 8-row half of a pair:
+// each row's 8 chunks fill 128 bytes, XOR-swizzled by the row so that 8 lanes reading one chunk
+// of 8 rows hit 8 different bank groups.
+__device__ __forceinline__ int gv_slot(int rr, int c) { return rr * 8 + (c ^ rr); }
+
+// XHI: M > 8, so X rows 8-15 are loaded too (otherwise MFMA rows 8-15 of X repeat rows 0-7; they
+// only reach output rows past M, which are not written).
+template <bool XHI>
 __global__ __launch_bounds__(GV_THREADS) void gemv_bf16_nt(const GemmArgs p) {
-    __shared__ f32x4 part[4][GV_NB][64];
+    // Per wave: two slots (pairs alternate), each W rows 0-7, W rows 8-15, X rows 0-7, X rows 8-15.
+    __shared__ u32x4 stage[4][2][4][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int64_t n0 = (int64_t)blockIdx.x * (16 * GV_NB);
+    const int r = lane & 15, g = lane >> 4;   // operand layout: row r, k group g
+    const int rl = lane >> 3, kc = lane & 7;  // load layout: row rl (+8), k chunk kc
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
     const int64_t z = blockIdx.y;
     const int64_t bo = z / p.batch_inner, bi = z % p.batch_inner;
     const uint16_t *X = (const uint16_t *)p.A + bo * p.sA_out + bi * p.sA_in;
-    const uint16_t *W = (const uint16_t *)p.B + bo * p.sB_out + bi * p.sB_in;
+    const uint16_t *W = (const uint16_t *)p.B + bo * p.sB_out + bi * p.sB_in + n0 * p.ldb;
     const int64_t coff = bo * p.sC_out + bi * p.sC_in;
+
+    // Buffer descriptors over exactly the block's W rows and X's M rows (byte extents below 2^31,
+    // checked by the host): rows past N or M, and chunks past the wave's k range (offset GV_OOB),
+    // read as zeros with no memory access.
+    const int64_t nrows = min((int64_t)16, p.N - n0);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(W), (short)0, (int)(((nrows - 1) * p.ldb + p.K) * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(X), (short)0, (int)(((p.M - 1) * p.lda + p.K) * 2), 0x00020000);
+    const uint32_t wo0 = (uint32_t)(rl * p.ldb * 2), wo1 = (uint32_t)((8 + rl) * p.ldb * 2);
+    const uint32_t xo0 = (uint32_t)(rl * p.lda * 2), xo1 = (uint32_t)((8 + rl) * p.lda * 2);
+    // LDS slots: where this lane's loaded chunk goes, and where its operand chunks come from.
+    const int wslot = gv_slot(rl, kc);
+    const int rq = r >> 3, rr = r & 7;
+    const int lo_slot = gv_slot(rr, g), hi_slot = gv_slot(rr, 4 + g);
+    const int xq = XHI ? rq : 0;
 
     // K split over the 4 waves in multiples of the 32-wide chunk.
     const int64_t span = ((p.K + 4 * GV_KCHUNK - 1) / (4 * GV_KCHUNK)) * GV_KCHUNK;
     const int64_t kb = wave * span, ke = min(p.K, kb + span);
-    const bool xrow_ok = r < p.M;
-    const uint16_t *xrow = X + (xrow_ok ? r * p.lda : 0) + 8 * g;
-    const uint16_t *wrow[GV_NB];
-    bool wrow_ok[GV_NB];
-#pragma unroll
-    for (int j = 0; j < GV_NB; ++j) {
-        wrow_ok[j] = n0 + 16 * j + r < p.N;
-        wrow[j] = W + (wrow_ok[j] ? (n0 + 16 * j + r) * p.ldb : 0) + 8 * g;
-    }
 
-    f32x4 acc[GV_NB];
-#pragma unroll
-    for (int j = 0; j < GV_NB; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int64_t k = kb; k < ke; k += GV_UNROLL * GV_KCHUNK) {
-        u32x4 wf[GV_NB][GV_UNROLL], xf[GV_UNROLL];
+        u32x4 wr[GV_UNROLL], xr[GV_UNROLL];
 #pragma unroll
-        for (int u = 0; u < GV_UNROLL; ++u) {
-            const int64_t kk = k + u * GV_KCHUNK;
-            // Chunks are 8 elements and K % 8 == 0, so a chunk is either whole or past the end.
-            const bool ok = kk + 8 * g < ke;
-#pragma unroll
-            for (int j = 0; j < GV_NB; ++j) {
-                const u32x4 w = *(const u32x4 *)(wrow[j] + (ok ? kk : kb));
-                wf[j][u] = (ok && wrow_ok[j]) ? w : u32x4{0u, 0u, 0u, 0u};
-            }
-            // X rows past M are zero; their lanes issue no load.
-            xf[u] = u32x4{0u, 0u, 0u, 0u};
-            if (ok && xrow_ok) xf[u] = *(const u32x4 *)(xrow + kk);
+        for (int pr = 0; pr < GV_UNROLL / 2; ++pr) {
+            // This lane's chunk: 8 elements, and K % 8 == 0, so a chunk is whole or past the end.
+            const int64_t kk = k + 64 * pr + 8 * kc;
+            const bool ok = kk < ke;
+            const uint32_t ko = (uint32_t)(kk * 2);
+            wr[2 * pr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? wo0 + ko : GV_OOB, 0, 0));
+            wr[2 * pr + 1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, ok ? wo1 + ko : GV_OOB, 0, 0));
+            xr[2 * pr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, ok ? xo0 + ko : GV_OOB, 0, 0));
+            if constexpr (XHI)
+                xr[2 * pr + 1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, ok ? xo1 + ko : GV_OOB, 0, 0));
         }
+        // Every load is issued before the first use: left to itself the scheduler interleaves
+        // them with the waits and keeps only a few in flight.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < GV_UNROLL; ++u)
-#pragma unroll
-            for (int j = 0; j < GV_NB; ++j) mma16<uint16_t>(acc[j], xf[u], wf[j][u]);
+        for (int pr = 0; pr < GV_UNROLL / 2; ++pr) {
+            // Through LDS from the load layout (lane: row rl, chunk kc) to the operand layout
+            // (lane: row r, chunk g and 4 + g). A wave's LDS accesses complete in issue order, so
+            // the slot written two pairs ago has been read, and the reads see these writes.
+            u32x4 (&st)[4][64] = stage[wave][pr & 1];
+            st[0][wslot] = wr[2 * pr];
+            st[1][wslot] = wr[2 * pr + 1];
+            st[2][wslot] = xr[2 * pr];
+            if constexpr (XHI) st[3][wslot] = xr[2 * pr + 1];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            const u32x4 wlo = st[rq][lo_slot], whi = st[rq][hi_slot];
+            const u32x4 xlo = st[2 + xq][lo_slot], xhi = st[2 + xq][hi_slot];
+            mma16<uint16_t>(acc, xlo, wlo);
+            mma16<uint16_t>(acc, xhi, whi);
+        }
     }
-    // acc[j]: lane l holds column n0 + 16j + l%16 and rows 4*(l/16) + i.
-#pragma unroll
-    for (int j = 0; j < GV_NB; ++j) part[wave][j][lane] = acc[j];
+    // acc: lane l holds column n0 + l%16 and rows 4*(l/16) + i.
+    // The four partial tiles go through each wave's own first slot (its reads of it are done).
+    stage[wave][0][0][lane] = __builtin_bit_cast(u32x4, acc);
     __syncthreads();
-    // Wave j (< GV_NB) sums column block j over the four K quarters and writes it.
-    if (wave < GV_NB) {
-        const int j = wave;
-        f32x4 sum = part[0][j][lane];
+    // Wave 0 sums the four K quarters in wave order and writes the tile.
+    if (wave == 0) {
+        f32x4 sum = __builtin_bit_cast(f32x4, stage[0][0][0][lane]);
 #pragma unroll
-        for (int w = 1; w < 4; ++w) sum += part[w][j][lane];
-        const int64_t col = n0 + 16 * j + r;
+        for (int w = 1; w < 4; ++w) sum += __builtin_bit_cast(f32x4, stage[w][0][0][lane]);
+        const int64_t col = n0 + r;
         if (col < p.N) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -339,15 +378,20 @@ it_status launch_gemv_kn(hipStream_t s, bool transA, const GemmArgs &a, int *cou
     return IT_OK;
 }
 
+// The buffer descriptors span 16 rows of W and M rows of X: byte extents and offsets below 2^31.
 bool gemv_applicable(const GemmArgs &a, bool bf16, bool transA, bool transB) {
     return bf16 && !transA && transB && a.M >= 1 && a.M <= 16 && !a.dual && a.causal == CAUSAL_NONE &&
-           a.kmode == KMODE_FULL && a.K % 8 == 0 && a.a_vec_ok && a.b_vec_ok &&
+           a.kmode == KMODE_FULL && a.K % 8 == 0 && a.a_vec_ok && a.b_vec_ok && a.lda >= a.K &&
+           a.ldb >= a.K && 16 * a.lda + a.K < (1ll << 30) && 16 * a.ldb + a.K < (1ll << 30) &&
            (a.N + 15) / 16 <= 0x7fffffff && a.batch <= 65535;
 }
 
 it_status launch_gemv(hipStream_t s, const GemmArgs &a) {
-    dim3 grid((unsigned)((a.N + 16 * GV_NB - 1) / (16 * GV_NB)), (unsigned)a.batch);
-    hipLaunchKernelGGL(gemv_bf16_nt, grid, dim3(GV_THREADS), 0, s, a);
+    dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)a.batch);
+    if (a.M > 8)
+        hipLaunchKernelGGL(gemv_bf16_nt<true>, grid, dim3(GV_THREADS), 0, s, a);
+    else
+        hipLaunchKernelGGL(gemv_bf16_nt<false>, grid, dim3(GV_THREADS), 0, s, a);
     IT_HIP_TRY(hipGetLastError());
     return IT_OK;
 }

@@ -326,6 +326,61 @@ def test_bf16_decode_kn_ragged(it, m, k, n, ta):
     assert np.array_equal(out.numpy(), (2.0 * exact + c0 + bias).astype(np.float32))
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 11008), (16, 4096, 11008), (3, 72, 1000), (16, 4104, 77),
+                                   (7, 8, 33), (13, 520, 2050), (9, 40, 17), (16, 136, 24)])
+def test_bf16_decode_nt_kernel(it, m, k, n):
+    """The decode kernel for a weight stored [N, K] (the Linear layout: each load instruction reads 8
+    rows x 128 contiguous bytes and DPP moves rearrange each pair of loads into the MFMA operand
+    layout): the BASELINE shapes, K not a multiple of 64 or 32, a wave's k range shorter than one
+    64-wide block, row and column counts that are not multiples of 8 or 16. Exact small integers
+    against a float64 product, BF16 output against the RNE rounding of the exact result, the
+    epilogue (alpha, beta, bias), and the plan key names the kernel."""
+    from irontensor_amd import profiler
+    _log(f"[decode nt kernel] m={m} k={k} n={n}")
+    a = synth.small_ints(300 + m, (m, k), -3, 3)
+    b = synth.small_ints(301, (n, k), -3, 3)
+    A, B = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    c = it.gemm(A, B, trans_b=True, out_precision=it.Precision.FP32)
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    assert any(key.startswith("gemv_bf16_NT") for key in keys), keys
+    exact = a.astype(np.float64) @ b.astype(np.float64).T
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    c16 = it.gemm(A, B, trans_b=True, out_precision=it.Precision.BF16)
+    assert np.array_equal(c16.as_bf16_slice().reshape(m, n), synth_bf16(exact))
+    bias = synth.small_ints(302, (n,), -4, 4)
+    c0 = synth.small_ints(303, (m, n), -4, 4)
+    out = it.Tensor.from_f32_slice(c0, [m, n])
+    it.gemm(A, B, trans_b=True, alpha=2.0, beta=1.0, out=out, bias=it.Tensor.from_f32_slice(bias, [n]))
+    assert np.array_equal(out.numpy(), (2.0 * exact + c0 + bias).astype(np.float32))
+
+
+def test_bf16_decode_nt_batched_and_broadcast(it):
+    """The [N, K]-weight decode kernel on a batched product (3 items, each its own weight) and with
+    one weight broadcast over the batch."""
+    from irontensor_amd import profiler
+    bt, m, k, n = 3, 5, 264, 40
+    a = synth.small_ints(310, (bt, m, k), -3, 3)
+    b = synth.small_ints(311, (bt, n, k), -3, 3)
+    A, B = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    c = it.gemm(A, B, trans_b=True)
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    _log(f"[decode nt batched] {keys}")
+    assert any(key.startswith("gemv_bf16_NT") for key in keys), keys
+    exact = np.matmul(a.astype(np.float64), np.swapaxes(b, 1, 2).astype(np.float64))
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    b0 = b[0]
+    c2 = it.gemm(A, it.Tensor.from_f32_as_bf16(b0, b0.shape), trans_b=True)
+    assert np.array_equal(c2.numpy(), np.matmul(a.astype(np.float64), b0.T.astype(np.float64)).astype(np.float32))
+
+
 @pytest.mark.parametrize("m,k,n,ta", [(1, 4096, 11008, 0), (4, 4096, 11008, 1), (16, 4096, 11008, 0),
                                       (16, 4096, 11008, 1), (5, 1024, 1032, 1), (16, 256, 136, 0), (3, 32, 8, 0)])
 def test_bf16_decode_kn_kernel(it, m, k, n, ta):
