@@ -349,6 +349,52 @@ def vs_library(it, timer, sizes=((1024, 50), (2048, 30), (4096, 20), (8192, 6)))
     return res
 
 
+F32_LM_HEAD = (("forward_NT", 4096, 16384, 256, False, True), ("data_grad_NN", 4096, 256, 16384, False, False),
+               ("weight_grad_TN", 16384, 256, 4096, True, False))
+
+
+def vs_library_f32(it, timer, iters: int = 10) -> dict:
+    """The TINY step's three FP32 LM-head GEMMs against AMD's library in the same process: torch.mm
+    on FP32 tensors (hipBLASLt; the transposed operand a 2-D transposed view, TF32 off), then this
+    library's own GEMM on seeded operands of the same layout; three batches of `iters` launches each,
+    microseconds per launch per batch."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda:0")
+    res = {}
+    for name, m, n, k, ta, tb in F32_LM_HEAD:
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        a = torch.randn(*((k, m) if ta else (m, k)), device=dev, generator=g)
+        b = torch.randn(*((n, k) if tb else (k, n)), device=dev, generator=g)
+        x, y = (a.t() if ta else a), (b.t() if tb else b)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(3):
+            torch.mm(x, y)
+        torch.cuda.synchronize()
+        lib_us = []
+        for _ in range(3):
+            e0.record()
+            for _ in range(iters):
+                torch.mm(x, y)
+            e1.record()
+            torch.cuda.synchronize()
+            lib_us.append(round(e0.elapsed_time(e1) / iters * 1e3, 1))
+        del a, b, x, y
+        torch.cuda.empty_cache()
+        A = _dev(it, 3, (k, m) if ta else (m, k))
+        B = _dev(it, 4, (n, k) if tb else (k, n))
+        Cm = it.Tensor.empty([m, n])
+        this_us = [round(time_gemm(it, timer, A, B, Cm, ta, tb, iters) * 1e3, 1) for _ in range(3)]
+        del A, B, Cm
+        fl = 2.0 * m * n * k
+        res[f"f32_lm_head_{name}_{m}x{n}x{k}"] = {
+            "hipblaslt_torch_mm_us": lib_us, "this_us": this_us,
+            "hipblaslt_tflops_best": round(fl / (min(lib_us) * 1e-6) / 1e12, 1),
+            "this_tflops_best": round(fl / (min(this_us) * 1e-6) / 1e12, 1)}
+    return res
+
+
 def extra_sweep(it, timer) -> dict:
     """Config 5: BF16 square GEMMs n^3, n in {1024 .. 16384}, NN/NT/TN, BF16 out; and the decode
     shapes (decode_shapes)."""
@@ -694,6 +740,9 @@ def main() -> int:
     ap.add_argument("--vs-library", action="store_true",
                     help="time the BF16 4096^3 GEMM through torch.mm (hipBLASLt) and through this library, "
                          "in one process (for same-box A/B traces and counters)")
+    ap.add_argument("--vs-library-f32", action="store_true",
+                    help="time the TINY step's three FP32 LM-head GEMMs through torch.mm (hipBLASLt) and through "
+                         "this library, in one process, --steps launches per batch (for same-box traces and counters)")
     ap.add_argument("--decode", action="store_true",
                     help="run only the BF16 decode shapes (M 1/4/16, K 4096, N 11008; NT, NN, TN) with cold "
                          "weights, --steps passes over the rotated copies (for rocprofv3)")
@@ -709,15 +758,15 @@ def main() -> int:
         print("bench.py: launched with WORLD_SIZE > 1; this build runs on one GPU only", file=sys.stderr)
         return 2
     if os.environ.get("IRONTENSOR_LIB") and not (args.attention or args.medium_step or args.bf16_square or args.decode
-                                                 or args.vs_library):
+                                                 or args.vs_library or args.vs_library_f32):
         print("bench.py: IRONTENSOR_LIB is set; the bench times only the in-tree library "
               "(irontensor_amd/libirontensor_hip.so), unset it", file=sys.stderr)
         return 2
 
-    if args.vs_library or args.attention or not (args.no_extra or args.kernel_only or args.train_only
-                                                 or args.bf16_square or args.medium_step or args.decode):
+    if args.vs_library or args.vs_library_f32 or args.attention or not (
+            args.no_extra or args.kernel_only or args.train_only or args.bf16_square or args.medium_step or args.decode):
         init_torch_first()
-        if args.vs_library and not TORCH_STATE["ready"]:
+        if (args.vs_library or args.vs_library_f32) and not TORCH_STATE["ready"]:
             print(f"bench.py: torch could not take the device: {TORCH_STATE['error']}", file=sys.stderr)
             return 1
     import irontensor_amd as it
@@ -748,6 +797,9 @@ def main() -> int:
     if args.vs_library:
         print(json.dumps(vs_library(it, Timer(ctx), sizes=((1024, 2 * args.steps), (2048, args.steps), (4096, args.steps),
                                                             (8192, max(2, args.steps // 4))))), flush=True)
+        return 0
+    if args.vs_library_f32:
+        print(json.dumps(vs_library_f32(it, Timer(ctx), iters=args.steps)), flush=True)
         return 0
     if args.decode:
         print(json.dumps(decode_shapes(it, Timer(ctx), rounds=max(1, args.steps))), flush=True)

@@ -1448,6 +1448,13 @@ bool tiles_exact(const GemmArgs &a, int bm, int bn, int bk) {
            a.a_vec_ok && a.b_vec_ok;
 }
 
+// The FP32 256 x 128 tile (one block per CU, 64 x 128 accumulators per wave): plain products with a
+// k-contiguous A (X.W and X.W^T) on whole tiles and whole k-tiles.
+bool f32_256_applicable(bool ta, const GemmArgs &a) {
+    return !ta && !a.dual && !a.xent_stats && !a.a_kscale && !a.swiglu_bwd && !a.rope_table &&
+           a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && tiles_exact(a, 256, 128, ET<float>::BK);
+}
+
 
 // The direct-to-LDS kernel takes whole tiles without epilogue masks or k limits, an even number of
 // k-tiles per split, and 32-bit buffer offsets: a k-contiguous operand's 256 rows, or an
@@ -1514,6 +1521,12 @@ hipError_t launch_bf16_256(bool ta, bool tb, int bn, const GemmArgs &a, dim3 gri
 template <typename T, bool TA, bool TB, bool DUAL, int LM, bool KS = false>
 void launch_cfg_lm(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t s) {
     constexpr int PF64 = sizeof(T) == 4 ? 2 : 1;
+    if constexpr (sizeof(T) == 4 && !TA && !DUAL && !KS && LM == LOAD_EXACT) {
+        if (cfg.bm == 256) {
+            hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 256, 128, 2, 2, DUAL, LM, KS, 1>), grid, dim3(NTHREADS), 0, s, a);
+            return;
+        }
+    }
     if (cfg.bm == 128)
         hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 128, 128, 2, 2, DUAL, LM, KS>), grid, dim3(NTHREADS), 0, s, a);
     else
@@ -1648,7 +1661,13 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
         int b, bn, occ;  // b x bn tiles (bn 0: square)
         double eff;
     };
-    const Cand f32c[] = {{128, 0, 2, 0.50}, {64, 0, 4, 0.60}};
+    // FP32 256 x 128 (one block per CU): fitted on the LM-head data gradient [4096,256,16384] (eight
+    // splits: 274 us against 291-302 us for the best 64 x 64 plans), with a per-round cost that
+    // covers its 128 KB epilogue (the LM-head forward, 8 rounds of 8 k-steps: 361 us). Offered for
+    // long k ranges only (32 k-steps per split or more), where it measured faster.
+    const Cand f32c[] = {{128, 0, 2, 0.50}, {64, 0, 4, 0.60}, {256, 128, 1, 0.87}};
+    constexpr double F32_256_ROUND = 14e-6;
+    constexpr int64_t F32_256_MIN_KSTEPS = 32;
     // 256 x 128 exists only as the direct-to-LDS kernel (eff 0: skipped where that does not apply).
     // The register-staged 64 x 64 BF16 tile transposes [k][mn] operands in registers on the way to
     // LDS: measured (1536^3, 2048^3) about 0.24 of the per-CU rate with no transpose (NT), 0.20 with
@@ -1666,7 +1685,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
     constexpr double DTL128_FLOOR = 0.35e-6;
     const double DTL_HALF_EFF = ta ? 0.42 : 0.52;
     const Cand *cands = bf16 ? b16c : f32c;
-    const int ncand = bf16 ? 4 : 2;
+    const int ncand = bf16 ? 4 : 3;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
     const double cu_peak = (bf16 ? 2.5e15 : 157.3e12) / 256.0;  // FLOP/s per CU
     const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = 4e12;
@@ -1708,7 +1727,12 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
             const int64_t ksteps = std::max<int64_t>(1, cdiv(kps, bk));
             // A lone block on a CU whose tile could run two at once hides less latency.
             double eff = conc == 1 && occ > 1 ? 0.9 * cd.eff : cd.eff;
-            double floor = cd.bn == 128 ? DTL_HALF_FLOOR : step_floor;
+            double floor = bf16 && cd.bn == 128 ? DTL_HALF_FLOOR : step_floor;
+            double ro = round_overhead;
+            if (!bf16 && cd.b == 256) {
+                if (!f32_256_applicable(ta, d) || ksteps < F32_256_MIN_KSTEPS) continue;
+                ro = F32_256_ROUND;
+            }
             // The register-staged BF16 64 x 64 tile with one block per CU (1024^3: 16 k-steps on 256
             // CUs) measured 0.4 / 0.6 / 0.85 us per k-step for NT / NN / transposed A (9.6 / 13.0 /
             // 16.4 us), not the 1 us floor of the larger tiles' loads.
@@ -1721,7 +1745,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
             }
             if (eff <= 0.0) continue;
             const double step = (a.dual ? 4.0 : 2.0) * cd.b * bn * bk / (cu_peak * eff);
-            double t = rounds * (round_overhead + ksteps * std::max(conc * step, floor));
+            double t = rounds * (ro + ksteps * std::max(conc * step, floor));
             if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
             // Near ties (3%) keep the earlier, larger and less split plan, except that between two
             // unsplit plans the one with more blocks wins (more loads in flight per k-step).
@@ -1824,6 +1848,10 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     splits = (int)std::max<int64_t>(1, cdiv(a.K, kps));
     a.k_per_split = kps;
     a.splits = splits;
+    // The FP32 256 x 128 tile covers plain GEMMs with a k-contiguous A on whole tiles only (the
+    // planner offers it for nothing else).
+    if (!bf16 && cfg.bm == 256 && (cfg.bn != 128 || !f32_256_applicable(transA, a)))
+        return fail(IT_ERR_INVALID, "it_gemm: no FP32 256-row tile for this product");
     if (splits > 1) {
         void *ws = nullptr;
         it_status st = ensure_scratch(ctx, (size_t)splits * a.batch * a.M * a.N * sizeof(float), &ws);
@@ -1831,7 +1859,7 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
         a.partial = (float *)ws;
     }
     const bool dtl128 = bf16 && cfg.bm == 128 && cfg.bn == 128 && dtl128_applicable(transA, transB, a);
-    const bool dtl = dtl128 || (cfg.bm == 256 && dtl_applicable(transA, transB, a, a.dual ? 256 : cfg.bn));
+    const bool dtl = dtl128 || (bf16 && cfg.bm == 256 && dtl_applicable(transA, transB, a, a.dual ? 256 : cfg.bn));
 
     const int64_t gx = (int64_t)a.tiles_m * a.tiles_n;
     const int64_t gy = a.batch * splits;
@@ -1853,7 +1881,7 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
         key = buf;
         profile_begin(ctx, key, &ev);
     }
-    hipError_t e = cfg.bm == 256 ? launch_bf16_256(transA, transB, a.dual ? 256 : cfg.bn, a, grid, ctx->stream)
+    hipError_t e = bf16 && cfg.bm == 256 ? launch_bf16_256(transA, transB, a.dual ? 256 : cfg.bn, a, grid, ctx->stream)
                    : dtl128      ? launch_bf16_dtl128(transA, transB, a, grid, ctx->stream)
                    : bf16        ? launch_typed<uint16_t>(transA, transB, a.dual, cfg, a, grid, ctx->stream)
                                  : launch_typed<float>(transA, transB, a.dual, cfg, a, grid, ctx->stream);

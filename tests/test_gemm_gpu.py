@@ -741,3 +741,28 @@ def test_bf16_nt_128_tile_exact(it, m, n, k):
     assert "128x128_dtl" in keys[0], keys
     ref = x.astype(np.int64) @ w.T.astype(np.int64)
     assert np.array_equal(out.numpy(), ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("tb", [False, True])
+def test_f32_256_tile_exact(it, tb):
+    """FP32 data gradients of the LM-head shape ([4096, 256, 16384], X.W and X.W^T) run on the
+    256 x 128 FP32 tile with split K (one block per CU): exact on small integers against a float64
+    product (every partial sum is an integer below 2^24), with alpha and a bias in the epilogue
+    that follows the split-K reduction."""
+    from irontensor_amd import profiler
+    m, n, k = 4096, 256, 16384
+    x = synth.small_ints(820, (m, k), -3, 3)
+    w = synth.small_ints(821, (n, k) if tb else (k, n), -3, 3)
+    bias = synth.small_ints(822, (n,), -4, 4)
+    tx, tw = it.Tensor.from_f32_slice(x, list(x.shape)), it.Tensor.from_f32_slice(w, list(w.shape))
+    out = it.Tensor.zeros([m, n])
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    it.gemm(tx, tw, trans_b=tb, out=out, alpha=2.0, bias=it.Tensor.from_f32_slice(bias, [n]))
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    print(f"[f32 256] tb={tb} {keys}", flush=True)
+    assert keys[0].startswith("gemm_f32_N") and "_256x128|" in keys[0] and not keys[0].endswith(" s1"), keys
+    ref = x.astype(np.float64) @ (w.T if tb else w).astype(np.float64)  # exact: integers below 2^53
+    assert np.array_equal(out.numpy(), (2 * ref + bias).astype(np.float32))

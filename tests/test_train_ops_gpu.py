@@ -332,7 +332,9 @@ def test_gemm_cross_entropy_operand(it, oracle, T, V, H):
     ref_dh = it.gemm(grad, E).numpy()
     ref_de = it.gemm(grad, Hh, trans_a=True).numpy()
     # the rebuilt gradient is the stored one element for element, so the products agree to rounding
-    assert normwise_rel(dh.numpy(), ref_dh) <= 1e-6
+    # (dh to FP32 summation order: at the TINY shape the plain product runs on 256 x 128 tiles with
+    # eight k splits, the rebuilt-operand one on 64 x 64 tiles with two)
+    assert normwise_rel(dh.numpy(), ref_dh) <= FP32_TOL
     assert normwise_rel(de.numpy(), ref_de) <= 1e-6
     # and against float64: (softmax - onehot) / T contracted with E and h
     x = logits.astype(np.float64)

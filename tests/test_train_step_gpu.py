@@ -149,8 +149,9 @@ def test_train_step_grouped_weight_gradients(it):
 
 def test_train_step_xent_operand_matches_stored_gradient(it):
     """TINY: one step with the cross-entropy operand against one with the stored gradient: the
-    same loss, and gradients equal to rounding (the rebuilt gradient is the stored one element for
-    element; only the GEMMs' summation order can differ)."""
+    same loss, and gradients equal to FP32 rounding (the rebuilt gradient is the stored one element
+    for element; only the GEMMs' summation order differs: the LM-head data gradient runs on 256 x 128
+    tiles with eight k splits from the stored gradient, on 64 x 64 tiles with two from the logits)."""
     from irontensor_amd.train import TrainStep
     a = TrainStep(TINY, seed=13, xent_operand=False)
     b = TrainStep(TINY, seed=13, xent_operand=True)
@@ -159,7 +160,7 @@ def test_train_step_xent_operand_matches_stored_gradient(it):
     it.Context.global_().sync()
     assert a.loss_value() == b.loss_value()
     for i, (x, y) in enumerate(zip(a.grads, b.grads)):
-        assert normwise_rel(y.numpy(), x.numpy()) <= 1e-6, i
+        assert normwise_rel(y.numpy(), x.numpy()) <= FP32_TOL, i
 
 
 def test_train_step_tiny_loss_decreases(it):
