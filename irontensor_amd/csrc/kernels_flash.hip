@@ -60,10 +60,22 @@ __device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p;
 // for operands whose MFMA k index is the tile row), so a tensor needed both ways is read from HBM
 // once.
 //
-// Unit u covers rows 4rg..4rg+3 and 16-byte column cc. For a tile that is stored transposed,
-// consecutive lanes take consecutive rg, so the transposed writes of neighbouring lanes fill one LDS
-// row side by side (with cc fastest they would land 8 rows apart, on the same banks); a tile stored
-// only row-major keeps cc fastest (each lane group writes whole 128-byte rows).
+// Unit u covers rows 4rg..4rg+3 and 16-byte column cc. FP32: cc is fastest, so the 16 lanes that
+// share rg load 256 contiguous bytes of each row (the memory pipeline's cost follows the lanes'
+// addresses in lane order), and the 16-byte units of LDS row r are XOR-swizzled by (r >> 4) & 3
+// (swz): the row-major writes of 16 lanes fill one row, the transposed writes land in rows 4cc + j
+// at 16 distinct bank groups, and the fragment reads of 16 consecutive rows stay conflict-free.
+// BF16: a tile that is stored transposed takes consecutive rg in consecutive lanes, so the
+// transposed writes of neighbouring lanes fill one LDS row side by side; a tile stored only
+// row-major keeps cc fastest.
+template <typename T>
+__device__ __forceinline__ int swz(int row, int u) {
+    if constexpr (sizeof(T) == 4)
+        return u ^ ((row >> 4) & 3);
+    else
+        return u;
+}
+
 template <typename T>
 struct Unit4 {
     static constexpr int VEC = FE<T>::VEC;
@@ -72,8 +84,9 @@ struct Unit4 {
     u32x4 r[4];
 
     __device__ __forceinline__ static void decode(int u, bool rg_fast, int &rg, int &cc) {
-        rg = rg_fast ? u % RGS : u / CPR;
-        cc = rg_fast ? u / RGS : u % CPR;
+        const bool rf = rg_fast && sizeof(T) == 2;
+        rg = rf ? u % RGS : u / CPR;
+        cc = rf ? u / RGS : u % CPR;
     }
 
     __device__ __forceinline__ void load(const T *m, int64_t rs, int row0, int rows, int u, bool rg_fast) {
@@ -92,7 +105,7 @@ struct Unit4 {
         int rg, cc;
         decode(u, rg_fast, rg, cc);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) *(u32x4 *)(lds + (rg * 4 + q) * P + cc * 16) = r[q];
+        for (int q = 0; q < 4; ++q) *(u32x4 *)(lds + (rg * 4 + q) * P + swz<T>(rg * 4 + q, cc) * 16) = r[q];
     }
     __device__ __forceinline__ void store_cols(char *lds, int u, bool rg_fast) const {
         constexpr int P = pitch<T>();
@@ -103,7 +116,7 @@ struct Unit4 {
             // 4 rows x 4 columns -> LDS rows 4cc+j, columns 4rg..4rg+3
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                *(u32x4 *)(lds + (cc * 4 + j) * P + rg * 16) = u32x4{v0[j], v1[j], v2[j], v3[j]};
+                *(u32x4 *)(lds + (cc * 4 + j) * P + swz<T>(cc * 4 + j, rg) * 16) = u32x4{v0[j], v1[j], v2[j], v3[j]};
         } else {
             // 4 rows x 8 bf16 columns -> LDS rows 8cc+j, columns 4rg..4rg+3 (8 bytes)
 #pragma unroll
@@ -207,7 +220,8 @@ __device__ __forceinline__ void pipelined(TP &tp, char *smem, int stage_bytes, i
 // Fragment of LDS tile row `row`, contiguous k chunk c (lane group g).
 template <typename T>
 __device__ __forceinline__ u32x4 frag_c(const char *tile, int row, int c, int g) {
-    return *(const u32x4 *)(tile + row * pitch<T>() + (c * FE<T>::KC + g * FE<T>::VEC) * (int)sizeof(T));
+    // (c * KC + g * VEC) elements = 16-byte unit 4c + g, for both element types
+    return *(const u32x4 *)(tile + row * pitch<T>() + swz<T>(row, 4 * c + g) * 16);
 }
 
 // Fragment whose k assignment matches an accumulator-derived operand: FP32 chunk c = keys
