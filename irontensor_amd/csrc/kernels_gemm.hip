@@ -385,6 +385,8 @@ namespace sg {
 constexpr int MFMA = 0x008, VMEM_READ = 0x020, DS_READ = 0x100, DS_WRITE = 0x200;
 }
 
+constexpr int CP_DEVICE_SCOPE = 16;  // cache-policy bit sc1 of the buffer intrinsics: device scope
+
 // LDS bytes of one gemm_mfma block (two stages of the A and B tiles).
 template <typename T, bool TA, bool TB, int BM, int BN>
 constexpr int mfma_smem_bytes() {
@@ -393,9 +395,13 @@ constexpr int mfma_smem_bytes() {
 
 // One block of gemm_mfma: output tile `tile` (in map_tile order) of batch-and-split index z, with
 // `smem` of mfma_smem_bytes().
+// FIX (64 x 64 tiles of batch-1 products): with split K, each split's partial tile goes to p.partial
+// at device scope and the tile's last block to arrive at `arrive` (a zero counter, left at zero)
+// adds the splits in split order and runs the epilogue, so no separate reduction launch follows.
 template <typename T, bool TA, bool TB, int BM, int BN, int WM, int WN, bool DUAL, int LM, bool KS = false, int PF = 1,
-          bool XF = false>
-__device__ __forceinline__ void gemm_mfma_block(const GemmArgs &p, int tile, int64_t z, char *smem) {
+          bool XF = false, bool FIX = false>
+__device__ __forceinline__ void gemm_mfma_block(const GemmArgs &p, int tile, int64_t z, char *smem,
+                                                int *arrive = nullptr) {
     static_assert(WM * WN == 4, "4 waves per block");
     constexpr int BK = ET<T>::BK;
     constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
@@ -599,6 +605,55 @@ __device__ __forceinline__ void gemm_mfma_block(const GemmArgs &p, int tile, int
         }
     }
 
+    static_assert(!FIX || (XPOSE && !KS && !XF), "the in-kernel split-K sum covers plain 64 x 64 tiles");
+    if constexpr (FIX) {
+        if (p.splits > 1) {
+            // Partial tile of split z at device scope (written through this XCD's L2), then the
+            // arrival count: the tile's last block reads every split's partial at device scope
+            // (missing its own L2), adds them in split order from zero, as the separate reduction
+            // does, and finishes the tile. Offsets are 32-bit (splits * M * N * 4 < 2^31, checked
+            // by the host).
+            const __amdgpu_buffer_rsrc_t prt = __builtin_amdgcn_make_buffer_rsrc(
+                p.partial, (short)0, (int)(p.splits * p.M * p.N * 4), 0x00020000);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const int64_t row = m0 + wm * WTM + i * 16 + (lane & 15);
+                    const int64_t col = n0 + wn * WTN + j * 16 + (lane >> 4) * 4;
+                    if (row < p.M && col < p.N)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), prt,
+                                                               (uint32_t)(((z * p.M + row) * p.N + col) * 4), 0,
+                                                               CP_DEVICE_SCOPE);
+                }
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's partials reached device scope
+            __syncthreads();
+            __shared__ int last;
+            if (tid == 0) {
+                const int old = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                last = old == p.splits - 1;
+                if (last) __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            if (!last) return;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const int64_t row = m0 + wm * WTM + i * 16 + (lane & 15);
+                    const int64_t col = n0 + wn * WTN + j * 16 + (lane >> 4) * 4;
+                    if (row >= p.M || col >= p.N) continue;
+                    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+                    for (int sp = 0; sp < p.splits; ++sp)
+                        sum += sp == z ? acc[i][j]
+                                       : __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                       prt, (uint32_t)(((sp * p.M + row) * p.N + col) * 4),
+                                                                       0, CP_DEVICE_SCOPE));
+                    finish4<true, true>(p, sum, row, col, coff, 0);
+                }
+            return;
+        }
+    }
     if constexpr (XPOSE) {
         // The accumulator blocks hold C^T (B was the MFMA's row operand): lane l of block (i, j)
         // has output row i*16 + l%16 and its 4 consecutive columns j*16 + 4*(l/16) .. +3, so each
@@ -1330,7 +1385,8 @@ struct GroupChunk {
 };
 struct GemmGroupArgs {
     GemmArgs g[GEMM_GROUP_MAX];
-    int64_t rstart[GEMM_GROUP_MAX + 1];  // FP32 groups: first 4-element vector of each split-K sum
+    int *arrive;                         // FP32 groups: the split-K arrival counters (zero),
+    int cstart[GEMM_GROUP_MAX + 1];      // problem g's tiles at arrive[cstart[g]] ..
     int count;
     uint16_t xn[8];                      // blocks of XCD x
     uint16_t xstart[9];                  // its chunks: chunk[xstart[x]] .. chunk[xstart[x + 1] - 1]
@@ -1372,31 +1428,14 @@ void gemm_bf16_dtl_group(const GemmGroupArgs grp) {
 }
 
 // FP32: 64 x 64 tiles, batch 1, one split count for the group. Split-K partial sums go to each
-// problem's own region; splitk_reduce4_group then sums every problem's in one launch.
+// problem's own region, and each tile's last block to arrive adds its splits and finishes it.
 template <bool TA, bool TB, int LM>
 __global__ __launch_bounds__(NTHREADS) void gemm_f32_group(const GemmGroupArgs grp) {
     __shared__ __attribute__((aligned(16))) char smem[mfma_smem_bytes<float, TA, TB, 64, 64>()];
     int gi, split, tile;
     if (!group_block(grp, gi, split, tile)) return;
-    gemm_mfma_block<float, TA, TB, 64, 64, 2, 2, false, LM, false, 2>(grp.g[gi], tile, split, smem);
-}
-
-// The split-K sums of an FP32 group (N % 4 == 0 for every problem with splits): vector e of the
-// group belongs to problem g when rstart[g] <= e < rstart[g + 1]; each sums its splits in order, as
-// splitk_reduce4 does.
-__global__ __launch_bounds__(256) void splitk_reduce4_group(const GemmGroupArgs grp) {
-    const int64_t total4 = grp.rstart[grp.count];
-    for (int64_t e4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e4 < total4;
-         e4 += (int64_t)gridDim.x * blockDim.x) {
-        int gi = 0;
-        while (gi + 1 < grp.count && e4 >= grp.rstart[gi + 1]) ++gi;
-        const GemmArgs &p = grp.g[gi];
-        const int64_t mn = p.M * p.N, e = (e4 - grp.rstart[gi]) * 4;
-        const int64_t row = e / p.N, col = e % p.N;
-        f32x4 s = {0.f, 0.f, 0.f, 0.f};
-        for (int sp = 0; sp < p.splits; ++sp) s += *(const f32x4 *)(p.partial + (int64_t)sp * mn + e);
-        finish4<false, true>(p, s, row, col, 0, 0);
-    }
+    gemm_mfma_block<float, TA, TB, 64, 64, 2, 2, false, LM, false, 2, false, true>(grp.g[gi], tile, split, smem,
+                                                                                grp.arrive + grp.cstart[gi] + tile);
 }
 
 // Deterministic split-K reduction: partial sums are added in split order.
@@ -1986,8 +2025,8 @@ std::string group_key(const char *form, const GemmArgs *args, int count, const c
 }
 
 // FP32 calls of one layout: one gemm_f32_group launch (64 x 64 tiles, one split count for the
-// group) and one splitk_reduce4_group where the planner's model prices them below the separate
-// plans; false if they do not qualify or do not pay (nothing launched then).
+// group; each tile's last split block adds the partial sums) where the planner's model prices it
+// below the separate plans; false if they do not qualify or do not pay (nothing launched then).
 bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int count, const char *tag,
                       it_status *status) {
     constexpr int bk = ET<float>::BK;
@@ -2028,7 +2067,7 @@ bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int cou
         const double eff = conc == 1 ? 0.9 * eff0 : eff0;
         const double step = 2.0 * 64 * 64 * bk / (cu_peak * eff);
         double t = rounds * (3e-6 + ksteps * std::max(conc * step, 0.5e-6));
-        if (traffic > 0.0) t += traffic / 4e12 + 4e-6;
+        if (traffic > 0.0) t += traffic / 4e12 + 4e-6;  // partial sums out and back, the tiles' last-block sums
         if (t < best_t) {
             best_t = t;
             best_s = s;
@@ -2044,8 +2083,8 @@ bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int cou
     if (!best_s || best_t >= 0.97 * separate) return false;
     GemmGroupArgs grp{};
     grp.count = count;
-    int64_t r4 = 0, scratch = 0;
-    bool exact = true, masked = true, rsrc = true;
+    int64_t scratch = 0, tiles = 0;
+    bool split_any = false, exact = true, masked = true, rsrc = true;
     for (int i = 0; i < count; ++i) {
         GemmArgs &a = grp.g[i];
         a = args[i];
@@ -2054,18 +2093,26 @@ bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int cou
         a.k_per_split = best_s > 1 ? kps : cdiv(a.K, bk) * bk;
         a.tiles_m = (int)cdiv(a.M, 64);
         a.tiles_n = (int)cdiv(a.N, 64);
-        grp.rstart[i] = r4;
+        grp.cstart[i] = (int)tiles;
+        tiles += (int64_t)a.tiles_m * a.tiles_n;
         if (a.splits > 1) {
-            r4 += a.M * a.N / 4;
+            // the in-kernel sum addresses a problem's partials with 32-bit byte offsets
+            if ((int64_t)a.splits * a.M * a.N * 4 >= (1ll << 31)) return false;
+            split_any = true;
             scratch += (int64_t)a.splits * a.M * a.N;
         }
         exact = exact && tiles_exact(a, 64, 64, bk);
         masked = masked && vectors_exact<float>(a, ta, tb);
         rsrc = rsrc && load_mode_for<float>(a, ta, tb, 64, 64) != LOAD_MASKED && rsrc_ok(a, ta, tb);
     }
-    grp.rstart[count] = r4;
+    if (tiles > COUNTERS) return false;
+    grp.cstart[count] = (int)tiles;
     const int grid_blocks = xcd_schedule(grp);
     if (!grid_blocks) return false;
+    if (split_any) {
+        *status = ensure_counters(ctx, &grp.arrive);
+        if (*status != IT_OK) return true;
+    }
     if (scratch > 0) {
         void *ws = nullptr;
         *status = ensure_scratch(ctx, (size_t)scratch * sizeof(float), &ws);
@@ -2099,12 +2146,7 @@ bool launch_f32_group(it_context *ctx, bool ta, bool tb, GemmArgs *args, int cou
     else if (rsrc) go(std::integral_constant<int, LOAD_RSRC>{});
     else if (masked) go(std::integral_constant<int, LOAD_MASKED>{});
     else go(std::integral_constant<int, LOAD_CHECKED>{});
-    hipError_t e = hipGetLastError();
-    if (e == hipSuccess && r4 > 0) {
-        const int64_t blocks = std::min<int64_t>(cdiv(r4, 256), 65536);
-        hipLaunchKernelGGL(splitk_reduce4_group, dim3((unsigned)blocks), dim3(256), 0, ctx->stream, grp);
-        e = hipGetLastError();
-    }
+    const hipError_t e = hipGetLastError();
     *status = e == hipSuccess ? IT_OK : fail_hip(e, "gemm group launch");
     if (ctx->profiling && *status == IT_OK) profile_end(ctx, key, ev);
     return true;

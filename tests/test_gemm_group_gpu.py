@@ -184,3 +184,44 @@ def test_group_f32_ragged(it, oracle):
     for ga, gb, *_, o in gauss:
         ref = oracle.gemm_f32(np.ascontiguousarray(ga.T), gb)
         assert normwise_rel(o.numpy(), ref) <= FP32_TOL, o.shape()
+
+
+def test_group_f32_graph_replays(it):
+    """The FP32 group (split K summed by each tile's last block through the arrival counters),
+    captured and replayed three times with eager groups of other operands on the same counters
+    between the replays: every replay equals the eager result bit for bit, so each launch leaves
+    the counters at zero."""
+    import ctypes as C
+    from irontensor_amd import _lib
+    k = 4096
+    ops = []
+    for i, (m, n) in enumerate(TINY_DW):
+        a, b = synth.small_ints(700 + i, (k, m), -2, 2), synth.small_ints(710 + i, (k, n), -2, 2)
+        ops.append((it.Tensor.from_f32_slice(a, a.shape), it.Tensor.from_f32_slice(b, b.shape), it.Tensor.zeros([m, n])))
+    calls = [(a, b, o, True, False) for a, b, o in ops]
+    it.gemm_group(calls)  # eager first: sizes the scratch and allocates the counters
+    ref = [o.numpy() for *_, o in ops]
+    other = []
+    for i, (m, n) in enumerate(TINY_DW):
+        a, b = synth.small_ints(720 + i, (k, m), -2, 2), synth.small_ints(730 + i, (k, n), -2, 2)
+        other.append((it.Tensor.from_f32_slice(a, a.shape), it.Tensor.from_f32_slice(b, b.shape), it.Tensor.zeros([m, n])))
+    other_calls = [(a, b, o, True, False) for a, b, o in other]
+    ctx = it.Context.global_()
+    ctx.sync()
+    assert ctx.lib.it_capture_begin(ctx.handle) == 0
+    it.gemm_group(calls)
+    graph = C.c_void_p()
+    assert ctx.lib.it_capture_end(ctx.handle, C.byref(graph)) == 0, _lib.last_error()
+    try:
+        for rep in range(3):
+            for *_, o in ops:
+                zero = np.zeros(o.shape(), np.float32)
+                ctx.lib.it_memcpy_h2d(ctx.handle, C.c_void_p(o.ptr), zero.ctypes.data_as(C.c_void_p), zero.nbytes)
+            keys = _keys(it, lambda: it.gemm_group(other_calls))  # eager group on the same counters
+            assert len(keys) == 1 and "_group" in keys[0], keys
+            assert ctx.lib.it_graph_launch(ctx.handle, graph) == 0
+            ctx.sync()
+            for (*_, o), r in zip(ops, ref):
+                assert np.array_equal(o.numpy(), r), rep
+    finally:
+        ctx.lib.it_graph_destroy(graph)
