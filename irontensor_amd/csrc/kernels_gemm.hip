@@ -1489,6 +1489,11 @@ bool tiles_exact(const GemmArgs &a, int bm, int bn, int bk) {
 
 // The FP32 256 x 128 tile (one block per CU, 64 x 128 accumulators per wave): plain products with a
 // k-contiguous A (X.W and X.W^T) on whole tiles and whole k-tiles.
+// The FP32 64 x 32 tile: plain products (any layout).
+bool f32_6432_applicable(const GemmArgs &a) {
+    return !a.dual && !a.xent_stats && !a.a_kscale && a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL;
+}
+
 bool f32_256_applicable(bool ta, const GemmArgs &a) {
     return !ta && !a.dual && !a.xent_stats && !a.a_kscale && !a.swiglu_bwd && !a.rope_table &&
            a.causal == CAUSAL_NONE && a.kmode == KMODE_FULL && tiles_exact(a, 256, 128, ET<float>::BK);
@@ -1563,6 +1568,12 @@ void launch_cfg_lm(const TileCfg &cfg, const GemmArgs &a, dim3 grid, hipStream_t
     if constexpr (sizeof(T) == 4 && !TA && !DUAL && !KS && LM == LOAD_EXACT) {
         if (cfg.bm == 256) {
             hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 256, 128, 2, 2, DUAL, LM, KS, 1>), grid, dim3(NTHREADS), 0, s, a);
+            return;
+        }
+    }
+    if constexpr (sizeof(T) == 4 && !DUAL && !KS) {
+        if (cfg.bm == 64 && cfg.bn == 32) {
+            hipLaunchKernelGGL((gemm_mfma<T, TA, TB, 64, 32, 2, 2, DUAL, LM, KS, PF64>), grid, dim3(NTHREADS), 0, s, a);
             return;
         }
     }
@@ -1704,7 +1715,10 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
     // splits: 274 us against 291-302 us for the best 64 x 64 plans), with a per-round cost that
     // covers its 128 KB epilogue (the LM-head forward, 8 rounds of 8 k-steps: 361 us). Offered for
     // long k ranges only (32 k-steps per split or more), where it measured faster.
-    const Cand f32c[] = {{128, 0, 2, 0.50}, {64, 0, 4, 0.60}, {256, 128, 1, 0.87}};
+    // FP32 64 x 32 (plain products): two blocks per CU where the 64 x 64 tiles leave one, e.g. the
+    // TINY step's [4096, 256, K] GEMMs (3-7% faster at K 256-1376); the model prices it at the 64 x 64
+    // tile's efficiency.
+    const Cand f32c[] = {{128, 0, 2, 0.50}, {64, 0, 4, 0.60}, {256, 128, 1, 0.87}, {64, 32, 4, 0.60}};
     constexpr double F32_256_ROUND = 14e-6;
     constexpr int64_t F32_256_MIN_KSTEPS = 32;
     // 256 x 128 exists only as the direct-to-LDS kernel (eff 0: skipped where that does not apply).
@@ -1724,7 +1738,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
     constexpr double DTL128_FLOOR = 0.35e-6;
     const double DTL_HALF_EFF = ta ? 0.42 : 0.52;
     const Cand *cands = bf16 ? b16c : f32c;
-    const int ncand = bf16 ? 4 : 3;
+    constexpr int ncand = 4;
     const int bk = bf16 ? ET<uint16_t>::BK : ET<float>::BK;
     const double cu_peak = (bf16 ? 2.5e15 : 157.3e12) / 256.0;  // FLOP/s per CU
     const double round_overhead = 3e-6, reduce_launch = 4e-6, partial_bw = 4e12;
@@ -1772,6 +1786,7 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
                 if (!f32_256_applicable(ta, d) || ksteps < F32_256_MIN_KSTEPS) continue;
                 ro = F32_256_ROUND;
             }
+            if (!bf16 && cd.bn == 32 && !f32_6432_applicable(d)) continue;
             // The register-staged BF16 64 x 64 tile with one block per CU (1024^3: 16 k-steps on 256
             // CUs) measured 0.4 / 0.6 / 0.85 us per k-step for NT / NN / transposed A (9.6 / 13.0 /
             // 16.4 us), not the 1 us floor of the larger tiles' loads.
@@ -1787,10 +1802,11 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
             double t = rounds * (ro + ksteps * std::max(conc * step, floor));
             if (splits > 1) t += 2.0 * splits * a.M * a.N * a.batch * 4.0 / partial_bw + reduce_launch;
             // Near ties (3%) keep the earlier, larger and less split plan, except that between two
-            // unsplit plans the one with more blocks wins (more loads in flight per k-step).
+            // unsplit plans the one with more blocks wins (more loads in flight per k-step); the
+            // FP32 64 x 32 tile has to win outright.
             const bool better = t < best_t * 0.97;
             const bool tie_more_blocks = t < best_t * 1.03 && splits == 1 && best.splits == 1 &&
-                                         blocks > best_blocks;
+                                         blocks > best_blocks && cd.bn != 32;
             if (better || tie_more_blocks) {
                 best_t = better ? t : std::min(t, best_t);
                 best = Plan{cd.b, bn, (int)splits, splits > 1 ? kps : 0};
@@ -1891,6 +1907,8 @@ it_status launch_gemm(it_context *ctx, it_dtype dtype_in, bool transA, bool tran
     // planner offers it for nothing else).
     if (!bf16 && cfg.bm == 256 && (cfg.bn != 128 || !f32_256_applicable(transA, a)))
         return fail(IT_ERR_INVALID, "it_gemm: no FP32 256-row tile for this product");
+    if (!bf16 && !a.dual && cfg.bn == 32 && (cfg.bm != 64 || !f32_6432_applicable(a)))
+        return fail(IT_ERR_INVALID, "it_gemm: no FP32 64 x 32 tile for this product");
     if (splits > 1) {
         void *ws = nullptr;
         it_status st = ensure_scratch(ctx, (size_t)splits * a.batch * a.M * a.N * sizeof(float), &ws);

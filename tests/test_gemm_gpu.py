@@ -766,3 +766,30 @@ def test_f32_256_tile_exact(it, tb):
     assert keys[0].startswith("gemm_f32_N") and "_256x128|" in keys[0] and not keys[0].endswith(" s1"), keys
     ref = x.astype(np.float64) @ (w.T if tb else w).astype(np.float64)  # exact: integers below 2^53
     assert np.array_equal(out.numpy(), (2 * ref + bias).astype(np.float32))
+
+
+@pytest.mark.parametrize("m,n,k,lay", [(4096, 256, 1376, "NN"), (4096, 256, 688, "NT"), (4096, 256, 256, "NN"),
+                                       (4000, 250, 700, "NT"), (4000, 250, 700, "TN"), (1000, 90, 300, "NN")])
+def test_f32_64x32_tile_exact(it, m, n, k, lay):
+    """FP32 GEMMs the planner runs on the 64 x 32 tile (two blocks per CU where 64 x 64 tiles leave
+    one): the TINY step's [4096, 256, K] data gradients and projections, and ragged shapes (masked or
+    bounds-checked loads at every edge). Exact on small integers against a float64 product, with
+    alpha and a bias in the epilogue; the TINY shapes' plan key names the tile."""
+    from irontensor_amd import profiler
+    ta, tb = lay[0] == "T", lay[1] == "T"
+    a = synth.small_ints(840 + m % 7, (k, m) if ta else (m, k), -3, 3)
+    b = synth.small_ints(841 + n % 7, (n, k) if tb else (k, n), -3, 3)
+    bias = synth.small_ints(842, (n,), -4, 4)
+    A, B = it.Tensor.from_f32_slice(a, list(a.shape)), it.Tensor.from_f32_slice(b, list(b.shape))
+    out = it.Tensor.zeros([m, n])
+    ctx = it.Context.global_()
+    profiler.reset(ctx)
+    profiler.enable(ctx)
+    it.gemm(A, B, trans_a=ta, trans_b=tb, out=out, alpha=2.0, bias=it.Tensor.from_f32_slice(bias, [n]))
+    keys = list(profiler.stats(ctx))
+    profiler.enable(ctx, False)
+    print(f"[f32 64x32] {m}x{n}x{k} {lay} {keys}", flush=True)
+    if m == 4096:
+        assert "_64x32|" in keys[0], keys
+    ref = op(a, ta).astype(np.float64) @ (b.T if tb else b).astype(np.float64)
+    assert np.array_equal(out.numpy(), (2 * ref + bias).astype(np.float32))
