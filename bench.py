@@ -733,7 +733,7 @@ def main() -> int:
     ap.add_argument("--train-only", action="store_true",
                     help="run only the complete TINY training step, graph-replayed (for kernel traces)")
     ap.add_argument("--bf16-square", action="store_true",
-                    help="run only the BF16 4096^3 and 8192^3 GEMMs, NN/NT/TN (for rocprofv3 --pmc)")
+                    help="run only the BF16 4096^3, 8192^3 and 16384^3 GEMMs, NN/NT/TN (for rocprofv3 --pmc)")
     ap.add_argument("--medium-step", action="store_true",
                     help="run only config 4, the medium BF16 step (graph replay, single stream, and one "
                          "profiled eager step; for rocprofv3)")
@@ -784,8 +784,8 @@ def main() -> int:
                 "sha256": hashlib.sha256(lib_path.read_bytes()).hexdigest()}
     log(f"[bench] library {lib_info}")
     if args.bf16_square:
-        print(json.dumps(bf16_square(it, Timer(ctx), ((4096, args.steps), (8192, max(1, args.steps // 4))))),
-              flush=True)
+        print(json.dumps(bf16_square(it, Timer(ctx), ((4096, args.steps), (8192, max(1, args.steps // 4)),
+                                                      (16384, max(1, args.steps // 16))))), flush=True)
         return 0
     if args.attention:
         out = attention_only(it, Timer(ctx), args.steps)
