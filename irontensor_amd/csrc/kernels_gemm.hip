@@ -1202,7 +1202,7 @@ __device__ __forceinline__ void dtl_epilogue(const GemmArgs &p, char *st0, char 
     __syncthreads();
     char *lo, *hi;  // this wave's staging for rows 0-63 and 64-127 of its 128 (FA = 2: 64 rows, lo)
     if constexpr (FA == 2) {
-        // st0 and st1 are consecutive stages: four 16 KB halves in their 64 KB
+        // two 16 KB halves in each of st0 (waves 0-1) and st1 (waves 2-3)
         lo = (wave < 2 ? st0 : st1) + (wave & 1) * HALF;
         hi = lo;
     } else if constexpr (FB == 4) {
@@ -1357,16 +1357,22 @@ void gemm_bf16_dtl(const GemmArgs p) {
     dtl_block<TA, TB, DUAL, FB>(p, blockIdx.x, blockIdx.y, st0, st1, st2);
 }
 
-// 128 x 128 tiles (64 x 64 per wave), DTL128_STAGES stages of 32 KB in one LDS object: for shapes
-// whose 256-wide tiles would leave CUs idle (2048^3: 256 tiles, one per CU, where 256 x 256 gives 64).
+// 128 x 128 tiles (64 x 64 per wave), four stages of 32 KB: for shapes whose 256-wide tiles would
+// leave CUs idle (2048^3: 256 tiles, one per CU, where 256 x 256 gives 64). Each stage is an LDS
+// object of its own: with the four in one object the compiler put a wait for every outstanding
+// direct load (vmcnt(0)) before each transposing fragment read (ds_read_b64_tr_b16), so the loads
+// of an mn-contiguous operand never ran ahead of the k-tile being multiplied.
 constexpr int DTL128_STAGES = 4;
 template <bool TA, bool TB>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_bf16_dtl128(const GemmArgs p) {
     constexpr int STAGE = 2 * 128 * 64 * 2;
-    __shared__ __attribute__((aligned(1024))) char st[DTL128_STAGES * STAGE];
-    dtl_block<TA, TB, false, 2, true, 2, DTL128_STAGES>(p, blockIdx.x, blockIdx.y, st, st + STAGE, st + 2 * STAGE,
-                                                        st + (DTL128_STAGES > 3 ? 3 : 0) * STAGE);
+    static_assert(DTL128_STAGES == 4, "four stage objects");
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st2[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st3[STAGE];
+    dtl_block<TA, TB, false, 2, true, 2, DTL128_STAGES>(p, blockIdx.x, blockIdx.y, st0, st1, st2, st3);
 }
 
 // Several independent GEMMs of one layout in one launch. Workgroup w runs on XCD w % 8, and each
@@ -1731,10 +1737,11 @@ Plan choose_plan(const GemmArgs &a, bool bf16, int64_t cus, bool ta, bool tb, do
     // 256 x 128, whose waves read 50% more LDS per MFMA (two transposed reads per fragment of a
     // transposed A: lower still), and whose third stage lowers the memory-latency floor.
     constexpr double DTL_EFF = 0.53, DTL_HALF_FLOOR = 0.85e-6;
-    // The 128 x 128 direct-to-LDS tile (four stages: three k-tiles of loads in flight). Measured
-    // (2048^3, one tile per CU): NT 23.6 us; NN and TN, whose transposed fragments take two reads
-    // each, 35-36 us, slower than their 256 x 128 split plans.
-    const double DTL128_EFF = !ta && tb ? 0.35 : 0.22;
+    // The 128 x 128 direct-to-LDS tile (four stages: three k-tiles of loads in flight), the same in
+    // every layout: 1024^3 11.5-11.8 us, 1280^3 13.9-14.1, 1536^3 15.9-16.3, 2048^3 (one tile per
+    // CU) 22.0-22.8 against 32-35 us for the 256 x 128 plans; 0.38 of the per-CU rate with the
+    // 3 us round cost fits them within 3%.
+    constexpr double DTL128_EFF = 0.38;
     constexpr double DTL128_FLOOR = 0.35e-6;
     const double DTL_HALF_EFF = ta ? 0.42 : 0.52;
     const Cand *cands = bf16 ? b16c : f32c;

@@ -556,11 +556,12 @@ def test_bf16_large_tile_ragged_batched(it, ta, tb):
     assert np.array_equal(c.numpy(), exact.astype(np.float32))
 
 
-@pytest.mark.parametrize("m,n,k", [(1024, 2816, 8192), (1000, 2800, 8010)])
+@pytest.mark.parametrize("m,n,k", [(5632, 1024, 8192), (1000, 2800, 8010)])
 def test_bf16_large_tile_split_k(it, m, n, k):
-    """Long-K weight-gradient shapes (the medium step's down.dW) take the 256x256 kernel with
-    split-K (exact and ragged); the profiler key shows the plan. Small integers: exact in BF16 and
-    in every FP32 summation order, checked against a float64 product."""
+    """Long-K weight-gradient shapes take a 256x256 kernel with split-K: whole tiles (the medium
+    step's up/gate dW, on the direct-to-LDS kernel) and ragged (the register-staged kernel); the
+    profiler key shows the plan. Small integers: exact in BF16 and in every FP32 summation order,
+    checked against a float64 product."""
     a = synth.small_ints(210, (k, m), -2, 2)
     b = synth.small_ints(211, (k, n), -2, 2)
     ta, tb = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
@@ -609,12 +610,12 @@ def test_bf16_uneven_tile_counts_exact(it, ta, tb, m, n, k):
     assert np.array_equal(c.numpy(), again.numpy())
 
 
-@pytest.mark.parametrize("ta,tb,m,n,k", [(0, 0, 4096, 1152, 1024), (0, 1, 4096, 1152, 2048), (1, 0, 1024, 896, 4096),
-                                         (1, 1, 4096, 1152, 256), (0, 0, 8192, 1024, 1024), (1, 0, 1024, 1024, 8192)])
+@pytest.mark.parametrize("ta,tb,m,n,k", [(0, 0, 4096, 1152, 1024), (0, 1, 4096, 1152, 2048), (1, 0, 1536, 1024, 8192),
+                                         (1, 1, 4096, 1152, 256), (0, 0, 8192, 1024, 1024)])
 def test_bf16_dtl_256x128_exact(it, ta, tb, m, n, k):
     """The 256 x 128 direct-to-LDS tile (each wave 128 x 64; B staged as 128 rows) in every
-    layout: N an odd multiple of 128 rules the 256 x 256 tile out, and the medium step's
-    N = 1024 data gradient and 1024 x 1024 weight gradient (split-K) take it to fill the CUs.
+    layout: N an odd multiple of 128 rules the 256 x 256 tile out, the medium step's N = 1024
+    data gradient takes it to fill the CUs, and a 1536 x 1024 weight gradient with split-K.
     Small integers are exact in any FP32 summation order: the result equals a float64 product
     bit for bit, and a second run repeats it."""
     a = synth.small_ints(250 + m, (k, m) if ta else (m, k), -2, 2)
@@ -722,25 +723,45 @@ def test_bf16_large_tile_epilogues(it, oracle):
     assert normwise_rel(y.numpy(), ref) <= FP32_TOL
 
 
+@pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
 @pytest.mark.parametrize("m,n,k", [(1536, 1536, 1536), (2048, 2048, 2048), (1920, 1280, 1344)])
-def test_bf16_nt_128_tile_exact(it, m, n, k):
-    """BF16 Y = X.W^T at shapes the planner runs on the 128 x 128 direct-to-LDS tile (four LDS
-    stages; 1344 = 21 k-tiles, an odd count): exact on small integers against an int64 product."""
+def test_bf16_128_tile_exact(it, m, n, k, layout):
+    """BF16 products at shapes the planner runs on the 128 x 128 direct-to-LDS tile (four LDS
+    stages; 1344 = 21 k-tiles, an odd count), in every layout (a transposed operand is read through
+    transposing LDS reads): exact on small integers against an int64 product."""
     from irontensor_amd import profiler
-    x = synth.small_ints(800 + m, (m, k), -3, 3)
-    w = synth.small_ints(801 + n, (n, k), -3, 3)
+    ta, tb = layout[0] == "T", layout[1] == "T"
+    x = synth.small_ints(800 + m, (k, m) if ta else (m, k), -3, 3)
+    w = synth.small_ints(801 + n, (n, k) if tb else (k, n), -3, 3)
     tx, tw = it.Tensor.from_f32_as_bf16(x, x.shape), it.Tensor.from_f32_as_bf16(w, w.shape)
     out = it.Tensor.zeros([m, n])
     ctx = it.Context.global_()
     profiler.reset(ctx)
     profiler.enable(ctx)
-    it.gemm(tx, tw, trans_b=True, out=out)
+    it.gemm(tx, tw, trans_a=ta, trans_b=tb, out=out)
     keys = list(profiler.stats(ctx))
     profiler.enable(ctx, False)
-    print(f"[bf16 nt 128] {keys}", flush=True)
+    print(f"[bf16 128 {layout}] {keys}", flush=True)
     assert "128x128_dtl" in keys[0], keys
-    ref = x.astype(np.int64) @ w.T.astype(np.int64)
+    ref = (x.T if ta else x).astype(np.int64) @ (w.T if tb else w).astype(np.int64)
     assert np.array_equal(out.numpy(), ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 1024, 8192), (512, 1024, 16384), (1024, 896, 4096)])
+def test_bf16_128_tile_split_k_exact(it, m, n, k):
+    """Long-K weight gradients (A transposed) whose 128 x 128 tiles are too few for the CUs run on
+    that tile with split-K (the medium step's 1024 x 1024 weight gradient, and 4-8 splits): exact on
+    small integers against a float64 product, and a second run repeats it (ordered reduction)."""
+    a = synth.small_ints(860 + m, (k, m), -2, 2)
+    b = synth.small_ints(861 + n, (k, n), -2, 2)
+    at, bt = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    c, keys = _plan_keys(it, lambda: it.gemm(at, bt, trans_a=True))
+    _log(f"[128 split-K exact] {m}x{n}x{k}: {keys}")
+    assert any("128x128_dtl" in key and not key.endswith(" s1") for key in keys), keys
+    exact = a.T.astype(np.float64) @ b.astype(np.float64)
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    again = it.gemm(at, bt, trans_a=True)
+    assert np.array_equal(c.numpy(), again.numpy())
 
 
 @pytest.mark.parametrize("tb", [False, True])
