@@ -728,7 +728,8 @@ def test_bf16_large_tile_epilogues(it, oracle):
 def test_bf16_128_tile_exact(it, m, n, k, layout):
     """BF16 products at shapes the planner runs on the 128 x 128 direct-to-LDS tile (four LDS
     stages; 1344 = 21 k-tiles, an odd count), in every layout (a transposed operand is read through
-    transposing LDS reads): exact on small integers against an int64 product."""
+    transposing LDS reads): exact on small integers against a float64 product (every partial sum is
+    an integer below 2^15, exact in float64 and in FP32)."""
     from irontensor_amd import profiler
     ta, tb = layout[0] == "T", layout[1] == "T"
     x = synth.small_ints(800 + m, (k, m) if ta else (m, k), -3, 3)
@@ -743,8 +744,30 @@ def test_bf16_128_tile_exact(it, m, n, k, layout):
     profiler.enable(ctx, False)
     print(f"[bf16 128 {layout}] {keys}", flush=True)
     assert "128x128_dtl" in keys[0], keys
-    ref = (x.T if ta else x).astype(np.int64) @ (w.T if tb else w).astype(np.int64)
+    ref = (x.T if ta else x).astype(np.float64) @ (w.T if tb else w).astype(np.float64)
     assert np.array_equal(out.numpy(), ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_bf16_128_tile_batched_exact(it, ta, tb):
+    """Batched BF16 products whose 128 x 128 tiles fill the CUs only across the batch (4 x 64
+    tiles of [1024, 1024, 1024]) run on the 128 x 128 direct-to-LDS tile in every layout, the batch
+    index on the grid's second axis: exact on small integers against a float64 product (exact at
+    these magnitudes), and a B shared by the whole batch (batch stride 0) gives the same result as
+    the B repeated."""
+    bt, m, n, k = 4, 1024, 1024, 1024
+    a = synth.small_ints(870, (bt, k, m) if ta else (bt, m, k), -3, 3)
+    b = synth.small_ints(871, (bt, n, k) if tb else (bt, k, n), -3, 3)
+    at, bt_ = it.Tensor.from_f32_as_bf16(a, a.shape), it.Tensor.from_f32_as_bf16(b, b.shape)
+    c, keys = _plan_keys(it, lambda: it.gemm(at, bt_, trans_a=bool(ta), trans_b=bool(tb)))
+    _log(f"[128 batched exact] ta={ta} tb={tb}: {keys}")
+    assert any("128x128_dtl" in key for key in keys), keys
+    exact = np.matmul(op(a, ta).astype(np.float64), op(b, tb).astype(np.float64))
+    assert np.array_equal(c.numpy(), exact.astype(np.float32))
+    b0 = b[0]
+    shared = it.gemm(at, it.Tensor.from_f32_as_bf16(b0, b0.shape), trans_a=bool(ta), trans_b=bool(tb))
+    exact0 = np.matmul(op(a, ta).astype(np.float64), op(b0, tb).astype(np.float64))
+    assert np.array_equal(shared.numpy(), exact0.astype(np.float32))
 
 
 @pytest.mark.parametrize("m,n,k", [(1024, 1024, 8192), (512, 1024, 16384), (1024, 896, 4096)])
