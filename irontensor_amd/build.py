@@ -3,6 +3,11 @@
 Usage: python -m irontensor_amd.build   (or irontensor_amd.build.build_library()).
 The compile always runs; objects go to irontensor_amd/_build/ and the shared library next to this
 file, so it travels with the repository snapshot to the GPU box.
+
+python -m irontensor_amd.build --tuning also builds libirontensor_hip_tuning.so: the same library
+with kernels_gemm.hip compiled under IT_TUNING, where the environment variable IT_PLAN="tile,
+splits[,width]" forces every GEMM's plan and IT_GROUP_SPLITS an FP32 group's split count (planner
+measurements only: load it with IRONTENSOR_LIB=...; nothing else uses it).
 """
 from __future__ import annotations
 
@@ -16,6 +21,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libirontensor_hip.so"
+TUNING_LIB = PKG / "libirontensor_hip_tuning.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["runtime.cpp", "api.cpp", "api_train.cpp", "kernels_gemm.hip", "kernels_misc.hip", "kernels_flash.hip",
@@ -63,6 +69,26 @@ def build_library(verbose: bool = False) -> Path:
         raise RuntimeError(f"link failed:\n{res.stdout}")
     os.replace(tmp, LIB)
     return LIB
+
+
+def build_tuning_library() -> Path:
+    """The library with kernels_gemm.hip under IT_TUNING (plans forced through IT_PLAN), linked with
+    the other objects of the last build_library()."""
+    tdir = BUILD / "tuning"
+    tdir.mkdir(parents=True, exist_ok=True)
+    obj = tdir / "kernels_gemm.hip.o"
+    cmd = [HIPCC, *HIP_FLAGS, "-DIT_TUNING", "-x", "hip", "-c", str(CSRC / "kernels_gemm.hip"), "-o", str(obj)]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed:\n{res.stdout}")
+    objs = [str(BUILD / (name + ".o")) for name in SOURCES if name != "kernels_gemm.hip"] + [str(obj)]
+    tmp = TUNING_LIB.with_suffix(".so.tmp")
+    res = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *objs],
+                         stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}")
+    os.replace(tmp, TUNING_LIB)
+    return TUNING_LIB
 
 
 CPP_TEST_SRC = ROOT / "tests" / "cpp" / "test_host_api.cpp"
@@ -138,3 +164,5 @@ def build_sanitized_host() -> Path:
 if __name__ == "__main__":
     print(build_library(verbose=True))
     print(build_cpp_tests())
+    if "--tuning" in sys.argv[1:]:
+        print(build_tuning_library())
